@@ -1,0 +1,139 @@
+/*
+ * pz_sampler.h -- C ABI of libpzsample.so, the MI355X (gfx950) token sampler.
+ *
+ * Two surfaces:
+ *   1. A batched, device-resident API (pz_*): [B, V] fp32 logits stay in HBM,
+ *      only int32 ids (and optionally p(chosen)) come back.  This replaces the
+ *      per-step hand-off at src/transformer/generate.c:143-174, where
+ *      transformer_forward() returns one host row of logits and the sampling
+ *      block picks one id.
+ *   2. The reference's own sampler symbols (pz_sampling_compat.h), so the
+ *      objects of src/sampling can be swapped for this library at link time.
+ *
+ * Conventions: every pz_* call returns 0 (PZ_OK) or a negative PZ_E* code,
+ * mirroring the project's TernaryError convention (include/core/error.h:4-31);
+ * no exception or longjmp crosses the ABI.  A pz_sampler owns one HIP stream,
+ * its scratch memory and pinned staging buffers; use one per host thread (the
+ * reference sampler, by contrast, is non-reentrant: src/sampling/top_p.c:22-28).
+ */
+#ifndef PZ_SAMPLER_H
+#define PZ_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Symbols of the ABI are the only ones the library exports. */
+#ifndef PZ_API
+#define PZ_API __attribute__((visibility("default")))
+#endif
+
+#define PZ_OK       0
+#define PZ_EINVAL  (-1) /* bad argument (NULL pointer, negative size, ...)    */
+#define PZ_ENOMEM  (-2) /* device or pinned allocation failed                 */
+#define PZ_EDEVICE (-3) /* HIP runtime error (launch, copy, sync)             */
+#define PZ_ERANGE  (-4) /* size above what the sampler was created for        */
+#define PZ_ENOTSUP (-5) /* request the build does not support                 */
+
+/* Temperature forms of src/sampling/temperature.c: the AVX-512 build
+ * multiplies by 1.0f/T (:11-20), the scalar build divides by T (:22-23).
+ * The default is PZ_TEMP_MUL_RECIP (reference built with -march=native on an
+ * AVX-512 host, the case on MI355X servers). */
+#define PZ_TEMP_MUL_RECIP 0
+#define PZ_TEMP_DIV       1
+
+typedef struct pz_sampler pz_sampler;
+
+/* Per-row sampling parameters.  Dispatch mirrors generate.c:145-169:
+ *   temperature <= 0 or < 1e-6          -> greedy argmax (argmax.c:3-13)
+ *   else temperature is applied, then
+ *     top_k > 0                         -> top-k (top_k.c:8-73), chained with
+ *                                          top-p over the k survivors when
+ *                                          0 < top_p < 1
+ *     else 0 < top_p < 1                -> top-p (top_p.c:30-108)
+ *     else                              -> softmax + ascending-id categorical
+ *                                          draw (generate.c:157-169)
+ * Penalties (absent from the reference; applied before temperature, only to
+ * ids of the row's history): repetition x>0 ? x/rep : x*rep once per distinct
+ * id (1.0 = off), then x -= (float)count*frequency + presence (0 = off). */
+typedef struct {
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  float rep_penalty;
+  float presence_penalty;
+  float frequency_penalty;
+} pz_row_params;
+
+/* Creates a sampler on `device` for batches of up to max_batch rows of up to
+ * max_vocab logits and histories of up to max_hist ids (max_hist <= 2048). */
+PZ_API int pz_sampler_create(pz_sampler **out, int max_batch, int max_vocab,
+                      int max_hist, int device);
+PZ_API void pz_sampler_destroy(pz_sampler *s);
+
+/* PZ_TEMP_MUL_RECIP or PZ_TEMP_DIV. */
+PZ_API int pz_sampler_set_temp_mode(pz_sampler *s, int mode);
+
+/* Last error message of this sampler ("" when none). */
+PZ_API const char *pz_sampler_last_error(const pz_sampler *s);
+
+/* The sampler's hipStream_t (as void*) for callers that order their own work
+ * against it. */
+PZ_API void *pz_sampler_stream(pz_sampler *s);
+
+/* Samples B rows.  d_logits: device [B, ld] fp32 (ld >= V), caller-owned and
+ * not modified.  params: host, n_params = 1 (shared) or B entries.  d_hist:
+ * device [B, H] int32 token history (NULL when H == 0); ids outside [0, V)
+ * are ignored.  u: host [B] uniforms in [0, 1], one per row, exactly as
+ * rng_float() would return them (unused by greedy rows).  ids_out: host [B].
+ * p_out: host [B] or NULL, receives p(chosen) in the distribution the draw
+ * used (1.0 for greedy).  Synchronous on the sampler's stream. */
+PZ_API int pz_sample_batch(pz_sampler *s, const float *d_logits, int B, int V,
+                    long ld, const pz_row_params *params, int n_params,
+                    const int32_t *d_hist, int H, const float *u,
+                    int32_t *ids_out, float *p_out);
+
+/* Asynchronous form: uniforms, ids and p are device pointers ([B] each,
+ * d_p_out may be NULL); the work is enqueued on the sampler's stream and the
+ * call returns without waiting.  params stay host-side (they select the
+ * kernels).  Wait with pz_sampler_sync(). */
+PZ_API int pz_sample_batch_async(pz_sampler *s, const float *d_logits, int B, int V,
+                          long ld, const pz_row_params *params, int n_params,
+                          const int32_t *d_hist, int H, const float *d_u,
+                          int32_t *d_ids_out, float *d_p_out);
+
+PZ_API int pz_sampler_sync(pz_sampler *s);
+
+/* Speculative-draft verification (Leviathan et al. 2023, Alg. 1; absent from
+ * the reference, whose plan is docs/architecture/IMPLEMENTATION_PLAN.md:
+ * 1664-1693).  For each sequence b and draft position j < K:
+ *   p = softmax(target[b,j] / temperature), q = softmax(draft[b,j] / temperature)
+ *   (temperature as apply_temperature, softmax as src/math/softmax.c:4-23);
+ *   accept draft_ids[b,j] iff u_acc[b,j] < p(d)/q(d) (q(d) == 0 rejects).
+ * On the first rejection a token is drawn from r = max(0, p - q) (ascending-id
+ * CDF of r, threshold u_res[b] * sum(r)); when sum(r) == 0 it is drawn from p
+ * with the categorical rule of generate.c:157-169.  If every draft is accepted
+ * and has_bonus, a bonus token is drawn from p of target row K with u_res[b].
+ *   d_target: device [B, K + has_bonus, ld] fp32;  d_draft: device [B, K, ld]
+ *   draft_ids, u_acc: host [B, K];  u_res: host [B]
+ *   acc_len_out: host [B] accepted count;  ids_out: host [B, K+1] accepted
+ *   drafts followed by the resampled / bonus token, -1 pads. */
+PZ_API int pz_spec_verify(pz_sampler *s, const float *d_target, const float *d_draft,
+                   int B, int K, int V, long ld, int has_bonus,
+                   float temperature, const int32_t *draft_ids,
+                   const float *u_acc, const float *u_res,
+                   int32_t *acc_len_out, int32_t *ids_out);
+
+/* Device memory helpers for C hosts (hipMalloc / hipFree / hipMemcpy). */
+PZ_API int pz_device_alloc(void **ptr, size_t bytes, int device);
+PZ_API int pz_device_free(void *ptr);
+PZ_API int pz_memcpy_h2d(void *dst, const void *src, size_t bytes);
+PZ_API int pz_memcpy_d2h(void *dst, const void *src, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PZ_SAMPLER_H */

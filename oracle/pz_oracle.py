@@ -1,0 +1,189 @@
+"""ctypes wrapper of the CPU oracle (libpzoracle.so) and of the reference
+sampler compiled from its own sources (_ref/libpzref_*.so).
+
+TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_LIB = os.path.join(HERE, "libpzoracle.so")
+REF_DIR = os.path.join(HERE, "_ref")
+
+TEMP_MUL_RECIP, TEMP_DIV = 0, 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_long
+_F = ctypes.c_float
+_ULL = ctypes.c_ulonglong
+_pULL = ctypes.POINTER(ctypes.c_ulonglong)
+
+PATH_ARGMAX, PATH_CATEGORICAL, PATH_TOPK, PATH_TOPP, PATH_CHAIN, PATH_TOPP_ARGMAX = range(6)
+
+
+class OrcInfo(ctypes.Structure):
+    _fields_ = [
+        ("p_chosen", ctypes.c_float),
+        ("dist_draw", ctypes.c_float),
+        ("dist_cut", ctypes.c_float),
+        ("cutoff", ctypes.c_int),
+        ("n_cand", ctypes.c_int),
+        ("trunc_sum", ctypes.c_float),
+        ("norm_sum", ctypes.c_float),
+        ("path", ctypes.c_int),
+    ]
+
+
+class OrcParams(ctypes.Structure):
+    _fields_ = [
+        ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_int),
+        ("top_p", ctypes.c_float),
+        ("rep_penalty", ctypes.c_float),
+        ("presence_penalty", ctypes.c_float),
+        ("frequency_penalty", ctypes.c_float),
+    ]
+
+
+def params(temperature=1.0, top_k=0, top_p=1.0, rep_penalty=1.0,
+           presence_penalty=0.0, frequency_penalty=0.0):
+    return OrcParams(temperature, top_k, top_p, rep_penalty, presence_penalty,
+                     frequency_penalty)
+
+
+def _np(a):
+    return a.ctypes.data_as(_P) if a is not None else None
+
+
+_orc = None
+
+
+def oracle():
+    global _orc
+    if _orc is not None:
+        return _orc
+    if not os.path.exists(ORACLE_LIB):
+        raise RuntimeError(f"{ORACLE_LIB} missing: run make -C oracle")
+    o = ctypes.CDLL(ORACLE_LIB)
+    o.orc_rng_seed.argtypes = [_pULL, _ULL]
+    o.orc_rng_seed.restype = None
+    o.orc_rng_float.argtypes = [_pULL]
+    o.orc_rng_float.restype = _F
+    o.orc_argmax.argtypes = [_P, _I]
+    o.orc_apply_temperature.argtypes = [_P, _I, _F, _I]
+    o.orc_apply_temperature.restype = None
+    o.orc_softmax.argtypes = [_P, _I]
+    o.orc_softmax.restype = None
+    o.orc_categorical.argtypes = [_P, _I, _F, ctypes.POINTER(OrcInfo)]
+    o.orc_top_k.argtypes = [_P, _I, _I, _F, ctypes.POINTER(OrcInfo)]
+    o.orc_top_p.argtypes = [_P, _I, _F, _F, ctypes.POINTER(OrcInfo)]
+    o.orc_penalties.argtypes = [_P, _I, _P, _I, _F, _F, _F]
+    o.orc_penalties.restype = None
+    o.orc_chain.argtypes = [_P, _I, _I, _F, _F, ctypes.POINTER(OrcInfo)]
+    o.orc_sample_row.argtypes = [_P, _I, ctypes.POINTER(OrcParams), _P, _I, _F, _I,
+                                 ctypes.POINTER(OrcInfo)]
+    o.orc_sample_batch.argtypes = [_P, _I, _I, _L, _P, _I, _P, _I, _P, _I, _P, _P, _P, _P]
+    o.orc_sample_batch.restype = None
+    o.orc_spec_verify.argtypes = [_P, _P, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P]
+    o.orc_spec_verify.restype = None
+    o.orc_expf.argtypes = [_F]
+    o.orc_expf.restype = _F
+    _orc = o
+    return o
+
+
+def sample_batch(x, params_list, u=None, hist=None, temp_mode=TEMP_MUL_RECIP):
+    """Oracle over a [B, V] float32 array.  Returns ids, p_chosen, dist_draw, dist_cut."""
+    x = np.ascontiguousarray(x, np.float32)
+    B, V = x.shape
+    if isinstance(params_list, OrcParams):
+        params_list = [params_list]
+    parr = (OrcParams * len(params_list))(*params_list)
+    u = np.zeros(B, np.float32) if u is None else np.ascontiguousarray(u, np.float32)
+    H = 0
+    if hist is not None:
+        hist = np.ascontiguousarray(hist, np.int32)
+        H = hist.shape[1]
+    ids = np.empty(B, np.int32)
+    pc = np.empty(B, np.float32)
+    dd = np.empty(B, np.float32)
+    dc = np.empty(B, np.float32)
+    oracle().orc_sample_batch(_np(x), B, V, V, parr, len(params_list), _np(hist), H, _np(u),
+                              temp_mode, _np(ids), _np(pc), _np(dd), _np(dc))
+    return ids, pc, dd, dc
+
+
+def sample_row(x, prm, u=0.0, hist=None, temp_mode=TEMP_MUL_RECIP):
+    x = np.ascontiguousarray(x, np.float32)
+    info = OrcInfo()
+    H = 0
+    if hist is not None:
+        hist = np.ascontiguousarray(hist, np.int32)
+        H = hist.shape[-1]
+    rid = oracle().orc_sample_row(_np(x), x.shape[-1], ctypes.byref(prm), _np(hist), H,
+                                  float(u), temp_mode, ctypes.byref(info))
+    return rid, info
+
+
+def spec_verify(target, draft, K, has_bonus, tau, draft_ids, u_acc, u_res,
+                temp_mode=TEMP_MUL_RECIP):
+    target = np.ascontiguousarray(target, np.float32)
+    draft = np.ascontiguousarray(draft, np.float32)
+    B = draft.shape[0] // K if draft.ndim == 2 else draft.shape[0]
+    V = draft.shape[-1]
+    acc = np.empty(B, np.int32)
+    out = np.empty((B, K + 1), np.int32)
+    dist = np.empty(B, np.float32)
+    oracle().orc_spec_verify(_np(target), _np(draft), B, K, V, int(has_bonus), tau, temp_mode,
+                             _np(np.ascontiguousarray(draft_ids, np.int32)),
+                             _np(np.ascontiguousarray(u_acc, np.float32)),
+                             _np(np.ascontiguousarray(u_res, np.float32)),
+                             _np(acc), _np(out), _np(dist))
+    return acc, out, dist
+
+
+# ---------------------------------------------------------------------------
+# The reference sampler compiled from its sources (oracle/Makefile `ref`).
+# ---------------------------------------------------------------------------
+def host_has_avx512():
+    try:
+        with open("/proc/cpuinfo") as f:
+            return " avx512f" in f.read()
+    except OSError:
+        return False
+
+
+def ref_lib_path(avx512=None):
+    if avx512 is None:
+        avx512 = host_has_avx512()
+    return os.path.join(REF_DIR, "libpzref_avx512.so" if avx512 else "libpzref_avx2.so")
+
+
+_refs = {}
+
+
+def ref(avx512=None):
+    """The reference sampler (.so built from its own C sources), or None."""
+    path = ref_lib_path(avx512)
+    if path in _refs:
+        return _refs[path]
+    if not os.path.exists(path):
+        return None
+    r = ctypes.CDLL(path)
+    r.rng_seed.argtypes = [_pULL, _ULL]
+    r.rng_seed.restype = None
+    r.rng_float.argtypes = [_pULL]
+    r.rng_float.restype = _F
+    r.sample_argmax.argtypes = [_P, _I]
+    r.apply_temperature.argtypes = [_P, _I, _F]
+    r.apply_temperature.restype = None
+    r.sample_top_p.argtypes = [_P, _I, _F, _pULL]
+    r.sample_top_k.argtypes = [_P, _I, _I, _pULL]
+    r.softmax.argtypes = [_P, _I]
+    r.softmax.restype = None
+    _refs[path] = r
+    return r

@@ -1,0 +1,360 @@
+// pz_sampler.hip -- host side of the C ABI (include/pz_sampler.h).
+//
+// Replaces the per-step hand-off of src/transformer/generate.c:143-174: the
+// engine keeps [B, V] logits in HBM and this dispatcher resolves each row's
+// sampling mode once (generate.c:151-169 order), groups rows by mode, and
+// launches one batched kernel per group on the sampler's stream.  Only ids
+// (and p(chosen)) travel back.
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include "../../include/pz_sampler.h"
+#include "pz_launch.h"
+#include "pz_params.h"
+
+namespace {
+
+constexpr int kTopKMax = 1024;  // top_k.c:6
+constexpr int kMaxHist = 2048;
+
+int next_pow2(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+}  // namespace
+
+struct pz_sampler {
+  int device = 0;
+  int max_batch = 0, max_vocab = 0, max_hist = 0;
+  int temp_mode = PZ_TEMP_MUL_RECIP;
+  int max_lds = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t staged = nullptr;  // guards reuse of the pinned staging area
+
+  // pinned host staging and their device mirrors
+  pz_row_params_dev* h_params = nullptr;
+  pz_row_params_dev* d_params = nullptr;
+  int32_t* h_rows = nullptr;
+  int32_t* d_rows = nullptr;
+  float* h_u = nullptr;
+  float* d_u = nullptr;
+  int32_t* h_ids = nullptr;
+  int32_t* d_ids = nullptr;
+  float* h_p = nullptr;
+  float* d_p = nullptr;
+
+  void* d_scratch = nullptr;
+  size_t scratch_bytes = 0;
+
+  pz_row_params_dev* res_params = nullptr;  // host work area (max_batch)
+  int staged_n = -1, staged_B = -1;         // what d_params / d_rows hold
+
+  char err[512] = {0};
+};
+
+static int fail(pz_sampler* s, int code, const char* fmt, ...) {
+  if (s) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(s->err, sizeof(s->err), fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+#define PZ_HIP(s, expr)                                                      \
+  do {                                                                       \
+    hipError_t e_ = (expr);                                                  \
+    if (e_ != hipSuccess)                                                    \
+      return fail((s), PZ_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+// Scratch needed by the multi-pass kernels for a batch of rows of V logits.
+size_t pz_scratch_bytes_for(int max_batch, int max_vocab);
+
+extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
+                                 int max_hist, int device) {
+  if (!out || max_batch <= 0 || max_vocab <= 0 || max_hist < 0) return PZ_EINVAL;
+  if (max_hist > kMaxHist) return PZ_ERANGE;
+  *out = nullptr;
+  pz_sampler* s = new (std::nothrow) pz_sampler();
+  if (!s) return PZ_ENOMEM;
+  s->device = device;
+  s->max_batch = max_batch;
+  s->max_vocab = max_vocab;
+  s->max_hist = max_hist;
+  int rc = PZ_OK;
+  auto bail = [&](int code) {
+    pz_sampler_destroy(s);
+    return code;
+  };
+  if (hipSetDevice(device) != hipSuccess) return bail(PZ_EDEVICE);
+  if (hipDeviceGetAttribute(&s->max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock,
+                            device) != hipSuccess)
+    return bail(PZ_EDEVICE);
+  if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess)
+    return bail(PZ_EDEVICE);
+  if (hipEventCreateWithFlags(&s->staged, hipEventDisableTiming) != hipSuccess)
+    return bail(PZ_EDEVICE);
+  const size_t B = (size_t)max_batch;
+  if (hipHostMalloc((void**)&s->h_params, B * sizeof(pz_row_params_dev), 0) != hipSuccess ||
+      hipHostMalloc((void**)&s->h_rows, B * sizeof(int32_t), 0) != hipSuccess ||
+      hipHostMalloc((void**)&s->h_u, B * sizeof(float), 0) != hipSuccess ||
+      hipHostMalloc((void**)&s->h_ids, B * sizeof(int32_t), 0) != hipSuccess ||
+      hipHostMalloc((void**)&s->h_p, B * sizeof(float), 0) != hipSuccess)
+    return bail(PZ_ENOMEM);
+  if (hipMalloc((void**)&s->d_params, B * sizeof(pz_row_params_dev)) != hipSuccess ||
+      hipMalloc((void**)&s->d_rows, B * sizeof(int32_t)) != hipSuccess ||
+      hipMalloc((void**)&s->d_u, B * sizeof(float)) != hipSuccess ||
+      hipMalloc((void**)&s->d_ids, B * sizeof(int32_t)) != hipSuccess ||
+      hipMalloc((void**)&s->d_p, B * sizeof(float)) != hipSuccess)
+    return bail(PZ_ENOMEM);
+  s->res_params = new (std::nothrow) pz_row_params_dev[B];
+  if (!s->res_params) return bail(PZ_ENOMEM);
+  s->scratch_bytes = pz_scratch_bytes_for(max_batch, max_vocab);
+  if (s->scratch_bytes &&
+      hipMalloc(&s->d_scratch, s->scratch_bytes) != hipSuccess)
+    return bail(PZ_ENOMEM);
+  *out = s;
+  return rc;
+}
+
+extern "C" void pz_sampler_destroy(pz_sampler* s) {
+  if (!s) return;
+  // Teardown: errors here have no caller to report to.
+  if (s->stream) (void)hipStreamSynchronize(s->stream);
+  (void)hipFree(s->d_params);
+  (void)hipFree(s->d_rows);
+  (void)hipFree(s->d_u);
+  (void)hipFree(s->d_ids);
+  (void)hipFree(s->d_p);
+  (void)hipFree(s->d_scratch);
+  (void)hipHostFree(s->h_params);
+  (void)hipHostFree(s->h_rows);
+  (void)hipHostFree(s->h_u);
+  (void)hipHostFree(s->h_ids);
+  (void)hipHostFree(s->h_p);
+  if (s->staged) (void)hipEventDestroy(s->staged);
+  if (s->stream) (void)hipStreamDestroy(s->stream);
+  delete[] s->res_params;
+  delete s;
+}
+
+extern "C" int pz_sampler_set_temp_mode(pz_sampler* s, int mode) {
+  if (!s || (mode != PZ_TEMP_MUL_RECIP && mode != PZ_TEMP_DIV)) return PZ_EINVAL;
+  s->temp_mode = mode;
+  return PZ_OK;
+}
+
+extern "C" const char* pz_sampler_last_error(const pz_sampler* s) {
+  return s ? s->err : "null sampler";
+}
+
+extern "C" void* pz_sampler_stream(pz_sampler* s) { return s ? (void*)s->stream : nullptr; }
+
+extern "C" int pz_sampler_sync(pz_sampler* s) {
+  if (!s) return PZ_EINVAL;
+  PZ_HIP(s, hipStreamSynchronize(s->stream));
+  return PZ_OK;
+}
+
+// Resolves one row's host parameters into the kernel form (mode decided as
+// generate.c:151-169; clamps of temperature.c:10 and top_k.c:11-17).
+static pz_row_params_dev resolve(const pz_row_params& p, int V, int temp_mode) {
+  pz_row_params_dev d;
+  memset(&d, 0, sizeof(d));
+  d.rep_penalty = p.rep_penalty;
+  d.presence_penalty = p.presence_penalty;
+  d.frequency_penalty = p.frequency_penalty;
+  d.top_p = p.top_p;
+  float T = p.temperature;
+  if (T <= 0.0f || T < 1e-6f) {
+    d.mode = PZ_MODE_GREEDY;
+    T = 1.0f;
+  } else if (p.top_k > 0) {
+    d.mode = PZ_MODE_TOPK;
+  } else if (p.top_p < 1.0f && p.top_p > 0.0f) {
+    d.mode = PZ_MODE_TOPP;
+  } else {
+    d.mode = PZ_MODE_CATEGORICAL;
+  }
+  if (T < 1e-6f) T = 1e-6f;
+  d.temp = T;
+  d.inv_temp = 1.0f / T;
+  d.temp_div = temp_mode == PZ_TEMP_DIV;
+  int k = p.top_k;
+  if (k > V) k = V;
+  if (k <= 0) k = 1;
+  if (k > kTopKMax) k = kTopKMax;
+  d.top_k = k;
+  return d;
+}
+
+static bool penalty_active(const pz_row_params& p) {
+  return p.rep_penalty != 1.0f || p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f;
+}
+
+static bool needs_counts(const pz_row_params& p) {
+  return p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f;
+}
+
+typedef int (*pz_launcher)(const pz_launch&, int, const int32_t*);
+
+// Common body of the sync and async entry points.  Stages params (and, when
+// the batch mixes modes, a mode-grouped row list) through pinned memory and
+// launches one kernel per mode present.
+static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
+                    const pz_row_params* params, int n_params, const int32_t* d_hist,
+                    int H, const float* d_u, int32_t* d_ids, float* d_p) {
+  if (!s) return PZ_EINVAL;
+  if (!d_logits || !params || B < 0 || V <= 0 || ld < V) return fail(s, PZ_EINVAL, "bad logits/shape");
+  if (n_params != 1 && n_params != B) return fail(s, PZ_EINVAL, "n_params must be 1 or B");
+  if (B > s->max_batch) return fail(s, PZ_ERANGE, "B=%d > max_batch=%d", B, s->max_batch);
+  if (V > s->max_vocab) return fail(s, PZ_ERANGE, "V=%d > max_vocab=%d", V, s->max_vocab);
+  if (H < 0 || H > s->max_hist) return fail(s, PZ_ERANGE, "H=%d > max_hist=%d", H, s->max_hist);
+  if (H > 0 && !d_hist) return fail(s, PZ_EINVAL, "H>0 needs d_hist");
+  if (!d_ids) return fail(s, PZ_EINVAL, "null ids");
+  if (B == 0) return PZ_OK;
+
+  bool pen_any = false, counts_any = false;
+  int count[PZ_MODE_COUNT] = {0, 0, 0, 0};
+  pz_row_params_dev* res = s->res_params;
+  for (int i = 0; i < n_params; i++) {
+    res[i] = resolve(params[i], V, s->temp_mode);
+    if (H > 0 && penalty_active(params[i])) {
+      pen_any = true;
+      counts_any |= needs_counts(params[i]);
+    }
+  }
+  for (int b = 0; b < B; b++) count[res[n_params == 1 ? 0 : b].mode]++;
+  if (!d_u) {
+    for (int b = 0; b < B; b++)
+      if (res[n_params == 1 ? 0 : b].mode != PZ_MODE_GREEDY)
+        return fail(s, PZ_EINVAL, "sampling rows need uniforms");
+  }
+  int modes_present = 0;
+  for (int m = 0; m < PZ_MODE_COUNT; m++) modes_present += count[m] > 0;
+  int offset[PZ_MODE_COUNT] = {0, 0, 0, 0};
+  {
+    int acc = 0;
+    for (int m = 0; m < PZ_MODE_COUNT; m++) { offset[m] = acc; acc += count[m]; }
+  }
+  // Parameters (and the row grouping they imply) usually repeat from step to
+  // step: upload only when they changed, so back-to-back calls queue their
+  // kernels without a host wait.
+  const bool same = s->staged_n == n_params && s->staged_B == B &&
+                    memcmp(s->h_params, res, (size_t)n_params * sizeof(pz_row_params_dev)) == 0;
+  if (!same) {
+    // The previous staging copy must have left pinned memory first.
+    PZ_HIP(s, hipEventSynchronize(s->staged));
+    memcpy(s->h_params, res, (size_t)n_params * sizeof(pz_row_params_dev));
+    if (modes_present > 1) {
+      int fill[PZ_MODE_COUNT];
+      memcpy(fill, offset, sizeof(fill));
+      for (int b = 0; b < B; b++) s->h_rows[fill[res[n_params == 1 ? 0 : b].mode]++] = b;
+      PZ_HIP(s, hipMemcpyAsync(s->d_rows, s->h_rows, (size_t)B * sizeof(int32_t),
+                               hipMemcpyHostToDevice, s->stream));
+    }
+    PZ_HIP(s, hipMemcpyAsync(s->d_params, s->h_params,
+                             (size_t)n_params * sizeof(pz_row_params_dev),
+                             hipMemcpyHostToDevice, s->stream));
+    PZ_HIP(s, hipEventRecord(s->staged, s->stream));
+    s->staged_n = n_params;
+    s->staged_B = B;
+  }
+
+  pz_launch L;
+  L.logits = d_logits;
+  L.ld = ld;
+  L.V = V;
+  L.params = s->d_params;
+  L.n_params = n_params;
+  L.hist = H > 0 ? d_hist : nullptr;
+  L.H = H;
+  L.pen_any = pen_any;
+  L.hcap = counts_any ? next_pow2(2 * (H > 0 ? H : 1)) : 0;
+  L.u = d_u;
+  L.ids = d_ids;
+  L.p_out = d_p;
+  L.scratch = s->d_scratch;
+  L.scratch_bytes = s->scratch_bytes;
+  L.max_lds = s->max_lds;
+  L.stream = s->stream;
+
+  static const pz_launcher launchers[PZ_MODE_COUNT] = {
+      pz_launch_greedy, pz_launch_categorical, pz_launch_topk, pz_launch_topp};
+  for (int m = 0; m < PZ_MODE_COUNT; m++) {
+    if (!count[m]) continue;
+    const int32_t* rows = modes_present > 1 ? s->d_rows + offset[m] : nullptr;
+    const int rc = launchers[m](L, count[m], rows);
+    if (rc == -2) return fail(s, PZ_ENOTSUP, "sampling mode %d not supported for V=%d", m, V);
+    if (rc != 0) return fail(s, PZ_EDEVICE, "launch of mode %d failed: %s", m,
+                             hipGetErrorString(hipGetLastError()));
+  }
+  return PZ_OK;
+}
+
+extern "C" int pz_sample_batch_async(pz_sampler* s, const float* d_logits, int B, int V,
+                                     long ld, const pz_row_params* params, int n_params,
+                                     const int32_t* d_hist, int H, const float* d_u,
+                                     int32_t* d_ids_out, float* d_p_out) {
+  if (!s) return PZ_EINVAL;
+  PZ_HIP(s, hipSetDevice(s->device));
+  return dispatch(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u, d_ids_out, d_p_out);
+}
+
+extern "C" int pz_sample_batch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
+                               const pz_row_params* params, int n_params,
+                               const int32_t* d_hist, int H, const float* u,
+                               int32_t* ids_out, float* p_out) {
+  if (!s) return PZ_EINVAL;
+  if (!ids_out) return fail(s, PZ_EINVAL, "null ids_out");
+  if (B > s->max_batch) return fail(s, PZ_ERANGE, "B=%d > max_batch=%d", B, s->max_batch);
+  if (B <= 0) return B == 0 ? PZ_OK : fail(s, PZ_EINVAL, "B<0");
+  PZ_HIP(s, hipSetDevice(s->device));
+  const float* d_u = nullptr;
+  if (u) {
+    PZ_HIP(s, hipStreamSynchronize(s->stream));  // h_u may still be in flight
+    memcpy(s->h_u, u, (size_t)B * sizeof(float));
+    PZ_HIP(s, hipMemcpyAsync(s->d_u, s->h_u, (size_t)B * sizeof(float),
+                             hipMemcpyHostToDevice, s->stream));
+    d_u = s->d_u;
+  }
+  int rc = dispatch(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u, s->d_ids,
+                    p_out ? s->d_p : nullptr);
+  if (rc != PZ_OK) return rc;
+  PZ_HIP(s, hipMemcpyAsync(s->h_ids, s->d_ids, (size_t)B * sizeof(int32_t),
+                           hipMemcpyDeviceToHost, s->stream));
+  if (p_out)
+    PZ_HIP(s, hipMemcpyAsync(s->h_p, s->d_p, (size_t)B * sizeof(float),
+                             hipMemcpyDeviceToHost, s->stream));
+  PZ_HIP(s, hipStreamSynchronize(s->stream));
+  memcpy(ids_out, s->h_ids, (size_t)B * sizeof(int32_t));
+  if (p_out) memcpy(p_out, s->h_p, (size_t)B * sizeof(float));
+  return PZ_OK;
+}
+
+extern "C" int pz_device_alloc(void** ptr, size_t bytes, int device) {
+  if (!ptr) return PZ_EINVAL;
+  if (hipSetDevice(device) != hipSuccess) return PZ_EDEVICE;
+  return hipMalloc(ptr, bytes) == hipSuccess ? PZ_OK : PZ_ENOMEM;
+}
+
+extern "C" int pz_device_free(void* ptr) {
+  return hipFree(ptr) == hipSuccess ? PZ_OK : PZ_EDEVICE;
+}
+
+extern "C" int pz_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) == hipSuccess ? PZ_OK : PZ_EDEVICE;
+}
+
+extern "C" int pz_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) == hipSuccess ? PZ_OK : PZ_EDEVICE;
+}
