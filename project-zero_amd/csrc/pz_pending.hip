@@ -3,7 +3,6 @@
 #include "../../include/pz_sampler.h"
 
 size_t pz_scratch_bytes_for(int, int) { return 0; }
-int pz_launch_topk(const pz_launch&, int, const int32_t*) { return -2; }
 int pz_launch_topp(const pz_launch&, int, const int32_t*) { return -2; }
 int pz_launch_categorical(const pz_launch&, int, const int32_t*) { return -2; }
 extern "C" int pz_spec_verify(pz_sampler*, const float*, const float*, int, int, int, long, int,
