@@ -120,7 +120,7 @@ __device__ __forceinline__ uint32_t pz_hash(uint32_t id) {
 }
 
 template <int BLOCK>
-__device__ void pz_penalty_build(PzPenalty& P, char* lds, int V, int hcap,
+__device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V, int hcap,
                                  const int32_t* hist_row, int H,
                                  const pz_row_params_dev& prm) {
   const int tid = threadIdx.x;
@@ -186,6 +186,14 @@ __device__ __forceinline__ bool pz_pen_member(const PzPenalty& P, int i) {
 // the scalar build.  inv_t is 1.0f/T rounded on the host, t is T clamped.
 __device__ __forceinline__ float pz_temper(float x, const pz_row_params_dev& p) {
   return p.temp_div ? x / p.temp : x * p.inv_temp;
+}
+
+// Value the sampling chain sees for raw logit x of id i: penalties (when the
+// row has any), then temperature.
+__device__ __forceinline__ float pz_transform(const PzPenalty& P, const pz_row_params_dev& prm,
+                                              float x, int i) {
+  if (P.active && pz_pen_member(P, i)) x = pz_penalize(P, x, i);
+  return pz_temper(x, prm);
 }
 
 // ---------------------------------------------------------------------------

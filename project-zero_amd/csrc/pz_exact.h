@@ -1,0 +1,315 @@
+// pz_exact.h -- exact, parallel evaluation of a sequential fp32 sum of
+// non-negative terms:  s = 0; for i: s = fl(s + v_i)  (round to nearest even).
+//
+// The reference accumulates every normaliser and CDF this way, one term at a
+// time in fp32 (src/math/softmax.c:12-16, src/sampling/top_p.c:57-65 and
+// :80-105, src/transformer/generate.c:162-168).  With ~10^5 terms that sum
+// loses mass to swamping (up to ~3e-4 relative on a 128K-vocab row), so an
+// accurate parallel sum does not reproduce the reference's probabilities.
+//
+// Method.  While s stays inside one binade [2^E, 2^(E+1)) every fp32 value
+// there is a multiple of the grid G = ulp(s), so
+//     fl(s + v) = s + G * rne(v / G)
+// and the sequential sum is an INTEGER sum of per-term increments
+// inc(v) = rne(v / G), which can be scanned in parallel.  The two exceptions
+// are handled one element at a time with a real fp32 add:
+//   * a term that makes s leave its binade (the integer state reaches 2^24, or
+//     the term alone is at least 2^24 G), after which the grid doubles;
+//   * a term sitting exactly halfway between two grid points (a tie), whose
+//     rounding depends on the parity of the running state.
+// The state is (n, g): s = n * 2^(g - 150) with g = max(biased exponent, 1),
+// n < 2^24 (n >= 2^23 when g > 1).  Subnormals and the first normal binade
+// share g = 1, whose grid is 2^-149 for both.
+//
+// The scalar part compiles for host and device, so the CPU tests can check
+// pz_acc_add against plain fp32 addition.
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define PZ_HD __host__ __device__ __forceinline__
+#else
+#define PZ_HD static inline
+#endif
+
+PZ_HD uint32_t pz_fbits(float f) { return __builtin_bit_cast(uint32_t, f); }
+PZ_HD float pz_bitsf(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+struct PzAcc {
+  uint32_t n;  // integer state, < 2^24
+  uint32_t g;  // grid exponent: s = n * 2^(g - 150), g >= 1
+};
+
+enum { PZ_INC_PLAIN = 0, PZ_INC_TIE = 1, PZ_INC_BIG = 2 };
+
+PZ_HD PzAcc pz_acc_of(float s) {
+  const uint32_t b = pz_fbits(s);
+  const uint32_t e = b >> 23;
+  const uint32_t g = e > 1u ? e : 1u;
+  PzAcc a;
+  a.n = b - ((g - 1u) << 23);
+  a.g = g;
+  return a;
+}
+
+PZ_HD float pz_acc_value_ng(uint32_t n, uint32_t g) { return pz_bitsf(((g - 1u) << 23) + n); }
+PZ_HD float pz_acc_value(PzAcc a) { return pz_acc_value_ng(a.n, a.g); }
+
+// Increment of a term v >= 0 (finite) at grid exponent g.  *cls is PLAIN
+// (the increment is exact), TIE (v / G is exactly m + 1/2: the increment is m
+// and the caller rounds by parity) or BIG (v alone is >= 2^24 G: the sum
+// certainly leaves the binade; the increment is 0 and meaningless).
+PZ_HD uint32_t pz_inc(float v, uint32_t g, uint32_t* cls) {
+  const uint32_t b = pz_fbits(v);
+  const uint32_t ev = b >> 23;
+  uint32_t mv = b & 0x7fffffu;
+  uint32_t evb = 1u;
+  if (ev) {
+    mv |= 0x800000u;
+    evb = ev;
+  }
+  *cls = PZ_INC_PLAIN;
+  if (evb > g) {
+    *cls = PZ_INC_BIG;
+    return 0u;
+  }
+  const uint32_t k = g - evb;
+  if (k == 0u) return mv;
+  if (k > 25u) return 0u;
+  const uint32_t half = 1u << (k - 1u);
+  const uint32_t rem = mv & ((half << 1) - 1u);
+  if (rem == half) *cls = PZ_INC_TIE;
+  return (mv >> k) + (rem > half ? 1u : 0u);
+}
+
+// s = fl(s + v) on the integer state, v >= 0 finite.
+PZ_HD PzAcc pz_acc_add(PzAcc a, float v) {
+  if (a.g >= 255u) return a;  // +inf stays +inf
+  uint32_t cls;
+  uint32_t inc = pz_inc(v, a.g, &cls);
+  if (cls != PZ_INC_BIG) {
+    if (cls == PZ_INC_TIE) inc += (a.n + inc) & 1u;
+    const uint32_t m = a.n + inc;
+    if (m < (1u << 24)) {
+      PzAcc r;
+      r.n = m;
+      r.g = a.g;
+      return r;
+    }
+  }
+  // the sum leaves the binade: one real fp32 add (round to nearest even)
+  return pz_acc_of(pz_acc_value(a) + v);
+}
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#include <hip/hip_runtime.h>
+
+// ---------------------------------------------------------------------------
+// Wave64 building blocks (DPP row shifts + row broadcasts, gfx9 family).
+// ---------------------------------------------------------------------------
+#define PZ_DPP(v, ctrl, rmask) \
+  ((uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), (ctrl), (rmask), 0xf, false))
+
+// Inclusive prefix sum over the 64 lanes (lane 0 first).
+__device__ __forceinline__ uint32_t pz_wave_scan_u32(uint32_t v) {
+  v += PZ_DPP(v, 0x111, 0xf);  // row_shr:1
+  v += PZ_DPP(v, 0x112, 0xf);  // row_shr:2
+  v += PZ_DPP(v, 0x114, 0xf);  // row_shr:4
+  v += PZ_DPP(v, 0x118, 0xf);  // row_shr:8
+  v += PZ_DPP(v, 0x142, 0xa);  // row_bcast:15 -> rows 1, 3
+  v += PZ_DPP(v, 0x143, 0xc);  // row_bcast:31 -> rows 2, 3
+  return v;
+}
+
+__device__ __forceinline__ uint32_t pz_readlane_u32(uint32_t v, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+__device__ __forceinline__ float pz_readlane_f32(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ uint32_t pz_wave_sum_u32(uint32_t v) {
+  return pz_readlane_u32(pz_wave_scan_u32(v), 63);
+}
+
+// Inclusive prefix sum of floats over the lanes (any rounding: used only for
+// estimates).
+__device__ __forceinline__ float pz_wave_scan_f32(float v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float o = __shfl_up(v, off, 64);
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+
+// Comparison used to stop an accumulation: GT stops at the first element
+// whose running sum is > thr (the reference's `r < cdf`), GE at the first
+// whose running sum is >= thr (top_p.c:83 `cumulative >= top_p`).
+enum { PZ_STOP_NONE = 0, PZ_STOP_GT = 1, PZ_STOP_GE = 2 };
+
+__device__ __forceinline__ bool pz_stop_hit(float s, float thr, int mode) {
+  return mode == PZ_STOP_GT ? (thr < s) : (mode == PZ_STOP_GE ? (s >= thr) : false);
+}
+
+// Exact sequential accumulation of the 64*C terms a wave holds, lane-major
+// (element index lane*C + c), starting at element `start`.  st is
+// wave-uniform and is advanced past the processed terms.  With a stop mode,
+// returns the index of the first element whose running sum hits thr (st is
+// then the sum including it); otherwise, or when nothing hits, returns -1.
+// cum (optional, LDS or global) receives every processed running sum.
+template <int C>
+__device__ __forceinline__ int pz_wave_accumulate(PzAcc& st, const float (&v)[C], int start, float thr,
+                                  int stop_mode, float* cum) {
+  const int lane = threadIdx.x & 63;
+  int pos = start;
+  while (pos < 64 * C) {
+    uint32_t inc[C];
+    int first_flag = C;
+    uint32_t lsum = 0;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      const int idx = lane * C + c;
+      uint32_t cls = PZ_INC_PLAIN, i = 0;
+      if (idx >= pos) i = pz_inc(v[c], st.g, &cls);
+      if (cls != PZ_INC_PLAIN) {
+        if (first_flag == C) first_flag = c;
+        i = 0;
+      }
+      inc[c] = i;
+      if (first_flag == C) lsum += i;
+    }
+    const uint32_t incl = pz_wave_scan_u32(lsum);
+    const uint32_t excl = incl - lsum;
+    // this lane's first event: a flagged term, a binade exit, or a stop hit
+    uint32_t run = st.n + excl;
+    int ev = C, ev_kind = 0;
+    uint32_t ev_n = 0;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      const int idx = lane * C + c;
+      if (ev < C || idx < pos) continue;
+      if (c == first_flag) {
+        ev = c; ev_kind = 1; ev_n = run;
+        continue;
+      }
+      const uint32_t nr = run + inc[c];
+      if (nr >= (1u << 24)) {
+        ev = c; ev_kind = 1; ev_n = run;
+        continue;
+      }
+      run = nr;
+      if (stop_mode != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(run, st.g), thr, stop_mode)) {
+        ev = c; ev_kind = 2; ev_n = run;
+      }
+    }
+    const uint64_t ball = __ballot(ev < C);
+    const int L = ball ? (int)__builtin_ctzll(ball) : 64;
+    if (cum) {
+      // running sums of the terms before the first event (plus a stop hit)
+      uint32_t r2 = st.n + excl;
+#pragma unroll
+      for (int c = 0; c < C; c++) {
+        const int idx = lane * C + c;
+        if (idx < pos) continue;
+        const bool valid = lane < L || (lane == L && (c < ev || (c == ev && ev_kind == 2)));
+        if (!valid) continue;
+        r2 += inc[c];
+        cum[idx] = pz_acc_value_ng(r2, st.g);
+      }
+    }
+    if (!ball) {
+      st.n += pz_readlane_u32(incl, 63);
+      return -1;
+    }
+    const int cL = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(ev, L));
+    const int kind = __builtin_amdgcn_readlane(ev_kind, L);
+    const int idx = L * C + cL;
+    st.n = pz_readlane_u32(ev_n, L);
+    if (kind == 2) return idx;
+    float vv = v[0];
+#pragma unroll
+    for (int c = 1; c < C; c++)
+      if (c == cL) vv = v[c];
+    vv = pz_readlane_f32(vv, L);
+    st = pz_acc_add(st, vv);
+    const float sv = pz_acc_value(st);
+    if (cum && lane == 0) cum[idx] = sv;
+    if (stop_mode != PZ_STOP_NONE && pz_stop_hit(sv, thr, stop_mode)) return idx;
+    pos = idx + 1;
+  }
+  return -1;
+}
+
+// Per-segment record of a predicted-grid pass: the integer sum of the
+// segment's increments at grid g, and whether any term was a tie or BIG
+// (then the record is unusable).  Stored as d and gf = g | dirty << 8.
+__device__ __forceinline__ void pz_segment_record(const float (&v)[4], uint32_t g, bool valid,
+                                                  uint32_t* seg_d, uint32_t* seg_gf, int k) {
+  uint32_t s = 0;
+  bool dirty = false;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint32_t cls;
+    const uint32_t i = pz_inc(v[c], g, &cls);
+    dirty |= cls != PZ_INC_PLAIN;
+    s += i;
+  }
+  const uint32_t tot = pz_wave_sum_u32(valid ? s : 0u);
+  const bool any_dirty = __ballot(valid && dirty) != 0;
+  if ((threadIdx.x & 63) == 0) {
+    seg_d[k] = tot;
+    seg_gf[k] = g | (any_dirty ? 0x100u : 0u);
+  }
+}
+
+// Walk over segment records in order (one wave).  A record is used as is when
+// its grid equals the running state's grid, it is clean and the state stays
+// in the binade; every other segment is regenerated (regen(k, v) fills this
+// lane's 4 terms of segment k) and accumulated element by element.  With a
+// stop mode returns the global element index (k*256 + i) of the first hit,
+// else -1.  st is advanced accordingly.
+template <class Regen>
+__device__ __forceinline__ int pz_wave_walk(PzAcc& st, const uint32_t* seg_d, const uint32_t* seg_gf, int nseg,
+                            float thr, int stop_mode, Regen&& regen) {
+  const int lane = threadIdx.x & 63;
+  int k0 = 0;
+  while (k0 < nseg) {
+    const int k = k0 + lane;
+    uint32_t d = 0;
+    bool ok = false;
+    if (k < nseg) {
+      ok = seg_gf[k] == st.g;
+      d = ok ? seg_d[k] : 0u;
+    }
+    const uint32_t incl = pz_wave_scan_u32(d);
+    const uint32_t nend = st.n + incl;
+    bool bad = false;
+    if (k < nseg) {
+      bad = !ok || nend >= (1u << 24) ||
+            (stop_mode != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(nend, st.g), thr, stop_mode));
+    }
+    const uint64_t ball = __ballot(bad);
+    if (!ball) {
+      st.n += pz_readlane_u32(incl, 63);
+      k0 += 64;
+      continue;
+    }
+    const int L = (int)__builtin_ctzll(ball);
+    st.n += pz_readlane_u32(incl - d, L);
+    float v[4];
+    regen(k0 + L, v);
+    const int f = pz_wave_accumulate<4>(st, v, 0, thr, stop_mode, nullptr);
+    if (f >= 0) return (k0 + L) * 256 + f;
+    k0 += L + 1;
+  }
+  return -1;
+}
+
+// Grid exponent of the binade an estimate s >= 0 falls in.
+__device__ __forceinline__ uint32_t pz_grid_of(float s) {
+  const uint32_t e = __float_as_uint(s) >> 23;
+  return e > 1u ? e : 1u;
+}
+#endif

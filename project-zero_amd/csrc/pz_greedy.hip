@@ -30,6 +30,9 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
   PzPenalty P;
   pz_penalty_build<BLOCK>(P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
 
+  // top-p rows above the reference's vocabulary guard take argmax of the
+  // tempered row (top_p.c:33-34, after apply_temperature)
+  const bool temper = prm.mode == PZ_MODE_TOPP;
   float bv = -__builtin_inff();
   int bi = 0x7fffffff;
   const int tid = threadIdx.x;
@@ -59,6 +62,12 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
               if (nib & 8u) e3 = pz_penalize(P, e3, i + 3);
             }
           }
+          if (temper) {
+            e0 = pz_temper(e0, prm);
+            e1 = pz_temper(e1, prm);
+            e2 = pz_temper(e2, prm);
+            e3 = pz_temper(e3, prm);
+          }
           if (e0 > bv) { bv = e0; bi = i; }
           if (e1 > bv) { bv = e1; bi = i + 1; }
           if (e2 > bv) { bv = e2; bi = i + 2; }
@@ -69,12 +78,14 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
     for (int i = (n4 << 2) + tid; i < V; i += BLOCK) {
       float e = x[i];
       if (P.active && pz_pen_member(P, i)) e = pz_penalize(P, e, i);
+      if (temper) e = pz_temper(e, prm);
       if (e > bv) { bv = e; bi = i; }
     }
   } else {
     for (int i = tid; i < V; i += BLOCK) {
       float e = x[i];
       if (P.active && pz_pen_member(P, i)) e = pz_penalize(P, e, i);
+      if (temper) e = pz_temper(e, prm);
       if (e > bv) { bv = e; bi = i; }
     }
   }
@@ -83,6 +94,7 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
   if (tid == 0) {
     float x0 = x[0];
     if (P.active && pz_pen_member(P, 0)) x0 = pz_penalize(P, x0, 0);
+    if (temper) x0 = pz_temper(x0, prm);
     // argmax.c:4-5 starts from x[0]: a NaN there is never replaced; and if
     // nothing beats -inf the scan also ends on index 0.
     if (x0 != x0 || bi == 0x7fffffff) bi = 0;

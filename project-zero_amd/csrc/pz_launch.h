@@ -6,6 +6,23 @@
 
 #include "pz_params.h"
 
+// Device scratch owned by a sampler (carved from one allocation).
+constexpr int PZ_FB_SLOTS = 32;        // rows the top-p fallback kernel sorts at once
+constexpr int PZ_TOPP_MAX_V = 200000;  // top_p.c:27 (larger rows take argmax)
+
+struct pz_scratch {
+  float* row_stat;    // [max_batch][4] per-row values handed between kernels
+  int32_t* fb_list;   // [max_batch] rows queued for the top-p fallback
+  int32_t* counters;  // [16] queue counters
+  uint64_t* fb_keys;  // [PZ_FB_SLOTS][slot_n] sort buffers of the fallback
+  float* fb_cum;      // [PZ_FB_SLOTS][slot_n] running sums of the fallback
+  int slot_n;         // power of two >= min(max_vocab, PZ_TOPP_MAX_V)
+};
+
+// Bytes of scratch for a sampler of this size; with base != nullptr also
+// fills *out with the carved pointers.
+size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* out);
+
 struct pz_launch {
   const float* logits;  // device [B, ld] fp32, caller-owned, read-only
   long ld;              // row stride in elements
@@ -19,8 +36,7 @@ struct pz_launch {
   const float* u;       // device [B] uniforms
   int32_t* ids;         // device [B] sampled ids
   float* p_out;         // device [B] p(chosen) or nullptr
-  void* scratch;        // device scratch owned by the sampler
-  size_t scratch_bytes;
+  pz_scratch sc;         // device scratch owned by the sampler
   int max_lds;          // max dynamic LDS per workgroup on this device
   hipStream_t stream;
 };

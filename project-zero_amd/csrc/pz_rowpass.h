@@ -1,0 +1,171 @@
+// pz_rowpass.h -- streaming passes of one 1024-thread workgroup over one
+// logits row, shared by the kernels whose normaliser is a full-row sequential
+// fp32 sum (top-p, plain categorical, speculative verification).
+//
+// Layout: the row is walked in tiles of 4096 elements, one 128-bit load per
+// thread per tile; thread t of a tile holds elements 4t..4t+3.  A segment is
+// one wave's 256-element slice of a tile (segment k = tile*16 + wave), the
+// unit at which the exact-sum walk (pz_exact.h) keeps integer records.
+#pragma once
+#include "pz_device.h"
+#include "pz_exact.h"
+
+constexpr int PZ_RB = 1024;           // threads per row workgroup
+constexpr int PZ_TILE = PZ_RB * 4;    // elements per tile
+constexpr int PZ_SEG = 256;           // elements per segment
+constexpr int PZ_SEGS_PER_TILE = PZ_RB / 64;
+
+__host__ __device__ inline int pz_tiles(int V) { return (V + PZ_TILE - 1) / PZ_TILE; }
+__host__ __device__ inline int pz_nseg(int V) { return pz_tiles(V) * PZ_SEGS_PER_TILE; }
+
+// First element of this thread's 4 in tile t, and of this lane's 4 in segment k.
+__device__ __forceinline__ int pz_tile_e0(int t) { return t * PZ_TILE + 4 * (int)threadIdx.x; }
+__device__ __forceinline__ int pz_seg_e0(int k) {
+  return (k >> 4) * PZ_TILE + (k & 15) * PZ_SEG + 4 * ((int)threadIdx.x & 63);
+}
+
+// Raw logits of elements e0..e0+3 (e0 a multiple of 4); entries at or past V
+// read as 0.  Returns how many are < V.
+template <bool VEC, bool NT>
+__device__ __forceinline__ int pz_load4(const float* __restrict__ x, int V, int e0, float (&r)[4]) {
+  if (VEC && e0 + 3 < V) {
+    const pz_f4* p = reinterpret_cast<const pz_f4*>(x + e0);
+    const pz_f4 v = NT ? __builtin_nontemporal_load(p) : *p;
+    r[0] = v.x;
+    r[1] = v.y;
+    r[2] = v.z;
+    r[3] = v.w;
+    return 4;
+  }
+  int n = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    r[c] = 0.0f;
+    if (e0 + c < V) {
+      r[c] = x[e0 + c];
+      n++;
+    }
+  }
+  return n;
+}
+
+// One row as the sampling chain sees it: y_i = temperature(penalties(x_i)).
+template <bool VEC>
+struct PzRow {
+  const float* x;
+  int V;
+  PzPenalty P;
+  const pz_row_params_dev* prm;
+
+  __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
+    const int n = pz_load4<VEC, false>(x, V, e0, y);
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (c < n) y[c] = pz_transform(P, *prm, y[c], e0 + c);
+    return n;
+  }
+};
+
+// A plain row scaled by temperature only (speculative verification).
+template <bool VEC>
+struct PzTempRow {
+  const float* x;
+  int V;
+  const pz_row_params_dev* prm;
+
+  __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
+    const int n = pz_load4<VEC, false>(x, V, e0, y);
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (c < n) y[c] = pz_temper(y[c], *prm);
+    return n;
+  }
+};
+
+struct PzPass1Shared {
+  float red[PZ_RB / 64];
+  int any_nan;
+  float y0;
+};
+
+// Pass 1 (the one compulsory HBM read of the row): the row maximum (NaN
+// ignored, as the reference's strict '>' scans do), whether any y is NaN,
+// y[0], and per segment k an estimate seg_m[k] = max, seg_s[k] =
+// sum exp(y - seg_m[k]) (hardware exp: estimates only, used to predict the
+// binade of the running sum).  Returns the maximum in every thread.
+template <int U, class Row>
+__device__ __forceinline__ float pz_pass1(const Row& row, int ntiles, float* seg_m, float* seg_s,
+                          PzPass1Shared& S) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  if (tid == 0) S.any_nan = 0;
+  float tmax = -__builtin_inff();
+  bool nan = false;
+  for (int t0 = 0; t0 < ntiles; t0 += U) {
+    float r[U][4];
+    int nv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      nv[u] = 0;
+      if (t0 + u < ntiles) nv[u] = row.get(pz_tile_e0(t0 + u), r[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int t = t0 + u;
+      if (t >= ntiles) continue;
+      float lm = -__builtin_inff();
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if (c >= nv[u]) continue;
+        const float y = r[u][c];
+        if (y != y) nan = true;
+        else lm = fmaxf(lm, y);
+      }
+      if (t == 0 && tid == 0) S.y0 = r[u][0];
+      tmax = fmaxf(tmax, lm);
+      const float sm = pz_wave_max(lm);
+      float s = 0.0f;
+      if (sm > -__builtin_inff() && sm < __builtin_inff()) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const float y = r[u][c];
+          if (c < nv[u] && y > -__builtin_inff()) s += __expf(y - sm);
+        }
+      }
+      s = pz_wave_sum(s);
+      if (lane == 0) {
+        seg_m[t * PZ_SEGS_PER_TILE + w] = sm;
+        seg_s[t * PZ_SEGS_PER_TILE + w] = s;
+      }
+    }
+  }
+  tmax = pz_wave_max(tmax);
+  if (__ballot(nan) && lane == 0) S.any_nan = 1;
+  if (lane == 0) S.red[w] = tmax;
+  __syncthreads();
+  float M = S.red[0];
+#pragma unroll
+  for (int i = 1; i < PZ_RB / 64; i++) M = fmaxf(M, S.red[i]);
+  return M;
+}
+
+// One wave: grid exponent of the estimated running sum at the start of each
+// segment, where segment k adds about scale * seg_s[k] * exp(seg_m[k] - M).
+// Writes seg_gf[k] and returns the estimated total.
+__device__ __forceinline__ float pz_predict_grids(const float* seg_m, const float* seg_s,
+                                                  int nseg, float M, float scale,
+                                                  uint32_t* seg_gf) {
+  const int lane = threadIdx.x & 63;
+  float carry = 0.0f;
+  for (int k0 = 0; k0 < nseg; k0 += 64) {
+    const int k = k0 + lane;
+    float a = 0.0f;
+    if (k < nseg) {
+      const float m = seg_m[k];
+      if (m > -__builtin_inff()) a = seg_s[k] * __expf(m - M) * scale;
+    }
+    const float incl = pz_wave_scan_f32(a);
+    if (k < nseg) seg_gf[k] = pz_grid_of(carry + (incl - a));
+    carry += pz_readlane_f32(incl, 63);
+  }
+  return carry;
+}

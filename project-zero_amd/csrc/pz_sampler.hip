@@ -52,6 +52,7 @@ struct pz_sampler {
 
   void* d_scratch = nullptr;
   size_t scratch_bytes = 0;
+  pz_scratch sc{};
 
   pz_row_params_dev* res_params = nullptr;  // host work area (max_batch)
   int staged_n = -1, staged_B = -1;         // what d_params / d_rows hold
@@ -76,8 +77,29 @@ static int fail(pz_sampler* s, int code, const char* fmt, ...) {
       return fail((s), PZ_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
 
-// Scratch needed by the multi-pass kernels for a batch of rows of V logits.
-size_t pz_scratch_bytes_for(int max_batch, int max_vocab);
+size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* out) {
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  int vt = max_vocab < PZ_TOPP_MAX_V ? max_vocab : PZ_TOPP_MAX_V;
+  int slot = 64;  // >= one wave's group of running sums
+  while (slot < vt) slot <<= 1;
+  const size_t B = (size_t)max_batch;
+  size_t off = 0;
+  const size_t o_stat = off; off = up(off + B * 4 * sizeof(float));
+  const size_t o_list = off; off = up(off + B * sizeof(int32_t));
+  const size_t o_cnt = off;  off = up(off + 16 * sizeof(int32_t));
+  const size_t o_keys = off; off = up(off + (size_t)PZ_FB_SLOTS * slot * sizeof(uint64_t));
+  const size_t o_cum = off;  off = up(off + (size_t)PZ_FB_SLOTS * slot * sizeof(float));
+  if (base && out) {
+    char* b = static_cast<char*>(base);
+    out->row_stat = reinterpret_cast<float*>(b + o_stat);
+    out->fb_list = reinterpret_cast<int32_t*>(b + o_list);
+    out->counters = reinterpret_cast<int32_t*>(b + o_cnt);
+    out->fb_keys = reinterpret_cast<uint64_t*>(b + o_keys);
+    out->fb_cum = reinterpret_cast<float*>(b + o_cum);
+    out->slot_n = slot;
+  }
+  return off;
+}
 
 extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
                                  int max_hist, int device) {
@@ -118,10 +140,9 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
     return bail(PZ_ENOMEM);
   s->res_params = new (std::nothrow) pz_row_params_dev[B];
   if (!s->res_params) return bail(PZ_ENOMEM);
-  s->scratch_bytes = pz_scratch_bytes_for(max_batch, max_vocab);
-  if (s->scratch_bytes &&
-      hipMalloc(&s->d_scratch, s->scratch_bytes) != hipSuccess)
-    return bail(PZ_ENOMEM);
+  s->scratch_bytes = pz_scratch_layout(max_batch, max_vocab, nullptr, nullptr);
+  if (hipMalloc(&s->d_scratch, s->scratch_bytes) != hipSuccess) return bail(PZ_ENOMEM);
+  pz_scratch_layout(max_batch, max_vocab, s->d_scratch, &s->sc);
   *out = s;
   return rc;
 }
@@ -283,8 +304,7 @@ static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
   L.u = d_u;
   L.ids = d_ids;
   L.p_out = d_p;
-  L.scratch = s->d_scratch;
-  L.scratch_bytes = s->scratch_bytes;
+  L.sc = s->sc;
   L.max_lds = s->max_lds;
   L.stream = s->stream;
 

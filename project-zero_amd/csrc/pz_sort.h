@@ -1,0 +1,27 @@
+// pz_sort.h -- in-workgroup bitonic sort of 64-bit composite keys.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// Descending bitonic sort of buf[0..N) (N a power of two) by all BLOCK
+// threads of the workgroup.  buf may live in LDS or in global memory owned by
+// the workgroup (every stage ends in a workgroup barrier, which also orders
+// the global accesses of the workgroup).
+template <int BLOCK>
+__device__ void pz_bitonic_desc(uint64_t* buf, int N) {
+  for (int size = 2; size <= N; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = threadIdx.x; i < (N >> 1); i += BLOCK) {
+        const int lo = 2 * stride * (i / stride) + (i % stride);
+        const int hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t a = buf[lo], b = buf[hi];
+        if ((a < b) == desc) {
+          buf[lo] = b;
+          buf[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+  }
+}

@@ -24,13 +24,13 @@
 #include "pz_device.h"
 #include "pz_launch.h"
 #include "pz_seq.h"
+#include "pz_sort.h"
 
 namespace {
 
 constexpr int TOPK_BLOCK = 1024;
 constexpr int TOPK_CAP = 4096;      // candidate buffer entries (8 B each)
 constexpr int HBINS = 2048;         // 11-bit key digit
-constexpr int TOPK_MAXK = 1024;
 
 struct TopkShared {
   uint32_t hist[HBINS];
@@ -43,13 +43,6 @@ struct TopkShared {
 
 __device__ __forceinline__ uint64_t comp_of(uint32_t key, int id) {
   return ((uint64_t)key << 32) | (uint32_t)(0xffffffffu - (uint32_t)id);
-}
-
-// Transformed value of element i (penalty, then temperature).
-__device__ __forceinline__ float tk_value(const PzPenalty& P, const pz_row_params_dev& prm,
-                                          float raw, int i) {
-  if (P.active && pz_pen_member(P, i)) raw = pz_penalize(P, raw, i);
-  return pz_temper(raw, prm);
 }
 
 __device__ __forceinline__ bool tk_pass(const TopkShared& S, uint32_t key, int id) {
@@ -74,23 +67,6 @@ __device__ __forceinline__ void tk_append(TopkShared& S, uint64_t* buf, bool wan
     const int slot = base + before;
     if (slot < TOPK_CAP) buf[slot] = comp;
     else S.over = 1;
-  }
-}
-
-// Descending bitonic sort of buf[0..N), N a power of two, all threads.
-template <int BLOCK>
-__device__ void bitonic_desc(uint64_t* buf, int N) {
-  for (int size = 2; size <= N; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = threadIdx.x; i < (N >> 1); i += BLOCK) {
-        const int lo = 2 * stride * (i / stride) + (i % stride);
-        const int hi = lo + stride;
-        const bool desc = (lo & size) == 0;
-        const uint64_t a = buf[lo], b = buf[hi];
-        if ((a < b) == desc) { buf[lo] = b; buf[hi] = a; }
-      }
-      __syncthreads();
-    }
   }
 }
 
@@ -119,7 +95,7 @@ __device__ void tk_stream(TopkShared& S, uint64_t* buf, const float* x, int V,
           bool want = false;
           uint64_t comp = 0;
           if (in) {
-            const float y = tk_value(P, prm, v[u][c], i);
+            const float y = pz_transform(P, prm, v[u][c], i);
             if (y > -1e30f) {
               const uint32_t key = pz_key(y);
               want = tk_pass(S, key, i);
@@ -135,7 +111,7 @@ __device__ void tk_stream(TopkShared& S, uint64_t* buf, const float* x, int V,
     bool want = false;
     uint64_t comp = 0;
     if (i < V) {
-      const float y = tk_value(P, prm, x[i], i);
+      const float y = pz_transform(P, prm, x[i], i);
       if (y > -1e30f) {
         const uint32_t key = pz_key(y);
         want = tk_pass(S, key, i);
@@ -149,7 +125,7 @@ __device__ void tk_stream(TopkShared& S, uint64_t* buf, const float* x, int V,
       bool want = false;
       uint64_t comp = 0;
       if (i < V) {
-        const float y = tk_value(P, prm, x[i], i);
+        const float y = pz_transform(P, prm, x[i], i);
         if (y > -1e30f) {
           const uint32_t key = pz_key(y);
           want = tk_pass(S, key, i);
@@ -186,7 +162,7 @@ __global__ __launch_bounds__(BLOCK) void k_topk(
   __syncthreads();
   const int ns = V < BLOCK * 4 ? V : BLOCK * 4;
   for (int i = tid; i < ns; i += BLOCK) {
-    const float y = tk_value(P, prm, x[i], i);
+    const float y = pz_transform(P, prm, x[i], i);
     if (y > -1e30f) atomicAdd(&S.hist[pz_key(y) >> 21], 1u);
   }
   __syncthreads();
@@ -228,7 +204,7 @@ __global__ __launch_bounds__(BLOCK) void k_topk(
     if (!S.over) break;
     // the buffer holds TOPK_CAP >= k candidates of the row: its k-th largest
     // (key, id) bounds the row's k-th largest from below
-    bitonic_desc<BLOCK>(buf, TOPK_CAP);
+    pz_bitonic_desc<BLOCK>(buf, TOPK_CAP);
     if (tid == 0) {
       const uint64_t c = buf[k - 1];
       S.tau_key = (uint32_t)(c >> 32);
@@ -246,7 +222,7 @@ __global__ __launch_bounds__(BLOCK) void k_topk(
   while (N < n) N <<= 1;
   for (int i = n + tid; i < N; i += BLOCK) buf[i] = 0;  // sentinel below any key
   __syncthreads();
-  bitonic_desc<BLOCK>(buf, N);
+  pz_bitonic_desc<BLOCK>(buf, N);
 
   // ---- 4. softmax over k slots, cut-off and draw (wave 0).  Lane l owns
   // slots l, l+64, ...: every LDS word of pv is written and read by the same

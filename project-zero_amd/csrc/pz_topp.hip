@@ -1,0 +1,462 @@
+// pz_topp.hip -- batched top-p (nucleus) sampling, bit-exact with the
+// reference's fp32 arithmetic.
+//
+// Reference semantics (src/sampling/top_p.c:30-108), applied after penalties
+// and temperature:
+//   * V > 200000 -> argmax (:33-34);  maximum by strict '>' from x[0] (:37-41);
+//   * candidates x >= max - 20 (:53-58), e = expf(x - max), a sequential fp32
+//     sum in ascending id order (:57-65); no candidate -> argmax (:68-69);
+//   * p = e * (1/sum) (:72-74); stable sort by p descending (:77), so equal p
+//     stay in ascending id;
+//   * cut-off: first i with sequential cumulative >= top_p, else all (:80-88);
+//     trunc_sum = the same sequential sum (:91-93); r = u * trunc_sum;
+//     first i < cut-off with r < cdf, else slot 0 (:96-105).
+//
+// Design (one 1024-thread workgroup per row):
+//   pass 1  (HBM)   row maximum + per-segment estimates of the normaliser;
+//   pass 2  (L2)    exact e = expf(x - max) (glibc-identical pz_expf) of every
+//                   candidate -> integer segment records at the predicted
+//                   binade (pz_exact.h) + an LDS histogram of e (1/128
+//                   binade bins);
+//   walk    (wave 0) the exact sequential normaliser; meanwhile wave 1 picks,
+//                   from the histogram, the smallest set of top bins whose
+//                   estimated mass clears top_p with margin;
+//   pass 3  (L2)    gathers the candidates with p >= p(threshold) into LDS as
+//                   (p, ~id) keys -- a prefix of the reference's sort order;
+//   sort + exact cumulative walk + draw (binary search over the stored sums).
+// A row whose selected set does not fit in LDS, or whose exact cumulative
+// does not reach top_p inside it, is queued for the fallback kernel, which
+// sorts every candidate of the row in its global scratch slot.
+#include <limits.h>
+
+#include "pz_device.h"
+#include "pz_exact.h"
+#include "pz_launch.h"
+#include "pz_rowpass.h"
+#include "pz_sort.h"
+
+namespace {
+
+// Histogram of e in (0, 1]: bins of 1/128 binade, e >= 2^-29 (candidates are
+// >= expf(-20) ~ 2.06e-9); smaller values fall in bin 0.
+constexpr int EBIN_BASE = 98 << 7;
+constexpr int EBINS = (127 << 7) - EBIN_BASE + 1;
+constexpr int TOPP_CAP_MAX = 8192;
+
+__device__ __forceinline__ int ebin(float e) {
+  const int b = (int)(__float_as_uint(e) >> 16) - EBIN_BASE;
+  return b < 0 ? 0 : (b >= EBINS ? EBINS - 1 : b);
+}
+__device__ __forceinline__ float ebin_lo(int b) {
+  return __uint_as_float((uint32_t)(b + EBIN_BASE) << 16);
+}
+__device__ __forceinline__ float ebin_mid(int b) {
+  return __uint_as_float(((uint32_t)(b + EBIN_BASE) << 16) | 0x8000u);
+}
+
+__device__ __forceinline__ uint64_t topp_key(float p, int id) {
+  return ((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
+__device__ __forceinline__ float key_p(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
+
+struct ToppShared {
+  PzPass1Shared p1;
+  float sum;
+  int bsel;
+  uint32_t nsel;
+  int count;
+  int over;
+  int cutoff;
+  int first;
+};
+
+// Wave-aggregated append of up to one key per lane into buf (capacity cap).
+__device__ __forceinline__ void append_key(int* count, int* over, uint64_t* buf, int cap,
+                                           bool want, uint64_t key) {
+  const uint64_t ball = __ballot(want);
+  if (!ball) return;
+  const int lane = threadIdx.x & 63;
+  const int leader = (int)__builtin_ctzll(ball);
+  int base = 0;
+  if (lane == leader) base = atomicAdd(count, __popcll(ball));
+  base = __shfl(base, leader, 64);
+  if (want) {
+    const int slot = base + __popcll(ball & ((1ull << lane) - 1ull));
+    if (slot < cap) buf[slot] = key;
+    else *over = 1;
+  }
+}
+
+// Exact candidate term of one element (0 for non-candidates).
+__device__ __forceinline__ float cand_e(float y, bool valid, float thr, float M) {
+  return (valid && y >= thr) ? pz_expf(y - M) : 0.0f;
+}
+
+// Reference cumulative/draw over a descending key list (wave 0 computes the
+// cut-off, thread 0 draws).  keys/cum may be LDS or global.  all_gathered:
+// the list holds every candidate (then a cumulative that never reaches top_p
+// keeps all of them, top_p.c:81).  Returns the cut-off, or -1 when the
+// list is a strict prefix whose cumulative stays below top_p.
+__device__ __forceinline__ int nucleus_cutoff(const uint64_t* keys, float* cum, int m, float top_p,
+                              bool all_gathered, int* cutoff_sh) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid < 64) {
+    PzAcc st;
+    st.n = 0;
+    st.g = 1;
+    int cutoff = -1;
+    for (int j0 = 0; j0 < m; j0 += 64) {
+      const int j = j0 + lane;
+      float v[1];
+      v[0] = j < m ? key_p(keys[j]) : 0.0f;
+      const int f = pz_wave_accumulate<1>(st, v, 0, top_p, PZ_STOP_GE, cum + j0);
+      if (f >= 0) {
+        cutoff = j0 + f + 1;
+        break;
+      }
+    }
+    if (cutoff < 0 && all_gathered) cutoff = m;
+    if (lane == 0) *cutoff_sh = cutoff;
+  }
+  __syncthreads();
+  return *cutoff_sh;
+}
+
+__device__ __forceinline__ void nucleus_draw(const uint64_t* keys, const float* cum, int cutoff, float uu,
+                             int32_t* id_out, float* p_out) {
+  const float trunc_sum = cum[cutoff - 1];
+  const float r = uu * trunc_sum;
+  int lo = 0, hi = cutoff;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (r < cum[mid]) hi = mid;
+    else lo = mid + 1;
+  }
+  const int pick = lo < cutoff ? lo : 0;
+  const uint64_t k = keys[pick];
+  *id_out = key_id(k);
+  if (p_out) *p_out = key_p(k);
+}
+
+// Regenerates one segment's candidate terms for the exact-sum walk.
+template <bool VEC>
+struct CandRegen {
+  PzRow<VEC> R;
+  float thr, M;
+  __device__ __forceinline__ void operator()(int k, float (&v)[4]) const {
+    float yy[4];
+    const int n = R.get(pz_seg_e0(k), yy);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = cand_e(yy[c], c < n, thr, M);
+  }
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(PZ_RB) void k_topp(
+    const float* __restrict__ logits, long ld, int V, const int32_t* __restrict__ rows,
+    const pz_row_params_dev* __restrict__ params, int n_params,
+    const int32_t* __restrict__ hist, int H, int hcap, int pen_bytes, int cap,
+    const float* __restrict__ u, int32_t* __restrict__ ids_out, float* __restrict__ p_out,
+    pz_scratch sc) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ ToppShared S;
+  const int row = pz_row_of(rows, blockIdx.x);
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+
+  PzRow<VEC> R;
+  R.x = logits + (long)row * ld;
+  R.V = V;
+  R.prm = &prm;
+  pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
+
+  const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
+  char* reg = lds + pen_bytes;
+  float* seg_m = reinterpret_cast<float*>(reg);
+  float* seg_s = seg_m + nseg;
+  uint32_t* seg_d = reinterpret_cast<uint32_t*>(seg_s + nseg);
+  uint32_t* seg_gf = seg_d + nseg;
+  uint32_t* ehist = seg_gf + nseg;
+  uint64_t* keys = reinterpret_cast<uint64_t*>(reg);
+  float* cum = reinterpret_cast<float*>(keys + cap);
+
+  for (int i = tid; i < EBINS; i += PZ_RB) ehist[i] = 0u;
+
+  // ---- pass 1: maximum + normaliser estimates
+  const float M = pz_pass1<8>(R, ntiles, seg_m, seg_s, S.p1);
+  const float y0 = S.p1.y0;
+  if (y0 != y0) {
+    // max_val = NaN: no candidate passes, argmax of a row starting with NaN -> 0
+    if (tid == 0) {
+      ids_out[row] = 0;
+      if (p_out) p_out[row] = 1.0f;
+    }
+    return;
+  }
+  if (!(M > -__builtin_inff() && M < __builtin_inff())) {
+    // every e is expf(NaN): the sort leaves candidates in id order and no
+    // comparison succeeds -> the first candidate, i.e. the first y == max
+    if (tid == 0) S.first = INT_MAX;
+    __syncthreads();
+    int mine = INT_MAX;
+    for (int t = 0; t < ntiles; t++) {
+      float y[4];
+      const int e0 = pz_tile_e0(t);
+      const int n = R.get(e0, y);
+      for (int c = 0; c < n; c++)
+        if (y[c] == M && e0 + c < mine) mine = e0 + c;
+    }
+    atomicMin(&S.first, mine);
+    __syncthreads();
+    if (tid == 0) {
+      ids_out[row] = S.first;
+      if (p_out) p_out[row] = __builtin_nanf("");
+    }
+    return;
+  }
+  const float thr = M - 20.0f;
+  if (w == 0) pz_predict_grids(seg_m, seg_s, nseg, M, 1.0f, seg_gf);
+  __syncthreads();
+
+  // ---- pass 2: exact candidate terms -> segment records + e histogram
+  constexpr int U2 = 4;
+  for (int t0 = 0; t0 < ntiles; t0 += U2) {
+    float y[U2][4];
+    int nv[U2];
+#pragma unroll
+    for (int uu = 0; uu < U2; uu++) {
+      nv[uu] = 0;
+      if (t0 + uu < ntiles) nv[uu] = R.get(pz_tile_e0(t0 + uu), y[uu]);
+    }
+#pragma unroll
+    for (int uu = 0; uu < U2; uu++) {
+      const int t = t0 + uu;
+      if (t >= ntiles) continue;
+      const int k = t * PZ_SEGS_PER_TILE + w;
+      float e[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        e[c] = cand_e(y[uu][c], c < nv[uu], thr, M);
+        if (e[c] > 0.0f) atomicAdd(&ehist[ebin(e[c])], 1u);
+      }
+      pz_segment_record(e, seg_gf[k], true, seg_d, seg_gf, k);
+    }
+  }
+  __syncthreads();
+
+  // ---- exact normaliser (wave 0) || nucleus bin selection (wave 1)
+  if (w == 0) {
+    PzAcc st;
+    st.n = 0;
+    st.g = 1;
+    CandRegen<VEC> regen{R, thr, M};
+    pz_wave_walk(st, seg_d, seg_gf, nseg, 0.0f, PZ_STOP_NONE, regen);
+    if (lane == 0) S.sum = pz_acc_value(st);
+  } else if (w == 1) {
+    float tot = 0.0f;
+    uint32_t ncand = 0;
+    for (int b = lane; b < EBINS; b += 64) {
+      const uint32_t c = ehist[b];
+      tot += (float)c * ebin_mid(b);
+      ncand += c;
+    }
+    tot = pz_wave_sum(tot);
+    ncand = pz_wave_sum_u32(ncand);
+    const float goal = (prm.top_p * 1.006f + 2e-4f) * tot;
+    float carry = 0.0f;
+    uint32_t ccarry = 0;
+    int bsel = 0;
+    uint32_t nsel = ncand;
+    for (int b0 = EBINS - 1; b0 >= 0; b0 -= 64) {
+      const int b = b0 - lane;
+      float m = 0.0f;
+      uint32_t c = 0;
+      if (b >= 0) {
+        c = ehist[b];
+        m = (float)c * ebin_mid(b);
+      }
+      const float incl = pz_wave_scan_f32(m);
+      const uint32_t cincl = pz_wave_scan_u32(c);
+      const uint64_t ball = __ballot(b >= 0 && carry + incl >= goal);
+      if (ball) {
+        const int L = (int)__builtin_ctzll(ball);
+        bsel = b0 - L;
+        nsel = ccarry + pz_readlane_u32(cincl, L);
+        break;
+      }
+      carry += pz_readlane_f32(incl, 63);
+      ccarry += pz_readlane_u32(cincl, 63);
+    }
+    if (lane == 0) {
+      S.bsel = bsel;
+      S.nsel = nsel;
+    }
+  }
+  if (tid == 0) {
+    S.count = 0;
+    S.over = 0;
+  }
+  __syncthreads();
+
+  const float inv = 1.0f / S.sum;  // top_p.c:72
+  const bool all = S.bsel == 0;
+  bool fallback = S.nsel > (uint32_t)cap;
+  if (!fallback) {
+    // ---- pass 3: gather every candidate with p >= p_thr (a prefix of the
+    // (p desc, id asc) order) into LDS
+    const float e_lo = ebin_lo(S.bsel);
+    const float p_thr = all ? 0.0f : e_lo * inv;
+    const float dgate = all ? -__builtin_inff() : __logf(e_lo) - 0.01f;
+    for (int t0 = 0; t0 < ntiles; t0 += U2) {
+      float y[U2][4];
+      int nv[U2];
+#pragma unroll
+      for (int uu = 0; uu < U2; uu++) {
+        nv[uu] = 0;
+        if (t0 + uu < ntiles) nv[uu] = R.get(pz_tile_e0(t0 + uu), y[uu]);
+      }
+#pragma unroll
+      for (int uu = 0; uu < U2; uu++) {
+        const int t = t0 + uu;
+        if (t >= ntiles) break;
+        const int e0 = pz_tile_e0(t);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const float yy = y[uu][c];
+          bool want = c < nv[uu] && yy >= thr && (yy - M) >= dgate;
+          uint64_t key = 0;
+          if (want) {
+            const float p = pz_expf(yy - M) * inv;
+            want = p >= p_thr;
+            key = topp_key(p, e0 + c);
+          }
+          append_key(&S.count, &S.over, keys, cap, want, key);
+        }
+      }
+    }
+    __syncthreads();
+    fallback = S.over != 0;
+  }
+  if (!fallback) {
+    const int m = S.count;
+    int N = 1;
+    while (N < m) N <<= 1;
+    for (int i = m + tid; i < N; i += PZ_RB) keys[i] = 0ull;
+    __syncthreads();
+    pz_bitonic_desc<PZ_RB>(keys, N);
+    const int cutoff = nucleus_cutoff(keys, cum, m, prm.top_p, all, &S.cutoff);
+    if (cutoff > 0) {
+      if (tid == 0) nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
+      return;
+    }
+  }
+  // ---- queue the row for the fallback kernel
+  if (tid == 0) {
+    float* st = sc.row_stat + 4 * (long)row;
+    st[0] = M;
+    st[1] = inv;
+    const int q = atomicAdd(&sc.counters[0], 1);
+    sc.fb_list[q] = row;
+  }
+}
+
+// Fallback: every candidate of the row, sorted in the workgroup's global
+// scratch slot, then the same cumulative and draw.
+template <bool VEC>
+__global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
+    const float* __restrict__ logits, long ld, int V,
+    const pz_row_params_dev* __restrict__ params, int n_params,
+    const int32_t* __restrict__ hist, int H, int hcap, const float* __restrict__ u,
+    int32_t* __restrict__ ids_out, float* __restrict__ p_out, pz_scratch sc) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ int count, over, cutoff_sh;
+  const int tid = threadIdx.x;
+  const int n_fb = sc.counters[0];
+  uint64_t* keys = sc.fb_keys + (size_t)blockIdx.x * sc.slot_n;
+  float* cum = sc.fb_cum + (size_t)blockIdx.x * sc.slot_n;
+  for (int q = blockIdx.x; q < n_fb; q += gridDim.x) {
+    const int row = sc.fb_list[q];
+    const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+    PzRow<VEC> R;
+    R.x = logits + (long)row * ld;
+    R.V = V;
+    R.prm = &prm;
+    pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
+    const float M = sc.row_stat[4 * (long)row];
+    const float inv = sc.row_stat[4 * (long)row + 1];
+    const float thr = M - 20.0f;
+    if (tid == 0) {
+      count = 0;
+      over = 0;
+    }
+    __syncthreads();
+    const int ntiles = pz_tiles(V);
+    for (int t = 0; t < ntiles; t++) {
+      float y[4];
+      const int e0 = pz_tile_e0(t);
+      const int n = R.get(e0, y);
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const bool want = c < n && y[c] >= thr;
+        uint64_t key = 0;
+        if (want) key = topp_key(pz_expf(y[c] - M) * inv, e0 + c);
+        append_key(&count, &over, keys, sc.slot_n, want, key);
+      }
+    }
+    __syncthreads();
+    const int m = count;
+    int N = 1;
+    while (N < m) N <<= 1;
+    for (int i = m + tid; i < N; i += PZ_RB) keys[i] = 0ull;
+    __syncthreads();
+    pz_bitonic_desc<PZ_RB>(keys, N);
+    const int cutoff = nucleus_cutoff(keys, cum, m, prm.top_p, true, &cutoff_sh);
+    if (tid == 0) nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
+    __syncthreads();
+  }
+}
+
+__global__ void k_reset_counters(int32_t* c) {
+  if (threadIdx.x < 16) c[threadIdx.x] = 0;
+}
+
+size_t topp_region_bytes(int V, int cap) {
+  const size_t a = (size_t)pz_nseg(V) * 16 + (size_t)EBINS * 4;
+  const size_t b = (size_t)cap * 12;
+  return a > b ? a : b;
+}
+
+template <bool VEC>
+int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
+  const int pen = L.pen_any ? (int)((pz_penalty_lds_bytes(L.V, L.hcap) + 15) & ~(size_t)15) : 0;
+  const int fixed = (int)sizeof(ToppShared) + 64;
+  int cap = TOPP_CAP_MAX;
+  while (cap > 256 && pen + topp_region_bytes(L.V, cap) + fixed > (size_t)L.max_lds) cap >>= 1;
+  const size_t lds = pen + topp_region_bytes(L.V, cap);
+  if (lds + fixed > (size_t)L.max_lds) return -2;
+  auto kern = k_topp<VEC>;
+  auto fb = k_topp_fallback<VEC>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return -1;
+  if (pen > 65536 && hipFuncSetAttribute((const void*)fb, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         pen) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(k_reset_counters, dim3(1), dim3(64), 0, L.stream, L.sc.counters);
+  hipLaunchKernelGGL(kern, dim3(n_rows), dim3(PZ_RB), lds, L.stream, L.logits, L.ld, L.V, d_rows,
+                     L.params, L.n_params, L.hist, L.H, L.hcap, pen, cap, L.u, L.ids, L.p_out,
+                     L.sc);
+  hipLaunchKernelGGL(fb, dim3(PZ_FB_SLOTS), dim3(PZ_RB), (size_t)pen, L.stream, L.logits, L.ld,
+                     L.V, L.params, L.n_params, L.hist, L.H, L.hcap, L.u, L.ids, L.p_out, L.sc);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace
+
+int pz_launch_topp(const pz_launch& L, int n_rows, const int32_t* d_rows) {
+  if (n_rows <= 0) return 0;
+  if (L.V > PZ_TOPP_MAX_V) return pz_launch_greedy(L, n_rows, d_rows);  // top_p.c:33-34
+  const bool vec = (L.ld % 4 == 0) && (((uintptr_t)L.logits & 15) == 0);
+  return vec ? launch_topp_t<true>(L, n_rows, d_rows) : launch_topp_t<false>(L, n_rows, d_rows);
+}
