@@ -148,14 +148,20 @@ __device__ __forceinline__ float pz_pass1(const Row& row, int ntiles, float* seg
   return M;
 }
 
+// Sentinel grid of a segment that has no record (the walk regenerates it).
+constexpr uint32_t PZ_NO_RECORD = 0xffffffffu;
+
 // One wave: grid exponent of the estimated running sum at the start of each
 // segment, where segment k adds about scale * seg_s[k] * exp(seg_m[k] - M).
-// Writes seg_gf[k] and returns the estimated total.
-__device__ __forceinline__ float pz_predict_grids(const float* seg_m, const float* seg_s,
-                                                  int nseg, float M, float scale,
-                                                  uint32_t* seg_gf) {
+// Segments whose estimated start exceeds `limit` get PZ_NO_RECORD.  Writes
+// seg_gf[k]; returns the last segment at or below the limit (-1 if none).
+__device__ __forceinline__ int pz_predict_grids(const float* seg_m, const float* seg_s,
+                                                int nseg, float M, float scale,
+                                                uint32_t* seg_gf,
+                                                float limit = __builtin_inff()) {
   const int lane = threadIdx.x & 63;
   float carry = 0.0f;
+  int kmax = -1;
   for (int k0 = 0; k0 < nseg; k0 += 64) {
     const int k = k0 + lane;
     float a = 0.0f;
@@ -164,8 +170,12 @@ __device__ __forceinline__ float pz_predict_grids(const float* seg_m, const floa
       if (m > -__builtin_inff()) a = seg_s[k] * __expf(m - M) * scale;
     }
     const float incl = pz_wave_scan_f32(a);
-    if (k < nseg) seg_gf[k] = pz_grid_of(carry + (incl - a));
+    const float start = carry + (incl - a);
+    const bool in = k < nseg && start <= limit;
+    if (k < nseg) seg_gf[k] = in ? pz_grid_of(start) : PZ_NO_RECORD;
+    const uint64_t ball = __ballot(in);
+    if (ball) kmax = k0 + 63 - (int)__builtin_clzll(ball);
     carry += pz_readlane_f32(incl, 63);
   }
-  return carry;
+  return kmax;
 }

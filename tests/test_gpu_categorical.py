@@ -1,0 +1,93 @@
+"""Plain categorical draw (softmax + ascending-id CDF, generate.c:157-169) on
+the GPU against the oracle: the normaliser and the CDF are reproduced with
+the reference's sequential fp32 rounding, so ids and p(chosen) must be
+identical on every row."""
+import numpy as np
+import pytest
+
+import pz_oracle as po
+import pzsample as pz
+from conftest import to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def orc(p):
+    return po.params(p.temperature, p.top_k, p.top_p, p.rep_penalty, p.presence_penalty,
+                     p.frequency_penalty)
+
+
+def check(torch, x, params, u, hist=None, temp_mode=pz.PZ_TEMP_MUL_RECIP, label=""):
+    B, V = x.shape
+    print(f"case {label} B={B} V={V}", flush=True)
+    d_x = to_dev(torch, np.ascontiguousarray(x))
+    H = hist.shape[1] if hist is not None else 0
+    d_h = to_dev(torch, np.ascontiguousarray(hist)) if hist is not None else None
+    with pz.Sampler(B, V, max_hist=max(H, 1), temp_mode=temp_mode) as s:
+        ids, p = s.sample(d_x, B, V, V, params, u=u, d_hist=d_h, H=H, want_p=True)
+    want, pw, dd, _ = po.sample_batch(x, [orc(q) for q in params], u=u, hist=hist,
+                                      temp_mode=temp_mode)
+    bad = ids != want
+    print(f"  boundary={int((dd < 1e-5).sum())} mismatches={int(bad.sum())}", flush=True)
+    assert not bad.any(), (label, np.nonzero(bad)[0][:8], ids[bad][:8], want[bad][:8])
+    same = (p == pw) | (np.isnan(p) & np.isnan(pw))
+    assert same.all(), (label, np.nonzero(~same)[0][:8])
+    return ids, p
+
+
+def test_full_vocab_batch(torch_cuda):
+    B, V = 256, 128256
+    x = pz.synth_normal(B, V, 3.0, 0xCA7)
+    u = pz.synth_draws(B, 0xCA8)
+    check(torch_cuda, x, [pz.row_params(temperature=1.0)], u, label="256x128256")
+
+
+@pytest.mark.parametrize("V", [1, 2, 7, 4096, 4097, 49152, 151936, 262144])
+def test_sizes(torch_cuda, V):
+    B = 5
+    x = pz.synth_normal(B, V, 2.0, 500 + V)
+    u = pz.synth_draws(B, 600 + V)
+    check(torch_cuda, x, [pz.row_params(temperature=0.8)], u, label=f"V={V}")
+
+
+def test_top_p_one_and_zero_take_the_plain_path(torch_cuda):
+    B, V = 8, 32000
+    x = pz.synth_normal(B, V, 2.0, 77)
+    u = pz.synth_draws(B, 78)
+    for tp in (1.0, 0.0, 1.5):
+        check(torch_cuda, x, [pz.row_params(temperature=0.9, top_p=tp)], u, label=f"top_p={tp}")
+
+
+def test_degenerate_rows(torch_cuda):
+    B, V = 7, 3000
+    x = pz.synth_normal(B, V, 2.0, 88)
+    x[0, 0] = np.nan            # NaN max -> V-1
+    x[1, 17] = np.nan           # NaN anywhere -> sum NaN -> V-1
+    x[2, 5] = np.inf            # +inf max -> NaN term -> V-1
+    x[3, :] = -np.inf           # -inf max -> V-1
+    x[4, :] = 0.0               # uniform
+    x[5, :] = -1e4              # very negative, finite
+    x[5, 1234] = -1e4 + 30
+    x[6, ::3] = -np.inf         # -inf entries contribute 0
+    u = pz.synth_draws(B, 89)
+    ids, _ = check(torch_cuda, x, [pz.row_params(temperature=1.0)], u, label="degenerate")
+    assert ids[0] == ids[1] == ids[2] == ids[3] == V - 1
+
+
+def test_uniform_edges(torch_cuda):
+    B, V = 4, 10000
+    x = pz.synth_normal(B, V, 3.0, 99)
+    for uval in (0.0, 1.0, 0.99999994, 0.5):
+        check(torch_cuda, x, [pz.row_params(temperature=1.0)], np.full(B, uval, np.float32),
+              label=f"u={uval}")
+
+
+def test_penalties_and_temperature_forms(torch_cuda):
+    B, V = 32, 50000
+    x = pz.synth_normal(B, V, 3.0, 111)
+    hist = pz.synth_uniform_ids(B, 200, V, 112)
+    u = pz.synth_draws(B, 113)
+    for mode in (pz.PZ_TEMP_MUL_RECIP, pz.PZ_TEMP_DIV):
+        check(torch_cuda, x, [pz.row_params(temperature=0.7, rep_penalty=1.2,
+                                             presence_penalty=0.3, frequency_penalty=0.2)],
+              u, hist=hist, temp_mode=mode, label=f"pen temp {mode}")
