@@ -26,26 +26,7 @@ namespace {
 
 struct CatShared {
   PzPass1Shared p1;
-  float sum;
-  int kmax;
-  int hit;
-};
-
-// Exact term of one element: e, or p = e * inv when as_p.
-template <bool VEC>
-struct CatRegen {
-  PzRow<VEC> R;
-  float M, inv;
-  bool as_p;
-  __device__ __forceinline__ void operator()(int k, float (&v)[4]) const {
-    float yy[4];
-    const int n = R.get(pz_seg_e0(k), yy);
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      float e = c < n ? pz_expf(yy[c] - M) : 0.0f;
-      v[c] = as_p ? e * inv : e;
-    }
-  }
+  PzDrawShared d;
 };
 
 template <bool VEC>
@@ -58,7 +39,7 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
   __shared__ CatShared S;
   const int row = pz_row_of(rows, blockIdx.x);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x;
 
   PzRow<VEC> R;
   R.x = logits + (long)row * ld;
@@ -72,7 +53,6 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
   uint32_t* seg_d = reinterpret_cast<uint32_t*>(seg_s + nseg);
   uint32_t* seg_gf = seg_d + nseg;
 
-  // ---- pass 1
   const float M = pz_pass1<8>(R, ntiles, seg_m, seg_s, S.p1);
   if (S.p1.any_nan || !(M > -__builtin_inff() && M < __builtin_inff())) {
     if (tid == 0) {
@@ -81,88 +61,13 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
     }
     return;
   }
-  if (w == 0) pz_predict_grids(seg_m, seg_s, nseg, M, 1.0f, seg_gf);
-  __syncthreads();
-
-  // ---- pass 2: exact e -> records; walk -> exact normaliser
-  constexpr int U2 = 4;
-  for (int t0 = 0; t0 < ntiles; t0 += U2) {
-    float y[U2][4];
-    int nv[U2];
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      nv[uu] = 0;
-      if (t0 + uu < ntiles) nv[uu] = R.get(pz_tile_e0(t0 + uu), y[uu]);
-    }
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      const int t = t0 + uu;
-      if (t >= ntiles) continue;
-      const int k = t * PZ_SEGS_PER_TILE + w;
-      float e[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) e[c] = c < nv[uu] ? pz_expf(y[uu][c] - M) : 0.0f;
-      pz_segment_record(e, seg_gf[k], true, seg_d, seg_gf, k);
-    }
-  }
-  __syncthreads();
-  if (w == 0) {
-    PzAcc st;
-    st.n = 0;
-    st.g = 1;
-    CatRegen<VEC> regen{R, M, 0.0f, false};
-    pz_wave_walk(st, seg_d, seg_gf, nseg, 0.0f, PZ_STOP_NONE, regen);
-    const float sum = pz_acc_value(st);
-    const float inv = 1.0f / sum;  // softmax.c:19-22
-    // CDF records only where the estimated CDF start can still be <= r
-    const float r = u[row];
-    const int kmax = pz_predict_grids(seg_m, seg_s, nseg, M, inv, seg_gf, r + 0.01f);
-    if (lane == 0) {
-      S.sum = sum;
-      S.kmax = kmax;
-    }
-  }
-  __syncthreads();
-
-  // ---- pass 3: exact p -> CDF records (segments up to kmax)
-  const float inv = 1.0f / S.sum;
-  const int kmax = S.kmax;
-  const int tmax = kmax < 0 ? -1 : kmax / PZ_SEGS_PER_TILE;
-  for (int t0 = 0; t0 <= tmax; t0 += U2) {
-    float y[U2][4];
-    int nv[U2];
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      nv[uu] = 0;
-      if (t0 + uu <= tmax) nv[uu] = R.get(pz_tile_e0(t0 + uu), y[uu]);
-    }
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      const int t = t0 + uu;
-      if (t > tmax) continue;
-      const int k = t * PZ_SEGS_PER_TILE + w;
-      const uint32_t g = seg_gf[k];
-      if (g == PZ_NO_RECORD) continue;
-      float p[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) p[c] = c < nv[uu] ? pz_expf(y[uu][c] - M) * inv : 0.0f;
-      pz_segment_record(p, g, true, seg_d, seg_gf, k);
-    }
-  }
-  __syncthreads();
-  if (w == 0) {
-    PzAcc st;
-    st.n = 0;
-    st.g = 1;
-    CatRegen<VEC> regen{R, M, inv, true};
-    const float r = u[row];
-    int hit = pz_wave_walk(st, seg_d, seg_gf, nseg, r, PZ_STOP_GT, regen);
-    if (hit >= V) hit = -1;  // padding terms are 0 and never raise the CDF
-    if (lane == 0) S.hit = hit;
-  }
-  __syncthreads();
+  const float sum = pz_exact_normaliser<4>(R, ntiles, M, -__builtin_inff(), seg_m, seg_s,
+                                           seg_d, seg_gf, S.d);
+  const float inv = 1.0f / sum;  // softmax.c:19-22
+  const int hit = pz_exact_cdf_draw<4>(R, V, ntiles, M, inv, u[row], seg_m, seg_s, seg_d,
+                                       seg_gf, S.d);
   if (tid == 0) {
-    const int id = S.hit >= 0 ? S.hit : V - 1;  // generate.c:161
+    const int id = hit >= 0 ? hit : V - 1;  // generate.c:161
     ids_out[row] = id;
     if (p_out) {
       float yy[4];

@@ -179,3 +179,116 @@ __device__ __forceinline__ int pz_predict_grids(const float* seg_m, const float*
   }
   return kmax;
 }
+
+struct PzDrawShared {
+  float sum;
+  int kmax;
+  int hit;
+};
+
+// Exact term of element i of a row: e = expf(y - M) for y >= thr (0
+// otherwise), times inv when as_p.
+template <class Row>
+struct PzTermRegen {
+  Row R;
+  float M, thr, inv;
+  bool as_p;
+  __device__ __forceinline__ void operator()(int k, float (&v)[4]) const {
+    float yy[4];
+    const int n = R.get(pz_seg_e0(k), yy);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float e = (c < n && yy[c] >= thr) ? pz_expf(yy[c] - M) : 0.0f;
+      v[c] = as_p ? e * inv : e;
+    }
+  }
+};
+
+// Records pass over tiles [0, tmax]: the exact terms of every segment whose
+// seg_gf holds a predicted grid are recorded at that grid.
+template <int U2, class Row>
+__device__ __forceinline__ void pz_record_terms(const PzTermRegen<Row>& G, int tmax,
+                                                uint32_t* seg_d, uint32_t* seg_gf) {
+  const int w = threadIdx.x >> 6;
+  for (int t0 = 0; t0 <= tmax; t0 += U2) {
+    float y[U2][4];
+    int nv[U2];
+#pragma unroll
+    for (int uu = 0; uu < U2; uu++) {
+      nv[uu] = 0;
+      if (t0 + uu <= tmax) nv[uu] = G.R.get(pz_tile_e0(t0 + uu), y[uu]);
+    }
+#pragma unroll
+    for (int uu = 0; uu < U2; uu++) {
+      const int t = t0 + uu;
+      if (t > tmax) continue;
+      const int k = t * PZ_SEGS_PER_TILE + w;
+      const uint32_t g = seg_gf[k];
+      if (g == PZ_NO_RECORD) continue;
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float e = (c < nv[uu] && y[uu][c] >= G.thr) ? pz_expf(y[uu][c] - G.M) : 0.0f;
+        v[c] = G.as_p ? e * G.inv : e;
+      }
+      pz_segment_record(v, g, true, seg_d, seg_gf, k);
+    }
+  }
+}
+
+// The reference's softmax normaliser (softmax.c:12-16; top_p.c:57-65 with
+// thr = max - 20): exact sequential fp32 sum of expf(y - M) over y >= thr in
+// ascending id.  seg_m/seg_s hold the row's pass-1 estimates.  Called by
+// every thread; returns the sum in every thread.
+template <int U2, class Row>
+__device__ __forceinline__ float pz_exact_normaliser(const Row& R, int ntiles, float M, float thr,
+                                                     const float* seg_m, const float* seg_s,
+                                                     uint32_t* seg_d, uint32_t* seg_gf,
+                                                     PzDrawShared& S) {
+  const int nseg = ntiles * PZ_SEGS_PER_TILE;
+  if (threadIdx.x < 64) pz_predict_grids(seg_m, seg_s, nseg, M, 1.0f, seg_gf);
+  __syncthreads();
+  PzTermRegen<Row> G{R, M, thr, 0.0f, false};
+  pz_record_terms<U2>(G, ntiles - 1, seg_d, seg_gf);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    PzAcc st;
+    st.n = 0;
+    st.g = 1;
+    pz_wave_walk(st, seg_d, seg_gf, nseg, 0.0f, PZ_STOP_NONE, G);
+    if (threadIdx.x == 0) S.sum = pz_acc_value(st);
+  }
+  __syncthreads();
+  return S.sum;
+}
+
+// The reference's categorical draw (generate.c:162-168): cdf += p_i with
+// p_i = expf(y_i - M) * inv in ascending id, the first i with r < cdf.
+// Records are made only for the segments the estimated CDF can reach.
+// Called by every thread; returns the index or -1 (no hit) in every thread.
+template <int U2, class Row>
+__device__ __forceinline__ int pz_exact_cdf_draw(const Row& R, int V, int ntiles, float M,
+                                                 float inv, float r, const float* seg_m,
+                                                 const float* seg_s, uint32_t* seg_d,
+                                                 uint32_t* seg_gf, PzDrawShared& S) {
+  const int nseg = ntiles * PZ_SEGS_PER_TILE;
+  if (threadIdx.x < 64) {
+    const int kmax = pz_predict_grids(seg_m, seg_s, nseg, M, inv, seg_gf, r + 0.01f);
+    if (threadIdx.x == 0) S.kmax = kmax;
+  }
+  __syncthreads();
+  const int kmax = S.kmax;
+  PzTermRegen<Row> G{R, M, -__builtin_inff(), inv, true};
+  pz_record_terms<U2>(G, kmax < 0 ? -1 : kmax / PZ_SEGS_PER_TILE, seg_d, seg_gf);
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    PzAcc st;
+    st.n = 0;
+    st.g = 1;
+    int hit = pz_wave_walk(st, seg_d, seg_gf, nseg, r, PZ_STOP_GT, G);
+    if (hit >= V) hit = -1;  // padding terms are 0 and never raise the CDF
+    if (threadIdx.x == 0) S.hit = hit;
+  }
+  __syncthreads();
+  return S.hit;
+}

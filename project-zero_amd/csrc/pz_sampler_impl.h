@@ -1,0 +1,64 @@
+// pz_sampler_impl.h -- the sampler object behind the opaque pz_sampler
+// handle of include/pz_sampler.h (shared by the host-side sources).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/pz_sampler.h"
+#include "pz_launch.h"
+#include "pz_params.h"
+
+struct pz_sampler {
+  int device = 0;
+  int max_batch = 0, max_vocab = 0, max_hist = 0;
+  int temp_mode = PZ_TEMP_MUL_RECIP;
+  int max_lds = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t staged = nullptr;  // guards reuse of the pinned staging area
+
+  // pinned host staging and their device mirrors
+  pz_row_params_dev* h_params = nullptr;
+  pz_row_params_dev* d_params = nullptr;
+  int32_t* h_rows = nullptr;
+  int32_t* d_rows = nullptr;
+  float* h_u = nullptr;
+  float* d_u = nullptr;
+  int32_t* h_ids = nullptr;
+  int32_t* d_ids = nullptr;
+  float* h_p = nullptr;
+  float* d_p = nullptr;
+
+  void* d_scratch = nullptr;
+  size_t scratch_bytes = 0;
+  pz_scratch sc{};
+
+  pz_row_params_dev* res_params = nullptr;  // host work area (max_batch)
+  int staged_n = -1, staged_B = -1;         // what d_params / d_rows hold
+
+  // speculative verification: device scratch and pinned staging, grown on
+  // demand by pz_spec_verify
+  void* spec_dev = nullptr;
+  size_t spec_dev_bytes = 0;
+  void* spec_host = nullptr;
+  size_t spec_host_bytes = 0;
+
+  char err[512] = {0};
+};
+
+static inline int fail(pz_sampler* s, int code, const char* fmt, ...) {
+  if (s) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(s->err, sizeof(s->err), fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+#define PZ_HIP(s, expr)                                                      \
+  do {                                                                       \
+    hipError_t e_ = (expr);                                                  \
+    if (e_ != hipSuccess)                                                    \
+      return fail((s), PZ_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)

@@ -1,0 +1,89 @@
+"""Speculative-draft verification on the GPU against the oracle: accepted
+lengths and every output id must be identical (the softmax normalisers, the
+residual mass and both CDFs use the reference's sequential fp32 rounding)."""
+import numpy as np
+import pytest
+
+import pz_oracle as po
+import pzsample as pz
+import workloads as wl
+from conftest import to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def run(torch, target, draft, draft_ids, u_acc, u_res, tau, has_bonus,
+        temp_mode=pz.PZ_TEMP_MUL_RECIP, label=""):
+    B, K, V = draft.shape
+    print(f"case {label} B={B} K={K} V={V} bonus={has_bonus}", flush=True)
+    d_t = to_dev(torch, np.ascontiguousarray(target))
+    d_d = to_dev(torch, np.ascontiguousarray(draft))
+    with pz.Sampler(B, V, temp_mode=temp_mode) as s:
+        acc, out = s.spec_verify(d_t, d_d, B, K, V, V, has_bonus, tau, draft_ids, u_acc, u_res)
+    wacc, wout, dist = po.spec_verify(target, draft, K, has_bonus, tau, draft_ids, u_acc, u_res,
+                                      temp_mode=temp_mode)
+    print(f"  accepted={acc.tolist()[:16]} boundary={int((dist < 1e-5).sum())}", flush=True)
+    assert (acc == wacc).all(), (label, acc, wacc)
+    bad = (out != wout).any(axis=1)
+    assert not bad.any(), (label, np.nonzero(bad)[0][:8], out[bad][:4], wout[bad][:4])
+    return acc, out
+
+
+def test_c5_full_size(torch_cuda):
+    w = wl.build_c5()
+    run(torch_cuda, w["target"], w["draft"], w["draft_ids"], w["u_acc"], w["u_res"], w["tau"],
+        True, label="c5")
+
+
+def test_c5_without_bonus_and_other_seeds(torch_cuda):
+    w = wl.build_c5(has_bonus=False, seed=0xC5 + 11)
+    run(torch_cuda, w["target"], w["draft"], w["draft_ids"], w["u_acc"], w["u_res"], w["tau"],
+        False, label="no bonus")
+    w = wl.build_c5(B=16, K=7, V=32000, seed=0xC5 + 12)
+    run(torch_cuda, w["target"], w["draft"], w["draft_ids"], w["u_acc"], w["u_res"], w["tau"],
+        True, label="K=7")
+
+
+def test_forced_paths(torch_cuda):
+    """draft == target accepts everything (u < 1) and reaches the bonus row;
+    u_acc == 1 then rejects with Z == 0 (draw from p); invalid draft ids
+    reject; a large gap forces the residual."""
+    B, K, V = 6, 3, 20000
+    rng = np.random.default_rng(5)
+    target = pz.synth_normal(B * (K + 1), V, 2.5, 77).reshape(B, K + 1, V)
+    draft = np.ascontiguousarray(target[:, :K, :]).copy()
+    draft[3] += pz.synth_normal(K, V, 3.0, 78).reshape(K, V)
+    draft_ids = rng.integers(0, V, size=(B, K)).astype(np.int32)
+    draft_ids[2, 0] = -1
+    draft_ids[4, 1] = V
+    u_acc = pz.synth_draws(B * K, 79).reshape(B, K)
+    u_acc[1, :] = 1.0
+    u_acc[5, 2] = 0.0
+    u_res = pz.synth_draws(B, 80)
+    u_res[0] = 1.0
+    acc, out = run(torch_cuda, target, draft, draft_ids, u_acc, u_res, 0.8, True, label="forced")
+    assert acc[0] == K and acc[1] == 0 and acc[2] == 0
+
+
+def test_degenerate_rows(torch_cuda):
+    B, K, V = 4, 2, 5000
+    target = pz.synth_normal(B * (K + 1), V, 2.0, 91).reshape(B, K + 1, V)
+    draft = np.ascontiguousarray(target[:, :K, :]) + 0.1
+    target[0, 0, 10] = np.nan       # p NaN at the first position -> V-1
+    draft[1, 0, 3] = np.nan         # q NaN -> Z == 0 -> draw from p
+    target[2, 2, :] = -np.inf       # degenerate bonus row
+    draft[2] = target[2, :K]        # accept both drafts
+    target[3, 0, 7] = np.inf
+    draft_ids = np.array([[1, 2], [3, 4], [5, 6], [7, 8]], np.int32)
+    draft_ids[2] = [int(np.argmax(target[2, 0])), int(np.argmax(target[2, 1]))]
+    u_acc = np.full((B, K), 0.5, np.float32)
+    u_res = pz.synth_draws(B, 92)
+    run(torch_cuda, target, draft, draft_ids, u_acc, u_res, 1.0, True, label="degenerate")
+
+
+@pytest.mark.parametrize("V", [1, 3, 4097, 151936])
+def test_sizes_and_temperature_forms(torch_cuda, V):
+    w = wl.build_c5(B=5, K=3, V=V, seed=0xC5 + V)
+    for mode in (pz.PZ_TEMP_MUL_RECIP, pz.PZ_TEMP_DIV):
+        run(torch_cuda, w["target"], w["draft"], w["draft_ids"], w["u_acc"], w["u_res"], 0.7,
+            True, temp_mode=mode, label=f"V={V} mode={mode}")
