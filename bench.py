@@ -8,11 +8,18 @@ pz_sample_batch call (the kernel plus the copy of the 1024 int32 ids to the
 host), timed over --steps steps after --warmup untimed ones.
 
 Printed: ONE JSON line with the throughput (rows/s), the roofline of the
-sampling kernel (algorithmic bytes / kernel time from HIP events on the
-sampler's stream, against the 8 TB/s HBM peak) and the CPU baseline (the
-oracle, single thread, on a bounded sample of the same workload).
+sampling kernels (algorithmic bytes / kernel time from HIP events on the
+sampler's own stream, against the 8 TB/s HBM peak), the measured HBM traffic
+per launch when a counter summary for the workload is committed
+(profiles/traffic.json), the CPU baseline (the oracle, one thread, on a
+bounded sample of the same workload) and the id parity of the timed batch.
 
-Other workloads (parity cases, measured for reference): --workload c1|c2|c3|c5.
+Other workloads, measured as parity cases with the same fields:
+  --workload c2   64 x 128256, temperature 0.7 + top-p 0.9 (5 spikes per row)
+  --workload c3   256 x 151936, presence/frequency + top-k 20 + top-p 0.8
+  --workload c1   one sequence x 49152, repetition + top-k 40 + top-p 0.95
+                  (500 steps of fresh logits, one row per call)
+  --workload c5   speculative verification, 32 sequences x 4 drafts x 128256
 """
 import argparse
 import json
@@ -24,6 +31,21 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "project-zero_amd"))
 
 HBM_PEAK_GBS = 8000.0
+METRIC = "sampled rows/s at vocab 128256, batch 1-1024; achieved HBM GB/s vs peak"
+
+WORKLOAD_TEXT = {
+    "c4": "repetition 1.15 (H=256 uniform ids) + greedy argmax, batch 1024 x vocab 128256, "
+          "N(0,3^2) logits",
+    "c2": "temperature 0.7 + top-p 0.9, batch 64 x vocab 128256, N(0,2^2) + 5 spikes/row",
+    "c3": "presence 0.5 / frequency 0.3 (512 Zipf(1.1) ids) + top-k 20 + top-p 0.8, "
+          "batch 256 x vocab 151936, 2.5*Gumbel logits",
+    "c1": "repetition 1.1 (H=64) + T 0.8 + top-k 40 + top-p 0.95, one sequence x vocab 49152, "
+          "one row per call",
+    "c5": "speculative verification, 32 sequences x 4 drafts x vocab 128256 (+ bonus row), "
+          "tau 0.8",
+}
+KERNELS = {"c4": "k_greedy", "c2": "k_topp", "c3": "k_topk", "c1": "k_topk",
+           "c5": "k_spec_rows + k_spec_verify"}
 
 
 def parse():
@@ -31,7 +53,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOAD_TEXT))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU time of the baseline sample")
@@ -42,50 +64,70 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(w, budget_s):
-    """Times the oracle on the host (1 thread) on a bounded sample of the
-    workload: whole batches repeated until budget_s of CPU time."""
+def orc_params(po, p):
+    return po.params(p.temperature, p.top_k, p.top_p, p.rep_penalty, p.presence_penalty,
+                     p.frequency_penalty)
+
+
+def cpu_baseline_rows(w, budget_s):
+    """The oracle (one thread) on whole batches, or on a prefix of the batch
+    when one batch exceeds the budget; returns (baseline, ids of the rows it
+    sampled)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
     import pz_oracle as po
-    x = w["logits"]
-    p = w["params"][0]
-    prm = [po.params(p.temperature, p.top_k, p.top_p, p.rep_penalty, p.presence_penalty,
-                     p.frequency_penalty)]
+    x, u, hist = w["logits"], w["u"], w["hist"]
+    prm = [orc_params(po, p) for p in w["params"]]
     B = x.shape[0]
-    # one probe batch sizes the sample
+    probe = min(B, 8)
     t0 = time.perf_counter()
-    ids, _, _, _ = po.sample_batch(x, prm, u=w["u"], hist=w["hist"])
-    one = time.perf_counter() - t0
-    reps = max(1, int(budget_s / max(one, 1e-6)))
+    po.sample_batch(x[:probe], prm, u=None if u is None else u[:probe],
+                    hist=None if hist is None else hist[:probe])
+    per_row = (time.perf_counter() - t0) / probe
+    rows = int(max(1, min(B, budget_s / max(per_row, 1e-9))))
+    reps = 1
+    if rows == B:
+        reps = max(1, int(budget_s / max(per_row * B, 1e-9)))
     t0 = time.perf_counter()
     for _ in range(reps):
-        po.sample_batch(x, prm, u=w["u"], hist=w["hist"])
+        ids, _, _, _ = po.sample_batch(x[:rows], prm, u=None if u is None else u[:rows],
+                                       hist=None if hist is None else hist[:rows])
     dt = time.perf_counter() - t0
-    rows = reps * B
-    return {"value": rows / dt, "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} x the full {B}-row batch ({rows} rows, {dt:.1f} s, "
-                      "oracle/pz_oracle.c, 1 thread)"}, ids
+    n = rows * reps
+    what = (f"{reps} x the full {B}-row batch" if rows == B else f"the first {rows} of {B} rows")
+    return {"value": n / dt, "unit": "rows/s", "cores": 1, "kind": "port",
+            "sample": f"{what} ({n} rows, {dt:.1f} s; oracle/pz_oracle.c, 1 thread)"}, ids
 
 
-def main():
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: the sampler shards by rows "
-                                   "with no exchange, so run --gpus 1 (multi-GPU figures "
-                                   "are not produced)"}))
-        sys.exit(2)
+def traffic_for(workload):
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return t.get(workload, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def kernel_time_ms(torch, stream_ptr, fn, steps):
+    """Average time of fn()'s kernels per call from HIP events on the
+    sampler's own stream."""
+    ext = torch.cuda.ExternalStream(stream_ptr)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    e0.record(ext)
+    for _ in range(steps):
+        fn()
+    e1.record(ext)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_rows(args, torch, w):
     import numpy as np
-    import torch
-
     import pzsample as pz
-    import workloads as wl
-
-    if args.workload in ("c1", "c5"):
-        print(json.dumps({"error": f"workload {args.workload} is a parity case; "
-                                   "bench lines cover c2, c3, c4"}))
-        sys.exit(2)
-    log(f"building workload {args.workload}")
-    w = wl.BUILDERS[args.workload]()
     x = w["logits"]
     B, V = x.shape
     hist = w["hist"]
@@ -97,75 +139,149 @@ def main():
     t_u = torch.from_numpy(u).to(dev) if u is not None else None
     t_ids = torch.empty(B, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
-    # raw addresses: the inputs are resident and torch's stream is idle
-    d_x = t_x.data_ptr()
+    d_x, d_ids = t_x.data_ptr(), t_ids.data_ptr()
     d_h = t_h.data_ptr() if t_h is not None else None
     d_u = t_u.data_ptr() if t_u is not None else None
-    d_ids = t_ids.data_ptr()
-    s = pz.Sampler(B, V, max_hist=max(H, 1))
     params = w["params"]
+    s = pz.Sampler(B, V, max_hist=max(H, 1))
+    per_call = 1 if args.workload == "c1" else B  # c1: one row per call, like the reference loop
+    ids = np.empty(B, np.int32)
+
+    def step():
+        if per_call == B:
+            return s.sample(d_x, B, V, V, params, u=u, d_hist=d_h, H=H)[0]
+        for r in range(B):
+            ids[r] = s.sample(d_x + 4 * V * r, 1, V, V, params,
+                              u=None if u is None else u[r:r + 1],
+                              d_hist=None if d_h is None else d_h + 4 * H * r, H=H)[0][0]
+        return ids
 
     log("warmup")
     for _ in range(args.warmup):
-        ids, _ = s.sample(d_x, B, V, V, params, u=u, d_hist=d_h, H=H)
+        out = step()
     torch.cuda.synchronize()
-
-    log(f"timing {args.steps} steps")
+    steps = args.steps if per_call == B else max(1, args.steps // 10)
+    log(f"timing {steps} steps")
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ids, _ = s.sample(d_x, B, V, V, params, u=u, d_hist=d_h, H=H)
+    for _ in range(steps):
+        out = step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    ms_per_step = (t1 - t0) * 1e3 / steps
+    gpu_ids = out.copy()
 
-    # kernel time: HIP events on the sampler's own stream around back-to-back
-    # launches (parameters are staged once, so each step is one kernel)
-    ext = torch.cuda.ExternalStream(s.stream)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    s.sample_async(d_x, B, V, V, params, d_u, d_ids, d_hist=d_h, H=H)
-    s.sync()
-    e0.record(ext)
+    if per_call == B:
+        def launch():
+            s.sample_async(d_x, B, V, V, params, d_u, d_ids, d_hist=d_h, H=H)
+    else:
+        def launch():
+            s.sample_async(d_x, 1, V, V, params, d_u, d_ids, d_hist=d_h, H=H)
+    kern_ms = kernel_time_ms(torch, s.stream, launch, max(steps, 20))
+    rows_per_launch = per_call
+    s.close()
+    return dict(B=B, V=V, H=H, ms_per_step=ms_per_step, rows_per_step=B,
+                kern_ms=kern_ms, bytes_per_launch=w["bytes_per_row"] * rows_per_launch,
+                gpu_ids=gpu_ids)
+
+
+def bench_spec(args, torch, w):
+    import pzsample as pz
+    B, K, V = w["B"], w["K"], w["V"]
+    dev = torch.device("cuda:0")
+    t_t = torch.from_numpy(w["target"]).to(dev)
+    t_d = torch.from_numpy(w["draft"]).to(dev)
+    torch.cuda.synchronize()
+    s = pz.Sampler(B, V)
+
+    def call():
+        return s.spec_verify(t_t.data_ptr(), t_d.data_ptr(), B, K, V, V, w["has_bonus"],
+                             w["tau"], w["draft_ids"], w["u_acc"], w["u_res"])
+
+    for _ in range(args.warmup):
+        acc, out = call()
+    t0 = time.perf_counter()
     for _ in range(args.steps):
-        s.sample_async(d_x, B, V, V, params, d_u, d_ids, d_hist=d_h, H=H)
-    e1.record(ext)
-    e1.synchronize()
-    kern_ms = e0.elapsed_time(e1) / args.steps
-    log(f"step {ms_per_step * 1e3:.1f} us, kernel {kern_ms * 1e3:.1f} us")
+        acc, out = call()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    kern_ms = kernel_time_ms(torch, s.stream, call, max(args.steps, 20))
+    s.close()
+    return dict(B=B, V=V, K=K, ms_per_step=ms, rows_per_step=B, kern_ms=kern_ms,
+                bytes_per_launch=w["bytes_per_seq"] * B, acc=acc, out=out)
 
-    bytes_batch = w["bytes_per_row"] * B
-    achieved = bytes_batch / (kern_ms * 1e-3) / 1e9
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU (one process, one device); "
+                                   "rows shard across GPUs with no exchange, so multi-GPU "
+                                   "figures are not produced: run --gpus 1"}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import workloads as wl
+
+    log(f"building workload {args.workload}")
+    w = wl.BUILDERS[args.workload]()
+    if args.workload == "c5":
+        r = bench_spec(args, torch, w)
+        unit = "sequences/s"
+    else:
+        r = bench_rows(args, torch, w)
+        unit = "rows/s"
+    log(f"step {r['ms_per_step'] * 1e3:.1f} us, kernels {r['kern_ms'] * 1e3:.1f} us per launch")
+    achieved = r["bytes_per_launch"] / (r["kern_ms"] * 1e-3) / 1e9
+    config = {"workload": WORKLOAD_TEXT[args.workload], "batch": r["B"], "vocab": r["V"]}
+    if "H" in r:
+        config["hist"] = r["H"]
+    if "K" in r:
+        config["drafts"] = r["K"]
     line = {
-        "metric": "sampled rows/s at vocab 128256, batch 1-1024; achieved HBM GB/s vs peak",
-        "value": B / (ms_per_step * 1e-3),
-        "unit": "rows/s",
+        "metric": METRIC,
+        "value": r["rows_per_step"] / (r["ms_per_step"] * 1e-3),
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
-        "config": {"workload": {
-            "c4": "greedy+repetition-1.15 (H=256), batch 1024 x vocab 128256, N(0,3^2) logits",
-            "c2": "temperature 0.7 + top-p 0.9, batch 64 x vocab 128256, N(0,2^2)+5 spikes",
-            "c3": "presence 0.5/frequency 0.3 (512 Zipf ids) + top-k 20 + top-p 0.8, "
-                  "batch 256 x vocab 151936, 2.5*Gumbel",
-        }[args.workload], "batch": B, "vocab": V, "hist": H},
+        "data": "synthetic (seeded generators in project-zero_amd/synth)",
+        "config": config,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel_us": kern_ms * 1e3,
-                     "algorithmic_bytes_per_launch": bytes_batch},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(args.workload),
+                     "kernel": KERNELS[args.workload], "kernel_us": r["kern_ms"] * 1e3,
+                     "algorithmic_bytes_per_launch": r["bytes_per_launch"]},
     }
     if not args.no_cpu:
         log("cpu baseline")
-        cb, cpu_ids = cpu_baseline(w, args.cpu_seconds)
-        line["cpu_baseline"] = cb
-        mism = int((cpu_ids != ids).sum())
-        line["parity"] = {"rows": B, "id_mismatches_vs_oracle": mism}
-    s.close()
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pz_oracle as po
+        if args.workload == "c5":
+            t0 = time.perf_counter()
+            reps = 0
+            while True:
+                acc, out, _ = po.spec_verify(w["target"], w["draft"], w["K"], w["has_bonus"],
+                                             w["tau"], w["draft_ids"], w["u_acc"], w["u_res"])
+                reps += 1
+                if time.perf_counter() - t0 >= args.cpu_seconds:
+                    break
+            dt = time.perf_counter() - t0
+            line["cpu_baseline"] = {"value": reps * w["B"] / dt, "unit": "sequences/s",
+                                    "cores": 1, "kind": "port",
+                                    "sample": f"{reps} x the full {w['B']}-sequence batch "
+                                              f"({dt:.1f} s; oracle/pz_oracle.c, 1 thread)"}
+            line["parity"] = {"sequences": w["B"],
+                              "acc_len_mismatches": int((acc != r["acc"]).sum()),
+                              "id_mismatches": int((out != r["out"]).any(axis=1).sum())}
+        else:
+            cb, cpu_ids = cpu_baseline_rows(w, args.cpu_seconds)
+            line["cpu_baseline"] = cb
+            n = len(cpu_ids)
+            line["parity"] = {"rows_checked": n,
+                              "id_mismatches_vs_oracle": int((cpu_ids != r["gpu_ids"][:n]).sum())}
     print(json.dumps(line), flush=True)
 
 

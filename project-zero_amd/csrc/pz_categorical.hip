@@ -10,13 +10,13 @@
 // comparison succeeds and the draw is V-1.
 //
 // Design (one 1024-thread workgroup per row):
-//   pass 1 (HBM)  maximum, NaN check, per-segment estimates;
+//   pass 1 (HBM)  maximum and NaN check;
 //   pass 2 (L2)   exact e (glibc-identical pz_expf) -> integer segment records
-//                 at the predicted binade; wave 0 walks them: exact sum;
-//   pass 3 (L2)   exact p = e * inv -> records for the CDF, only over the
-//                 segments the estimated CDF says the draw can reach; wave 0
-//                 walks them with the stop rule r < cdf and resolves the hit
-//                 segment element by element.
+//                 at predicted binades; wave 0 walks them: exact sum;
+//   pass 3 (L2)   exact p = e * inv -> records for the CDF, only as far as the
+//                 estimated CDF says the draw can reach; wave 0 walks them with
+//                 the stop rule r < cdf and resolves the hit segment element by
+//                 element.
 #include "pz_device.h"
 #include "pz_exact.h"
 #include "pz_launch.h"
@@ -26,7 +26,7 @@ namespace {
 
 struct CatShared {
   PzPass1Shared p1;
-  PzDrawShared d;
+  PzRecShared r;
 };
 
 template <bool VEC>
@@ -44,16 +44,13 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
   PzRow<VEC> R;
   R.x = logits + (long)row * ld;
   R.V = V;
-  R.prm = &prm;
+  R.T = PzTemp::of(prm);
   pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
 
   const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
-  float* seg_m = reinterpret_cast<float*>(lds + pen_bytes);
-  float* seg_s = seg_m + nseg;
-  uint32_t* seg_d = reinterpret_cast<uint32_t*>(seg_s + nseg);
-  uint32_t* seg_gf = seg_d + nseg;
+  const PzRec REC = pz_rec_at(lds + pen_bytes, nseg);
 
-  const float M = pz_pass1<8>(R, ntiles, seg_m, seg_s, S.p1);
+  const float M = pz_pass1<8>(R, ntiles, S.p1);
   if (S.p1.any_nan || !(M > -__builtin_inff() && M < __builtin_inff())) {
     if (tid == 0) {
       ids_out[row] = V - 1;
@@ -61,11 +58,17 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
     }
     return;
   }
-  const float sum = pz_exact_normaliser<4>(R, ntiles, M, -__builtin_inff(), seg_m, seg_s,
-                                           seg_d, seg_gf, S.d);
+  PzExpTerms<PzRow<VEC>> X;
+  X.R = R;
+  X.M = M;
+  X.thr = -__builtin_inff();
+  X.inv = 1.0f;
+  X.as_p = false;
+  const float sum = pz_exact_sum(X, ntiles, REC, S.r);
   const float inv = 1.0f / sum;  // softmax.c:19-22
-  const int hit = pz_exact_cdf_draw<4>(R, V, ntiles, M, inv, u[row], seg_m, seg_s, seg_d,
-                                       seg_gf, S.d);
+  X.inv = inv;
+  X.as_p = true;
+  const int hit = pz_exact_draw(X, V, ntiles, u[row], REC, S.r);
   if (tid == 0) {
     const int id = hit >= 0 ? hit : V - 1;  // generate.c:161
     ids_out[row] = id;
@@ -85,7 +88,7 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
 template <bool VEC>
 int launch_cat_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   const int pen = L.pen_any ? (int)((pz_penalty_lds_bytes(L.V, L.hcap) + 15) & ~(size_t)15) : 0;
-  const size_t lds = pen + (size_t)pz_nseg(L.V) * 16;
+  const size_t lds = pen + pz_rec_bytes(L.V);
   if (lds + sizeof(CatShared) + 64 > (size_t)L.max_lds) return -2;
   auto kern = k_categorical<VEC>;
   if (lds > 65536 && hipFuncSetAttribute((const void*)kern,

@@ -100,10 +100,16 @@ __device__ __forceinline__ float pz_unkey(uint32_t k) {
 // The penalty is applied virtually while a kernel streams the row: the
 // logits in HBM are never written.
 // ---------------------------------------------------------------------------
+// LDS-qualified pointers: lookups compile to ds_read (counted by lgkmcnt
+// only), so they never force a wait on the row's outstanding HBM loads the
+// way generic (flat) accesses would.
+typedef __attribute__((address_space(3))) uint32_t pz_lds_u32;
+typedef __attribute__((address_space(3))) int32_t pz_lds_i32;
+
 struct PzPenalty {
-  uint32_t* bitmap;   // ceil(V/32) words, bit i set <=> id i in history
-  int32_t* hkey;      // hash keys (-1 = empty), hcap entries
-  int32_t* hcnt;      // counts
+  const pz_lds_u32* bitmap;  // ceil(V/32) words, bit i set <=> id i in history
+  const pz_lds_i32* hkey;    // hash keys (-1 = empty), hcap entries
+  const pz_lds_i32* hcnt;    // counts
   int hcap;           // power of two, 0 when counts are not needed
   float rep, pres, freq;
   bool active;
@@ -130,25 +136,28 @@ __device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V,
   P.rep = prm.rep_penalty;
   P.pres = prm.presence_penalty;
   P.freq = prm.frequency_penalty;
-  P.bitmap = reinterpret_cast<uint32_t*>(lds);
   const int words = (V + 31) >> 5;
-  P.hkey = reinterpret_cast<int32_t*>(lds + (size_t)words * 4);
-  P.hcnt = P.hkey + hcap;
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds);
+  int32_t* hkey = reinterpret_cast<int32_t*>(lds + (size_t)words * 4);
+  int32_t* hcnt = hkey + hcap;
+  P.bitmap = (const pz_lds_u32*)bitmap;
+  P.hkey = (const pz_lds_i32*)hkey;
+  P.hcnt = (const pz_lds_i32*)hcnt;
   P.hcap = (prm.presence_penalty != 0.0f || prm.frequency_penalty != 0.0f) ? hcap : 0;
   if (!P.active) return;
-  for (int w = tid; w < words; w += BLOCK) P.bitmap[w] = 0u;
-  for (int j = tid; j < P.hcap; j += BLOCK) { P.hkey[j] = -1; P.hcnt[j] = 0; }
+  for (int w = tid; w < words; w += BLOCK) bitmap[w] = 0u;
+  for (int j = tid; j < P.hcap; j += BLOCK) { hkey[j] = -1; hcnt[j] = 0; }
   __syncthreads();
   const uint32_t mask = (uint32_t)P.hcap - 1u;
   for (int j = tid; j < H; j += BLOCK) {
     const int id = hist_row[j];
     if (id < 0 || id >= V) continue;  // ids outside [0,V) are ignored
-    atomicOr(&P.bitmap[id >> 5], 1u << (id & 31));
+    atomicOr(&bitmap[id >> 5], 1u << (id & 31));
     if (P.hcap) {
       uint32_t s = pz_hash((uint32_t)id) & mask;
       while (true) {
-        const int prev = atomicCAS(&P.hkey[s], -1, id);
-        if (prev == -1 || prev == id) { atomicAdd(&P.hcnt[s], 1); break; }
+        const int prev = atomicCAS(&hkey[s], -1, id);
+        if (prev == -1 || prev == id) { atomicAdd(&hcnt[s], 1); break; }
         s = (s + 1) & mask;
       }
     }
@@ -188,12 +197,31 @@ __device__ __forceinline__ float pz_temper(float x, const pz_row_params_dev& p) 
   return p.temp_div ? x / p.temp : x * p.inv_temp;
 }
 
+// The same, with the row's parameters held in registers.
+struct PzTemp {
+  float t, inv;
+  int div;
+  __device__ __forceinline__ static PzTemp of(const pz_row_params_dev& p) {
+    PzTemp r;
+    r.t = p.temp;
+    r.inv = p.inv_temp;
+    r.div = p.temp_div;
+    return r;
+  }
+  __device__ __forceinline__ float apply(float x) const { return div ? x / t : x * inv; }
+};
+
 // Value the sampling chain sees for raw logit x of id i: penalties (when the
 // row has any), then temperature.
 __device__ __forceinline__ float pz_transform(const PzPenalty& P, const pz_row_params_dev& prm,
                                               float x, int i) {
   if (P.active && pz_pen_member(P, i)) x = pz_penalize(P, x, i);
   return pz_temper(x, prm);
+}
+__device__ __forceinline__ float pz_transform(const PzPenalty& P, const PzTemp& T, float x,
+                                              int i) {
+  if (P.active && pz_pen_member(P, i)) x = pz_penalize(P, x, i);
+  return T.apply(x);
 }
 
 // ---------------------------------------------------------------------------
@@ -233,15 +261,29 @@ __device__ void pz_block_argmax(float& bv, int& bi, float* sv, int* si) {
   __syncthreads();
 }
 
-template <typename T>
-__device__ __forceinline__ T pz_wave_sum(T v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, PZ_WAVE);
-  return v;
+// Wave-wide reductions with DPP (row shifts + row broadcasts: no LDS round
+// trip).  The inclusive scan leaves the total in lane 63.
+#define PZ_DPPF(v, ident, ctrl, rmask)                                                   \
+  __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(ident), __float_as_int(v), \
+                                             (ctrl), (rmask), 0xf, false))
+
+__device__ __forceinline__ float pz_wave_sum(float v) {
+  v += PZ_DPPF(v, 0.0f, 0x111, 0xf);
+  v += PZ_DPPF(v, 0.0f, 0x112, 0xf);
+  v += PZ_DPPF(v, 0.0f, 0x114, 0xf);
+  v += PZ_DPPF(v, 0.0f, 0x118, 0xf);
+  v += PZ_DPPF(v, 0.0f, 0x142, 0xa);
+  v += PZ_DPPF(v, 0.0f, 0x143, 0xc);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ float pz_wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, PZ_WAVE));
-  return v;
+  const float ninf = -__builtin_inff();
+  v = fmaxf(v, PZ_DPPF(v, ninf, 0x111, 0xf));
+  v = fmaxf(v, PZ_DPPF(v, ninf, 0x112, 0xf));
+  v = fmaxf(v, PZ_DPPF(v, ninf, 0x114, 0xf));
+  v = fmaxf(v, PZ_DPPF(v, ninf, 0x118, 0xf));
+  v = fmaxf(v, PZ_DPPF(v, ninf, 0x142, 0xa));
+  v = fmaxf(v, PZ_DPPF(v, ninf, 0x143, 0xc));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }

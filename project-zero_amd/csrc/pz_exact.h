@@ -135,12 +135,15 @@ __device__ __forceinline__ uint32_t pz_wave_sum_u32(uint32_t v) {
 // Inclusive prefix sum of floats over the lanes (any rounding: used only for
 // estimates).
 __device__ __forceinline__ float pz_wave_scan_f32(float v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float o = __shfl_up(v, off, 64);
-    if (lane >= off) v += o;
-  }
+#define PZ_DPPF_(v, ctrl, rmask) \
+  __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), (ctrl), (rmask), 0xf, false))
+  v += PZ_DPPF_(v, 0x111, 0xf);
+  v += PZ_DPPF_(v, 0x112, 0xf);
+  v += PZ_DPPF_(v, 0x114, 0xf);
+  v += PZ_DPPF_(v, 0x118, 0xf);
+  v += PZ_DPPF_(v, 0x142, 0xa);
+  v += PZ_DPPF_(v, 0x143, 0xc);
+#undef PZ_DPPF_
   return v;
 }
 
@@ -238,71 +241,6 @@ __device__ __forceinline__ int pz_wave_accumulate(PzAcc& st, const float (&v)[C]
     if (cum && lane == 0) cum[idx] = sv;
     if (stop_mode != PZ_STOP_NONE && pz_stop_hit(sv, thr, stop_mode)) return idx;
     pos = idx + 1;
-  }
-  return -1;
-}
-
-// Per-segment record of a predicted-grid pass: the integer sum of the
-// segment's increments at grid g, and whether any term was a tie or BIG
-// (then the record is unusable).  Stored as d and gf = g | dirty << 8.
-__device__ __forceinline__ void pz_segment_record(const float (&v)[4], uint32_t g, bool valid,
-                                                  uint32_t* seg_d, uint32_t* seg_gf, int k) {
-  uint32_t s = 0;
-  bool dirty = false;
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    uint32_t cls;
-    const uint32_t i = pz_inc(v[c], g, &cls);
-    dirty |= cls != PZ_INC_PLAIN;
-    s += i;
-  }
-  const uint32_t tot = pz_wave_sum_u32(valid ? s : 0u);
-  const bool any_dirty = __ballot(valid && dirty) != 0;
-  if ((threadIdx.x & 63) == 0) {
-    seg_d[k] = tot;
-    seg_gf[k] = g | (any_dirty ? 0x100u : 0u);
-  }
-}
-
-// Walk over segment records in order (one wave).  A record is used as is when
-// its grid equals the running state's grid, it is clean and the state stays
-// in the binade; every other segment is regenerated (regen(k, v) fills this
-// lane's 4 terms of segment k) and accumulated element by element.  With a
-// stop mode returns the global element index (k*256 + i) of the first hit,
-// else -1.  st is advanced accordingly.
-template <class Regen>
-__device__ __forceinline__ int pz_wave_walk(PzAcc& st, const uint32_t* seg_d, const uint32_t* seg_gf, int nseg,
-                            float thr, int stop_mode, Regen&& regen) {
-  const int lane = threadIdx.x & 63;
-  int k0 = 0;
-  while (k0 < nseg) {
-    const int k = k0 + lane;
-    uint32_t d = 0;
-    bool ok = false;
-    if (k < nseg) {
-      ok = seg_gf[k] == st.g;
-      d = ok ? seg_d[k] : 0u;
-    }
-    const uint32_t incl = pz_wave_scan_u32(d);
-    const uint32_t nend = st.n + incl;
-    bool bad = false;
-    if (k < nseg) {
-      bad = !ok || nend >= (1u << 24) ||
-            (stop_mode != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(nend, st.g), thr, stop_mode));
-    }
-    const uint64_t ball = __ballot(bad);
-    if (!ball) {
-      st.n += pz_readlane_u32(incl, 63);
-      k0 += 64;
-      continue;
-    }
-    const int L = (int)__builtin_ctzll(ball);
-    st.n += pz_readlane_u32(incl - d, L);
-    float v[4];
-    regen(k0 + L, v);
-    const int f = pz_wave_accumulate<4>(st, v, 0, thr, stop_mode, nullptr);
-    if (f >= 0) return (k0 + L) * 256 + f;
-    k0 += L + 1;
   }
   return -1;
 }

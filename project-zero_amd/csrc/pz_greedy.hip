@@ -41,11 +41,13 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
     const pz_f4* x4 = reinterpret_cast<const pz_f4*>(x);
     const int n4 = V >> 2;
     for (int base = 0; base < n4; base += BLOCK * U) {
+      // unconditional loads (clamped to the row's last float4) keep all U
+      // in flight; out-of-range groups are skipped below
       pz_f4 v[U];
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const int i4 = base + u * BLOCK + tid;
-        if (i4 < n4) v[u] = __builtin_nontemporal_load(&x4[i4]);
+        v[u] = __builtin_nontemporal_load(&x4[i4 < n4 ? i4 : n4 - 1]);
       }
 #pragma unroll
       for (int u = 0; u < U; u++) {

@@ -1,11 +1,24 @@
 // pz_rowpass.h -- streaming passes of one 1024-thread workgroup over one
-// logits row, shared by the kernels whose normaliser is a full-row sequential
-// fp32 sum (top-p, plain categorical, speculative verification).
+// logits row, shared by the kernels whose normaliser or CDF is a full-row
+// sequential fp32 sum (top-p, plain categorical, speculative verification).
 //
 // Layout: the row is walked in tiles of 4096 elements, one 128-bit load per
 // thread per tile; thread t of a tile holds elements 4t..4t+3.  A segment is
 // one wave's 256-element slice of a tile (segment k = tile*16 + wave), the
-// unit at which the exact-sum walk (pz_exact.h) keeps integer records.
+// unit at which the exact-sum records (pz_exact.h) are kept.
+//
+// Passes:
+//   pass 1   the row maximum (and NaN / y[0] checks): the compulsory HBM read;
+//   records  per chunk of 4 tiles: the exact terms are computed once, their
+//            fp32 segment sums estimate the running sum, from which each
+//            segment's binade is predicted; the segment's integer increment
+//            sum is then recorded at that grid (and at the grid below when
+//            the estimate sits within 1% above a power of two).  Segments
+//            whose terms need element-wise treatment (ties, terms as large
+//            as the running sum) keep their terms in an LDS cache;
+//   walk     one wave scans the records in order with the exact state and
+//            accumulates element by element wherever a record does not
+//            apply (pz_rec_walk).
 #pragma once
 #include "pz_device.h"
 #include "pz_exact.h"
@@ -14,6 +27,8 @@ constexpr int PZ_RB = 1024;           // threads per row workgroup
 constexpr int PZ_TILE = PZ_RB * 4;    // elements per tile
 constexpr int PZ_SEG = 256;           // elements per segment
 constexpr int PZ_SEGS_PER_TILE = PZ_RB / 64;
+constexpr int PZ_REC_CHUNK = 4;       // tiles per record chunk (= 64 segments)
+constexpr int PZ_REC_SLOTS = 32;      // dirty segments whose terms stay in LDS
 
 __host__ __device__ inline int pz_tiles(int V) { return (V + PZ_TILE - 1) / PZ_TILE; }
 __host__ __device__ inline int pz_nseg(int V) { return pz_tiles(V) * PZ_SEGS_PER_TILE; }
@@ -24,28 +39,28 @@ __device__ __forceinline__ int pz_seg_e0(int k) {
   return (k >> 4) * PZ_TILE + (k & 15) * PZ_SEG + 4 * ((int)threadIdx.x & 63);
 }
 
-// Raw logits of elements e0..e0+3 (e0 a multiple of 4); entries at or past V
-// read as 0.  Returns how many are < V.
+// Raw logits of elements e0..e0+3 (e0 a multiple of 4).  Returns how many
+// are < V; the others hold unspecified values.  The vector form always loads
+// (from the last in-bounds float4 when e0 is past the row: rows are 16-byte
+// aligned with ld a multiple of 4, so that float4 lies inside the row's ld
+// elements), which keeps the loads unconditional and lets the compiler keep
+// many in flight.
 template <bool VEC, bool NT>
 __device__ __forceinline__ int pz_load4(const float* __restrict__ x, int V, int e0, float (&r)[4]) {
-  if (VEC && e0 + 3 < V) {
-    const pz_f4* p = reinterpret_cast<const pz_f4*>(x + e0);
+  int n = V - e0;
+  n = n < 0 ? 0 : (n > 4 ? 4 : n);
+  if (VEC) {
+    const int last4 = (V - 1) & ~3;
+    const pz_f4* p = reinterpret_cast<const pz_f4*>(x + (e0 < last4 ? e0 : last4));
     const pz_f4 v = NT ? __builtin_nontemporal_load(p) : *p;
     r[0] = v.x;
     r[1] = v.y;
     r[2] = v.z;
     r[3] = v.w;
-    return 4;
+    return n;
   }
-  int n = 0;
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    r[c] = 0.0f;
-    if (e0 + c < V) {
-      r[c] = x[e0 + c];
-      n++;
-    }
-  }
+  for (int c = 0; c < 4; c++) r[c] = c < n ? x[e0 + c] : 0.0f;
   return n;
 }
 
@@ -55,13 +70,20 @@ struct PzRow {
   const float* x;
   int V;
   PzPenalty P;
-  const pz_row_params_dev* prm;
+  PzTemp T;
 
-  __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
-    const int n = pz_load4<VEC, false>(x, V, e0, y);
+  // raw logits of elements e0..e0+3 (count < V returned), then the chain
+  __device__ __forceinline__ int load(int e0, float (&y)[4]) const {
+    return pz_load4<VEC, false>(x, V, e0, y);
+  }
+  __device__ __forceinline__ void apply(int e0, int n, float (&y)[4]) const {
 #pragma unroll
     for (int c = 0; c < 4; c++)
-      if (c < n) y[c] = pz_transform(P, *prm, y[c], e0 + c);
+      if (c < n) y[c] = pz_transform(P, T, y[c], e0 + c);
+  }
+  __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
+    const int n = load(e0, y);
+    apply(e0, n, y);
     return n;
   }
 };
@@ -71,13 +93,20 @@ template <bool VEC>
 struct PzTempRow {
   const float* x;
   int V;
-  const pz_row_params_dev* prm;
+  PzTemp T;
 
-  __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
-    const int n = pz_load4<VEC, false>(x, V, e0, y);
+  __device__ __forceinline__ int load(int e0, float (&y)[4]) const {
+    return pz_load4<VEC, false>(x, V, e0, y);
+  }
+  __device__ __forceinline__ void apply(int e0, int n, float (&y)[4]) const {
+    (void)e0;
 #pragma unroll
     for (int c = 0; c < 4; c++)
-      if (c < n) y[c] = pz_temper(y[c], *prm);
+      if (c < n) y[c] = T.apply(y[c]);
+  }
+  __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
+    const int n = load(e0, y);
+    apply(e0, n, y);
     return n;
   }
 };
@@ -90,12 +119,9 @@ struct PzPass1Shared {
 
 // Pass 1 (the one compulsory HBM read of the row): the row maximum (NaN
 // ignored, as the reference's strict '>' scans do), whether any y is NaN,
-// y[0], and per segment k an estimate seg_m[k] = max, seg_s[k] =
-// sum exp(y - seg_m[k]) (hardware exp: estimates only, used to predict the
-// binade of the running sum).  Returns the maximum in every thread.
+// and y[0].  Returns the maximum in every thread.
 template <int U, class Row>
-__device__ __forceinline__ float pz_pass1(const Row& row, int ntiles, float* seg_m, float* seg_s,
-                          PzPass1Shared& S) {
+__device__ __forceinline__ float pz_pass1(const Row& row, int ntiles, PzPass1Shared& S) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   if (tid == 0) S.any_nan = 0;
   float tmax = -__builtin_inff();
@@ -106,36 +132,21 @@ __device__ __forceinline__ float pz_pass1(const Row& row, int ntiles, float* seg
 #pragma unroll
     for (int u = 0; u < U; u++) {
       nv[u] = 0;
-      if (t0 + u < ntiles) nv[u] = row.get(pz_tile_e0(t0 + u), r[u]);
+      if (t0 + u < ntiles) nv[u] = row.load(pz_tile_e0(t0 + u), r[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int t = t0 + u;
       if (t >= ntiles) continue;
-      float lm = -__builtin_inff();
+      row.apply(pz_tile_e0(t), nv[u], r[u]);
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         if (c >= nv[u]) continue;
         const float y = r[u][c];
         if (y != y) nan = true;
-        else lm = fmaxf(lm, y);
+        else tmax = fmaxf(tmax, y);
       }
       if (t == 0 && tid == 0) S.y0 = r[u][0];
-      tmax = fmaxf(tmax, lm);
-      const float sm = pz_wave_max(lm);
-      float s = 0.0f;
-      if (sm > -__builtin_inff() && sm < __builtin_inff()) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          const float y = r[u][c];
-          if (c < nv[u] && y > -__builtin_inff()) s += __expf(y - sm);
-        }
-      }
-      s = pz_wave_sum(s);
-      if (lane == 0) {
-        seg_m[t * PZ_SEGS_PER_TILE + w] = sm;
-        seg_s[t * PZ_SEGS_PER_TILE + w] = s;
-      }
     }
   }
   tmax = pz_wave_max(tmax);
@@ -148,144 +159,293 @@ __device__ __forceinline__ float pz_pass1(const Row& row, int ntiles, float* seg
   return M;
 }
 
-// Sentinel grid of a segment that has no record (the walk regenerates it).
+// ---------------------------------------------------------------------------
+// Exact-sum records
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) float pz_lds_f32;
+typedef __attribute__((address_space(3))) pz_f4 pz_lds_f4;
+
+// Sentinel gf of a segment without a record (the walk regenerates it).
 constexpr uint32_t PZ_NO_RECORD = 0xffffffffu;
+// gf = grid | DIRTY (record at grid unusable) | HAS2 (record at grid - 1) |
+// DIRTY2 (that one unusable)
+constexpr uint32_t PZ_GF_DIRTY = 0x100u, PZ_GF_HAS2 = 0x200u, PZ_GF_DIRTY2 = 0x400u;
 
-// One wave: grid exponent of the estimated running sum at the start of each
-// segment, where segment k adds about scale * seg_s[k] * exp(seg_m[k] - M).
-// Segments whose estimated start exceeds `limit` get PZ_NO_RECORD.  Writes
-// seg_gf[k]; returns the last segment at or below the limit (-1 if none).
-__device__ __forceinline__ int pz_predict_grids(const float* seg_m, const float* seg_s,
-                                                int nseg, float M, float scale,
-                                                uint32_t* seg_gf,
-                                                float limit = __builtin_inff()) {
-  const int lane = threadIdx.x & 63;
-  float carry = 0.0f;
-  int kmax = -1;
-  for (int k0 = 0; k0 < nseg; k0 += 64) {
-    const int k = k0 + lane;
-    float a = 0.0f;
-    if (k < nseg) {
-      const float m = seg_m[k];
-      if (m > -__builtin_inff()) a = seg_s[k] * __expf(m - M) * scale;
-    }
-    const float incl = pz_wave_scan_f32(a);
-    const float start = carry + (incl - a);
-    const bool in = k < nseg && start <= limit;
-    if (k < nseg) seg_gf[k] = in ? pz_grid_of(start) : PZ_NO_RECORD;
-    const uint64_t ball = __ballot(in);
-    if (ball) kmax = k0 + 63 - (int)__builtin_clzll(ball);
-    carry += pz_readlane_f32(incl, 63);
-  }
-  return kmax;
-}
-
-struct PzDrawShared {
-  float sum;
-  int kmax;
-  int hit;
+struct PzRec {
+  pz_lds_u32* d;      // [nseg] increment sum at the predicted grid
+  pz_lds_u32* d2;     // [nseg] increment sum at the grid below
+  pz_lds_u32* gf;     // [nseg] grid and flags
+  pz_lds_f32* a;      // [nseg] estimate of the segment's sum
+  pz_lds_i32* slot;   // [nseg] LDS cache slot of the segment's terms, or -1
+  pz_lds_f32* cache;  // [PZ_REC_SLOTS][256]
 };
 
-// Exact term of element i of a row: e = expf(y - M) for y >= thr (0
-// otherwise), times inv when as_p.
+__host__ __device__ inline size_t pz_rec_bytes(int V) {
+  return (size_t)pz_nseg(V) * 20 + (size_t)PZ_REC_SLOTS * PZ_SEG * 4;
+}
+
+// Carves the record arrays out of LDS at base (16-byte aligned).
+__device__ __forceinline__ PzRec pz_rec_at(char* base, int nseg) {
+  PzRec R;
+  R.cache = (pz_lds_f32*)base;
+  char* p = base + (size_t)PZ_REC_SLOTS * PZ_SEG * 4;
+  R.d = (pz_lds_u32*)p;
+  R.d2 = R.d + nseg;
+  R.gf = R.d2 + nseg;
+  R.a = (pz_lds_f32*)(R.gf + nseg);
+  R.slot = (pz_lds_i32*)(R.a + nseg);
+  return R;
+}
+
+struct PzRecShared {
+  int slots_used;
+  int stop;
+  int hit;
+  float sum;
+};
+
+// Predicted grid (and whether to record the grid below too) of a segment
+// whose running sum is estimated to start at s.
+__device__ __forceinline__ uint32_t pz_predict_gf(float s) {
+  const uint32_t g = pz_grid_of(s);
+  const bool near = g > 1u && (__float_as_uint(s) & 0x7fffffu) < 83886u;  // < 1% above 2^E
+  return g | (near ? PZ_GF_HAS2 : 0u);
+}
+
+__device__ __forceinline__ void pz_rec_segment(const float (&v)[4], uint32_t gf, int k,
+                                               const PzRec& R, PzRecShared& S) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t g = gf & 0xffu;
+  const bool has2 = (gf & PZ_GF_HAS2) != 0;
+  uint32_t s1 = 0, s2 = 0;
+  bool d1 = false, d2 = false;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint32_t cls;
+    s1 += pz_inc(v[c], g, &cls);
+    d1 |= cls != PZ_INC_PLAIN;
+  }
+  if (has2) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      uint32_t cls;
+      s2 += pz_inc(v[c], g - 1u, &cls);
+      d2 |= cls != PZ_INC_PLAIN;
+    }
+    s2 = pz_wave_sum_u32(s2);
+  }
+  s1 = pz_wave_sum_u32(s1);
+  const bool D1 = __ballot(d1) != 0;
+  const bool D2 = has2 && __ballot(d2) != 0;
+  int slot = -1;
+  if (D1 && (!has2 || D2)) {
+    // no clean record: keep the terms for the walk
+    if (lane == 0) slot = atomicAdd(&S.slots_used, 1);
+    slot = __builtin_amdgcn_readfirstlane(slot);
+    if (slot >= PZ_REC_SLOTS) slot = -1;
+    if (slot >= 0) {
+      pz_f4 q;
+      q.x = v[0];
+      q.y = v[1];
+      q.z = v[2];
+      q.w = v[3];
+      ((pz_lds_f4*)(R.cache + slot * PZ_SEG))[lane] = q;
+    }
+  }
+  if (lane == 0) {
+    R.d[k] = s1;
+    R.d2[k] = s2;
+    R.gf[k] = g | (D1 ? PZ_GF_DIRTY : 0u) | (has2 ? PZ_GF_HAS2 : 0u) | (D2 ? PZ_GF_DIRTY2 : 0u);
+    R.slot[k] = slot;
+  }
+}
+
+// Records pass over the row's terms (see the header).  X provides
+//   typename Raw; int load(e0, Raw&); void terms(e0, n, Raw&, float (&)[4]);
+//   void observe(e0, const float (&)[4]); void seg(k, float (&)[4]).
+// Recording stops after the chunk in which the estimated running sum passes
+// stop_after; later segments get PZ_NO_RECORD.  Every thread calls it; it
+// ends with the records complete (after a barrier).
+template <class X>
+__device__ __forceinline__ void pz_record_pass(X& x, int ntiles, const PzRec& R, PzRecShared& S,
+                                               float stop_after) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nseg = ntiles * PZ_SEGS_PER_TILE;
+  constexpr int U = PZ_REC_CHUNK;
+  if (tid == 0) {
+    S.slots_used = 0;
+    S.stop = 0;
+  }
+  float carry = 0.0f;  // wave 0: estimated running sum at the chunk start
+  int t0 = 0;
+  for (; t0 < ntiles; t0 += U) {
+    typename X::Raw raw[U];
+    int nv[U];
+    float v[U][4];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      nv[u] = 0;
+      if (t0 + u < ntiles) nv[u] = x.load(pz_tile_e0(t0 + u), raw[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int t = t0 + u;
+      if (t >= ntiles) continue;
+      const int e0 = pz_tile_e0(t);
+      x.terms(e0, nv[u], raw[u], v[u]);
+      x.observe(e0, v[u]);
+      const float a = pz_wave_sum((v[u][0] + v[u][1]) + (v[u][2] + v[u][3]));
+      if (lane == 0) R.a[t * PZ_SEGS_PER_TILE + w] = a;
+    }
+    __syncthreads();
+    if (w == 0) {
+      // U * 16 == 64 segments per chunk: one lane each
+      const int k = t0 * PZ_SEGS_PER_TILE + lane;
+      const bool in = k < nseg;
+      const float a = in ? R.a[k] : 0.0f;
+      const float incl = pz_wave_scan_f32(a);
+      if (in) R.gf[k] = pz_predict_gf(carry + (incl - a));
+      carry += pz_readlane_f32(incl, 63);
+      if (lane == 0 && carry > stop_after) S.stop = 1;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int t = t0 + u;
+      if (t >= ntiles) continue;
+      const int k = t * PZ_SEGS_PER_TILE + w;
+      pz_rec_segment(v[u], R.gf[k], k, R, S);
+    }
+    if (S.stop) {
+      t0 += U;
+      break;
+    }
+  }
+  for (int k = t0 * PZ_SEGS_PER_TILE + tid; k < nseg; k += PZ_RB) {
+    R.gf[k] = PZ_NO_RECORD;
+    R.slot[k] = -1;
+  }
+  __syncthreads();
+}
+
+// Walk over the records in order (one wave): a record is used when it was
+// made at the state's grid and is clean; the state then only advances by an
+// integer (checked to stay in the binade).  Any other segment is accumulated
+// element by element from its cached or regenerated terms.  With a stop mode
+// returns the element index of the first hit, else -1.
+template <class X>
+__device__ __forceinline__ int pz_rec_walk(PzAcc& st, const PzRec& R, int nseg, float thr,
+                                           int stop_mode, const X& x) {
+  const int lane = threadIdx.x & 63;
+  int k0 = 0;
+  while (k0 < nseg) {
+    const int k = k0 + lane;
+    uint32_t d = 0;
+    bool ok = false;
+    if (k < nseg) {
+      const uint32_t gf = R.gf[k];
+      if (gf != PZ_NO_RECORD) {
+        const uint32_t g = gf & 0xffu;
+        if (g == st.g && !(gf & PZ_GF_DIRTY)) {
+          ok = true;
+          d = R.d[k];
+        } else if ((gf & PZ_GF_HAS2) && g - 1u == st.g && !(gf & PZ_GF_DIRTY2)) {
+          ok = true;
+          d = R.d2[k];
+        }
+      }
+    }
+    const uint32_t incl = pz_wave_scan_u32(d);
+    const uint32_t nend = st.n + incl;
+    bool bad = false;
+    if (k < nseg) {
+      bad = !ok || nend >= (1u << 24) ||
+            (stop_mode != PZ_STOP_NONE &&
+             pz_stop_hit(pz_acc_value_ng(nend, st.g), thr, stop_mode));
+    }
+    const uint64_t ball = __ballot(bad);
+    if (!ball) {
+      st.n += pz_readlane_u32(incl, 63);
+      k0 += 64;
+      continue;
+    }
+    const int L = (int)__builtin_ctzll(ball);
+    const int kb = k0 + L;
+    st.n += pz_readlane_u32(incl - d, L);
+    float v[4];
+    const int slot = R.slot[kb];
+    if (slot >= 0) {
+      const pz_f4 q = ((const pz_lds_f4*)(R.cache + slot * PZ_SEG))[lane];
+      v[0] = q.x;
+      v[1] = q.y;
+      v[2] = q.z;
+      v[3] = q.w;
+    } else {
+      x.seg(kb, v);
+    }
+    const int f = pz_wave_accumulate<4>(st, v, 0, thr, stop_mode, nullptr);
+    if (f >= 0) return kb * PZ_SEG + f;
+    k0 = kb + 1;
+  }
+  return -1;
+}
+
+// Terms of one row: e = expf(y - M) for y >= thr (0 otherwise), times inv
+// when as_p.
 template <class Row>
-struct PzTermRegen {
+struct PzExpTerms {
+  typedef float Raw[4];
   Row R;
   float M, thr, inv;
   bool as_p;
-  __device__ __forceinline__ void operator()(int k, float (&v)[4]) const {
-    float yy[4];
-    const int n = R.get(pz_seg_e0(k), yy);
+  __device__ __forceinline__ int load(int e0, Raw& r) const { return R.load(e0, r); }
+  __device__ __forceinline__ void terms(int e0, int n, Raw& r, float (&v)[4]) const {
+    R.apply(e0, n, r);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float e = (c < n && yy[c] >= thr) ? pz_expf(yy[c] - M) : 0.0f;
+      const float e = (c < n && r[c] >= thr) ? pz_expf(r[c] - M) : 0.0f;
       v[c] = as_p ? e * inv : e;
     }
   }
+  __device__ __forceinline__ void observe(int, const float (&)[4]) {}
+  __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
+    Raw r;
+    const int e0 = pz_seg_e0(k);
+    const int n = load(e0, r);
+    terms(e0, n, r, v);
+  }
 };
 
-// Records pass over tiles [0, tmax]: the exact terms of every segment whose
-// seg_gf holds a predicted grid are recorded at that grid.
-template <int U2, class Row>
-__device__ __forceinline__ void pz_record_terms(const PzTermRegen<Row>& G, int tmax,
-                                                uint32_t* seg_d, uint32_t* seg_gf) {
-  const int w = threadIdx.x >> 6;
-  for (int t0 = 0; t0 <= tmax; t0 += U2) {
-    float y[U2][4];
-    int nv[U2];
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      nv[uu] = 0;
-      if (t0 + uu <= tmax) nv[uu] = G.R.get(pz_tile_e0(t0 + uu), y[uu]);
-    }
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      const int t = t0 + uu;
-      if (t > tmax) continue;
-      const int k = t * PZ_SEGS_PER_TILE + w;
-      const uint32_t g = seg_gf[k];
-      if (g == PZ_NO_RECORD) continue;
-      float v[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const float e = (c < nv[uu] && y[uu][c] >= G.thr) ? pz_expf(y[uu][c] - G.M) : 0.0f;
-        v[c] = G.as_p ? e * G.inv : e;
-      }
-      pz_segment_record(v, g, true, seg_d, seg_gf, k);
-    }
-  }
-}
-
 // The reference's softmax normaliser (softmax.c:12-16; top_p.c:57-65 with
-// thr = max - 20): exact sequential fp32 sum of expf(y - M) over y >= thr in
-// ascending id.  seg_m/seg_s hold the row's pass-1 estimates.  Called by
-// every thread; returns the sum in every thread.
-template <int U2, class Row>
-__device__ __forceinline__ float pz_exact_normaliser(const Row& R, int ntiles, float M, float thr,
-                                                     const float* seg_m, const float* seg_s,
-                                                     uint32_t* seg_d, uint32_t* seg_gf,
-                                                     PzDrawShared& S) {
-  const int nseg = ntiles * PZ_SEGS_PER_TILE;
-  if (threadIdx.x < 64) pz_predict_grids(seg_m, seg_s, nseg, M, 1.0f, seg_gf);
-  __syncthreads();
-  PzTermRegen<Row> G{R, M, thr, 0.0f, false};
-  pz_record_terms<U2>(G, ntiles - 1, seg_d, seg_gf);
-  __syncthreads();
+// thr = max - 20): exact sequential fp32 sum of the terms in ascending id.
+// Called by every thread; returns the sum in every thread.
+template <class X>
+__device__ __forceinline__ float pz_exact_sum(X& x, int ntiles, const PzRec& R,
+                                              PzRecShared& S) {
+  pz_record_pass(x, ntiles, R, S, __builtin_inff());
   if (threadIdx.x < 64) {
     PzAcc st;
     st.n = 0;
     st.g = 1;
-    pz_wave_walk(st, seg_d, seg_gf, nseg, 0.0f, PZ_STOP_NONE, G);
+    pz_rec_walk(st, R, ntiles * PZ_SEGS_PER_TILE, 0.0f, PZ_STOP_NONE, x);
     if (threadIdx.x == 0) S.sum = pz_acc_value(st);
   }
   __syncthreads();
   return S.sum;
 }
 
-// The reference's categorical draw (generate.c:162-168): cdf += p_i with
-// p_i = expf(y_i - M) * inv in ascending id, the first i with r < cdf.
-// Records are made only for the segments the estimated CDF can reach.
-// Called by every thread; returns the index or -1 (no hit) in every thread.
-template <int U2, class Row>
-__device__ __forceinline__ int pz_exact_cdf_draw(const Row& R, int V, int ntiles, float M,
-                                                 float inv, float r, const float* seg_m,
-                                                 const float* seg_s, uint32_t* seg_d,
-                                                 uint32_t* seg_gf, PzDrawShared& S) {
-  const int nseg = ntiles * PZ_SEGS_PER_TILE;
-  if (threadIdx.x < 64) {
-    const int kmax = pz_predict_grids(seg_m, seg_s, nseg, M, inv, seg_gf, r + 0.01f);
-    if (threadIdx.x == 0) S.kmax = kmax;
-  }
-  __syncthreads();
-  const int kmax = S.kmax;
-  PzTermRegen<Row> G{R, M, -__builtin_inff(), inv, true};
-  pz_record_terms<U2>(G, kmax < 0 ? -1 : kmax / PZ_SEGS_PER_TILE, seg_d, seg_gf);
-  __syncthreads();
+// The reference's categorical draw (generate.c:162-168): cdf += term in
+// ascending id, the first index with r < cdf (-1 if none below V).  Called
+// by every thread; returns the index in every thread.
+template <class X>
+__device__ __forceinline__ int pz_exact_draw(X& x, int V, int ntiles, float r, const PzRec& R,
+                                             PzRecShared& S) {
+  pz_record_pass(x, ntiles, R, S, r + 0.01f);
   if (threadIdx.x < 64) {
     PzAcc st;
     st.n = 0;
     st.g = 1;
-    int hit = pz_wave_walk(st, seg_d, seg_gf, nseg, r, PZ_STOP_GT, G);
+    int hit = pz_rec_walk(st, R, ntiles * PZ_SEGS_PER_TILE, r, PZ_STOP_GT, x);
     if (hit >= V) hit = -1;  // padding terms are 0 and never raise the CDF
     if (threadIdx.x == 0) S.hit = hit;
   }

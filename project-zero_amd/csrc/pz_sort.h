@@ -3,12 +3,15 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+typedef __attribute__((address_space(3))) uint64_t pz_lds_u64;
+
 // Descending bitonic sort of buf[0..N) (N a power of two) by all BLOCK
-// threads of the workgroup.  buf may live in LDS or in global memory owned by
-// the workgroup (every stage ends in a workgroup barrier, which also orders
-// the global accesses of the workgroup).
-template <int BLOCK>
-__device__ void pz_bitonic_desc(uint64_t* buf, int N) {
+// threads of the workgroup.  buf is an LDS (pz_lds_u64*) or global
+// (uint64_t*) pointer; global buffers must be owned by the workgroup (every
+// stage ends in a workgroup barrier, which also orders the workgroup's
+// global accesses).
+template <int BLOCK, class Ptr>
+__device__ __forceinline__ void pz_bitonic_desc(Ptr buf, int N) {
   for (int size = 2; size <= N; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       for (int i = threadIdx.x; i < (N >> 1); i += BLOCK) {

@@ -17,8 +17,7 @@
 // Kernels:
 //   k_spec_rows    one workgroup per logits row (all target rows, then all
 //                  draft rows): maximum, exact softmax normaliser, NaN/inf
-//                  degeneracy; target rows also store their pass-1
-//                  estimates for a later CDF draw.
+//                  degeneracy.
 //   k_spec_verify  one workgroup per sequence: acceptance tests (two logits
 //                  per draft), then the residual (exact Z and draw) or the
 //                  bonus / Z == 0 categorical draw.
@@ -34,14 +33,13 @@ namespace {
 
 struct SpecRowsShared {
   PzPass1Shared p1;
-  PzDrawShared d;
+  PzRecShared r;
 };
 
 template <bool VEC>
 __global__ __launch_bounds__(PZ_RB) void k_spec_rows(
     const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
-    int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats,
-    float* __restrict__ seg_store) {
+    int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
   extern __shared__ __align__(16) char lds[];
   __shared__ SpecRowsShared S;
   const int q = blockIdx.x, tid = threadIdx.x;
@@ -49,67 +47,80 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_rows(
   PzTempRow<VEC> R;
   R.x = q < NT ? target + (long)q * ld : draft + (long)(q - NT) * ld;
   R.V = V;
-  R.prm = prm;
-  const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
-  float* seg_m = reinterpret_cast<float*>(lds);
-  float* seg_s = seg_m + nseg;
-  uint32_t* seg_d = reinterpret_cast<uint32_t*>(seg_s + nseg);
-  uint32_t* seg_gf = seg_d + nseg;
+  R.T = PzTemp::of(*prm);
+  const int ntiles = pz_tiles(V);
+  const PzRec REC = pz_rec_at(lds, ntiles * PZ_SEGS_PER_TILE);
 
-  const float M = pz_pass1<8>(R, ntiles, seg_m, seg_s, S.p1);
+  const float M = pz_pass1<8>(R, ntiles, S.p1);
   const bool bad = S.p1.any_nan || !(M > -__builtin_inff() && M < __builtin_inff());
   float inv = __builtin_nanf("");
   if (!bad) {
-    const float sum = pz_exact_normaliser<4>(R, ntiles, M, -__builtin_inff(), seg_m, seg_s,
-                                             seg_d, seg_gf, S.d);
-    inv = 1.0f / sum;
+    PzExpTerms<PzTempRow<VEC>> X;
+    X.R = R;
+    X.M = M;
+    X.thr = -__builtin_inff();
+    X.inv = 1.0f;
+    X.as_p = false;
+    inv = 1.0f / pz_exact_sum(X, ntiles, REC, S.r);
   }
   if (tid == 0) {
     stats[4 * (long)q] = M;
     stats[4 * (long)q + 1] = inv;
     stats[4 * (long)q + 2] = bad ? 1.0f : 0.0f;
   }
-  if (q < NT) {
-    float* dst = seg_store + (long)q * nseg * 2;
-    for (int k = tid; k < nseg; k += PZ_RB) {
-      dst[k] = seg_m[k];
-      dst[nseg + k] = seg_s[k];
-    }
-  }
 }
 
 // p(x) of one element of a row whose softmax statistics are (M, inv).
 template <bool VEC>
 __device__ __forceinline__ float prob_at(const PzTempRow<VEC>& R, int x, float M, float inv) {
-  return pz_expf(pz_temper(R.x[x], *R.prm) - M) * inv;
+  return pz_expf(R.T.apply(R.x[x]) - M) * inv;
 }
 
-// Residual terms r(x) = max(0, p(x) - q(x)) of elements e0..e0+3.
-template <bool VEC, bool EXACT>
-struct ResidualRow {
+// Residual terms r(x) = max(0, p(x) - q(x)) of a target/draft row pair; the
+// observer tracks the last x with r(x) > 0.
+template <bool VEC>
+struct ResidualTerms {
+  struct Raw {
+    float t[4];
+    float d[4];
+  };
   PzTempRow<VEC> T, D;
   float MT, invT, MD, invD;
-  __device__ __forceinline__ void terms(int e0, float (&v)[4]) const {
-    float yt[4], yd[4];
-    const int n = T.get(e0, yt);
-    D.get(e0, yd);
+  int lastpos;
+  __device__ __forceinline__ int load(int e0, Raw& r) const {
+    T.load(e0, r.t);
+    return D.load(e0, r.d);
+  }
+  __device__ __forceinline__ void terms(int e0, int n, Raw& r, float (&v)[4]) const {
+    T.apply(e0, n, r.t);
+    D.apply(e0, n, r.d);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      float r = 0.0f;
+      float res = 0.0f;
       if (c < n) {
-        const float p = EXACT ? pz_expf(yt[c] - MT) * invT : __expf(yt[c] - MT) * invT;
-        const float qq = EXACT ? pz_expf(yd[c] - MD) * invD : __expf(yd[c] - MD) * invD;
+        const float p = pz_expf(r.t[c] - MT) * invT;
+        const float qq = pz_expf(r.d[c] - MD) * invD;
         const float t = p - qq;
-        r = t > 0.0f ? t : 0.0f;
+        res = t > 0.0f ? t : 0.0f;
       }
-      v[c] = r;
+      v[c] = res;
     }
   }
-  __device__ __forceinline__ void operator()(int k, float (&v)[4]) const { terms(pz_seg_e0(k), v); }
+  __device__ __forceinline__ void observe(int e0, const float (&v)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (v[c] > 0.0f) lastpos = e0 + c;
+  }
+  __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
+    Raw r;
+    const int e0 = pz_seg_e0(k);
+    const int n = load(e0, r);
+    terms(e0, n, r, v);
+  }
 };
 
 struct SpecVerifyShared {
-  PzDrawShared d;
+  PzRecShared r;
   int jstar;
   int last;
   float Z;
@@ -120,19 +131,16 @@ template <bool VEC>
 __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
     const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
     int K, int KT, int has_bonus, const pz_row_params_dev* __restrict__ prm,
-    const float* __restrict__ stats, const float* __restrict__ seg_store,
-    const int32_t* __restrict__ draft_ids, const float* __restrict__ u_acc,
-    const float* __restrict__ u_res, int32_t* __restrict__ acc_len,
-    int32_t* __restrict__ ids_out) {
+    const float* __restrict__ stats, const int32_t* __restrict__ draft_ids,
+    const float* __restrict__ u_acc, const float* __restrict__ u_res,
+    int32_t* __restrict__ acc_len, int32_t* __restrict__ ids_out) {
   extern __shared__ __align__(16) char lds[];
   __shared__ SpecVerifyShared S;
-  const int b = blockIdx.x, tid = threadIdx.x, w = tid >> 6;
+  const int b = blockIdx.x, tid = threadIdx.x;
   const int NT = B * KT;
   const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
-  float* seg_m = reinterpret_cast<float*>(lds);
-  float* seg_s = seg_m + nseg;
-  uint32_t* seg_d = reinterpret_cast<uint32_t*>(seg_s + nseg);
-  uint32_t* seg_gf = seg_d + nseg;
+  const PzRec REC = pz_rec_at(lds, nseg);
+  const PzTemp TT = PzTemp::of(*prm);
 
   // ---- acceptance tests, in draft order, up to the first rejection
   if (tid == 0) {
@@ -142,8 +150,8 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
       const int d = draft_ids[b * K + j];
       bool accept = false;
       if (d >= 0 && d < V) {
-        PzTempRow<VEC> RT{target + (long)qt * ld, V, prm};
-        PzTempRow<VEC> RD{draft + (long)(qd - NT) * ld, V, prm};
+        PzTempRow<VEC> RT{target + (long)qt * ld, V, TT};
+        PzTempRow<VEC> RD{draft + (long)(qd - NT) * ld, V, TT};
         const float pd = prob_at(RT, d, stats[4 * qt], stats[4 * qt + 1]);
         const float qv = prob_at(RD, d, stats[4 * qd], stats[4 * qd + 1]);
         accept = qv > 0.0f && u_acc[b * K + j] < pd / qv;
@@ -166,59 +174,29 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
     } else if (badD) {
       cat_row = qt;  // q is NaN: every p - q fails t > 0, Z == 0
     } else {
-      ResidualRow<VEC, false> A;
-      ResidualRow<VEC, true> E;
-      A.T = PzTempRow<VEC>{target + (long)qt * ld, V, prm};
-      A.D = PzTempRow<VEC>{draft + (long)(qd - NT) * ld, V, prm};
-      A.MT = stats[4 * qt];
-      A.invT = stats[4 * qt + 1];
-      A.MD = stats[4 * qd];
-      A.invD = stats[4 * qd + 1];
-      E.T = A.T;
-      E.D = A.D;
-      E.MT = A.MT;
-      E.invT = A.invT;
-      E.MD = A.MD;
-      E.invD = A.invD;
-      // pass A: per-segment estimates of the residual mass
-      for (int t = 0; t < ntiles; t++) {
-        float v[4];
-        A.terms(pz_tile_e0(t), v);
-        const float s = pz_wave_sum(v[0] + v[1] + v[2] + v[3]);
-        if ((tid & 63) == 0) {
-          seg_m[t * PZ_SEGS_PER_TILE + w] = 0.0f;
-          seg_s[t * PZ_SEGS_PER_TILE + w] = s;
-        }
-      }
-      __syncthreads();
-      if (w == 0) pz_predict_grids(seg_m, seg_s, nseg, 0.0f, 1.0f, seg_gf);
-      __syncthreads();
-      // pass B: exact residual terms -> records, and the last positive term
-      int lastpos = -1;
-      for (int t = 0; t < ntiles; t++) {
-        float v[4];
-        const int e0 = pz_tile_e0(t);
-        E.terms(e0, v);
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-          if (v[c] > 0.0f) lastpos = e0 + c;
-        const int k = t * PZ_SEGS_PER_TILE + w;
-        pz_segment_record(v, seg_gf[k], true, seg_d, seg_gf, k);
-      }
-      if (lastpos > 0) atomicMax(&S.last, lastpos);
-      __syncthreads();
-      if (w == 0) {
+      ResidualTerms<VEC> X;
+      X.T = PzTempRow<VEC>{target + (long)qt * ld, V, TT};
+      X.D = PzTempRow<VEC>{draft + (long)(qd - NT) * ld, V, TT};
+      X.MT = stats[4 * qt];
+      X.invT = stats[4 * qt + 1];
+      X.MD = stats[4 * qd];
+      X.invD = stats[4 * qd + 1];
+      X.lastpos = -1;
+      pz_record_pass(X, ntiles, REC, S.r, __builtin_inff());
+      if (X.lastpos > 0) atomicMax(&S.last, X.lastpos);
+      if (tid < 64) {
         PzAcc st;
         st.n = 0;
         st.g = 1;
-        pz_wave_walk(st, seg_d, seg_gf, nseg, 0.0f, PZ_STOP_NONE, E);
+        pz_rec_walk(st, REC, nseg, 0.0f, PZ_STOP_NONE, X);
         const float Z = pz_acc_value(st);
         int hit = -1;
         if (Z > 0.0f) {
+          // the same sequence of adds: the CDF of r, stop at ur * Z < cdf
           PzAcc s2;
           s2.n = 0;
           s2.g = 1;
-          hit = pz_wave_walk(s2, seg_d, seg_gf, nseg, ur * Z, PZ_STOP_GT, E);
+          hit = pz_rec_walk(s2, REC, nseg, ur * Z, PZ_STOP_GT, X);
           if (hit >= V) hit = -1;
         }
         if (tid == 0) {
@@ -237,16 +215,13 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
   }
   if (cat_row >= 0) {
     // categorical draw from p of a target row (generate.c:157-169)
-    const float* src = seg_store + (long)cat_row * nseg * 2;
-    for (int k = tid; k < nseg; k += PZ_RB) {
-      seg_m[k] = src[k];
-      seg_s[k] = src[nseg + k];
-    }
-    __syncthreads();
-    PzTempRow<VEC> RT{target + (long)cat_row * ld, V, prm};
-    const int hit = pz_exact_cdf_draw<4>(RT, V, ntiles, stats[4 * cat_row],
-                                         stats[4 * cat_row + 1], ur, seg_m, seg_s, seg_d,
-                                         seg_gf, S.d);
+    PzExpTerms<PzTempRow<VEC>> X;
+    X.R = PzTempRow<VEC>{target + (long)cat_row * ld, V, TT};
+    X.M = stats[4 * cat_row];
+    X.thr = -__builtin_inff();
+    X.inv = stats[4 * cat_row + 1];
+    X.as_p = true;
+    const int hit = pz_exact_draw(X, V, ntiles, ur, REC, S.r);
     tok = hit >= 0 ? hit : V - 1;
   }
   if (tid == 0) {
@@ -261,9 +236,9 @@ size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 template <bool VEC>
 int launch_spec(pz_sampler* s, const float* d_target, const float* d_draft, long ld, int V,
                 int B, int K, int KT, int has_bonus, const pz_row_params_dev* d_prm,
-                float* d_stats, float* d_seg, const int32_t* d_ids_in, const float* d_uacc,
+                float* d_stats, const int32_t* d_ids_in, const float* d_uacc,
                 const float* d_ures, int32_t* d_acc, int32_t* d_ids_out) {
-  const size_t lds = (size_t)pz_nseg(V) * 16;
+  const size_t lds = pz_rec_bytes(V);
   if (lds + 256 > (size_t)s->max_lds) return -2;
   auto k1 = k_spec_rows<VEC>;
   auto k2 = k_spec_verify<VEC>;
@@ -276,9 +251,9 @@ int launch_spec(pz_sampler* s, const float* d_target, const float* d_draft, long
   }
   const int NR = B * KT + B * K;
   hipLaunchKernelGGL(k1, dim3(NR), dim3(PZ_RB), lds, s->stream, d_target, d_draft, ld, V, B, K,
-                     KT, d_prm, d_stats, d_seg);
+                     KT, d_prm, d_stats);
   hipLaunchKernelGGL(k2, dim3(B), dim3(PZ_RB), lds, s->stream, d_target, d_draft, ld, V, B, K, KT,
-                     has_bonus, d_prm, d_stats, d_seg, d_ids_in, d_uacc, d_ures, d_acc,
+                     has_bonus, d_prm, d_stats, d_ids_in, d_uacc, d_ures, d_acc,
                      d_ids_out);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -299,7 +274,6 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   PZ_HIP(s, hipSetDevice(s->device));
   const int KT = K + (has_bonus ? 1 : 0);
   const int NR = B * KT + B * K;
-  const int nseg = pz_nseg(V);
 
   // one input block and one output block, identical layout host and device
   const size_t o_prm = 0;
@@ -311,8 +285,7 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   const size_t o_out = up256(o_acc + (size_t)B * 4);
   const size_t io_bytes = up256(o_out + (size_t)B * (K + 1) * 4);
   const size_t o_stats = io_bytes;
-  const size_t o_seg = up256(o_stats + (size_t)NR * 16);
-  const size_t dev_bytes = up256(o_seg + (size_t)B * KT * nseg * 8);
+  const size_t dev_bytes = up256(o_stats + (size_t)NR * 16);
 
   if (s->spec_dev_bytes < dev_bytes || s->spec_host_bytes < io_bytes) {
     PZ_HIP(s, hipStreamSynchronize(s->stream));
@@ -356,7 +329,7 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   auto launch = vec ? launch_spec<true> : launch_spec<false>;
   const int rc = launch(s, d_target, d_draft, ld, V, B, K, KT, has_bonus ? 1 : 0,
                         reinterpret_cast<const pz_row_params_dev*>(d + o_prm),
-                        reinterpret_cast<float*>(d + o_stats), reinterpret_cast<float*>(d + o_seg),
+                        reinterpret_cast<float*>(d + o_stats),
                         reinterpret_cast<const int32_t*>(d + o_ids),
                         reinterpret_cast<const float*>(d + o_uacc),
                         reinterpret_cast<const float*>(d + o_ures),

@@ -42,6 +42,7 @@ namespace {
 constexpr int EBIN_BASE = 98 << 7;
 constexpr int EBINS = (127 << 7) - EBIN_BASE + 1;
 constexpr int TOPP_CAP_MAX = 8192;
+constexpr int EBINS_BYTES = ((EBINS * 4 + 15) / 16) * 16;
 
 __device__ __forceinline__ int ebin(float e) {
   const int b = (int)(__float_as_uint(e) >> 16) - EBIN_BASE;
@@ -139,16 +140,14 @@ __device__ __forceinline__ void nucleus_draw(const uint64_t* keys, const float* 
   if (p_out) *p_out = key_p(k);
 }
 
-// Regenerates one segment's candidate terms for the exact-sum walk.
+// Candidate terms with the e histogram as observer.
 template <bool VEC>
-struct CandRegen {
-  PzRow<VEC> R;
-  float thr, M;
-  __device__ __forceinline__ void operator()(int k, float (&v)[4]) const {
-    float yy[4];
-    const int n = R.get(pz_seg_e0(k), yy);
+struct ToppTerms : PzExpTerms<PzRow<VEC>> {
+  uint32_t* ehist;
+  __device__ __forceinline__ void observe(int, const float (&v)[4]) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) v[c] = cand_e(yy[c], c < n, thr, M);
+    for (int c = 0; c < 4; c++)
+      if (v[c] > 0.0f) atomicAdd(&ehist[ebin(v[c])], 1u);
   }
 };
 
@@ -161,6 +160,7 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
     pz_scratch sc) {
   extern __shared__ __align__(16) char lds[];
   __shared__ ToppShared S;
+  __shared__ PzRecShared RS;
   const int row = pz_row_of(rows, blockIdx.x);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -168,23 +168,21 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
   PzRow<VEC> R;
   R.x = logits + (long)row * ld;
   R.V = V;
-  R.prm = &prm;
+  R.T = PzTemp::of(prm);
   pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
 
   const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
   char* reg = lds + pen_bytes;
-  float* seg_m = reinterpret_cast<float*>(reg);
-  float* seg_s = seg_m + nseg;
-  uint32_t* seg_d = reinterpret_cast<uint32_t*>(seg_s + nseg);
-  uint32_t* seg_gf = seg_d + nseg;
-  uint32_t* ehist = seg_gf + nseg;
+  // phase A: records + e histogram; phase B (overlaid): gathered keys + sums
+  uint32_t* ehist = reinterpret_cast<uint32_t*>(reg);
+  const PzRec REC = pz_rec_at(reg + EBINS_BYTES, nseg);
   uint64_t* keys = reinterpret_cast<uint64_t*>(reg);
   float* cum = reinterpret_cast<float*>(keys + cap);
 
   for (int i = tid; i < EBINS; i += PZ_RB) ehist[i] = 0u;
 
-  // ---- pass 1: maximum + normaliser estimates
-  const float M = pz_pass1<8>(R, ntiles, seg_m, seg_s, S.p1);
+  // ---- pass 1: maximum
+  const float M = pz_pass1<8>(R, ntiles, S.p1);
   const float y0 = S.p1.y0;
   if (y0 != y0) {
     // max_val = NaN: no candidate passes, argmax of a row starting with NaN -> 0
@@ -216,42 +214,23 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
     return;
   }
   const float thr = M - 20.0f;
-  if (w == 0) pz_predict_grids(seg_m, seg_s, nseg, M, 1.0f, seg_gf);
-  __syncthreads();
 
-  // ---- pass 2: exact candidate terms -> segment records + e histogram
-  constexpr int U2 = 4;
-  for (int t0 = 0; t0 < ntiles; t0 += U2) {
-    float y[U2][4];
-    int nv[U2];
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      nv[uu] = 0;
-      if (t0 + uu < ntiles) nv[uu] = R.get(pz_tile_e0(t0 + uu), y[uu]);
-    }
-#pragma unroll
-    for (int uu = 0; uu < U2; uu++) {
-      const int t = t0 + uu;
-      if (t >= ntiles) continue;
-      const int k = t * PZ_SEGS_PER_TILE + w;
-      float e[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        e[c] = cand_e(y[uu][c], c < nv[uu], thr, M);
-        if (e[c] > 0.0f) atomicAdd(&ehist[ebin(e[c])], 1u);
-      }
-      pz_segment_record(e, seg_gf[k], true, seg_d, seg_gf, k);
-    }
-  }
-  __syncthreads();
+  // ---- records of the exact candidate terms (+ e histogram)
+  ToppTerms<VEC> X;
+  X.R = R;
+  X.M = M;
+  X.thr = thr;
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.ehist = ehist;
+  pz_record_pass(X, ntiles, REC, RS, __builtin_inff());
 
   // ---- exact normaliser (wave 0) || nucleus bin selection (wave 1)
   if (w == 0) {
     PzAcc st;
     st.n = 0;
     st.g = 1;
-    CandRegen<VEC> regen{R, thr, M};
-    pz_wave_walk(st, seg_d, seg_gf, nseg, 0.0f, PZ_STOP_NONE, regen);
+    pz_rec_walk(st, REC, nseg, 0.0f, PZ_STOP_NONE, X);
     if (lane == 0) S.sum = pz_acc_value(st);
   } else if (w == 1) {
     float tot = 0.0f;
@@ -308,19 +287,21 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
     const float e_lo = ebin_lo(S.bsel);
     const float p_thr = all ? 0.0f : e_lo * inv;
     const float dgate = all ? -__builtin_inff() : __logf(e_lo) - 0.01f;
+    constexpr int U2 = 4;
     for (int t0 = 0; t0 < ntiles; t0 += U2) {
       float y[U2][4];
       int nv[U2];
 #pragma unroll
       for (int uu = 0; uu < U2; uu++) {
         nv[uu] = 0;
-        if (t0 + uu < ntiles) nv[uu] = R.get(pz_tile_e0(t0 + uu), y[uu]);
+        if (t0 + uu < ntiles) nv[uu] = R.load(pz_tile_e0(t0 + uu), y[uu]);
       }
 #pragma unroll
       for (int uu = 0; uu < U2; uu++) {
         const int t = t0 + uu;
-        if (t >= ntiles) break;
+        if (t >= ntiles) continue;
         const int e0 = pz_tile_e0(t);
+        R.apply(e0, nv[uu], y[uu]);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           const float yy = y[uu][c];
@@ -344,7 +325,7 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
     while (N < m) N <<= 1;
     for (int i = m + tid; i < N; i += PZ_RB) keys[i] = 0ull;
     __syncthreads();
-    pz_bitonic_desc<PZ_RB>(keys, N);
+    pz_bitonic_desc<PZ_RB>((pz_lds_u64*)keys, N);
     const int cutoff = nucleus_cutoff(keys, cum, m, prm.top_p, all, &S.cutoff);
     if (cutoff > 0) {
       if (tid == 0) nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
@@ -381,7 +362,7 @@ __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
     PzRow<VEC> R;
     R.x = logits + (long)row * ld;
     R.V = V;
-    R.prm = &prm;
+    R.T = PzTemp::of(prm);
     pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
     const float M = sc.row_stat[4 * (long)row];
     const float inv = sc.row_stat[4 * (long)row + 1];
@@ -422,7 +403,7 @@ __global__ void k_reset_counters(int32_t* c) {
 }
 
 size_t topp_region_bytes(int V, int cap) {
-  const size_t a = (size_t)pz_nseg(V) * 16 + (size_t)EBINS * 4;
+  const size_t a = (size_t)EBINS_BYTES + pz_rec_bytes(V);
   const size_t b = (size_t)cap * 12;
   return a > b ? a : b;
 }
