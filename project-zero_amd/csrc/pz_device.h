@@ -49,7 +49,7 @@ __constant__ static const uint64_t pz_exp2_tab[32] = {
     0x3fef3720dcef9069ull, 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
     0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-__device__ __forceinline__ float pz_expf(float x) {
+__device__ __forceinline__ float pz_expf_inline(float x) {
   const uint32_t ux = __float_as_uint(x);
   const uint32_t abstop = (ux >> 20) & 0x7ff;
   if (__builtin_expect(abstop >= 0x42b, 0)) {  // |x| >= 88 or non-finite
@@ -78,6 +78,11 @@ __device__ __forceinline__ float pz_expf(float x) {
   y = y * s;
   return (float)y;
 }
+
+// Out of line: the exact exponential sits on paths that are rare next to the
+// streaming passes, and inlining it into every one of them multiplies the
+// kernels' code size beyond the instruction cache.
+__device__ __noinline__ float pz_expf(float x) { return pz_expf_inline(x); }
 
 // ---------------------------------------------------------------------------
 // Order key: monotone uint32 image of an fp32 value (larger value -> larger
@@ -167,19 +172,27 @@ __device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V,
 
 // Penalised value of a history member (caller checked the bitmap bit).
 // Repetition first (x>0 ? x/rep : x*rep, each distinct id once), then
-// t = (float)c*freq; t = t + pres; x = x - t.
-__device__ __forceinline__ float pz_penalize(const PzPenalty& P, float x, int id) {
-  x = x > 0.0f ? x / P.rep : x * P.rep;
-  if (P.hcap) {
-    const uint32_t mask = (uint32_t)P.hcap - 1u;
+// t = (float)c*freq; t = t + pres; x = x - t.  Out of line (only history
+// members take it; inlined at every element of every unrolled pass it bloats
+// the kernels), with every operand passed by value.
+__device__ __noinline__ float pz_penalize_v(float x, int id, float rep, float pres, float freq,
+                                            int hcap, const pz_lds_i32* hkey,
+                                            const pz_lds_i32* hcnt) {
+  x = x > 0.0f ? x / rep : x * rep;
+  if (hcap) {
+    const uint32_t mask = (uint32_t)hcap - 1u;
     uint32_t s = pz_hash((uint32_t)id) & mask;
-    while (P.hkey[s] != id) s = (s + 1) & mask;
-    const int c = P.hcnt[s];
-    float t = (float)c * P.freq;
-    t = t + P.pres;
+    while (hkey[s] != id) s = (s + 1) & mask;
+    const int c = hcnt[s];
+    float t = (float)c * freq;
+    t = t + pres;
     x = x - t;
   }
   return x;
+}
+
+__device__ __forceinline__ float pz_penalize(const PzPenalty& P, float x, int id) {
+  return pz_penalize_v(x, id, P.rep, P.pres, P.freq, P.hcap, P.hkey, P.hcnt);
 }
 
 // 4-bit membership nibble for the aligned group of 4 ids starting at i4*4.
@@ -197,6 +210,10 @@ __device__ __forceinline__ float pz_temper(float x, const pz_row_params_dev& p) 
   return p.temp_div ? x / p.temp : x * p.inv_temp;
 }
 
+// Correctly rounded x / t, out of line (the division form is the reference's
+// scalar-build temperature, temperature.c:22-23).
+__device__ __noinline__ float pz_div(float x, float t) { return x / t; }
+
 // The same, with the row's parameters held in registers.
 struct PzTemp {
   float t, inv;
@@ -208,7 +225,7 @@ struct PzTemp {
     r.div = p.temp_div;
     return r;
   }
-  __device__ __forceinline__ float apply(float x) const { return div ? x / t : x * inv; }
+  __device__ __forceinline__ float apply(float x) const { return div ? pz_div(x, t) : x * inv; }
 };
 
 // Value the sampling chain sees for raw logit x of id i: penalties (when the

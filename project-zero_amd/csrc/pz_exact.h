@@ -156,6 +156,31 @@ __device__ __forceinline__ bool pz_stop_hit(float s, float thr, int mode) {
   return mode == PZ_STOP_GT ? (thr < s) : (mode == PZ_STOP_GE ? (s >= thr) : false);
 }
 
+// The same accumulation as pz_wave_accumulate, one real fp32 add per term
+// (wave-uniform): faster when events are dense, e.g. while the running sum
+// is still smaller than the terms at the start of a row.
+template <int C>
+__device__ __forceinline__ int pz_wave_serial(PzAcc& st, const float (&v)[C], int start,
+                                              float thr, int stop_mode, float* cum) {
+  const int lane = threadIdx.x & 63;
+  float s = pz_acc_value(st);
+  for (int l = start / C; l < 64; l++) {
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      const int idx = l * C + c;
+      if (idx < start) continue;
+      s = s + pz_readlane_f32(v[c], l);
+      if (cum && lane == 0) cum[idx] = s;
+      if (stop_mode != PZ_STOP_NONE && pz_stop_hit(s, thr, stop_mode)) {
+        st = pz_acc_of(s);
+        return idx;
+      }
+    }
+  }
+  st = pz_acc_of(s);
+  return -1;
+}
+
 // Exact sequential accumulation of the 64*C terms a wave holds, lane-major
 // (element index lane*C + c), starting at element `start`.  st is
 // wave-uniform and is advanced past the processed terms.  With a stop mode,
@@ -167,7 +192,9 @@ __device__ __forceinline__ int pz_wave_accumulate(PzAcc& st, const float (&v)[C]
                                   int stop_mode, float* cum) {
   const int lane = threadIdx.x & 63;
   int pos = start;
+  int rounds = 0;
   while (pos < 64 * C) {
+    if (++rounds > 4) return pz_wave_serial<C>(st, v, pos, thr, stop_mode, cum);
     uint32_t inc[C];
     int first_flag = C;
     uint32_t lsum = 0;

@@ -168,8 +168,10 @@ typedef __attribute__((address_space(3))) pz_f4 pz_lds_f4;
 // Sentinel gf of a segment without a record (the walk regenerates it).
 constexpr uint32_t PZ_NO_RECORD = 0xffffffffu;
 // gf = grid | DIRTY (record at grid unusable) | HAS2 (record at grid - 1) |
-// DIRTY2 (that one unusable)
-constexpr uint32_t PZ_GF_DIRTY = 0x100u, PZ_GF_HAS2 = 0x200u, PZ_GF_DIRTY2 = 0x400u;
+// DIRTY2 (that one unusable) | XING (the estimate leaves the binade inside
+// the segment)
+constexpr uint32_t PZ_GF_DIRTY = 0x100u, PZ_GF_HAS2 = 0x200u, PZ_GF_DIRTY2 = 0x400u,
+                   PZ_GF_XING = 0x800u;
 
 struct PzRec {
   pz_lds_u32* d;      // [nseg] increment sum at the predicted grid
@@ -212,7 +214,9 @@ __device__ __forceinline__ uint32_t pz_predict_gf(float s) {
   return g | (near ? PZ_GF_HAS2 : 0u);
 }
 
-__device__ __forceinline__ void pz_rec_segment(const float (&v)[4], uint32_t gf, int k,
+template <class X>
+__device__ __forceinline__ void pz_rec_segment(const X& x, const typename X::Raw& raw,
+                                               const float (&a)[4], uint32_t gf, int k,
                                                const PzRec& R, PzRecShared& S) {
   const int lane = threadIdx.x & 63;
   const uint32_t g = gf & 0xffu;
@@ -222,14 +226,14 @@ __device__ __forceinline__ void pz_rec_segment(const float (&v)[4], uint32_t gf,
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     uint32_t cls;
-    s1 += pz_inc(v[c], g, &cls);
+    s1 += x.inc(raw, a, c, g, &cls);
     d1 |= cls != PZ_INC_PLAIN;
   }
   if (has2) {
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       uint32_t cls;
-      s2 += pz_inc(v[c], g - 1u, &cls);
+      s2 += x.inc(raw, a, c, g - 1u, &cls);
       d2 |= cls != PZ_INC_PLAIN;
     }
     s2 = pz_wave_sum_u32(s2);
@@ -238,31 +242,33 @@ __device__ __forceinline__ void pz_rec_segment(const float (&v)[4], uint32_t gf,
   const bool D1 = __ballot(d1) != 0;
   const bool D2 = has2 && __ballot(d2) != 0;
   int slot = -1;
-  if (D1 && (!has2 || D2)) {
-    // no clean record: keep the terms for the walk
+  if ((D1 && (!has2 || D2)) || (gf & PZ_GF_XING)) {
+    // the walk will go through this segment element by element: keep what
+    // it needs in LDS
     if (lane == 0) slot = atomicAdd(&S.slots_used, 1);
     slot = __builtin_amdgcn_readfirstlane(slot);
     if (slot >= PZ_REC_SLOTS) slot = -1;
-    if (slot >= 0) {
-      pz_f4 q;
-      q.x = v[0];
-      q.y = v[1];
-      q.z = v[2];
-      q.w = v[3];
-      ((pz_lds_f4*)(R.cache + slot * PZ_SEG))[lane] = q;
-    }
+    if (slot >= 0) x.cache_put(R.cache + slot * PZ_SEG, raw, a);
   }
   if (lane == 0) {
     R.d[k] = s1;
     R.d2[k] = s2;
-    R.gf[k] = g | (D1 ? PZ_GF_DIRTY : 0u) | (has2 ? PZ_GF_HAS2 : 0u) | (D2 ? PZ_GF_DIRTY2 : 0u);
+    R.gf[k] = (gf & (0xffu | PZ_GF_HAS2 | PZ_GF_XING)) | (D1 ? PZ_GF_DIRTY : 0u) |
+              (D2 ? PZ_GF_DIRTY2 : 0u);
     R.slot[k] = slot;
   }
 }
 
 // Records pass over the row's terms (see the header).  X provides
-//   typename Raw; int load(e0, Raw&); void terms(e0, n, Raw&, float (&)[4]);
-//   void observe(e0, const float (&)[4]); void seg(k, float (&)[4]).
+//   typename Raw;                  per-thread data of 4 elements
+//   int  load(e0, Raw&)            issues the loads, returns the count < V
+//   void prep(e0, n, Raw&, a[4])   finishes the element data, estimates the
+//                                  terms (relative error < 2^-16)
+//   void observe(e0, Raw&, a[4])   per-kernel side work (histograms, ...)
+//   uint32_t inc(Raw&, a[4], c, g, cls*)  exact increment of term c at grid g
+//   void cache_put(lds, Raw&, a[4]) / cache_terms(lds, v[4])
+//                                  keep / rebuild a segment's exact terms
+//   void seg(k, v[4])              exact terms of segment k from memory
 // Recording stops after the chunk in which the estimated running sum passes
 // stop_after; later segments get PZ_NO_RECORD.  Every thread calls it; it
 // ends with the records complete (after a barrier).
@@ -281,7 +287,7 @@ __device__ __forceinline__ void pz_record_pass(X& x, int ntiles, const PzRec& R,
   for (; t0 < ntiles; t0 += U) {
     typename X::Raw raw[U];
     int nv[U];
-    float v[U][4];
+    float a[U][4];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       nv[u] = 0;
@@ -292,19 +298,21 @@ __device__ __forceinline__ void pz_record_pass(X& x, int ntiles, const PzRec& R,
       const int t = t0 + u;
       if (t >= ntiles) continue;
       const int e0 = pz_tile_e0(t);
-      x.terms(e0, nv[u], raw[u], v[u]);
-      x.observe(e0, v[u]);
-      const float a = pz_wave_sum((v[u][0] + v[u][1]) + (v[u][2] + v[u][3]));
-      if (lane == 0) R.a[t * PZ_SEGS_PER_TILE + w] = a;
+      x.prep(e0, nv[u], raw[u], a[u]);
+      x.observe(e0, raw[u], a[u]);
+      const float sa = pz_wave_sum((a[u][0] + a[u][1]) + (a[u][2] + a[u][3]));
+      if (lane == 0) R.a[t * PZ_SEGS_PER_TILE + w] = sa;
     }
     __syncthreads();
     if (w == 0) {
       // U * 16 == 64 segments per chunk: one lane each
       const int k = t0 * PZ_SEGS_PER_TILE + lane;
       const bool in = k < nseg;
-      const float a = in ? R.a[k] : 0.0f;
-      const float incl = pz_wave_scan_f32(a);
-      if (in) R.gf[k] = pz_predict_gf(carry + (incl - a));
+      const float sa = in ? R.a[k] : 0.0f;
+      const float incl = pz_wave_scan_f32(sa);
+      const float start = carry + (incl - sa), end = carry + incl;
+      if (in)
+        R.gf[k] = pz_predict_gf(start) | (pz_grid_of(end) != pz_grid_of(start) ? PZ_GF_XING : 0u);
       carry += pz_readlane_f32(incl, 63);
       if (lane == 0 && carry > stop_after) S.stop = 1;
     }
@@ -314,7 +322,7 @@ __device__ __forceinline__ void pz_record_pass(X& x, int ntiles, const PzRec& R,
       const int t = t0 + u;
       if (t >= ntiles) continue;
       const int k = t * PZ_SEGS_PER_TILE + w;
-      pz_rec_segment(v[u], R.gf[k], k, R, S);
+      pz_rec_segment(x, raw[u], a[u], R.gf[k], k, R, S);
     }
     if (S.stop) {
       t0 += U;
@@ -374,15 +382,8 @@ __device__ __forceinline__ int pz_rec_walk(PzAcc& st, const PzRec& R, int nseg, 
     st.n += pz_readlane_u32(incl - d, L);
     float v[4];
     const int slot = R.slot[kb];
-    if (slot >= 0) {
-      const pz_f4 q = ((const pz_lds_f4*)(R.cache + slot * PZ_SEG))[lane];
-      v[0] = q.x;
-      v[1] = q.y;
-      v[2] = q.z;
-      v[3] = q.w;
-    } else {
-      x.seg(kb, v);
-    }
+    if (slot >= 0) x.cache_terms(R.cache + slot * PZ_SEG, v);
+    else x.seg(kb, v);
     const int f = pz_wave_accumulate<4>(st, v, 0, thr, stop_mode, nullptr);
     if (f >= 0) return kb * PZ_SEG + f;
     k0 = kb + 1;
@@ -390,8 +391,42 @@ __device__ __forceinline__ int pz_rec_walk(PzAcc& st, const PzRec& R, int nseg, 
   return -1;
 }
 
+// Estimate of expf(d) with the hardware exp2: the fp32 product d*log2(e)
+// carries the error (relative < |d| * 2^-23.6 in the exponent, so the result
+// is within 2^-16.9 of expf(d) for d >= -104), plus v_exp_f32's own.  Only
+// used where pz_inc_from_estimate can prove the rounding it decides.
+__device__ __forceinline__ float pz_fast_exp(float d) {
+  return __builtin_amdgcn_exp2f(d * 1.44269504088896341f);
+}
+
+// Increment of a term at grid g from an estimate a (relative error below
+// 2^-16) when that settles the rounding; otherwise sets *exact (the caller
+// then evaluates the term exactly).  Grids below 2^-100 (only at the very
+// start of a row) always take the exact path, so estimates that underflow
+// cannot matter.
+__device__ __forceinline__ uint32_t pz_inc_from_estimate(float a, uint32_t g, bool* exact) {
+  *exact = false;
+  if (g < 50u) {
+    *exact = true;
+    return 0u;
+  }
+  if (a == 0.0f) return 0u;
+  const float t = a * __uint_as_float((277u - g) << 23);  // a / 2^(g - 150), exact
+  if (t >= 1024.0f) {
+    *exact = true;
+    return 0u;
+  }
+  const float fl = floorf(t);
+  const float fr = t - fl;
+  if (fabsf(fr - 0.5f) <= t * 0x1p-15f + 0x1p-20f) {
+    *exact = true;
+    return 0u;
+  }
+  return (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+}
+
 // Terms of one row: e = expf(y - M) for y >= thr (0 otherwise), times inv
-// when as_p.
+// when as_p.  Raw holds the elements' y (-inf past the row).
 template <class Row>
 struct PzExpTerms {
   typedef float Raw[4];
@@ -399,20 +434,49 @@ struct PzExpTerms {
   float M, thr, inv;
   bool as_p;
   __device__ __forceinline__ int load(int e0, Raw& r) const { return R.load(e0, r); }
-  __device__ __forceinline__ void terms(int e0, int n, Raw& r, float (&v)[4]) const {
+  __device__ __forceinline__ float exact_term(float y) const {
+    const float e = y >= thr ? pz_expf(y - M) : 0.0f;
+    return as_p ? e * inv : e;
+  }
+  __device__ __forceinline__ void prep(int e0, int n, Raw& r, float (&a)[4]) const {
     R.apply(e0, n, r);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      const float e = (c < n && r[c] >= thr) ? pz_expf(r[c] - M) : 0.0f;
-      v[c] = as_p ? e * inv : e;
+      if (c >= n) r[c] = -__builtin_inff();
+      const float e = r[c] >= thr ? pz_fast_exp(r[c] - M) : 0.0f;
+      a[c] = as_p ? e * inv : e;
     }
   }
-  __device__ __forceinline__ void observe(int, const float (&)[4]) {}
+  __device__ __forceinline__ void observe(int, const Raw&, const float (&)[4]) {}
+  __device__ __forceinline__ uint32_t inc(const Raw& y, const float (&a)[4], int c, uint32_t g,
+                                          uint32_t* cls) const {
+    bool ex;
+    *cls = PZ_INC_PLAIN;
+    const uint32_t i = pz_inc_from_estimate(a[c], g, &ex);
+    return ex ? pz_inc(exact_term(y[c]), g, cls) : i;
+  }
+  __device__ __forceinline__ void cache_put(pz_lds_f32* base, const Raw& y,
+                                            const float (&)[4]) const {
+    pz_f4 q;
+    q.x = y[0];
+    q.y = y[1];
+    q.z = y[2];
+    q.w = y[3];
+    ((pz_lds_f4*)base)[threadIdx.x & 63] = q;
+  }
+  __device__ __forceinline__ void cache_terms(const pz_lds_f32* base, float (&v)[4]) const {
+    const pz_f4 q = ((const pz_lds_f4*)base)[threadIdx.x & 63];
+    v[0] = exact_term(q.x);
+    v[1] = exact_term(q.y);
+    v[2] = exact_term(q.z);
+    v[3] = exact_term(q.w);
+  }
   __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
     Raw r;
     const int e0 = pz_seg_e0(k);
-    const int n = load(e0, r);
-    terms(e0, n, r, v);
+    const int n = R.get(e0, r);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = c < n ? exact_term(r[c]) : 0.0f;
   }
 };
 

@@ -76,8 +76,8 @@ __device__ __forceinline__ float prob_at(const PzTempRow<VEC>& R, int x, float M
   return pz_expf(R.T.apply(R.x[x]) - M) * inv;
 }
 
-// Residual terms r(x) = max(0, p(x) - q(x)) of a target/draft row pair; the
-// observer tracks the last x with r(x) > 0.
+// Residual terms r(x) = max(0, p(x) - q(x)) of a target/draft row pair,
+// evaluated exactly in prep; the observer tracks the last x with r(x) > 0.
 template <bool VEC>
 struct ResidualTerms {
   struct Raw {
@@ -91,31 +91,54 @@ struct ResidualTerms {
     T.load(e0, r.t);
     return D.load(e0, r.d);
   }
-  __device__ __forceinline__ void terms(int e0, int n, Raw& r, float (&v)[4]) const {
+  __device__ __forceinline__ void residual(int e0, int n, Raw& r, float (&v)[4]) const {
     T.apply(e0, n, r.t);
     D.apply(e0, n, r.d);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       float res = 0.0f;
       if (c < n) {
-        const float p = pz_expf(r.t[c] - MT) * invT;
-        const float qq = pz_expf(r.d[c] - MD) * invD;
+        const float p = pz_expf_inline(r.t[c] - MT) * invT;
+        const float qq = pz_expf_inline(r.d[c] - MD) * invD;
         const float t = p - qq;
         res = t > 0.0f ? t : 0.0f;
       }
       v[c] = res;
     }
   }
-  __device__ __forceinline__ void observe(int e0, const float (&v)[4]) {
+  __device__ __forceinline__ void prep(int e0, int n, Raw& r, float (&a)[4]) const {
+    residual(e0, n, r, a);
+  }
+  __device__ __forceinline__ void observe(int e0, const Raw&, const float (&a)[4]) {
 #pragma unroll
     for (int c = 0; c < 4; c++)
-      if (v[c] > 0.0f) lastpos = e0 + c;
+      if (a[c] > 0.0f) lastpos = e0 + c;
+  }
+  __device__ __forceinline__ uint32_t inc(const Raw&, const float (&a)[4], int c, uint32_t g,
+                                          uint32_t* cls) const {
+    return pz_inc(a[c], g, cls);
+  }
+  __device__ __forceinline__ void cache_put(pz_lds_f32* base, const Raw&,
+                                            const float (&a)[4]) const {
+    pz_f4 q;
+    q.x = a[0];
+    q.y = a[1];
+    q.z = a[2];
+    q.w = a[3];
+    ((pz_lds_f4*)base)[threadIdx.x & 63] = q;
+  }
+  __device__ __forceinline__ void cache_terms(const pz_lds_f32* base, float (&v)[4]) const {
+    const pz_f4 q = ((const pz_lds_f4*)base)[threadIdx.x & 63];
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
   }
   __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
     Raw r;
     const int e0 = pz_seg_e0(k);
     const int n = load(e0, r);
-    terms(e0, n, r, v);
+    residual(e0, n, r, v);
   }
 };
 

@@ -144,10 +144,10 @@ __device__ __forceinline__ void nucleus_draw(const uint64_t* keys, const float* 
 template <bool VEC>
 struct ToppTerms : PzExpTerms<PzRow<VEC>> {
   uint32_t* ehist;
-  __device__ __forceinline__ void observe(int, const float (&v)[4]) {
+  __device__ __forceinline__ void observe(int, const float (&)[4], const float (&a)[4]) {
 #pragma unroll
     for (int c = 0; c < 4; c++)
-      if (v[c] > 0.0f) atomicAdd(&ehist[ebin(v[c])], 1u);
+      if (a[c] > 0.0f) atomicAdd(&ehist[ebin(a[c])], 1u);
   }
 };
 
