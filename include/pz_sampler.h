@@ -26,7 +26,8 @@
 extern "C" {
 #endif
 
-/* Symbols of the ABI are the only ones the library exports. */
+/* Symbols of the ABI (this header and pz_sampling_compat.h) are the only
+ * ones the library exports. */
 #ifndef PZ_API
 #define PZ_API __attribute__((visibility("default")))
 #endif
@@ -126,6 +127,18 @@ PZ_API int pz_spec_verify(pz_sampler *s, const float *d_target, const float *d_d
                    float temperature, const int32_t *draft_ids,
                    const float *u_acc, const float *u_res,
                    int32_t *acc_len_out, int32_t *ids_out);
+
+/* The reference's temperature (src/sampling/temperature.c:8-25) over device
+ * rows [B, ld], in place, on the sampler's stream (asynchronous). */
+PZ_API int pz_temperature_batch(pz_sampler *s, float *d_x, long ld, int B, int V,
+                                float temperature);
+
+/* The reference's softmax (src/math/softmax.c:4-23, the tn_softmax slot)
+ * of temperature-scaled device rows: d_out[b, i] = p_i, bit-identical to
+ * the reference (sequential fp32 normaliser).  d_in and d_out may be the same
+ * buffer.  Asynchronous on the sampler's stream. */
+PZ_API int pz_softmax_batch(pz_sampler *s, const float *d_in, long ld_in, float *d_out,
+                            long ld_out, int B, int V, float temperature);
 
 /* Device memory helpers for C hosts (hipMalloc / hipFree / hipMemcpy). */
 PZ_API int pz_device_alloc(void **ptr, size_t bytes, int device);

@@ -202,7 +202,6 @@ static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
   if (B == 0) return PZ_OK;
 
   bool pen_any = false, counts_any = false;
-  int count[PZ_MODE_COUNT] = {0, 0, 0, 0};
   pz_row_params_dev* res = s->res_params;
   for (int i = 0; i < n_params; i++) {
     res[i] = resolve(params[i], V, s->temp_mode);
@@ -211,6 +210,15 @@ static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
       counts_any |= needs_counts(params[i]);
     }
   }
+  return pz_dispatch_resolved(s, d_logits, B, V, ld, n_params, d_hist, H, pen_any, counts_any,
+                              d_u, d_ids, d_p);
+}
+
+int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, long ld,
+                         int n_params, const int32_t* d_hist, int H, bool pen_any,
+                         bool counts_any, const float* d_u, int32_t* d_ids, float* d_p) {
+  int count[PZ_MODE_COUNT] = {0, 0, 0, 0};
+  pz_row_params_dev* res = s->res_params;
   for (int b = 0; b < B; b++) count[res[n_params == 1 ? 0 : b].mode]++;
   if (!d_u) {
     for (int b = 0; b < B; b++)

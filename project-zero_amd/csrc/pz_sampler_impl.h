@@ -62,3 +62,11 @@ static inline int fail(pz_sampler* s, int code, const char* fmt, ...) {
     if (e_ != hipSuccess)                                                    \
       return fail((s), PZ_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
+
+// Launches the kernels for B rows whose kernel parameters are already in
+// s->res_params (n_params entries).  Used by the public entry points after
+// resolving pz_row_params, and by the reference-compatible calls, which set
+// a row's mode directly.
+int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, long ld,
+                         int n_params, const int32_t* d_hist, int H, bool pen_any,
+                         bool counts_any, const float* d_u, int32_t* d_ids, float* d_p);

@@ -89,11 +89,6 @@ __device__ __forceinline__ void append_key(int* count, int* over, uint64_t* buf,
   }
 }
 
-// Exact candidate term of one element (0 for non-candidates).
-__device__ __forceinline__ float cand_e(float y, bool valid, float thr, float M) {
-  return (valid && y >= thr) ? pz_expf(y - M) : 0.0f;
-}
-
 // Reference cumulative/draw over a descending key list (wave 0 computes the
 // cut-off, thread 0 draws).  keys/cum may be LDS or global.  all_gathered:
 // the list holds every candidate (then a cumulative that never reaches top_p

@@ -24,6 +24,10 @@ ABI_SYMBOLS = (
     "pz_sampler_last_error", "pz_sampler_stream", "pz_sample_batch",
     "pz_sample_batch_async", "pz_sampler_sync", "pz_spec_verify",
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
+    "pz_temperature_batch", "pz_softmax_batch",
+    # include/pz_sampling_compat.h: the reference sampler's own symbols
+    "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
+    "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
 )
 
 
@@ -85,6 +89,23 @@ def load():
     lib.pz_device_free.argtypes = [_P]
     lib.pz_memcpy_h2d.argtypes = [_P, _P, ctypes.c_size_t]
     lib.pz_memcpy_d2h.argtypes = [_P, _P, ctypes.c_size_t]
+    lib.pz_temperature_batch.argtypes = [_P, _P, _L, _I, _I, _F]
+    lib.pz_softmax_batch.argtypes = [_P, _P, _L, _P, _L, _I, _I, _F]
+    pull = ctypes.POINTER(ctypes.c_ulonglong)
+    lib.sample_argmax.argtypes = [_P, _I]
+    lib.apply_temperature.argtypes = [_P, _I, _F]
+    lib.apply_temperature.restype = None
+    lib.sample_top_p.argtypes = [_P, _I, _F, pull]
+    lib.sample_top_k.argtypes = [_P, _I, _I, pull]
+    lib.rng_seed.argtypes = [pull, ctypes.c_ulonglong]
+    lib.rng_seed.restype = None
+    lib.rng_float.argtypes = [pull]
+    lib.rng_float.restype = _F
+    lib.pz_tn_softmax.argtypes = [_P, _I]
+    lib.pz_tn_softmax.restype = None
+    lib.pz_compat_set_temp_mode.argtypes = [_I]
+    lib.pz_compat_set_temp_mode.restype = None
+    lib.pz_compat_last_status.argtypes = []
     _lib = lib
     return lib
 
@@ -188,6 +209,17 @@ class Sampler:
 
     def sync(self):
         self._check(self.lib.pz_sampler_sync(self.h))
+
+    def temperature(self, d_x, B, V, ld, temperature):
+        """In-place apply_temperature over device rows (asynchronous)."""
+        _sync_torch(d_x)
+        self._check(self.lib.pz_temperature_batch(self.h, _ptr(d_x), ld, B, V, temperature))
+
+    def softmax(self, d_in, d_out, B, V, ld_in, ld_out, temperature=1.0):
+        """Reference softmax of device rows into d_out (asynchronous)."""
+        _sync_torch(d_in, d_out)
+        self._check(self.lib.pz_softmax_batch(self.h, _ptr(d_in), ld_in, _ptr(d_out), ld_out, B,
+                                              V, temperature))
 
     def spec_verify(self, d_target, d_draft, B, K, V, ld, has_bonus, temperature,
                     draft_ids, u_acc, u_res):
