@@ -13,17 +13,26 @@
  * and every exponential goes through the host libm expf, exactly like the
  * reference.  Each function names the reference lines it follows.
  *
- * Parity pins (what checks each function; see tests/test_oracle_*.py):
- *   orc_rng_*            golden sequences from the compiled reference (FIX)
- *   orc_argmax           reference KATs + compiled reference (KAT, FIX)
+ * Parity pins (what checks each function; tests/test_oracle_golden.py,
+ * tests/test_oracle_extensions.py):
+ *   orc_rng_*            golden sequences from the compiled reference (FIX),
+ *                        closed form of xorshift64* (CF)
+ *   orc_argmax           reference KATs (tests/test_sampling.c:76-104) +
+ *                        compiled reference (KAT, FIX)
  *   orc_apply_temperature compiled reference, both forms (FIX)
- *   orc_softmax          compiled reference softmax.c (FIX) + sum=1 (INV)
- *   orc_categorical      brute force on tiny V (BF) + CDF closed form (CF)
- *   orc_top_k            compiled reference top_k.c (FIX) + sort model (BF)
- *   orc_top_p            compiled reference top_p.c (FIX) + sort model (BF)
- *   orc_penalties        brute force / closed form (BF, CF)
- *   orc_chain            reduces to orc_top_k when p>=1 (INV) + BF
- *   orc_spec_verify      closed form on tiny V + distribution test (CF, INV)
+ *   orc_softmax          compiled reference softmax.c (FIX) + reference
+ *                        KATs (test_math.c:70-88, audit_math.c:19-33)
+ *   orc_categorical      hand-computed CDF cases incl. the V-1 fallback (CF)
+ *                        + draw frequencies vs float64 probabilities (INV)
+ *   orc_top_k            compiled reference top_k.c (FIX) + reference tests
+ *   orc_top_p            compiled reference top_p.c (FIX) + reference tests
+ *   orc_penalties        hand-computed exact cases (CF) + a np.bincount
+ *                        formulation on random histories (BF)
+ *   orc_chain            equals orc_top_k outside (0,1) (INV) + float64
+ *                        model away from rounding boundaries (BF)
+ *   orc_spec_verify      draft == target accepts all (CF), rejected drafts
+ *                        never resampled (INV), emitted token distributed as
+ *                        the target softmax (INV, simulation)
  */
 #ifndef PZ_ORACLE_H
 #define PZ_ORACLE_H
