@@ -18,6 +18,34 @@
 
 float orc_expf(float x) { return expf(x); }
 
+/* Order-independent hash of libm expf over the fp32 bit patterns lo..hi
+ * (every stride-th one), for the exhaustive comparison with the GPU's
+ * exponential: sum over inputs of a 64-bit finaliser of (result, input). */
+static uint64_t mix64(uint64_t z) {
+  z ^= z >> 33;
+  z *= 0xff51afd7ed558ccdULL;
+  z ^= z >> 33;
+  z *= 0xc4ceb9fe1a85ec53ULL;
+  z ^= z >> 33;
+  return z;
+}
+
+uint64_t orc_expf_hash(uint32_t lo, uint32_t hi, uint32_t stride) {
+  uint64_t h = 0;
+  const uint64_t n = ((uint64_t)hi - lo) / stride + 1;
+#pragma omp parallel for reduction(+ : h) schedule(static)
+  for (int64_t i = 0; i < (int64_t)n; i++) {
+    const uint32_t b = lo + (uint32_t)((uint64_t)i * stride);
+    float x, r;
+    uint32_t rb;
+    memcpy(&x, &b, 4);
+    r = expf(x);
+    memcpy(&rb, &r, 4);
+    h += mix64(((uint64_t)rb << 32) | b);
+  }
+  return h;
+}
+
 static void info_reset(orc_info *info) {
   if (!info) return;
   info->p_chosen = 1.0f;

@@ -131,8 +131,9 @@ void orc_spec_verify(const float *target, const float *draft, int B, int K,
                      const float *u_res, int32_t *acc_len, int32_t *out_ids,
                      float *dist);
 
-/* Exposed for the expf-agreement test. */
+/* Exposed for the expf-agreement tests. */
 float orc_expf(float x);
+uint64_t orc_expf_hash(uint32_t lo_bits, uint32_t hi_bits, uint32_t stride);
 
 #ifdef __cplusplus
 }

@@ -92,6 +92,8 @@ def oracle():
     o.orc_spec_verify.restype = None
     o.orc_expf.argtypes = [_F]
     o.orc_expf.restype = _F
+    o.orc_expf_hash.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+    o.orc_expf_hash.restype = ctypes.c_uint64
     _orc = o
     return o
 

@@ -42,3 +42,38 @@ extern "C" int pzcheck_exp_bound(float* max_rel, unsigned int* n_bad_small) {
   *n_bad_small = h[1];
   return 0;
 }
+
+// The same hash as oracle/pz_oracle.c orc_expf_hash, of the GPU's pz_expf.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z ^= z >> 33;
+  z *= 0xff51afd7ed558ccdULL;
+  z ^= z >> 33;
+  z *= 0xc4ceb9fe1a85ec53ULL;
+  z ^= z >> 33;
+  return z;
+}
+
+__global__ void k_expf_hash(uint32_t lo, uint64_t n, uint32_t stride,
+                            unsigned long long* out) {
+  unsigned long long h = 0;
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint32_t b = lo + (uint32_t)(i * stride);
+    const float r = pz_expf(__uint_as_float(b));
+    h += mix64(((uint64_t)__float_as_uint(r) << 32) | b);
+  }
+  atomicAdd(out, h);
+}
+
+extern "C" int pzcheck_expf_hash(uint32_t lo, uint32_t hi, uint32_t stride, uint64_t* hash) {
+  unsigned long long* d = nullptr;
+  if (hipMalloc(&d, 8) != hipSuccess) return -1;
+  if (hipMemset(d, 0, 8) != hipSuccess) return -1;
+  const uint64_t n = ((uint64_t)hi - lo) / stride + 1;
+  hipLaunchKernelGGL(k_expf_hash, dim3(16384), dim3(256), 0, 0, lo, n, stride, d);
+  unsigned long long h = 0;
+  if (hipMemcpy(&h, d, 8, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  hipFree(d);
+  *hash = h;
+  return 0;
+}
