@@ -49,7 +49,10 @@ __constant__ static const uint64_t pz_exp2_tab[32] = {
     0x3fef3720dcef9069ull, 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
     0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-__device__ __forceinline__ float pz_expf_inline(float x) {
+// The method with the table read through `tab` (the constant table, or a
+// copy of it in LDS for latency-bound callers).
+template <class Tab>
+__device__ __forceinline__ float pz_expf_tab(float x, Tab tab) {
   const uint32_t ux = __float_as_uint(x);
   const uint32_t abstop = (ux >> 20) & 0x7ff;
   if (__builtin_expect(abstop >= 0x42b, 0)) {  // |x| >= 88 or non-finite
@@ -68,7 +71,7 @@ __device__ __forceinline__ float pz_expf_inline(float x) {
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd = kd - Shift;
   const double r = __builtin_fma(InvLn2N, xd, -kd);
-  uint64_t t = pz_exp2_tab[ki & 31];
+  uint64_t t = tab[ki & 31];
   t += ki << 47;
   const double s = __longlong_as_double((long long)t);
   const double z = __builtin_fma(C0, r, C1);
@@ -78,6 +81,8 @@ __device__ __forceinline__ float pz_expf_inline(float x) {
   y = y * s;
   return (float)y;
 }
+
+__device__ __forceinline__ float pz_expf_inline(float x) { return pz_expf_tab(x, pz_exp2_tab); }
 
 // Out of line: the exact exponential sits on paths that are rare next to the
 // streaming passes, and inlining it into every one of them multiplies the
@@ -130,14 +135,13 @@ __device__ __forceinline__ uint32_t pz_hash(uint32_t id) {
   return (id * 0x9E3779B1u) >> 7;
 }
 
+// Set-up half of the build: fills P and clears the tables (no barrier).
 template <int BLOCK>
-__device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V, int hcap,
-                                 const int32_t* hist_row, int H,
-                                 const pz_row_params_dev& prm) {
+__device__ __forceinline__ void pz_penalty_setup(PzPenalty& P, char* lds, int V, int hcap,
+                                                 bool has_hist, const pz_row_params_dev& prm) {
   const int tid = threadIdx.x;
-  P.active = hist_row != nullptr && H > 0 &&
-             (prm.rep_penalty != 1.0f || prm.presence_penalty != 0.0f ||
-              prm.frequency_penalty != 0.0f);
+  P.active = has_hist && (prm.rep_penalty != 1.0f || prm.presence_penalty != 0.0f ||
+                          prm.frequency_penalty != 0.0f);
   P.rep = prm.rep_penalty;
   P.pres = prm.presence_penalty;
   P.freq = prm.frequency_penalty;
@@ -152,32 +156,50 @@ __device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V,
   if (!P.active) return;
   for (int w = tid; w < words; w += BLOCK) bitmap[w] = 0u;
   for (int j = tid; j < P.hcap; j += BLOCK) { hkey[j] = -1; hcnt[j] = 0; }
-  __syncthreads();
-  const uint32_t mask = (uint32_t)P.hcap - 1u;
-  for (int j = tid; j < H; j += BLOCK) {
-    const int id = hist_row[j];
-    if (id < 0 || id >= V) continue;  // ids outside [0,V) are ignored
-    atomicOr(&bitmap[id >> 5], 1u << (id & 31));
-    if (P.hcap) {
-      uint32_t s = pz_hash((uint32_t)id) & mask;
-      while (true) {
-        const int prev = atomicCAS(&hkey[s], -1, id);
-        if (prev == -1 || prev == id) { atomicAdd(&hcnt[s], 1); break; }
-        s = (s + 1) & mask;
-      }
+}
+
+// Inserts one history id (after the set-up and a barrier).  With dlist !=
+// nullptr every distinct valid id is also appended once to dlist, *dcount
+// counting them (zeroed by the caller before the set-up barrier).
+__device__ __forceinline__ void pz_penalty_insert(const PzPenalty& P, char* lds, int V, int id,
+                                                  int32_t* dlist, int* dcount) {
+  if (id < 0 || id >= V) return;  // ids outside [0,V) are ignored
+  const int words = (V + 31) >> 5;
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds);
+  int32_t* hkey = reinterpret_cast<int32_t*>(lds + (size_t)words * 4);
+  int32_t* hcnt = hkey + P.hcap;
+  const uint32_t bit = 1u << (id & 31);
+  const uint32_t before = atomicOr(&bitmap[id >> 5], bit);
+  if (dlist && !(before & bit)) dlist[atomicAdd(dcount, 1)] = id;
+  if (P.hcap) {
+    const uint32_t mask = (uint32_t)P.hcap - 1u;
+    uint32_t s = pz_hash((uint32_t)id) & mask;
+    while (true) {
+      const int prev = atomicCAS(&hkey[s], -1, id);
+      if (prev == -1 || prev == id) { atomicAdd(&hcnt[s], 1); break; }
+      s = (s + 1) & mask;
     }
   }
+}
+
+template <int BLOCK>
+__device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V, int hcap,
+                                                 const int32_t* hist_row, int H,
+                                                 const pz_row_params_dev& prm) {
+  pz_penalty_setup<BLOCK>(P, lds, V, hcap, hist_row != nullptr && H > 0, prm);
+  if (!P.active) return;
+  __syncthreads();
+  for (int j = threadIdx.x; j < H; j += BLOCK)
+    pz_penalty_insert(P, lds, V, hist_row[j], nullptr, nullptr);
   __syncthreads();
 }
 
 // Penalised value of a history member (caller checked the bitmap bit).
 // Repetition first (x>0 ? x/rep : x*rep, each distinct id once), then
-// t = (float)c*freq; t = t + pres; x = x - t.  Out of line (only history
-// members take it; inlined at every element of every unrolled pass it bloats
-// the kernels), with every operand passed by value.
-__device__ __noinline__ float pz_penalize_v(float x, int id, float rep, float pres, float freq,
-                                            int hcap, const pz_lds_i32* hkey,
-                                            const pz_lds_i32* hcnt) {
+// t = (float)c*freq; t = t + pres; x = x - t.
+__device__ __forceinline__ float pz_penalize_inline(float x, int id, float rep, float pres,
+                                                   float freq, int hcap, const pz_lds_i32* hkey,
+                                                   const pz_lds_i32* hcnt) {
   x = x > 0.0f ? x / rep : x * rep;
   if (hcap) {
     const uint32_t mask = (uint32_t)hcap - 1u;
@@ -189,6 +211,15 @@ __device__ __noinline__ float pz_penalize_v(float x, int id, float rep, float pr
     x = x - t;
   }
   return x;
+}
+
+// Out of line for the streaming passes (only history members take it;
+// inlined at every element of every unrolled pass it bloats the kernels),
+// with every operand passed by value.
+__device__ __noinline__ float pz_penalize_v(float x, int id, float rep, float pres, float freq,
+                                            int hcap, const pz_lds_i32* hkey,
+                                            const pz_lds_i32* hcnt) {
+  return pz_penalize_inline(x, id, rep, pres, freq, hcap, hkey, hcnt);
 }
 
 __device__ __forceinline__ float pz_penalize(const PzPenalty& P, float x, int id) {

@@ -33,6 +33,7 @@ struct pz_launch {
   int H;
   int hcap;             // LDS hash capacity for presence/frequency counts (0: none)
   bool pen_any;         // any row has an active penalty
+  bool temp_div;        // temperature as x / T (scalar build) rather than x * (1/T)
   const float* u;       // device [B] uniforms
   int32_t* ids;         // device [B] sampled ids
   float* p_out;         // device [B] p(chosen) or nullptr

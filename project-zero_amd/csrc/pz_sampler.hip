@@ -265,6 +265,7 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
   L.hist = H > 0 ? d_hist : nullptr;
   L.H = H;
   L.pen_any = pen_any;
+  L.temp_div = s->temp_mode == PZ_TEMP_DIV;
   L.hcap = counts_any ? next_pow2(2 * (H > 0 ? H : 1)) : 0;
   L.u = d_u;
   L.ids = d_ids;

@@ -15,7 +15,7 @@ __device__ __forceinline__ void pz_bitonic_desc(Ptr buf, int N) {
   for (int size = 2; size <= N; size <<= 1) {
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
       for (int i = threadIdx.x; i < (N >> 1); i += BLOCK) {
-        const int lo = 2 * stride * (i / stride) + (i % stride);
+        const int lo = ((i & ~(stride - 1)) << 1) | (i & (stride - 1));  // stride: power of two
         const int hi = lo + stride;
         const bool desc = (lo & size) == 0;
         const uint64_t a = buf[lo], b = buf[hi];

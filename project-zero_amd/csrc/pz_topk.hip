@@ -9,135 +9,350 @@
 // Chain (0 < top_p < 1): cut-off, truncated mass and draw of
 // src/sampling/top_p.c:79-105 over those k sorted probabilities.
 //
-// Design (one workgroup per row, BLOCK threads):
-//   1. LDS histogram of the order keys of a sample tile -> a lower bound tau
-//      on the k-th largest key (the sample's k-th largest lies in a bin whose
-//      lower edge is <= the row's k-th largest).
-//   2. One streaming pass over the row (128-bit loads; penalties and
-//      temperature applied on the fly) appends every (key, id) >= tau to an
-//      LDS candidate buffer with one atomic per wave.  If the buffer
-//      overflows, the k-th largest (key, id) of the buffer is a tighter lower
-//      bound and the row is rescanned (from L2 / Infinity Cache).
-//   3. Bitonic sort of the candidates in LDS by (key desc, id asc).
-//   4. Wave 0 evaluates the k-slot softmax, cut-off and draw with the exact
-//      sequential fp32 sums of the reference (lane-ordered scans).
+// Design (one workgroup per row, 1024 threads):
+//   0. The loads of the first tiles, the history ids and the expf table are
+//      issued before anything else, so their latency overlaps the set-up.
+//   1. Penalty tables in LDS (membership bitmap, id -> count hash); the
+//      streaming pass reads one bitmap word per four ids and penalises the
+//      rare history members in registers.
+//   2. LDS histogram of the order keys of the first tile (a sample of the
+//      row) -> a lower bound on the row's k-th largest (key, id).
+//   3. One software-pipelined streaming pass (128-bit loads, the next group
+//      of tiles in flight while the current one is processed).  The bound is
+//      carried back through the temperature to the raw logits (the
+//      temperature map is monotone), so each element costs one compare; the
+//      few candidates that pass are keyed and appended to an LDS buffer with
+//      one LDS atomic per wave.  On overflow the buffer's k-th largest is a
+//      tighter bound and the row is streamed again (from L2 / Infinity
+//      Cache).
+//   4. Radix select (11-bit digits over the candidates' actual range, LDS
+//      histograms) of the exact k-th largest candidate, compaction of the k
+//      survivors, and their order: a rank count for small k, a bitonic sort
+//      otherwise.
+//   5. Wave 0 evaluates the k-slot softmax (expf from an LDS copy of its
+//      table), cut-off and draw with the exact sequential fp32 sums of the
+//      reference (lane-ordered scans).
 #include "pz_device.h"
+#include "pz_exact.h"
 #include "pz_launch.h"
+#include "pz_rowpass.h"
 #include "pz_seq.h"
 #include "pz_sort.h"
 
 namespace {
 
 constexpr int TOPK_BLOCK = 1024;
-constexpr int TOPK_CAP = 4096;      // candidate buffer entries (8 B each)
-constexpr int HBINS = 2048;         // 11-bit key digit
+constexpr int TOPK_CAP = 4096;    // candidate buffer entries (8 B each)
+constexpr int TOPK_MAXK = 1024;   // top_k.c:11-17 clamps k to 1024
+constexpr int HBINS = 2048;       // 11-bit digit
+constexpr int TK_U = 4;           // tiles per load group
+constexpr int TK_RANK_MAX = 128;  // survivors ordered by a rank count up to this many
 
 struct TopkShared {
-  uint32_t hist[HBINS];
-  int count;
-  int over;
-  uint32_t tau_key;
-  uint32_t tau_nid;  // composite mode: accept (key, ~id) >= (tau_key, tau_nid)
-  int composite;
+  uint32_t hist[HBINS];     // sample / radix histograms (kept zeroed), then p and cdf
+  uint64_t top[TOPK_MAXK];  // the k survivors
+  uint64_t etab[32];        // expf table
+  uint64_t thr;             // candidates are the (key, ~id) >= thr
+  uint64_t maxc;            // largest candidate appended
+  uint64_t base;            // radix select state
+  float rlo, rhi;           // the pass bound in raw logits (TkRaw)
+  int ridmax;
+  int need;
+  int done;
+  int count;  // candidates appended (may exceed TOPK_CAP)
+  int ntop;   // survivors
 };
+
+typedef __attribute__((address_space(3))) uint32_t tk_lds_u32;
+typedef __attribute__((address_space(3))) float tk_lds_f32;
 
 __device__ __forceinline__ uint64_t comp_of(uint32_t key, int id) {
   return ((uint64_t)key << 32) | (uint32_t)(0xffffffffu - (uint32_t)id);
 }
 
-__device__ __forceinline__ bool tk_pass(const TopkShared& S, uint32_t key, int id) {
-  if (!S.composite) return key >= S.tau_key;
-  const uint32_t nid = 0xffffffffu - (uint32_t)id;
-  return key > S.tau_key || (key == S.tau_key && nid >= S.tau_nid);
+__device__ __forceinline__ int id_of(uint64_t c) { return (int)(0xffffffffu - (uint32_t)c); }
+
+template <bool DIV>
+__device__ __forceinline__ float tk_temper(float x, const PzTemp& T) {
+  return DIV ? x / T.t : x * T.inv;
 }
 
-// Wave-aggregated append of up to one candidate per lane.
-__device__ __forceinline__ void tk_append(TopkShared& S, uint64_t* buf, bool want,
-                                          uint64_t comp) {
-  const uint64_t ball = __ballot(want);
-  if (ball == 0) return;
-  const int lane = threadIdx.x & (PZ_WAVE - 1);
-  const int n = __popcll(ball);
-  const int before = __popcll(ball & ((1ull << lane) - 1ull));
-  int base = 0;
-  const int leader = __ffsll((long long)ball) - 1;
-  if (lane == leader) base = atomicAdd(&S.count, n);
-  base = __shfl(base, leader, PZ_WAVE);
-  if (want) {
-    const int slot = base + before;
-    if (slot < TOPK_CAP) buf[slot] = comp;
-    else S.over = 1;
+// Order key of y + 0.0f (pz_key without the -0.0 test: the addition has
+// already folded -0.0 onto +0.0).
+__device__ __forceinline__ uint32_t tk_key(float y) {
+  const uint32_t u = __float_as_uint(y);
+  return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+
+// Smallest raw logit x (in key order) whose tempered value reaches f:
+// temper(x) >= f  <=>  x >= tk_raw_bound(f) for every non-NaN x, since
+// x -> fl(x * inv) and x -> fl(x / t) are monotone non-decreasing.  A 64-way
+// search by one wave over the keys of [-inf, +inf] (six rounds); NaN
+// (nothing passes) when f is NaN.  Wave-uniform result.
+template <bool DIV>
+__device__ __forceinline__ float tk_raw_bound(float f, const PzTemp& T) {
+  if (!(f <= __builtin_inff())) return __builtin_nanf("");
+  const uint32_t lane = threadIdx.x & 63;
+  // invariant: temper(unkey(lo)) < f <= temper(unkey(hi)); -inf < f always
+  uint32_t lo = 0x007fffffu, hi = 0xff800000u;  // keys of -inf and +inf
+  while (hi - lo > 1u) {
+    const uint64_t span = hi - lo;
+    // lane l tests lo + ceil(span * (l + 1) / 64), the last lane tests hi
+    const uint32_t m = lo + (uint32_t)((span * (lane + 1) + 63) >> 6);
+    const uint64_t ok = __ballot(tk_temper<DIV>(pz_unkey(m), T) >= f);
+    const int j = (int)__builtin_ctzll(ok);  // lane 63 (m == hi) always passes
+    const uint32_t mj = __builtin_amdgcn_readlane(m, j);
+    const uint32_t mp = j > 0 ? __builtin_amdgcn_readlane(m, j - 1) : lo;
+    hi = mj;
+    lo = mp;
+  }
+  return pz_unkey(hi);
+}
+
+// The pass bound (key, ~id) >= thr, with y > -1e30, in raw logits:
+//   plain (~id part 0):  key(y) >= K                    <=>  x >= lo
+//   composite:           key(y) > K, or key(y) == K and id <= idmax
+//                                                       <=>  x >= hi, or x >= lo and id <= idmax
+struct TkRaw {
+  float lo, hi;
+  int idmax;
+};
+
+template <bool DIV>
+__device__ __forceinline__ TkRaw tk_raw_of(uint64_t thr, const PzTemp& T) {
+  const uint32_t kk = (uint32_t)(thr >> 32);
+  const float fk = pz_unkey(kk);
+  const float valid = __uint_as_float(0xf149f2c9u);  // smallest float > -1e30f
+  TkRaw r;
+  r.lo = tk_raw_bound<DIV>(fk > valid ? fk : valid, T);
+  r.hi = r.lo;
+  r.idmax = (int)(0xffffffffu - (uint32_t)thr);
+  if ((uint32_t)thr != 0u) {
+    // composite bounds come from real candidates: fk is above -1e30, not NaN
+    r.hi = fk < __builtin_inff() ? tk_raw_bound<DIV>(pz_unkey(kk + 1u), T)
+                                 : __builtin_nanf("");
+  }
+  return r;
+}
+
+// Wave 0 publishes the raw form of a new pass bound.
+template <bool DIV>
+__device__ __forceinline__ void tk_publish(TopkShared& S, uint64_t thr, const PzTemp& T) {
+  const TkRaw r = tk_raw_of<DIV>(thr, T);
+  if ((threadIdx.x & 63) == 0) {
+    S.thr = thr;
+    S.rlo = r.lo;
+    S.rhi = r.hi;
+    S.ridmax = r.idmax;
   }
 }
 
-template <int BLOCK, bool VEC>
-__device__ void tk_stream(TopkShared& S, uint64_t* buf, const float* x, int V,
-                          const PzPenalty& P, const pz_row_params_dev& prm) {
+// Loads tiles t0..t0+TK_U-1 of the row (tiles past the end re-load the last
+// one, so every load is unconditional and in bounds).
+template <bool VEC>
+__device__ __forceinline__ void tk_load(const float* x, int V, int t0, int ntiles,
+                                        float (&a)[TK_U][4]) {
+#pragma unroll
+  for (int u = 0; u < TK_U; u++) {
+    const int t = t0 + u < ntiles ? t0 + u : ntiles - 1;
+    (void)pz_load4<VEC, false>(x, V, pz_tile_e0(t), a[u]);
+  }
+}
+
+// Reads every register of a group, so that loads still in flight when a
+// streaming pass ends are waited for there, not at the next pass's first
+// use of the registers (which would stall every iteration of its loop).
+__device__ __forceinline__ void tk_drain(const float (&a)[TK_U][4]) {
+#pragma unroll
+  for (int u = 0; u < TK_U; u++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) asm volatile("" ::"v"(a[u][c]));
+}
+
+// Wave-cooperative search over a 2048-bin histogram (bin 2047 = largest
+// digit): the bin holding the need-th largest element, with above = the
+// count in larger bins.  Returns false when the histogram holds fewer than
+// need.  The histogram is zeroed afterwards (same wave, program order).
+__device__ __forceinline__ bool tk_find_bin(tk_lds_u32* hist, uint32_t need, uint32_t& bin,
+                                            uint32_t& above, uint32_t& cnt) {
+  const int lane = threadIdx.x & 63;
+  tk_lds_u32* h = hist + 32 * lane;  // lane l owns bins [32l, 32l+32)
+  uint32_t own = 0;
+#pragma unroll
+  for (int j = 0; j < 32; j++) own += h[j];
+  const uint32_t incl = pz_wave_scan_u32(own);
+  const uint32_t total = pz_readlane_u32(incl, 63);
+  bool found = false;
+  if (total >= need) {
+    const uint32_t abv = total - incl;  // bins of lanes > l
+    const uint64_t b = __ballot(abv < need && abv + own >= need);
+    const int l = (int)__builtin_ctzll(b);
+    const uint32_t above_l = pz_readlane_u32(abv, l);
+    // lanes 0..31 take the 32 bins of lane l, largest first
+    const uint32_t hj = lane < 32 ? hist[32 * l + 31 - lane] : 0u;
+    const uint32_t sj = pz_wave_scan_u32(hj);
+    const uint64_t f = __ballot(lane < 32 && above_l + sj >= need);
+    const int fl = (int)__builtin_ctzll(f);
+    bin = (uint32_t)(32 * l + 31 - fl);
+    cnt = pz_readlane_u32(hj, fl);
+    above = above_l + pz_readlane_u32(sj, fl) - cnt;
+    found = true;
+  }
+#pragma unroll
+  for (int j = 0; j < 32; j++) h[j] = 0u;
+  return found;
+}
+
+// Exact radix select over buf[0..n) (distinct composite keys, all in
+// [base, maxc], n >= k >= 1): returns thr such that exactly k entries are
+// >= thr.  Digits are 11-bit slices of (c - base) over the live range, so
+// the first pass already resolves the candidates' actual spread.  S.hist is
+// zero on entry and on exit.
+template <int BLOCK>
+__device__ uint64_t tk_select(TopkShared& S, const pz_lds_u64* buf, int n, int k, uint64_t base,
+                              uint64_t maxc) {
   const int tid = threadIdx.x;
-  if (VEC) {
-    const pz_f4* x4 = reinterpret_cast<const pz_f4*>(x);
-    const int n4 = V >> 2;
-    constexpr int U = 4;
-    for (int base = 0; base < n4; base += BLOCK * U) {
-      pz_f4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int i4 = base + u * BLOCK + tid;
-        if (i4 < n4) v[u] = x4[i4];
-      }
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int i4 = base + u * BLOCK + tid;
-        const bool in = i4 < n4;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          const int i = (i4 << 2) + c;
-          bool want = false;
-          uint64_t comp = 0;
-          if (in) {
-            const float y = pz_transform(P, prm, v[u][c], i);
-            if (y > -1e30f) {
-              const uint32_t key = pz_key(y);
-              want = tk_pass(S, key, i);
-              comp = comp_of(key, i);
-            }
-          }
-          tk_append(S, buf, want, comp);
-        }
+  uint32_t need = (uint32_t)k;
+  const uint64_t span = maxc - base;
+  int w = span == 0 ? 0 : 64 - __builtin_clzll(span);  // range [base, base + 2^w)
+  if (w == 0) return base;
+  for (;;) {
+    const int bits = w >= 11 ? 11 : w;
+    const int sh = w - bits;
+    for (int i = tid; i < n; i += BLOCK) {
+      const uint64_t d = buf[i] - base;
+      if (w >= 64 || (d >> w) == 0) atomicAdd(&S.hist[(uint32_t)(d >> sh)], 1u);
+    }
+    __syncthreads();
+    if (tid < PZ_WAVE) {
+      uint32_t bin = 0, above = 0, cnt = 0;
+      tk_find_bin((tk_lds_u32*)S.hist, need, bin, above, cnt);
+      if (tid == 0) {
+        S.base = base + ((uint64_t)bin << sh);
+        S.need = (int)(need - above);
+        S.done = sh == 0 || cnt == need - above;
       }
     }
-    // tail (V not a multiple of 4): at most 3 elements
-    const int i = (n4 << 2) + tid;
-    bool want = false;
-    uint64_t comp = 0;
-    if (i < V) {
-      const float y = pz_transform(P, prm, x[i], i);
-      if (y > -1e30f) {
-        const uint32_t key = pz_key(y);
-        want = tk_pass(S, key, i);
-        comp = comp_of(key, i);
-      }
-    }
-    tk_append(S, buf, want, comp);
-  } else {
-    for (int base = 0; base < V; base += BLOCK) {
-      const int i = base + tid;
-      bool want = false;
-      uint64_t comp = 0;
-      if (i < V) {
-        const float y = pz_transform(P, prm, x[i], i);
-        if (y > -1e30f) {
-          const uint32_t key = pz_key(y);
-          want = tk_pass(S, key, i);
-          comp = comp_of(key, i);
-        }
-      }
-      tk_append(S, buf, want, comp);
-    }
+    __syncthreads();
+    base = S.base;
+    need = (uint32_t)S.need;
+    w = sh;
+    if (S.done) return base;
   }
 }
 
-template <int BLOCK, bool VEC>
+// Element j (0..15) of a group's registers: a[j >> 2][j & 3] by selects
+// (indexing the register array by a run-time value would go through scratch).
+__device__ __forceinline__ float tk_pick(const float (&a)[TK_U][4], uint32_t j) {
+  float r[TK_U];
+#pragma unroll
+  for (int u = 0; u < TK_U; u++) {
+    const float lo = (j & 1u) ? a[u][1] : a[u][0];
+    const float hi = (j & 1u) ? a[u][3] : a[u][2];
+    r[u] = (j & 2u) ? hi : lo;
+  }
+  const float lo = (j & 4u) ? r[1] : r[0];
+  const float hi = (j & 4u) ? r[3] : r[2];
+  return (j & 8u) ? hi : lo;
+}
+
+// Processes one group of tiles: history members take their penalised logit
+// in place (rare lanes, a divergent branch), then every element passing the
+// raw bound is keyed and appended to buf, with one LDS atomic per wave and
+// one loop trip per candidate of the busiest lane.  lmax tracks the lane's
+// largest appended candidate.
+template <bool DIV, bool COMP>
+__device__ __forceinline__ void tk_group(TopkShared& S, pz_lds_u64* buf, const PzPenalty& P,
+                                         const PzTemp& T, int V, int t0, int ntiles,
+                                         float (&a)[TK_U][4], const TkRaw& rb, uint64_t& lmax) {
+  const int lane = threadIdx.x & (PZ_WAVE - 1);
+  uint32_t vm[TK_U];
+#pragma unroll
+  for (int u = 0; u < TK_U; u++) {
+    const int lim = t0 + u < ntiles ? V - pz_tile_e0(t0 + u) : 0;  // row elements in the float4
+    vm[u] = lim >= 4 ? 0xfu : (lim > 0 ? (1u << lim) - 1u : 0u);
+  }
+  const int e00 = pz_tile_e0(t0);
+  if (P.active) {
+    // the four bitmap reads are issued together (clamped into the bitmap;
+    // bits of elements past the end are masked by vm)
+    uint32_t pb = 0;
+#pragma unroll
+    for (int u = 0; u < TK_U; u++) {
+      const int e0 = pz_tile_e0(t0 + u);
+      pb |= ((P.bitmap[(e0 < V ? e0 : V - 1) >> 5] >> (e0 & 31)) & vm[u]) << (4 * u);
+    }
+    while (pb) {  // one trip per history member of the busiest lane
+      const uint32_t j = (uint32_t)__builtin_ctz(pb);
+      pb &= pb - 1u;
+      const int id = e00 + (int)(j >> 2) * PZ_TILE + (int)(j & 3u);
+      const float y = pz_penalize_inline(tk_pick(a, j), id, P.rep, P.pres, P.freq, P.hcap,
+                                         P.hkey, P.hcnt);
+#pragma unroll
+      for (int u = 0; u < TK_U; u++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) a[u][c] = j == (uint32_t)(4 * u + c) ? y : a[u][c];
+    }
+  }
+  uint32_t want = 0;
+#pragma unroll
+  for (int u = 0; u < TK_U; u++) {
+    const int e0 = pz_tile_e0(t0 + u);
+    uint32_t nib = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float xv = a[u][c];
+      const bool w = COMP ? (xv >= rb.hi) | ((xv >= rb.lo) & (e0 + c <= rb.idmax))
+                          : xv >= rb.lo;
+      nib |= (w ? 1u : 0u) << c;
+    }
+    want |= (nib & vm[u]) << (4 * u);
+  }
+  if (__ballot(want != 0u) == 0) return;
+  const uint32_t cnt = (uint32_t)__builtin_popcount(want);
+  const uint32_t incl = pz_wave_scan_u32(cnt);
+  const uint32_t total = pz_readlane_u32(incl, 63);
+  int base = 0;
+  if (lane == 0) base = atomicAdd(&S.count, (int)total);
+  base = __builtin_amdgcn_readfirstlane(base);
+  int slot = base + (int)(incl - cnt);
+  while (want) {
+    const uint32_t j = (uint32_t)__builtin_ctz(want);
+    want &= want - 1u;
+    const int id = e00 + (int)(j >> 2) * PZ_TILE + (int)(j & 3u);
+    const uint64_t cc = comp_of(tk_key(tk_temper<DIV>(tk_pick(a, j), T) + 0.0f), id);
+    if (slot < TOPK_CAP) buf[slot] = cc;
+    lmax = cc > lmax ? cc : lmax;
+    slot++;
+  }
+}
+
+// One streaming pass over the row.  The first group is in a on entry.
+// sched_barrier keeps each group's loads below the processing of the group
+// whose registers they reuse (hoisted above it, the loaded values would need
+// registers of their own and copies at every iteration); the next group's
+// loads are issued unconditionally (past the end they re-read the last
+// tile), so the wait before each group counts exactly the group behind it.
+template <bool VEC, bool DIV, bool COMP>
+__device__ __forceinline__ void tk_pass(TopkShared& S, pz_lds_u64* buf, const PzPenalty& P,
+                                        const PzTemp& T, const float* x, int V, int ntiles,
+                                        float (&a)[TK_U][4], float (&b)[TK_U][4],
+                                        const TkRaw& rb, uint64_t& lmax) {
+  for (int t0 = 0;; t0 += 2 * TK_U) {
+    tk_load<VEC>(x, V, t0 + TK_U, ntiles, b);
+    tk_group<DIV, COMP>(S, buf, P, T, V, t0, ntiles, a, rb, lmax);
+    if (t0 + TK_U >= ntiles) break;
+    __builtin_amdgcn_sched_barrier(0);
+    tk_load<VEC>(x, V, t0 + 2 * TK_U, ntiles, a);
+    tk_group<DIV, COMP>(S, buf, P, T, V, t0 + TK_U, ntiles, b, rb, lmax);
+    if (t0 + 2 * TK_U >= ntiles) break;
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  tk_drain(a);
+  tk_drain(b);
+}
+
+template <int BLOCK, bool VEC, bool DIV>
 __global__ __launch_bounds__(BLOCK) void k_topk(
     const float* __restrict__ logits, long ld, int V, const int32_t* __restrict__ rows,
     const pz_row_params_dev* __restrict__ params, int n_params,
@@ -146,163 +361,204 @@ __global__ __launch_bounds__(BLOCK) void k_topk(
   extern __shared__ __align__(16) char lds[];
   __shared__ TopkShared S;
   const int row = pz_row_of(rows, blockIdx.x);
-  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-  const float* x = logits + (long)row * ld;
   const int tid = threadIdx.x;
   const int lane = tid & (PZ_WAVE - 1);
-  uint64_t* buf = reinterpret_cast<uint64_t*>(lds + pen_bytes);
+  const float* x = logits + (long)row * ld;
+  const int ntiles = pz_tiles(V);
+  const int32_t* hrow = hist ? hist + (long)row * H : nullptr;
 
+  // ---- 0. history ids, expf table and the first group of tiles in flight
+  const int hid = (hrow && tid < H) ? hrow[tid] : -1;
+  const uint64_t tab = tid < 32 ? pz_exp2_tab[tid] : 0ull;
+  float a[TK_U][4], b[TK_U][4];
+  tk_load<VEC>(x, V, 0, ntiles, a);
+  float uu = 0.0f;
+  if (tid == 0) uu = u[row];
+
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  pz_lds_u64* buf = (pz_lds_u64*)(lds + pen_bytes);
+
+  // ---- 1. penalty tables and the penalised values of the distinct history ids
   PzPenalty P;
-  pz_penalty_build<BLOCK>(P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
+  pz_penalty_setup<BLOCK>(P, lds, V, hcap, hrow != nullptr && H > 0, prm);
+  for (int j = tid; j < HBINS; j += BLOCK) S.hist[j] = 0u;
+  if (tid == 0) {
+    S.count = 0;
+    S.maxc = 0ull;
+  }
+  if (tid < 32) S.etab[tid] = tab;
+  __syncthreads();
+  if (P.active) {
+    pz_penalty_insert(P, lds, V, hid, nullptr, nullptr);
+    for (int j = tid + BLOCK; j < H; j += BLOCK)
+      pz_penalty_insert(P, lds, V, hrow[j], nullptr, nullptr);
+    __syncthreads();
+  }
+  const PzTemp T = PzTemp::of(prm);
   const int k = prm.top_k;
 
-  // ---- 1. sample tile -> lower bound on the k-th key
-  for (int j = tid; j < HBINS; j += BLOCK) S.hist[j] = 0;
-  if (tid == 0) { S.count = 0; S.over = 0; S.composite = 0; S.tau_nid = 0; }
-  __syncthreads();
-  const int ns = V < BLOCK * 4 ? V : BLOCK * 4;
-  for (int i = tid; i < ns; i += BLOCK) {
-    const float y = pz_transform(P, prm, x[i], i);
-    if (y > -1e30f) atomicAdd(&S.hist[pz_key(y) >> 21], 1u);
+  // ---- 2. the first tile as a sample -> lower bound on the k-th key
+  {
+    const int e0 = pz_tile_e0(0);
+    const uint32_t pen = (P.active && e0 < V) ? pz_pen_nibble(P, e0) : 0u;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const float y = tk_temper<DIV>(a[0][c], T);
+      if (e0 + c < V && y > -1e30f && !((pen >> c) & 1u))
+        atomicAdd(&S.hist[pz_key(y) >> 21], 1u);
+    }
   }
   __syncthreads();
   if (tid < PZ_WAVE) {
-    // lane l owns bins [32*l, 32*l+32); suffix counts from the top bin down
-    uint32_t own = 0;
-    for (int j = 0; j < 32; j++) own += S.hist[32 * lane + j];
-    uint32_t above = 0;  // count in lanes > l
-    for (int l = PZ_WAVE - 1; l >= 0; l--) {
-      const uint32_t o = __shfl(own, l, PZ_WAVE);
-      if (l > lane) above += o;
-    }
-    const uint32_t total = __shfl(above + own, 0, PZ_WAVE);
-    uint32_t tau = 0;
-    if (total >= (uint32_t)k) {
-      // lane whose range holds the k-th largest: above < k <= above + own
-      const bool mine = above < (uint32_t)k && above + own >= (uint32_t)k;
-      const uint64_t b = __ballot(mine);
-      const int l = __ffsll((long long)b) - 1;
-      if (lane == l) {
-        uint32_t acc = above;
-        int bin = 32 * lane + 31;
-        for (; bin >= 32 * lane; bin--) {
-          acc += S.hist[bin];
-          if (acc >= (uint32_t)k) break;
-        }
-        S.tau_key = (uint32_t)bin << 21;
-      }
-    } else if (lane == 0) {
-      S.tau_key = tau;  // fewer than k valid in the sample: keep every valid value
-    }
+    uint32_t bin = 0, above = 0, cnt = 0;
+    // fewer than k valid in the sample: keep every valid value
+    const bool found = tk_find_bin((tk_lds_u32*)S.hist, (uint32_t)k, bin, above, cnt);
+    tk_publish<DIV>(S, found ? (uint64_t)(bin << 21) << 32 : 0ull, T);
   }
   __syncthreads();
 
-  // ---- 2. stream the row, rescanning with a tighter bound on overflow
+  // ---- 3. stream the row, rescanning with a tighter bound on overflow
+  uint64_t bd;
   for (;;) {
-    tk_stream<BLOCK, VEC>(S, buf, x, V, P, prm);
+    bd = S.thr;
+    TkRaw rb;
+    rb.lo = S.rlo;
+    rb.hi = S.rhi;
+    rb.idmax = S.ridmax;
+    uint64_t lmax = 0ull;
+    if ((uint32_t)bd == 0u)
+      tk_pass<VEC, DIV, false>(S, buf, P, T, x, V, ntiles, a, b, rb, lmax);
+    else
+      tk_pass<VEC, DIV, true>(S, buf, P, T, x, V, ntiles, a, b, rb, lmax);
+    // one LDS atomic per wave for the largest candidate
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint64_t o = __shfl_xor(lmax, off, PZ_WAVE);
+      lmax = o > lmax ? o : lmax;
+    }
+    if (lane == 0 && lmax != 0ull) atomicMax(&S.maxc, lmax);
     __syncthreads();
-    if (!S.over) break;
+    if (S.count <= TOPK_CAP) break;
     // the buffer holds TOPK_CAP >= k candidates of the row: its k-th largest
     // (key, id) bounds the row's k-th largest from below
-    pz_bitonic_desc<BLOCK>(buf, TOPK_CAP);
+    const uint64_t thr = tk_select<BLOCK>(S, buf, TOPK_CAP, k, bd, S.maxc);
+    if (tid < PZ_WAVE) tk_publish<DIV>(S, thr, T);
     if (tid == 0) {
-      const uint64_t c = buf[k - 1];
-      S.tau_key = (uint32_t)(c >> 32);
-      S.tau_nid = (uint32_t)c;
-      S.composite = 1;
       S.count = 0;
-      S.over = 0;
+      S.maxc = 0ull;
     }
+    tk_load<VEC>(x, V, 0, ntiles, a);
     __syncthreads();
   }
 
-  // ---- 3. sort the candidates
+  // ---- 4. the k survivors, in order
   const int n = S.count;
-  int N = 1;
-  while (N < n) N <<= 1;
-  for (int i = n + tid; i < N; i += BLOCK) buf[i] = 0;  // sentinel below any key
+  const uint64_t thr = n > k ? tk_select<BLOCK>(S, buf, n, k, bd, S.maxc) : 0ull;
+  if (tid == 0) S.ntop = 0;
   __syncthreads();
-  pz_bitonic_desc<BLOCK>(buf, N);
+  for (int i = tid; i < n; i += BLOCK) {
+    const uint64_t c = buf[i];
+    if (c >= thr) S.top[atomicAdd(&S.ntop, 1)] = c;
+  }
+  __syncthreads();
+  const int m = S.ntop;  // min(n, k)
+  const pz_lds_u64* res;
+  if (m <= TK_RANK_MAX) {
+    // rank = number of survivors above; all distinct
+    const pz_lds_u64* top = (const pz_lds_u64*)S.top;
+    if (tid < m) {
+      const uint64_t c = top[tid];
+      int rank = 0;
+      for (int j = 0; j < m; j++) rank += top[j] > c ? 1 : 0;
+      buf[rank] = c;
+    }
+    res = buf;
+  } else {
+    int N = 1;
+    while (N < m) N <<= 1;
+    pz_lds_u64* top = (pz_lds_u64*)S.top;
+    for (int i = m + tid; i < N; i += BLOCK) top[i] = 0ull;  // below any key
+    __syncthreads();
+    pz_bitonic_desc<BLOCK>(top, N);
+    res = top;
+  }
+  __syncthreads();
 
-  // ---- 4. softmax over k slots, cut-off and draw (wave 0).  Lane l owns
-  // slots l, l+64, ...: every LDS word of pv is written and read by the same
-  // lane, so no cross-lane LDS ordering is needed.
+  // ---- 5. softmax over k slots, cut-off and draw (wave 0).  pv holds the
+  // probabilities, cv their sequential cumulative sums (the cut-off scan of
+  // top_p.c:80-88 and the draw's cdf add the same terms in the same order).
+  // Lane l owns slots l, l+64, ... of pv; cv is read across lanes only after
+  // the scan that wrote it (same wave, program order).
   if (tid < PZ_WAVE) {
-    float* pv = reinterpret_cast<float*>(S.hist);  // k <= 1024 probabilities
-    const float v0 = n > 0 ? pz_unkey((uint32_t)(buf[0] >> 32)) : -1e30f;
+    tk_lds_f32* pv = (tk_lds_f32*)S.hist;             // k <= 1024 probabilities
+    tk_lds_f32* cv = (tk_lds_f32*)S.hist + TOPK_MAXK;  // and cumulative sums
+    const pz_lds_u64* et = (const pz_lds_u64*)S.etab;
+    const float v0 = m > 0 ? pz_unkey((uint32_t)(res[0] >> 32)) : -1e30f;
     // e_i = expf(v_i - v0), then the sequential sum
     float sum = 0.0f;
     for (int c0 = 0; c0 < k; c0 += PZ_WAVE) {
       const int i = c0 + lane;
       float e = 0.0f;
       if (i < k) {
-        const float v = i < n ? pz_unkey((uint32_t)(buf[i] >> 32)) : -1e30f;
-        e = pz_expf(v - v0);
+        const float v = i < m ? pz_unkey((uint32_t)(res[i] >> 32)) : -1e30f;
+        e = pz_expf_tab(v - v0, et);
         pv[i] = e;
       }
       sum = pz_seq_sum_lanes(sum, e, k - c0);
     }
-    for (int i = lane; i < k; i += PZ_WAVE) pv[i] = pv[i] / sum;
-    const float uu = u[row];
+    float cum = 0.0f;
+    for (int c0 = 0; c0 < k; c0 += PZ_WAVE) {
+      const int i = c0 + lane;
+      float p = 0.0f;
+      if (i < k) p = pv[i] / sum;
+      const float cs = pz_seq_scan_lanes(cum, p, k - c0);
+      if (i < k) {
+        pv[i] = p;
+        cv[i] = cs;
+      }
+      cum = pz_readlane_f(cs, PZ_WAVE - 1);
+    }
+    const float ur = pz_readlane_f(uu, 0);
     const bool chain = prm.top_p > 0.0f && prm.top_p < 1.0f;
     int cutoff = k;
-    float r = uu;
+    float r = ur;
     if (chain) {
-      // cumulative (top_p.c:80-88): first slot with cum >= top_p
-      float cum = 0.0f;
+      // first slot with cum >= top_p; the truncated mass is the sequential
+      // sum of the same slots (top_p.c:91-93), i.e. cum there
       int found = -1;
       for (int c0 = 0; c0 < k && found < 0; c0 += PZ_WAVE) {
         const int i = c0 + lane;
-        const float p = i < k ? pv[i] : 0.0f;
-        const float cs = pz_seq_scan_lanes(cum, p, k - c0);
-        const uint64_t hit = __ballot(i < k && cs >= prm.top_p);
-        if (hit) {
-          const int l = __ffsll((long long)hit) - 1;
-          found = c0 + l;
-          cum = __shfl(cs, l, PZ_WAVE);
-        } else {
-          cum = __shfl(cs, PZ_WAVE - 1, PZ_WAVE);
-        }
+        const uint64_t hit = __ballot(i < k && cv[i] >= prm.top_p);
+        if (hit) found = c0 + __ffsll((long long)hit) - 1;
       }
-      float trunc_sum = cum;  // sequential sum of the same slots (top_p.c:91-93)
       if (found >= 0) cutoff = found + 1;
-      r = uu * trunc_sum;
+      r = ur * cv[cutoff - 1];  // every lane reads the same word
     }
     // draw: first slot < cutoff with r < cdf, else slot 0
-    float cdf = 0.0f;
-    int pick = -1;
-    float p_pick = 0.0f;
-    for (int c0 = 0; c0 < cutoff && pick < 0; c0 += PZ_WAVE) {
+    int pick = 0;
+    for (int c0 = 0; c0 < cutoff; c0 += PZ_WAVE) {
       const int i = c0 + lane;
-      const float p = i < cutoff ? pv[i] : 0.0f;
-      if (c0 == 0) p_pick = __shfl(p, 0, PZ_WAVE);  // fallback slot 0
-      const float cs = pz_seq_scan_lanes(cdf, p, cutoff - c0);
-      const uint64_t hit = __ballot(i < cutoff && r < cs);
+      const uint64_t hit = __ballot(i < cutoff && r < cv[i]);
       if (hit) {
-        const int l = __ffsll((long long)hit) - 1;
-        pick = c0 + l;
-        p_pick = __shfl(p, l, PZ_WAVE);
-      } else {
-        cdf = __shfl(cs, PZ_WAVE - 1, PZ_WAVE);
+        pick = c0 + __ffsll((long long)hit) - 1;
+        break;
       }
     }
-    if (pick < 0) pick = 0;
     if (lane == 0) {
-      const int id = pick < n ? (int)(0xffffffffu - (uint32_t)buf[pick]) : -1;
-      ids_out[row] = id;
-      if (p_out) p_out[row] = p_pick;
+      ids_out[row] = pick < m ? id_of(res[pick]) : -1;
+      if (p_out) p_out[row] = pv[pick];
     }
   }
 }
 
 }  // namespace
 
-template <bool VEC>
+template <bool VEC, bool DIV>
 static int launch_topk_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   const size_t pen = L.pen_any ? (pz_penalty_lds_bytes(L.V, L.hcap) + 15) & ~(size_t)15 : 0;
   const size_t lds = pen + (size_t)TOPK_CAP * 8;
   if ((int)(lds + sizeof(TopkShared)) > L.max_lds) return -2;
-  auto kern = k_topk<TOPK_BLOCK, VEC>;
+  auto kern = k_topk<TOPK_BLOCK, VEC, DIV>;
   if (lds > 65536 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                           (int)lds) != hipSuccess)
@@ -316,5 +572,9 @@ static int launch_topk_t(const pz_launch& L, int n_rows, const int32_t* d_rows) 
 int pz_launch_topk(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (n_rows <= 0) return 0;
   const bool vec = (L.ld % 4 == 0) && (((uintptr_t)L.logits & 15) == 0);
-  return vec ? launch_topk_t<true>(L, n_rows, d_rows) : launch_topk_t<false>(L, n_rows, d_rows);
+  if (L.temp_div)
+    return vec ? launch_topk_t<true, true>(L, n_rows, d_rows)
+               : launch_topk_t<false, true>(L, n_rows, d_rows);
+  return vec ? launch_topk_t<true, false>(L, n_rows, d_rows)
+             : launch_topk_t<false, false>(L, n_rows, d_rows);
 }
