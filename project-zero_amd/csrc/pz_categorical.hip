@@ -37,6 +37,9 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
     const float* __restrict__ u, int32_t* __restrict__ ids_out, float* __restrict__ p_out) {
   extern __shared__ __align__(16) char lds[];
   __shared__ CatShared S;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);  // ordered by pz_pass1's barriers
   const int row = pz_row_of(rows, blockIdx.x);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const int tid = threadIdx.x;
@@ -64,6 +67,7 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
   X.thr = -__builtin_inff();
   X.inv = 1.0f;
   X.as_p = false;
+  X.et = et;
   const float sum = pz_exact_sum(X, ntiles, REC, S.r);
   const float inv = 1.0f / sum;  // softmax.c:19-22
   X.inv = inv;
@@ -80,7 +84,7 @@ __global__ __launch_bounds__(PZ_RB) void k_categorical(
 #pragma unroll
       for (int c = 1; c < 4; c++)
         if (e0 + c == id) y = yy[c];
-      p_out[row] = pz_expf(y - M) * inv;
+      p_out[row] = pz_expf_l(y - M, et) * inv;
     }
   }
 }

@@ -84,6 +84,20 @@ __device__ __forceinline__ float pz_expf_tab(float x, Tab tab) {
 
 __device__ __forceinline__ float pz_expf_inline(float x) { return pz_expf_tab(x, pz_exp2_tab); }
 
+typedef __attribute__((address_space(3))) uint64_t pz_lds_u64;
+
+// A workgroup's LDS copy of the table (read at LDS latency instead of a
+// global-memory round trip on the serial paths).  Threads 0..31 fill it; the
+// caller puts a barrier between the fill and the first use.
+__device__ __forceinline__ void pz_etab_fill(pz_lds_u64* t) {
+  if (threadIdx.x < 32) t[threadIdx.x] = pz_exp2_tab[threadIdx.x];
+}
+
+// Out of line, with the table in LDS.
+__device__ __noinline__ float pz_expf_l(float x, const pz_lds_u64* tab) {
+  return pz_expf_tab(x, tab);
+}
+
 // Out of line: the exact exponential sits on paths that are rare next to the
 // streaming passes, and inlining it into every one of them multiplies the
 // kernels' code size beyond the instruction cache.

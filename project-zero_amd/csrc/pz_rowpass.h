@@ -433,9 +433,10 @@ struct PzExpTerms {
   Row R;
   float M, thr, inv;
   bool as_p;
+  const pz_lds_u64* et;  // the workgroup's LDS copy of the expf table
   __device__ __forceinline__ int load(int e0, Raw& r) const { return R.load(e0, r); }
   __device__ __forceinline__ float exact_term(float y) const {
-    const float e = y >= thr ? pz_expf(y - M) : 0.0f;
+    const float e = y >= thr ? pz_expf_l(y - M, et) : 0.0f;
     return as_p ? e * inv : e;
   }
   __device__ __forceinline__ void prep(int e0, int n, Raw& r, float (&a)[4]) const {

@@ -37,6 +37,9 @@ __global__ __launch_bounds__(PZ_RB) void k_softmax(const float* in, long ld_in, 
                                                    long ld_out, int V, PzTemp T) {
   extern __shared__ __align__(16) char lds[];
   __shared__ SoftmaxShared S;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);  // ordered by pz_pass1's barriers
   const int row = blockIdx.x, tid = threadIdx.x;
   PzTempRow<VEC> R;
   R.x = in + (long)row * ld_in;
@@ -57,6 +60,7 @@ __global__ __launch_bounds__(PZ_RB) void k_softmax(const float* in, long ld_in, 
   X.thr = -__builtin_inff();
   X.inv = 1.0f;
   X.as_p = false;
+  X.et = et;
   const float inv = 1.0f / pz_exact_sum(X, ntiles, REC, S.r);
   // every read of the row is done: the write pass may overwrite it (in == out)
   for (int t = 0; t < ntiles; t++) {
@@ -65,7 +69,7 @@ __global__ __launch_bounds__(PZ_RB) void k_softmax(const float* in, long ld_in, 
     const int n = R.get(e0, y);
 #pragma unroll
     for (int c = 0; c < 4; c++)
-      if (c < n) o[e0 + c] = pz_expf_inline(y[c] - M) * inv;
+      if (c < n) o[e0 + c] = pz_expf_tab(y[c] - M, et) * inv;
   }
 }
 

@@ -3,7 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-typedef __attribute__((address_space(3))) uint64_t pz_lds_u64;
+#include "pz_device.h"
+
 
 // Descending bitonic sort of buf[0..N) (N a power of two) by all BLOCK
 // threads of the workgroup.  buf is an LDS (pz_lds_u64*) or global

@@ -42,6 +42,8 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_rows(
     int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
   extern __shared__ __align__(16) char lds[];
   __shared__ SpecRowsShared S;
+  __shared__ uint64_t etab[32];
+  pz_etab_fill((pz_lds_u64*)etab);  // ordered by pz_pass1's barriers
   const int q = blockIdx.x, tid = threadIdx.x;
   const int NT = B * KT;
   PzTempRow<VEC> R;
@@ -61,6 +63,7 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_rows(
     X.thr = -__builtin_inff();
     X.inv = 1.0f;
     X.as_p = false;
+    X.et = (const pz_lds_u64*)etab;
     inv = 1.0f / pz_exact_sum(X, ntiles, REC, S.r);
   }
   if (tid == 0) {
@@ -72,8 +75,9 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_rows(
 
 // p(x) of one element of a row whose softmax statistics are (M, inv).
 template <bool VEC>
-__device__ __forceinline__ float prob_at(const PzTempRow<VEC>& R, int x, float M, float inv) {
-  return pz_expf(R.T.apply(R.x[x]) - M) * inv;
+__device__ __forceinline__ float prob_at(const PzTempRow<VEC>& R, int x, float M, float inv,
+                                        const pz_lds_u64* et) {
+  return pz_expf_l(R.T.apply(R.x[x]) - M, et) * inv;
 }
 
 // Residual terms r(x) = max(0, p(x) - q(x)) of a target/draft row pair,
@@ -87,6 +91,7 @@ struct ResidualTerms {
   PzTempRow<VEC> T, D;
   float MT, invT, MD, invD;
   int lastpos;
+  const pz_lds_u64* et;  // the workgroup's LDS copy of the expf table
   __device__ __forceinline__ int load(int e0, Raw& r) const {
     T.load(e0, r.t);
     return D.load(e0, r.d);
@@ -98,8 +103,8 @@ struct ResidualTerms {
     for (int c = 0; c < 4; c++) {
       float res = 0.0f;
       if (c < n) {
-        const float p = pz_expf_inline(r.t[c] - MT) * invT;
-        const float qq = pz_expf_inline(r.d[c] - MD) * invD;
+        const float p = pz_expf_tab(r.t[c] - MT, et) * invT;
+        const float qq = pz_expf_tab(r.d[c] - MD, et) * invD;
         const float t = p - qq;
         res = t > 0.0f ? t : 0.0f;
       }
@@ -159,6 +164,10 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
     int32_t* __restrict__ acc_len, int32_t* __restrict__ ids_out) {
   extern __shared__ __align__(16) char lds[];
   __shared__ SpecVerifyShared S;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  __syncthreads();
   const int b = blockIdx.x, tid = threadIdx.x;
   const int NT = B * KT;
   const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
@@ -175,8 +184,8 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
       if (d >= 0 && d < V) {
         PzTempRow<VEC> RT{target + (long)qt * ld, V, TT};
         PzTempRow<VEC> RD{draft + (long)(qd - NT) * ld, V, TT};
-        const float pd = prob_at(RT, d, stats[4 * qt], stats[4 * qt + 1]);
-        const float qv = prob_at(RD, d, stats[4 * qd], stats[4 * qd + 1]);
+        const float pd = prob_at(RT, d, stats[4 * qt], stats[4 * qt + 1], et);
+        const float qv = prob_at(RD, d, stats[4 * qd], stats[4 * qd + 1], et);
         accept = qv > 0.0f && u_acc[b * K + j] < pd / qv;
       }
       if (!accept) break;
@@ -205,6 +214,7 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
       X.MD = stats[4 * qd];
       X.invD = stats[4 * qd + 1];
       X.lastpos = -1;
+      X.et = et;
       pz_record_pass(X, ntiles, REC, S.r, __builtin_inff());
       if (X.lastpos > 0) atomicMax(&S.last, X.lastpos);
       if (tid < 64) {
@@ -244,6 +254,7 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_verify(
     X.thr = -__builtin_inff();
     X.inv = stats[4 * cat_row + 1];
     X.as_p = true;
+    X.et = et;
     const int hit = pz_exact_draw(X, V, ntiles, ur, REC, S.r);
     tok = hit >= 0 ? hit : V - 1;
   }

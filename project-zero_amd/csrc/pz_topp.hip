@@ -156,6 +156,9 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
   extern __shared__ __align__(16) char lds[];
   __shared__ ToppShared S;
   __shared__ PzRecShared RS;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);  // ordered by pz_pass1's barriers
   const int row = pz_row_of(rows, blockIdx.x);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -217,6 +220,7 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
   X.thr = thr;
   X.inv = 1.0f;
   X.as_p = false;
+  X.et = et;
   X.ehist = ehist;
   pz_record_pass(X, ntiles, REC, RS, __builtin_inff());
 
@@ -303,7 +307,7 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
           bool want = c < nv[uu] && yy >= thr && (yy - M) >= dgate;
           uint64_t key = 0;
           if (want) {
-            const float p = pz_expf(yy - M) * inv;
+            const float p = pz_expf_l(yy - M, et) * inv;
             want = p >= p_thr;
             key = topp_key(p, e0 + c);
           }
@@ -347,6 +351,10 @@ __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
     int32_t* __restrict__ ids_out, float* __restrict__ p_out, pz_scratch sc) {
   extern __shared__ __align__(16) char lds[];
   __shared__ int count, over, cutoff_sh;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  __syncthreads();
   const int tid = threadIdx.x;
   const int n_fb = sc.counters[0];
   uint64_t* keys = sc.fb_keys + (size_t)blockIdx.x * sc.slot_n;
@@ -376,7 +384,7 @@ __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
       for (int c = 0; c < 4; c++) {
         const bool want = c < n && y[c] >= thr;
         uint64_t key = 0;
-        if (want) key = topp_key(pz_expf(y[c] - M) * inv, e0 + c);
+        if (want) key = topp_key(pz_expf_l(y[c] - M, et) * inv, e0 + c);
         append_key(&count, &over, keys, sc.slot_n, want, key);
       }
     }
