@@ -26,17 +26,26 @@ struct CompatCtx {
   pz_sampler* s = nullptr;
   int vmax = 0;
   float* d_row = nullptr;
-  float* d_u = nullptr;
-  int32_t* d_id = nullptr;
+  // the uniform in and the id out: coherent pinned host memory the kernels
+  // use directly (z_*: the device's addresses of the same words)
+  float* h_u = nullptr;
+  int32_t* h_id = nullptr;
+  const float* z_u = nullptr;
+  int32_t* z_id = nullptr;
   int temp_mode = PZ_TEMP_MUL_RECIP;
   int status = PZ_OK;
+  void release() {
+    (void)hipFree(d_row);
+    (void)hipHostFree(h_u);
+    (void)hipHostFree(h_id);
+    d_row = nullptr;
+    h_u = nullptr;
+    h_id = nullptr;
+    pz_sampler_destroy(s);
+    s = nullptr;
+  }
   ~CompatCtx() {
-    if (s) {
-      (void)hipFree(d_row);
-      (void)hipFree(d_u);
-      (void)hipFree(d_id);
-      pz_sampler_destroy(s);
-    }
+    if (s) release();
   }
 };
 
@@ -53,20 +62,22 @@ int ensure(int V) {
   if (c.s && V <= c.vmax) return PZ_OK;
   int vmax = c.vmax > 0 ? c.vmax : 1;
   while (vmax < V) vmax *= 2;
-  if (c.s) {
-    (void)hipFree(c.d_row);
-    (void)hipFree(c.d_u);
-    (void)hipFree(c.d_id);
-    pz_sampler_destroy(c.s);
-    c.s = nullptr;
-  }
+  if (c.s) c.release();
+  c.vmax = 0;
   int rc = pz_sampler_create(&c.s, 1, vmax, 0, compat_device());
   if (rc != PZ_OK) return rc;
   pz_sampler_set_temp_mode(c.s, c.temp_mode);
+  const unsigned zc = hipHostMallocMapped | hipHostMallocCoherent;
+  void *zu = nullptr, *zi = nullptr;
   if (hipMalloc((void**)&c.d_row, (size_t)vmax * sizeof(float)) != hipSuccess ||
-      hipMalloc((void**)&c.d_u, sizeof(float)) != hipSuccess ||
-      hipMalloc((void**)&c.d_id, sizeof(int32_t)) != hipSuccess)
+      hipHostMalloc((void**)&c.h_u, sizeof(float), zc) != hipSuccess ||
+      hipHostMalloc((void**)&c.h_id, sizeof(int32_t), zc) != hipSuccess)
     return PZ_ENOMEM;
+  if (hipHostGetDevicePointer(&zu, c.h_u, 0) != hipSuccess ||
+      hipHostGetDevicePointer(&zi, c.h_id, 0) != hipSuccess)
+    return PZ_EDEVICE;
+  c.z_u = static_cast<const float*>(zu);
+  c.z_id = static_cast<int32_t*>(zi);
   c.vmax = vmax;
   return PZ_OK;
 }
@@ -79,9 +90,9 @@ int run_row(const float* logits, int V, int mode, float temperature, int top_k, 
   c.status = ensure(V);
   if (c.status != PZ_OK) return -1;
   pz_sampler* s = c.s;
+  *c.h_u = u;  // the previous call drained the stream
   if (hipMemcpyAsync(c.d_row, logits, (size_t)V * sizeof(float), hipMemcpyHostToDevice,
-                     s->stream) != hipSuccess ||
-      hipMemcpyAsync(c.d_u, &u, sizeof(float), hipMemcpyHostToDevice, s->stream) != hipSuccess) {
+                     s->stream) != hipSuccess) {
     c.status = PZ_EDEVICE;
     return -1;
   }
@@ -94,15 +105,11 @@ int run_row(const float* logits, int V, int mode, float temperature, int top_k, 
   p.top_k = top_k;
   p.top_p = top_p;
   p.rep_penalty = 1.0f;
-  c.status = pz_dispatch_resolved(s, c.d_row, 1, V, V, 1, nullptr, 0, false, false, c.d_u,
-                                  c.d_id, nullptr);
-  int32_t id = -1;
-  if (c.status == PZ_OK &&
-      (hipMemcpyAsync(&id, c.d_id, sizeof(int32_t), hipMemcpyDeviceToHost, s->stream) !=
-           hipSuccess ||
-       hipStreamSynchronize(s->stream) != hipSuccess))
-    c.status = PZ_EDEVICE;
-  return c.status == PZ_OK ? id : -1;
+  c.status = pz_dispatch_resolved(s, c.d_row, 1, V, V, 1, nullptr, 0, false, false, c.z_u,
+                                  c.z_id, nullptr);
+  // drained on every path: the next call rewrites h_u
+  if (hipStreamSynchronize(s->stream) != hipSuccess && c.status == PZ_OK) c.status = PZ_EDEVICE;
+  return c.status == PZ_OK ? *c.h_id : -1;
 }
 
 // In-place row operation: copy in, op, copy back.

@@ -258,11 +258,14 @@ __device__ __forceinline__ int pz_wave_accumulate(PzAcc& st, const float (&v)[C]
     const int idx = L * C + cL;
     st.n = pz_readlane_u32(ev_n, L);
     if (kind == 2) return idx;
-    float vv = v[0];
+    // term cL of lane L: read every c and select (an index into v[] by the
+    // run-time cL would put the array in scratch memory)
+    float vv = pz_readlane_f32(v[0], L);
 #pragma unroll
-    for (int c = 1; c < C; c++)
-      if (c == cL) vv = v[c];
-    vv = pz_readlane_f32(vv, L);
+    for (int c = 1; c < C; c++) {
+      const float vc = pz_readlane_f32(v[c], L);
+      vv = c == cL ? vc : vv;
+    }
     st = pz_acc_add(st, vv);
     const float sv = pz_acc_value(st);
     if (cum && lane == 0) cum[idx] = sv;

@@ -456,21 +456,23 @@ struct PzExpTerms {
     const uint32_t i = pz_inc_from_estimate(a[c], g, &ex);
     return ex ? pz_inc(exact_term(y[c]), g, cls) : i;
   }
+  // The cache keeps the exact terms, evaluated here by the segment's whole
+  // wave in the parallel pass, so the serial walk only reads them.
   __device__ __forceinline__ void cache_put(pz_lds_f32* base, const Raw& y,
                                             const float (&)[4]) const {
     pz_f4 q;
-    q.x = y[0];
-    q.y = y[1];
-    q.z = y[2];
-    q.w = y[3];
+    q.x = exact_term(y[0]);
+    q.y = exact_term(y[1]);
+    q.z = exact_term(y[2]);
+    q.w = exact_term(y[3]);
     ((pz_lds_f4*)base)[threadIdx.x & 63] = q;
   }
   __device__ __forceinline__ void cache_terms(const pz_lds_f32* base, float (&v)[4]) const {
     const pz_f4 q = ((const pz_lds_f4*)base)[threadIdx.x & 63];
-    v[0] = exact_term(q.x);
-    v[1] = exact_term(q.y);
-    v[2] = exact_term(q.z);
-    v[3] = exact_term(q.w);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
   }
   __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
     Raw r;

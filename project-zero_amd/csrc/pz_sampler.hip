@@ -35,7 +35,7 @@ int next_pow2(int v) {
 size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* out) {
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   int vt = max_vocab < PZ_TOPP_MAX_V ? max_vocab : PZ_TOPP_MAX_V;
-  int slot = 64;  // >= one wave's group of running sums
+  int slot = 256;  // >= one call of the cut-off walk (64 lanes x 4 running sums)
   while (slot < vt) slot <<= 1;
   const size_t B = (size_t)max_batch;
   size_t off = 0;
@@ -81,17 +81,23 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   if (hipEventCreateWithFlags(&s->staged, hipEventDisableTiming) != hipSuccess)
     return bail(PZ_EDEVICE);
   const size_t B = (size_t)max_batch;
+  const unsigned zc = hipHostMallocMapped | hipHostMallocCoherent;
   if (hipHostMalloc((void**)&s->h_params, B * sizeof(pz_row_params_dev), 0) != hipSuccess ||
       hipHostMalloc((void**)&s->h_rows, B * sizeof(int32_t), 0) != hipSuccess ||
-      hipHostMalloc((void**)&s->h_u, B * sizeof(float), 0) != hipSuccess ||
-      hipHostMalloc((void**)&s->h_ids, B * sizeof(int32_t), 0) != hipSuccess ||
-      hipHostMalloc((void**)&s->h_p, B * sizeof(float), 0) != hipSuccess)
+      hipHostMalloc((void**)&s->h_u, B * sizeof(float), zc) != hipSuccess ||
+      hipHostMalloc((void**)&s->h_ids, B * sizeof(int32_t), zc) != hipSuccess ||
+      hipHostMalloc((void**)&s->h_p, B * sizeof(float), zc) != hipSuccess)
     return bail(PZ_ENOMEM);
+  void *zu = nullptr, *zi = nullptr, *zp = nullptr;
+  if (hipHostGetDevicePointer(&zu, s->h_u, 0) != hipSuccess ||
+      hipHostGetDevicePointer(&zi, s->h_ids, 0) != hipSuccess ||
+      hipHostGetDevicePointer(&zp, s->h_p, 0) != hipSuccess)
+    return bail(PZ_EDEVICE);
+  s->z_u = static_cast<const float*>(zu);
+  s->z_ids = static_cast<int32_t*>(zi);
+  s->z_p = static_cast<float*>(zp);
   if (hipMalloc((void**)&s->d_params, B * sizeof(pz_row_params_dev)) != hipSuccess ||
-      hipMalloc((void**)&s->d_rows, B * sizeof(int32_t)) != hipSuccess ||
-      hipMalloc((void**)&s->d_u, B * sizeof(float)) != hipSuccess ||
-      hipMalloc((void**)&s->d_ids, B * sizeof(int32_t)) != hipSuccess ||
-      hipMalloc((void**)&s->d_p, B * sizeof(float)) != hipSuccess)
+      hipMalloc((void**)&s->d_rows, B * sizeof(int32_t)) != hipSuccess)
     return bail(PZ_ENOMEM);
   s->res_params = new (std::nothrow) pz_row_params_dev[B];
   if (!s->res_params) return bail(PZ_ENOMEM);
@@ -108,9 +114,6 @@ extern "C" void pz_sampler_destroy(pz_sampler* s) {
   if (s->stream) (void)hipStreamSynchronize(s->stream);
   (void)hipFree(s->d_params);
   (void)hipFree(s->d_rows);
-  (void)hipFree(s->d_u);
-  (void)hipFree(s->d_ids);
-  (void)hipFree(s->d_p);
   (void)hipFree(s->d_scratch);
   (void)hipFree(s->spec_dev);
   (void)hipHostFree(s->spec_host);
@@ -305,22 +308,19 @@ extern "C" int pz_sample_batch(pz_sampler* s, const float* d_logits, int B, int 
   if (B > s->max_batch) return fail(s, PZ_ERANGE, "B=%d > max_batch=%d", B, s->max_batch);
   if (B <= 0) return B == 0 ? PZ_OK : fail(s, PZ_EINVAL, "B<0");
   PZ_HIP(s, hipSetDevice(s->device));
+  // Every synchronous call ends with the stream drained, and asynchronous
+  // calls never touch h_u / h_ids / h_p: the buffers are free here.
   const float* d_u = nullptr;
   if (u) {
-    PZ_HIP(s, hipStreamSynchronize(s->stream));  // h_u may still be in flight
     memcpy(s->h_u, u, (size_t)B * sizeof(float));
-    PZ_HIP(s, hipMemcpyAsync(s->d_u, s->h_u, (size_t)B * sizeof(float),
-                             hipMemcpyHostToDevice, s->stream));
-    d_u = s->d_u;
+    d_u = s->z_u;
   }
-  int rc = dispatch(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u, s->d_ids,
-                    p_out ? s->d_p : nullptr);
-  if (rc != PZ_OK) return rc;
-  PZ_HIP(s, hipMemcpyAsync(s->h_ids, s->d_ids, (size_t)B * sizeof(int32_t),
-                           hipMemcpyDeviceToHost, s->stream));
-  if (p_out)
-    PZ_HIP(s, hipMemcpyAsync(s->h_p, s->d_p, (size_t)B * sizeof(float),
-                             hipMemcpyDeviceToHost, s->stream));
+  int rc = dispatch(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u, s->z_ids,
+                    p_out ? s->z_p : nullptr);
+  if (rc != PZ_OK) {
+    (void)hipStreamSynchronize(s->stream);  // kernels already queued may use the buffers
+    return rc;
+  }
   PZ_HIP(s, hipStreamSynchronize(s->stream));
   memcpy(ids_out, s->h_ids, (size_t)B * sizeof(int32_t));
   if (p_out) memcpy(p_out, s->h_p, (size_t)B * sizeof(float));

@@ -22,12 +22,15 @@ struct pz_sampler {
   pz_row_params_dev* d_params = nullptr;
   int32_t* h_rows = nullptr;
   int32_t* d_rows = nullptr;
+  // uniforms in, ids and p out of the synchronous call: coherent pinned host
+  // memory that the kernels read and write directly (z_*: the device's
+  // addresses of the same buffers), so a call needs no copy commands
   float* h_u = nullptr;
-  float* d_u = nullptr;
+  const float* z_u = nullptr;
   int32_t* h_ids = nullptr;
-  int32_t* d_ids = nullptr;
+  int32_t* z_ids = nullptr;
   float* h_p = nullptr;
-  float* d_p = nullptr;
+  float* z_p = nullptr;
 
   void* d_scratch = nullptr;
   size_t scratch_bytes = 0;

@@ -5,7 +5,6 @@
 
 #include "pz_device.h"
 
-
 // Descending bitonic sort of buf[0..N) (N a power of two) by all BLOCK
 // threads of the workgroup.  buf is an LDS (pz_lds_u64*) or global
 // (uint64_t*) pointer; global buffers must be owned by the workgroup (every

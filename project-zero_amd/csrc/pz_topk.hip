@@ -352,6 +352,115 @@ __device__ __forceinline__ void tk_pass(TopkShared& S, pz_lds_u64* buf, const Pz
   tk_drain(b);
 }
 
+// The k survivors of buf[0..n) (distinct candidates in [base, maxc]) in
+// order, then the k-slot softmax, top-p cut-off and draw of row `row` (wave
+// 0; uu is the row's uniform in thread 0).  Every thread calls it.
+template <int BLOCK>
+__device__ __forceinline__ void tk_finish(TopkShared& S, pz_lds_u64* buf, int n, int k,
+                                          uint64_t base, uint64_t maxc,
+                                          const pz_row_params_dev& prm, float uu, int row,
+                                          int32_t* __restrict__ ids_out,
+                                          float* __restrict__ p_out) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (PZ_WAVE - 1);
+  const uint64_t thr = n > k ? tk_select<BLOCK>(S, buf, n, k, base, maxc) : 0ull;
+  if (tid == 0) S.ntop = 0;
+  __syncthreads();
+  for (int i = tid; i < n; i += BLOCK) {
+    const uint64_t c = buf[i];
+    if (c >= thr) S.top[atomicAdd(&S.ntop, 1)] = c;
+  }
+  __syncthreads();
+  const int m = S.ntop;  // min(n, k)
+  const pz_lds_u64* res;
+  if (m <= TK_RANK_MAX) {
+    // rank = number of survivors above; all distinct
+    const pz_lds_u64* top = (const pz_lds_u64*)S.top;
+    if (tid < m) {
+      const uint64_t c = top[tid];
+      int rank = 0;
+      for (int j = 0; j < m; j++) rank += top[j] > c ? 1 : 0;
+      buf[rank] = c;
+    }
+    res = buf;
+  } else {
+    int N = 1;
+    while (N < m) N <<= 1;
+    pz_lds_u64* top = (pz_lds_u64*)S.top;
+    for (int i = m + tid; i < N; i += BLOCK) top[i] = 0ull;  // below any key
+    __syncthreads();
+    pz_bitonic_desc<BLOCK>(top, N);
+    res = top;
+  }
+  __syncthreads();
+
+  // ---- 5. softmax over k slots, cut-off and draw (wave 0).  pv holds the
+  // probabilities, cv their sequential cumulative sums (the cut-off scan of
+  // top_p.c:80-88 and the draw's cdf add the same terms in the same order).
+  // Lane l owns slots l, l+64, ... of pv; cv is read across lanes only after
+  // the scan that wrote it (same wave, program order).
+  if (tid < PZ_WAVE) {
+    tk_lds_f32* pv = (tk_lds_f32*)S.hist;             // k <= 1024 probabilities
+    tk_lds_f32* cv = (tk_lds_f32*)S.hist + TOPK_MAXK;  // and cumulative sums
+    const pz_lds_u64* et = (const pz_lds_u64*)S.etab;
+    const float v0 = m > 0 ? pz_unkey((uint32_t)(res[0] >> 32)) : -1e30f;
+    // e_i = expf(v_i - v0), then the sequential sum
+    float sum = 0.0f;
+    for (int c0 = 0; c0 < k; c0 += PZ_WAVE) {
+      const int i = c0 + lane;
+      float e = 0.0f;
+      if (i < k) {
+        const float v = i < m ? pz_unkey((uint32_t)(res[i] >> 32)) : -1e30f;
+        e = pz_expf_tab(v - v0, et);
+        pv[i] = e;
+      }
+      sum = pz_seq_sum_lanes(sum, e, k - c0);
+    }
+    float cum = 0.0f;
+    for (int c0 = 0; c0 < k; c0 += PZ_WAVE) {
+      const int i = c0 + lane;
+      float p = 0.0f;
+      if (i < k) p = pv[i] / sum;
+      const float cs = pz_seq_scan_lanes(cum, p, k - c0);
+      if (i < k) {
+        pv[i] = p;
+        cv[i] = cs;
+      }
+      cum = pz_readlane_f(cs, PZ_WAVE - 1);
+    }
+    const float ur = pz_readlane_f(uu, 0);
+    const bool chain = prm.top_p > 0.0f && prm.top_p < 1.0f;
+    int cutoff = k;
+    float r = ur;
+    if (chain) {
+      // first slot with cum >= top_p; the truncated mass is the sequential
+      // sum of the same slots (top_p.c:91-93), i.e. cum there
+      int found = -1;
+      for (int c0 = 0; c0 < k && found < 0; c0 += PZ_WAVE) {
+        const int i = c0 + lane;
+        const uint64_t hit = __ballot(i < k && cv[i] >= prm.top_p);
+        if (hit) found = c0 + __ffsll((long long)hit) - 1;
+      }
+      if (found >= 0) cutoff = found + 1;
+      r = ur * cv[cutoff - 1];  // every lane reads the same word
+    }
+    // draw: first slot < cutoff with r < cdf, else slot 0
+    int pick = 0;
+    for (int c0 = 0; c0 < cutoff; c0 += PZ_WAVE) {
+      const int i = c0 + lane;
+      const uint64_t hit = __ballot(i < cutoff && r < cv[i]);
+      if (hit) {
+        pick = c0 + __ffsll((long long)hit) - 1;
+        break;
+      }
+    }
+    if (lane == 0) {
+      ids_out[row] = pick < m ? id_of(res[pick]) : -1;
+      if (p_out) p_out[row] = pv[pick];
+    }
+  }
+}
+
 template <int BLOCK, bool VEC, bool DIV>
 __global__ __launch_bounds__(BLOCK) void k_topk(
     const float* __restrict__ logits, long ld, int V, const int32_t* __restrict__ rows,
@@ -451,105 +560,11 @@ __global__ __launch_bounds__(BLOCK) void k_topk(
     __syncthreads();
   }
 
-  // ---- 4. the k survivors, in order
-  const int n = S.count;
-  const uint64_t thr = n > k ? tk_select<BLOCK>(S, buf, n, k, bd, S.maxc) : 0ull;
-  if (tid == 0) S.ntop = 0;
-  __syncthreads();
-  for (int i = tid; i < n; i += BLOCK) {
-    const uint64_t c = buf[i];
-    if (c >= thr) S.top[atomicAdd(&S.ntop, 1)] = c;
-  }
-  __syncthreads();
-  const int m = S.ntop;  // min(n, k)
-  const pz_lds_u64* res;
-  if (m <= TK_RANK_MAX) {
-    // rank = number of survivors above; all distinct
-    const pz_lds_u64* top = (const pz_lds_u64*)S.top;
-    if (tid < m) {
-      const uint64_t c = top[tid];
-      int rank = 0;
-      for (int j = 0; j < m; j++) rank += top[j] > c ? 1 : 0;
-      buf[rank] = c;
-    }
-    res = buf;
-  } else {
-    int N = 1;
-    while (N < m) N <<= 1;
-    pz_lds_u64* top = (pz_lds_u64*)S.top;
-    for (int i = m + tid; i < N; i += BLOCK) top[i] = 0ull;  // below any key
-    __syncthreads();
-    pz_bitonic_desc<BLOCK>(top, N);
-    res = top;
-  }
-  __syncthreads();
-
-  // ---- 5. softmax over k slots, cut-off and draw (wave 0).  pv holds the
-  // probabilities, cv their sequential cumulative sums (the cut-off scan of
-  // top_p.c:80-88 and the draw's cdf add the same terms in the same order).
-  // Lane l owns slots l, l+64, ... of pv; cv is read across lanes only after
-  // the scan that wrote it (same wave, program order).
-  if (tid < PZ_WAVE) {
-    tk_lds_f32* pv = (tk_lds_f32*)S.hist;             // k <= 1024 probabilities
-    tk_lds_f32* cv = (tk_lds_f32*)S.hist + TOPK_MAXK;  // and cumulative sums
-    const pz_lds_u64* et = (const pz_lds_u64*)S.etab;
-    const float v0 = m > 0 ? pz_unkey((uint32_t)(res[0] >> 32)) : -1e30f;
-    // e_i = expf(v_i - v0), then the sequential sum
-    float sum = 0.0f;
-    for (int c0 = 0; c0 < k; c0 += PZ_WAVE) {
-      const int i = c0 + lane;
-      float e = 0.0f;
-      if (i < k) {
-        const float v = i < m ? pz_unkey((uint32_t)(res[i] >> 32)) : -1e30f;
-        e = pz_expf_tab(v - v0, et);
-        pv[i] = e;
-      }
-      sum = pz_seq_sum_lanes(sum, e, k - c0);
-    }
-    float cum = 0.0f;
-    for (int c0 = 0; c0 < k; c0 += PZ_WAVE) {
-      const int i = c0 + lane;
-      float p = 0.0f;
-      if (i < k) p = pv[i] / sum;
-      const float cs = pz_seq_scan_lanes(cum, p, k - c0);
-      if (i < k) {
-        pv[i] = p;
-        cv[i] = cs;
-      }
-      cum = pz_readlane_f(cs, PZ_WAVE - 1);
-    }
-    const float ur = pz_readlane_f(uu, 0);
-    const bool chain = prm.top_p > 0.0f && prm.top_p < 1.0f;
-    int cutoff = k;
-    float r = ur;
-    if (chain) {
-      // first slot with cum >= top_p; the truncated mass is the sequential
-      // sum of the same slots (top_p.c:91-93), i.e. cum there
-      int found = -1;
-      for (int c0 = 0; c0 < k && found < 0; c0 += PZ_WAVE) {
-        const int i = c0 + lane;
-        const uint64_t hit = __ballot(i < k && cv[i] >= prm.top_p);
-        if (hit) found = c0 + __ffsll((long long)hit) - 1;
-      }
-      if (found >= 0) cutoff = found + 1;
-      r = ur * cv[cutoff - 1];  // every lane reads the same word
-    }
-    // draw: first slot < cutoff with r < cdf, else slot 0
-    int pick = 0;
-    for (int c0 = 0; c0 < cutoff; c0 += PZ_WAVE) {
-      const int i = c0 + lane;
-      const uint64_t hit = __ballot(i < cutoff && r < cv[i]);
-      if (hit) {
-        pick = c0 + __ffsll((long long)hit) - 1;
-        break;
-      }
-    }
-    if (lane == 0) {
-      ids_out[row] = pick < m ? id_of(res[pick]) : -1;
-      if (p_out) p_out[row] = pv[pick];
-    }
-  }
+  // ---- 4./5. the k survivors in order, softmax, cut-off and draw
+  tk_finish<BLOCK>(S, buf, S.count, k, bd, S.maxc, prm, uu, row, ids_out, p_out);
 }
+
+
 
 }  // namespace
 

@@ -282,37 +282,53 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
   bool fallback = S.nsel > (uint32_t)cap;
   if (!fallback) {
     // ---- pass 3: gather every candidate with p >= p_thr (a prefix of the
-    // (p desc, id asc) order) into LDS
+    // (p desc, id asc) order) into LDS.  A cheap gate on y - M picks the
+    // lanes' possible candidates (a superset: 0.01 below the bin edge); the
+    // exact p of those is evaluated one candidate per lane per trip, and the
+    // survivors are appended with one LDS atomic per wave per trip.
     const float e_lo = ebin_lo(S.bsel);
     const float p_thr = all ? 0.0f : e_lo * inv;
     const float dgate = all ? -__builtin_inff() : __logf(e_lo) - 0.01f;
-    constexpr int U2 = 4;
+    constexpr int U2 = 8;
     for (int t0 = 0; t0 < ntiles; t0 += U2) {
       float y[U2][4];
       int nv[U2];
 #pragma unroll
       for (int uu = 0; uu < U2; uu++) {
-        nv[uu] = 0;
-        if (t0 + uu < ntiles) nv[uu] = R.load(pz_tile_e0(t0 + uu), y[uu]);
+        const int t = t0 + uu < ntiles ? t0 + uu : ntiles - 1;  // unconditional loads
+        const int nl = R.load(pz_tile_e0(t), y[uu]);
+        nv[uu] = t0 + uu < ntiles ? nl : 0;
       }
+      uint32_t want = 0;
 #pragma unroll
       for (int uu = 0; uu < U2; uu++) {
-        const int t = t0 + uu;
-        if (t >= ntiles) continue;
-        const int e0 = pz_tile_e0(t);
+        const int e0 = pz_tile_e0(t0 + uu);
         R.apply(e0, nv[uu], y[uu]);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           const float yy = y[uu][c];
-          bool want = c < nv[uu] && yy >= thr && (yy - M) >= dgate;
-          uint64_t key = 0;
-          if (want) {
-            const float p = pz_expf_l(yy - M, et) * inv;
-            want = p >= p_thr;
-            key = topp_key(p, e0 + c);
-          }
-          append_key(&S.count, &S.over, keys, cap, want, key);
+          const bool w = (c < nv[uu]) & (yy >= thr) & ((yy - M) >= dgate);
+          want |= (w ? 1u : 0u) << (4 * uu + c);
         }
+      }
+      const int e00 = pz_tile_e0(t0);
+      while (__ballot(want != 0u)) {
+        bool take = false;
+        uint64_t key = 0;
+        if (want) {
+          const uint32_t j = (uint32_t)__builtin_ctz(want);
+          want &= want - 1u;
+          float yy = y[0][0];
+#pragma unroll
+          for (int uu = 0; uu < U2; uu++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+              if (j == (uint32_t)(4 * uu + c)) yy = y[uu][c];
+          const float p = pz_expf_l(yy - M, et) * inv;
+          take = p >= p_thr;
+          key = topp_key(p, e00 + (int)(j >> 2) * PZ_TILE + (int)(j & 3u));
+        }
+        append_key(&S.count, &S.over, keys, cap, take, key);
       }
     }
     __syncthreads();
