@@ -60,26 +60,23 @@ PZ_HD float pz_acc_value(PzAcc a) { return pz_acc_value_ng(a.n, a.g); }
 // and the caller rounds by parity) or BIG (v alone is >= 2^24 G: the sum
 // certainly leaves the binade; the increment is 0 and meaningless).
 PZ_HD uint32_t pz_inc(float v, uint32_t g, uint32_t* cls) {
+  // branch-free: k = g - (the term's exponent) is the right shift that puts
+  // the term on the grid; shifts are clamped below 32 (k > 25 rounds to 0)
   const uint32_t b = pz_fbits(v);
   const uint32_t ev = b >> 23;
-  uint32_t mv = b & 0x7fffffu;
-  uint32_t evb = 1u;
-  if (ev) {
-    mv |= 0x800000u;
-    evb = ev;
-  }
-  *cls = PZ_INC_PLAIN;
-  if (evb > g) {
-    *cls = PZ_INC_BIG;
-    return 0u;
-  }
-  const uint32_t k = g - evb;
-  if (k == 0u) return mv;
-  if (k > 25u) return 0u;
-  const uint32_t half = 1u << (k - 1u);
-  const uint32_t rem = mv & ((half << 1) - 1u);
-  if (rem == half) *cls = PZ_INC_TIE;
-  return (mv >> k) + (rem > half ? 1u : 0u);
+  const uint32_t mv = (b & 0x7fffffu) | (ev ? 0x800000u : 0u);
+  const uint32_t evb = ev ? ev : 1u;
+  const bool big = evb > g;
+  const uint32_t k = big ? 0u : g - evb;
+  const uint32_t ks = k > 26u ? 26u : k;
+  const uint32_t mask = (2u << (ks > 0u ? ks - 1u : 0u)) - 1u;  // the low k bits (k >= 1)
+  const uint32_t half = ks > 0u ? 1u << (ks - 1u) : 0u;
+  const uint32_t rem = mv & mask;
+  const bool far = k > 25u;
+  const bool tie = !big && !far && k > 0u && rem == half;
+  const uint32_t up = (k > 0u && rem > half) ? 1u : 0u;
+  *cls = big ? PZ_INC_BIG : (tie ? PZ_INC_TIE : PZ_INC_PLAIN);
+  return big || far ? 0u : (mv >> ks) + up;
 }
 
 // s = fl(s + v) on the integer state, v >= 0 finite.
@@ -156,26 +153,35 @@ __device__ __forceinline__ bool pz_stop_hit(float s, float thr, int mode) {
   return mode == PZ_STOP_GT ? (thr < s) : (mode == PZ_STOP_GE ? (s >= thr) : false);
 }
 
-// The same accumulation as pz_wave_accumulate, one real fp32 add per term
-// (wave-uniform): faster when events are dense, e.g. while the running sum
-// is still smaller than the terms at the start of a row.
+// The same accumulation as pz_wave_accumulate over elements [start, end),
+// one real fp32 add per term (wave-uniform): faster when events are dense,
+// e.g. while the running sum is still smaller than the terms at the start of
+// a row.  Returns the first hit index, or -1.
 template <int C>
-__device__ __forceinline__ int pz_wave_serial(PzAcc& st, const float (&v)[C], int start,
+__device__ __forceinline__ int pz_wave_serial(PzAcc& st, const float (&v)[C], int start, int end,
                                               float thr, int stop_mode, float* cum) {
   const int lane = threadIdx.x & 63;
   float s = pz_acc_value(st);
-  for (int l = start / C; l < 64; l++) {
+  int idx = start;
+  while (idx < end) {
+    const int l = idx / C;
+    float x[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) x[c] = pz_readlane_f32(v[c], l);
+    const int cs = idx - l * C;                            // first term of lane l to add
+    const int ce = end - l * C < C ? end - l * C : C;      // one past its last
 #pragma unroll
     for (int c = 0; c < C; c++) {
-      const int idx = l * C + c;
-      if (idx < start) continue;
-      s = s + pz_readlane_f32(v[c], l);
-      if (cum && lane == 0) cum[idx] = s;
-      if (stop_mode != PZ_STOP_NONE && pz_stop_hit(s, thr, stop_mode)) {
-        st = pz_acc_of(s);
-        return idx;
+      const bool in = c >= cs && c < ce;
+      const float sn = s + x[c];
+      if (cum && lane == 0 && in) cum[l * C + c] = sn;
+      if (stop_mode != PZ_STOP_NONE && in && pz_stop_hit(sn, thr, stop_mode)) {
+        st = pz_acc_of(sn);
+        return l * C + c;
       }
+      s = in ? sn : s;
     }
+    idx = l * C + ce;
   }
   st = pz_acc_of(s);
   return -1;
@@ -194,46 +200,54 @@ __device__ __forceinline__ int pz_wave_accumulate(PzAcc& st, const float (&v)[C]
   int pos = start;
   int rounds = 0;
   while (pos < 64 * C) {
-    if (++rounds > 4) return pz_wave_serial<C>(st, v, pos, thr, stop_mode, cum);
+    if (++rounds > 4) {
+      // dense events: the next 64 terms one real add at a time, then rounds again
+      const int end = pos + 64 < 64 * C ? pos + 64 : 64 * C;
+      const int r = pz_wave_serial<C>(st, v, pos, end, thr, stop_mode, cum);
+      if (r >= 0) return r;
+      pos = end;
+      rounds = 0;
+      continue;
+    }
+    // increments at the current grid; a flagged term (tie or big) ends the
+    // lane's run of plain terms
     uint32_t inc[C];
-    int first_flag = C;
+    uint32_t flag = 0;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+      uint32_t cls;
+      const uint32_t i = pz_inc(v[c], st.g, &cls);
+      const bool valid = lane * C + c >= pos;
+      const bool f = valid && cls != PZ_INC_PLAIN;
+      inc[c] = valid && !f ? i : 0u;
+      flag |= (f ? 1u : 0u) << c;
+    }
+    const int first_flag = flag ? (int)__builtin_ctz(flag) : C;
     uint32_t lsum = 0;
 #pragma unroll
-    for (int c = 0; c < C; c++) {
-      const int idx = lane * C + c;
-      uint32_t cls = PZ_INC_PLAIN, i = 0;
-      if (idx >= pos) i = pz_inc(v[c], st.g, &cls);
-      if (cls != PZ_INC_PLAIN) {
-        if (first_flag == C) first_flag = c;
-        i = 0;
-      }
-      inc[c] = i;
-      if (first_flag == C) lsum += i;
-    }
+    for (int c = 0; c < C; c++) lsum += c < first_flag ? inc[c] : 0u;
     const uint32_t incl = pz_wave_scan_u32(lsum);
     const uint32_t excl = incl - lsum;
-    // this lane's first event: a flagged term, a binade exit, or a stop hit
+    // this lane's first event: a binade exit, a stop hit, or the flagged
+    // term (selects, no branches)
     uint32_t run = st.n + excl;
-    int ev = C, ev_kind = 0;
+    int ev = first_flag, ev_kind = first_flag < C ? 1 : 0;
     uint32_t ev_n = 0;
+    bool open = true;  // no exit or hit yet among the terms before the flag
 #pragma unroll
     for (int c = 0; c < C; c++) {
-      const int idx = lane * C + c;
-      if (ev < C || idx < pos) continue;
-      if (c == first_flag) {
-        ev = c; ev_kind = 1; ev_n = run;
-        continue;
-      }
+      const bool live = open && c < first_flag;
       const uint32_t nr = run + inc[c];
-      if (nr >= (1u << 24)) {
-        ev = c; ev_kind = 1; ev_n = run;
-        continue;
-      }
-      run = nr;
-      if (stop_mode != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(run, st.g), thr, stop_mode)) {
-        ev = c; ev_kind = 2; ev_n = run;
-      }
+      const bool cross = live && nr >= (1u << 24);
+      const bool hit = live && !cross && stop_mode != PZ_STOP_NONE && lane * C + c >= pos &&
+                       pz_stop_hit(pz_acc_value_ng(nr, st.g), thr, stop_mode);
+      ev_n = cross ? run : (hit ? nr : ev_n);
+      ev = cross || hit ? c : ev;
+      ev_kind = cross ? 1 : (hit ? 2 : ev_kind);
+      run = live && !cross ? nr : run;
+      open = open && !cross && !hit;
     }
+    if (open) ev_n = run;  // the flagged term's state: every term before it
     const uint64_t ball = __ballot(ev < C);
     const int L = ball ? (int)__builtin_ctzll(ball) : 64;
     if (cum) {

@@ -15,7 +15,7 @@
 //   u_res the same way.
 //
 // Kernels:
-//   k_spec_rows    one workgroup per logits row (all target rows, then all
+//   k_spec_rows_*  one workgroup per logits row (all target rows, then all
 //                  draft rows): maximum, exact softmax normaliser, NaN/inf
 //                  degeneracy.
 //   k_spec_verify  one workgroup per sequence: acceptance tests (two logits
@@ -37,7 +37,7 @@ struct SpecRowsShared {
 };
 
 template <bool VEC>
-__global__ __launch_bounds__(PZ_RB) void k_spec_rows(
+__device__ __forceinline__ void spec_rows_body(
     const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
     int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
   extern __shared__ __align__(16) char lds[];
@@ -71,6 +71,17 @@ __global__ __launch_bounds__(PZ_RB) void k_spec_rows(
     stats[4 * (long)q + 1] = inv;
     stats[4 * (long)q + 2] = bad ? 1.0f : 0.0f;
   }
+}
+
+__global__ __launch_bounds__(PZ_RB) void k_spec_rows_v(
+    const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
+    int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
+  spec_rows_body<true>(target, draft, ld, V, B, K, KT, prm, stats);
+}
+__global__ __launch_bounds__(PZ_RB) void k_spec_rows_s(
+    const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
+    int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
+  spec_rows_body<false>(target, draft, ld, V, B, K, KT, prm, stats);
 }
 
 // p(x) of one element of a row whose softmax statistics are (M, inv).
@@ -274,7 +285,7 @@ int launch_spec(pz_sampler* s, const float* d_target, const float* d_draft, long
                 const float* d_ures, int32_t* d_acc, int32_t* d_ids_out) {
   const size_t lds = pz_rec_bytes(V);
   if (lds + 256 > (size_t)s->max_lds) return -2;
-  auto k1 = k_spec_rows<VEC>;
+  auto k1 = VEC ? k_spec_rows_v : k_spec_rows_s;
   auto k2 = k_spec_verify<VEC>;
   if (lds > 65536) {
     if (hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize,
