@@ -43,6 +43,12 @@ constexpr int EBIN_BASE = 98 << 7;
 constexpr int EBINS = (127 << 7) - EBIN_BASE + 1;
 constexpr int TOPP_CAP_MAX = 8192;
 constexpr int EBINS_BYTES = ((EBINS * 4 + 15) / 16) * 16;
+// Gathered lists of at least TOPP_BINSORT_MIN keys are ordered by a counting
+// sort over PBINS bins of p (1/128 binade each, 32 binades below 1.0) and a
+// rank count inside each bin; smaller ones by a bitonic sort.
+constexpr int PBINS = 4 * PZ_RB;
+constexpr int TOPP_BINSORT_MIN = 1024;
+constexpr int TOPP_BIN_MAX = 256;  // larger bins: bitonic sort
 
 __device__ __forceinline__ int ebin(float e) {
   const int b = (int)(__float_as_uint(e) >> 16) - EBIN_BASE;
@@ -63,6 +69,8 @@ __device__ __forceinline__ float key_p(uint64_t k) { return __uint_as_float((uin
 
 struct ToppShared {
   PzPass1Shared p1;
+  uint32_t wtot[PZ_RB / 64];
+  uint32_t bmax;
   float sum;
   int bsel;
   uint32_t nsel;
@@ -102,11 +110,16 @@ __device__ __forceinline__ int nucleus_cutoff(const uint64_t* keys, float* cum, 
     st.n = 0;
     st.g = 1;
     int cutoff = -1;
-    for (int j0 = 0; j0 < m; j0 += 64) {
-      const int j = j0 + lane;
-      float v[1];
-      v[0] = j < m ? key_p(keys[j]) : 0.0f;
-      const int f = pz_wave_accumulate<1>(st, v, 0, top_p, PZ_STOP_GE, cum + j0);
+    for (int j0 = 0; j0 < m; j0 += 256) {
+      // lane l holds keys j0 + 4l .. j0 + 4l + 3 (terms past m are 0; cum
+      // has room: cap and the fallback slots are multiples of 256)
+      float v[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int j = j0 + 4 * lane + c;
+        v[c] = j < m ? key_p(keys[j]) : 0.0f;
+      }
+      const int f = pz_wave_accumulate<4>(st, v, 0, top_p, PZ_STOP_GE, cum + j0);
       if (f >= 0) {
         cutoff = j0 + f + 1;
         break;
@@ -133,6 +146,159 @@ __device__ __forceinline__ void nucleus_draw(const uint64_t* keys, const float* 
   const uint64_t k = keys[pick];
   *id_out = key_id(k);
   if (p_out) *p_out = key_p(k);
+}
+
+typedef __attribute__((address_space(3))) uint16_t pz_lds_u16;
+typedef __attribute__((address_space(3))) uint32_t pz_lds_u32b;
+
+// p bin of a key, 0 for p in [1, 2) (p <= 1), growing as p falls.
+__device__ __forceinline__ int pbin(uint64_t key) {
+  const int q = 0x3f80 - (int)(key >> 48);  // bits(p) >> 16
+  return q < PBINS - 1 ? q : PBINS - 1;
+}
+
+// The (p desc, id asc) order of keys[0..m) without moving them: a counting
+// sort by p bin into perm1 (any order inside a bin), then each key's rank
+// inside its bin puts its slot at its sorted position in perm2.  Returns
+// false, having done nothing usable, when a bin holds more than
+// TOPP_BIN_MAX keys.  Every thread calls it.
+__device__ __forceinline__ bool binned_order(const pz_lds_u64* keys, int m, pz_lds_u16* perm1,
+                                             pz_lds_u16* perm2, pz_lds_u32b* bcnt,
+                                             pz_lds_u32b* bstart, ToppShared& S) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int i = tid; i < PBINS; i += PZ_RB) bcnt[i] = 0u;
+  if (tid == 0) S.bmax = 0u;
+  __syncthreads();
+  for (int i = tid; i < m; i += PZ_RB) atomicAdd((uint32_t*)&bcnt[pbin(keys[i])], 1u);
+  __syncthreads();
+  // exclusive scan over the bins; thread t owns bins 4t .. 4t+3
+  uint32_t c[4], local = 0, mx = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    c[j] = bcnt[4 * tid + j];
+    local += c[j];
+    mx = c[j] > mx ? c[j] : mx;
+  }
+  const uint32_t incl = pz_wave_scan_u32(local);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = __shfl_xor(mx, off, 64);
+    mx = o > mx ? o : mx;
+  }
+  if (lane == 63) S.wtot[w] = incl;
+  if (lane == 0) atomicMax(&S.bmax, mx);
+  __syncthreads();
+  uint32_t run = incl - local;
+  for (int j = 0; j < w; j++) run += S.wtot[j];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    bstart[4 * tid + j] = run;
+    bcnt[4 * tid + j] = run;  // cursor
+    run += c[j];
+  }
+  __syncthreads();
+  if (S.bmax > (uint32_t)TOPP_BIN_MAX) return false;
+  for (int i = tid; i < m; i += PZ_RB) {
+    const uint32_t pos = atomicAdd((uint32_t*)&bcnt[pbin(keys[i])], 1u);
+    perm1[pos] = (uint16_t)i;
+  }
+  __syncthreads();
+  for (int j = tid; j < m; j += PZ_RB) {
+    const int i = perm1[j];
+    const uint64_t key = keys[i];
+    const int q = pbin(key);
+    const uint32_t b0 = bstart[q], b1 = bcnt[q];
+    uint32_t r = 0;
+    for (uint32_t x = b0; x < b1; x++) r += keys[perm1[x]] > key ? 1u : 0u;
+    perm2[b0 + r] = (uint16_t)i;
+  }
+  __syncthreads();
+  return true;
+}
+
+// The sorted probabilities (p of keys[perm[j]], j < m) as the terms of an
+// exact-sum records pass: the values are exact, so every increment is too.
+struct SortedTerms {
+  typedef float Raw[4];
+  const pz_lds_u64* keys;
+  const pz_lds_u16* perm;
+  int m;
+  __device__ __forceinline__ int load(int e0, Raw& r) const {
+#pragma unroll
+    for (int c = 0; c < 4; c++) r[c] = e0 + c < m ? key_p(keys[perm[e0 + c]]) : 0.0f;
+    const int n = m - e0;
+    return n < 0 ? 0 : (n > 4 ? 4 : n);
+  }
+  __device__ __forceinline__ void prep(int, int, Raw& r, float (&a)[4]) const {
+#pragma unroll
+    for (int c = 0; c < 4; c++) a[c] = r[c];
+  }
+  __device__ __forceinline__ void observe(int, const Raw&, const float (&)[4]) {}
+  __device__ __forceinline__ uint32_t inc(const Raw&, const float (&a)[4], int c, uint32_t g,
+                                          uint32_t* cls) const {
+    return pz_inc(a[c], g, cls);
+  }
+  __device__ __forceinline__ void cache_put(pz_lds_f32* base, const Raw& r,
+                                            const float (&)[4]) const {
+    pz_f4 q;
+    q.x = r[0];
+    q.y = r[1];
+    q.z = r[2];
+    q.w = r[3];
+    ((pz_lds_f4*)base)[threadIdx.x & 63] = q;
+  }
+  __device__ __forceinline__ void cache_terms(const pz_lds_f32* base, float (&v)[4]) const {
+    const pz_f4 q = ((const pz_lds_f4*)base)[threadIdx.x & 63];
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  }
+  __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
+    Raw r;
+    load(pz_seg_e0(k), r);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = r[c];
+  }
+};
+
+// Cut-off and draw over the order in perm2 (top_p.c:80-105) with exact-sum
+// records of the sorted probabilities: the cumulative walk stops at the
+// first running sum >= top_p (the cut-off; its sum is the truncated mass),
+// a second walk over the same records at the first running sum > r.
+// Returns the picked sorted position, or -1 when the list is a strict prefix
+// whose cumulative stays below top_p.  Every thread calls it; rec is LDS of
+// pz_rec_bytes(m) bytes.
+__device__ __forceinline__ int binned_pick(const pz_lds_u64* keys, const pz_lds_u16* perm2, int m,
+                                           float top_p, bool all_gathered, float uu, char* rec,
+                                           PzRecShared& RS, int* sh) {
+  SortedTerms X;
+  X.keys = keys;
+  X.perm = perm2;
+  X.m = m;
+  const int ntiles = pz_tiles(m), nseg = ntiles * PZ_SEGS_PER_TILE;
+  const PzRec REC = pz_rec_at(rec, nseg);
+  pz_record_pass(X, ntiles, REC, RS, __builtin_inff());
+  if (threadIdx.x < 64) {
+    PzAcc st;
+    st.n = 0;
+    st.g = 1;
+    const int hit = pz_rec_walk(st, REC, nseg, top_p, PZ_STOP_GE, X);
+    int pick = -1;
+    int cutoff = hit >= 0 && hit < m ? hit + 1 : -1;
+    if (cutoff < 0 && all_gathered) cutoff = m;  // st then holds the whole sum
+    if (cutoff > 0) {
+      const float r = uu * pz_acc_value(st);  // trunc_sum: the cumulative at the cut-off
+      PzAcc s2;
+      s2.n = 0;
+      s2.g = 1;
+      const int d = pz_rec_walk(s2, REC, nseg, r, PZ_STOP_GT, X);
+      pick = d >= 0 && d < cutoff ? d : 0;
+    }
+    if (threadIdx.x == 0) *sh = pick;
+  }
+  __syncthreads();
+  return *sh;
 }
 
 // Candidate terms with the e histogram as observer.
@@ -336,15 +502,35 @@ __global__ __launch_bounds__(PZ_RB) void k_topp(
   }
   if (!fallback) {
     const int m = S.count;
-    int N = 1;
-    while (N < m) N <<= 1;
-    for (int i = m + tid; i < N; i += PZ_RB) keys[i] = 0ull;
-    __syncthreads();
-    pz_bitonic_desc<PZ_RB>((pz_lds_u64*)keys, N);
-    const int cutoff = nucleus_cutoff(keys, cum, m, prm.top_p, all, &S.cutoff);
-    if (cutoff > 0) {
-      if (tid == 0) nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
-      return;
+    pz_lds_u64* lkeys = (pz_lds_u64*)keys;
+    pz_lds_u16* perm1 = (pz_lds_u16*)cum;  // the running-sum area holds two u16 orders
+    pz_lds_u16* perm2 = perm1 + cap;
+    pz_lds_u32b* bcnt = (pz_lds_u32b*)(cum + cap);
+    pz_lds_u32b* bstart = bcnt + PBINS;
+    if (m >= TOPP_BINSORT_MIN && binned_order(lkeys, m, perm1, perm2, bcnt, bstart, S)) {
+      // the bin arrays are free again: they hold the records of the sorted list
+      const int pick = binned_pick(lkeys, perm2, m, prm.top_p, all, u[row], (char*)bcnt, RS,
+                                   &S.cutoff);
+      if (pick >= 0) {
+        if (tid == 0) {
+          const uint64_t k = lkeys[perm2[pick]];
+          ids_out[row] = key_id(k);
+          if (p_out) p_out[row] = key_p(k);
+        }
+        return;
+      }
+    } else {
+      int N = 1;
+      while (N < m) N <<= 1;
+      for (int i = m + tid; i < N; i += PZ_RB) keys[i] = 0ull;
+      __syncthreads();
+      pz_bitonic_desc<PZ_RB>(lkeys, N);
+      const int cutoff = nucleus_cutoff(keys, cum, m, prm.top_p, all, &S.cutoff);
+      if (cutoff > 0) {
+        if (tid == 0)
+          nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
+        return;
+      }
     }
   }
   // ---- queue the row for the fallback kernel
@@ -423,7 +609,10 @@ __global__ void k_reset_counters(int32_t* c) {
 
 size_t topp_region_bytes(int V, int cap) {
   const size_t a = (size_t)EBINS_BYTES + pz_rec_bytes(V);
-  const size_t b = (size_t)cap * 12;
+  // keys, running sums (or two u16 orders), then bin counts and starts or
+  // the records of the sorted list
+  const size_t bins = (size_t)PBINS * 8, recs = pz_rec_bytes(cap);
+  const size_t b = (size_t)cap * 12 + (bins > recs ? bins : recs);
   return a > b ? a : b;
 }
 
