@@ -43,6 +43,8 @@ struct pz_launch {
 };
 
 int pz_launch_greedy(const pz_launch& L, int n_rows, const int32_t* d_rows);
+// Argmax of the tempered row (top-p rows above the vocabulary guard).
+int pz_launch_greedy_tempered(const pz_launch& L, int n_rows, const int32_t* d_rows);
 int pz_launch_topk(const pz_launch& L, int n_rows, const int32_t* d_rows);
 int pz_launch_topp(const pz_launch& L, int n_rows, const int32_t* d_rows);
 int pz_launch_categorical(const pz_launch& L, int n_rows, const int32_t* d_rows);

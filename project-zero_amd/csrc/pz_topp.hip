@@ -645,7 +645,7 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
 
 int pz_launch_topp(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (n_rows <= 0) return 0;
-  if (L.V > PZ_TOPP_MAX_V) return pz_launch_greedy(L, n_rows, d_rows);  // top_p.c:33-34
+  if (L.V > PZ_TOPP_MAX_V) return pz_launch_greedy_tempered(L, n_rows, d_rows);  // top_p.c:33-34
   const bool vec = (L.ld % 4 == 0) && (((uintptr_t)L.logits & 15) == 0);
   return vec ? launch_topp_t<true>(L, n_rows, d_rows) : launch_topp_t<false>(L, n_rows, d_rows);
 }
