@@ -88,7 +88,8 @@ PZ_API void *pz_sampler_stream(pz_sampler *s);
 /* Samples B rows.  d_logits: device [B, ld] fp32 (ld >= V), caller-owned and
  * not modified.  params: host, n_params = 1 (shared) or B entries.  d_hist:
  * device [B, H] int32 token history (NULL when H == 0); ids outside [0, V)
- * are ignored.  u: host [B] uniforms in [0, 1], one per row, exactly as
+ * are ignored.  u: host [B] uniforms in [0, 1] (at least B floats are
+ * read), one per row, exactly as
  * rng_float() would return them (unused by greedy rows).  ids_out: host [B].
  * p_out: host [B] or NULL, receives p(chosen) in the distribution the draw
  * used (1.0 for greedy).  Synchronous on the sampler's stream. */

@@ -220,12 +220,18 @@ template <bool TEMPER>
 static int launch_argmax(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (n_rows <= 0) return 0;
   const size_t lds = L.pen_any ? pz_penalty_lds_bytes(L.V, L.hcap) : 0;
+  // static LDS: the block argmax scratch (2 words per wave)
+  constexpr size_t kStatic = 2 * (GREEDY_BLOCK / PZ_WAVE) * 4;
+  if (lds + kStatic > (size_t)L.max_lds) return -2;
   const bool vec = (L.ld % 4 == 0) && (((uintptr_t)L.logits & 15) == 0) && L.V >= 4;
   dim3 grid(n_rows), block(GREEDY_BLOCK);
   auto k = vec ? (L.pen_any ? k_greedy<GREEDY_BLOCK, GREEDY_U, true, TEMPER, true>
                             : k_greedy<GREEDY_BLOCK, GREEDY_U, true, TEMPER, false>)
                : (L.pen_any ? k_greedy<GREEDY_BLOCK, GREEDY_U, false, TEMPER, true>
                             : k_greedy<GREEDY_BLOCK, GREEDY_U, false, TEMPER, false>);
+  if (lds > 65536 && hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)lds) != hipSuccess)
+    return -1;
   hipLaunchKernelGGL(k, grid, block, lds, L.stream, L.logits, L.ld, L.V, d_rows, L.params,
                      L.n_params, L.hist, L.H, L.hcap, L.ids, L.p_out);
   return hipGetLastError() == hipSuccess ? 0 : -1;

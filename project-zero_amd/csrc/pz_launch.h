@@ -13,10 +13,12 @@ constexpr int PZ_TOPP_MAX_V = 200000;  // top_p.c:27 (larger rows take argmax)
 struct pz_scratch {
   float* row_stat;    // [max_batch][4] per-row values handed between kernels
   int32_t* fb_list;   // [max_batch] rows queued for the top-p fallback
-  int32_t* counters;  // [16] queue counters
-  uint64_t* fb_keys;  // [PZ_FB_SLOTS][slot_n] sort buffers of the fallback
-  float* fb_cum;      // [PZ_FB_SLOTS][slot_n] running sums of the fallback
+  int32_t* counters;  // [16] queue counters: [0] rows queued, [1] fallback
+                      // workgroups done (both zero between calls)
+  uint64_t* fb_keys;  // [fb_slots][slot_n] sort buffers of the fallback
+  float* fb_cum;      // [fb_slots][slot_n] running sums of the fallback
   int slot_n;         // power of two >= min(max_vocab, PZ_TOPP_MAX_V)
+  int fb_slots;       // min(PZ_FB_SLOTS, max_batch) sort slots
 };
 
 // Bytes of scratch for a sampler of this size; with base != nullptr also

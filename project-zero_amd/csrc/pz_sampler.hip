@@ -38,12 +38,15 @@ size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* o
   int slot = 256;  // >= one call of the cut-off walk (64 lanes x 4 running sums)
   while (slot < vt) slot <<= 1;
   const size_t B = (size_t)max_batch;
+  // the fallback sorts at most one queued row per slot at a time: a sampler
+  // for max_batch rows never needs more than max_batch slots
+  const size_t slots = (size_t)(max_batch < PZ_FB_SLOTS ? max_batch : PZ_FB_SLOTS);
   size_t off = 0;
   const size_t o_stat = off; off = up(off + B * 4 * sizeof(float));
   const size_t o_list = off; off = up(off + B * sizeof(int32_t));
   const size_t o_cnt = off;  off = up(off + 16 * sizeof(int32_t));
-  const size_t o_keys = off; off = up(off + (size_t)PZ_FB_SLOTS * slot * sizeof(uint64_t));
-  const size_t o_cum = off;  off = up(off + (size_t)PZ_FB_SLOTS * slot * sizeof(float));
+  const size_t o_keys = off; off = up(off + slots * slot * sizeof(uint64_t));
+  const size_t o_cum = off;  off = up(off + slots * slot * sizeof(float));
   if (base && out) {
     char* b = static_cast<char*>(base);
     out->row_stat = reinterpret_cast<float*>(b + o_stat);
@@ -52,6 +55,7 @@ size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* o
     out->fb_keys = reinterpret_cast<uint64_t*>(b + o_keys);
     out->fb_cum = reinterpret_cast<float*>(b + o_cum);
     out->slot_n = slot;
+    out->fb_slots = (int)slots;
   }
   return off;
 }
@@ -104,6 +108,9 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   s->scratch_bytes = pz_scratch_layout(max_batch, max_vocab, nullptr, nullptr);
   if (hipMalloc(&s->d_scratch, s->scratch_bytes) != hipSuccess) return bail(PZ_ENOMEM);
   pz_scratch_layout(max_batch, max_vocab, s->d_scratch, &s->sc);
+  // queue counters start at zero; the fallback kernel re-zeroes them after
+  // each launch that read them
+  if (hipMemset(s->sc.counters, 0, 16 * sizeof(int32_t)) != hipSuccess) return bail(PZ_EDEVICE);
   *out = s;
   return rc;
 }

@@ -75,7 +75,7 @@ __global__ __launch_bounds__(PZ_RB) void k_softmax(const float* in, long ld_in, 
 
 PzTemp temp_of(pz_sampler* s, float temperature) {
   float T = temperature;
-  if (!(T >= 1e-6f)) T = 1e-6f;  // temperature.c:10 (NaN clamps too)
+  if (T < 1e-6f) T = 1e-6f;  // temperature.c:10 (a NaN temperature stays NaN)
   PzTemp t;
   t.t = T;
   t.inv = 1.0f / T;

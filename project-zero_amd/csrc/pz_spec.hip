@@ -358,7 +358,7 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   pz_row_params_dev prm;
   memset(&prm, 0, sizeof(prm));
   float T = temperature;
-  if (!(T >= 1e-6f)) T = 1e-6f;  // temperature.c:10
+  if (T < 1e-6f) T = 1e-6f;  // temperature.c:10 (a NaN temperature stays NaN)
   prm.temp = T;
   prm.inv_temp = 1.0f / T;
   prm.temp_div = s->temp_mode == PZ_TEMP_DIV;

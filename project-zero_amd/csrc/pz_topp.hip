@@ -601,10 +601,15 @@ __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
     if (tid == 0) nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
     __syncthreads();
   }
-}
-
-__global__ void k_reset_counters(int32_t* c) {
-  if (threadIdx.x < 16) c[threadIdx.x] = 0;
+  // the last workgroup out re-arms the queue for the next launch (every
+  // workgroup has read counters[0] before it counts itself done)
+  if (tid == 0) {
+    __threadfence();
+    if (atomicAdd(&sc.counters[1], 1) == (int)gridDim.x - 1) {
+      atomicExch(&sc.counters[0], 0);
+      atomicExch(&sc.counters[1], 0);
+    }
+  }
 }
 
 size_t topp_region_bytes(int V, int cap) {
@@ -632,11 +637,11 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (pen > 65536 && hipFuncSetAttribute((const void*)fb, hipFuncAttributeMaxDynamicSharedMemorySize,
                                          pen) != hipSuccess)
     return -1;
-  hipLaunchKernelGGL(k_reset_counters, dim3(1), dim3(64), 0, L.stream, L.sc.counters);
   hipLaunchKernelGGL(kern, dim3(n_rows), dim3(PZ_RB), lds, L.stream, L.logits, L.ld, L.V, d_rows,
                      L.params, L.n_params, L.hist, L.H, L.hcap, pen, cap, L.u, L.ids, L.p_out,
                      L.sc);
-  hipLaunchKernelGGL(fb, dim3(PZ_FB_SLOTS), dim3(PZ_RB), (size_t)pen, L.stream, L.logits, L.ld,
+  const int fb_grid = n_rows < L.sc.fb_slots ? n_rows : L.sc.fb_slots;
+  hipLaunchKernelGGL(fb, dim3(fb_grid), dim3(PZ_RB), (size_t)pen, L.stream, L.logits, L.ld,
                      L.V, L.params, L.n_params, L.hist, L.H, L.hcap, L.u, L.ids, L.p_out, L.sc);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

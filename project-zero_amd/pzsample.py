@@ -192,7 +192,9 @@ class Sampler:
         parr, n = _params_array(params, B)
         ids = np.empty(B, np.int32)
         p = np.empty(B, np.float32) if want_p else None
-        ua = np.ascontiguousarray(u, np.float32) if u is not None else None
+        ua = np.ascontiguousarray(u, np.float32).ravel() if u is not None else None
+        if ua is not None and ua.size < B:
+            raise ValueError(f"u holds {ua.size} uniforms, B={B} rows need {B}")
         rc = self.lib.pz_sample_batch(self.h, _ptr(d_logits), B, V, ld, parr, n,
                                       _ptr(d_hist), H, _np_ptr(ua), _np_ptr(ids),
                                       _np_ptr(p))
@@ -226,9 +228,12 @@ class Sampler:
         _sync_torch(d_target, d_draft)
         acc = np.empty(B, np.int32)
         out = np.empty((B, K + 1), np.int32)
-        di = np.ascontiguousarray(draft_ids, np.int32)
-        ua = np.ascontiguousarray(u_acc, np.float32)
-        ur = np.ascontiguousarray(u_res, np.float32)
+        di = np.ascontiguousarray(draft_ids, np.int32).ravel()
+        ua = np.ascontiguousarray(u_acc, np.float32).ravel()
+        ur = np.ascontiguousarray(u_res, np.float32).ravel()
+        for name, a, need in (("draft_ids", di, B * K), ("u_acc", ua, B * K), ("u_res", ur, B)):
+            if a.size < need:
+                raise ValueError(f"{name} holds {a.size} entries, B={B}, K={K} need {need}")
         rc = self.lib.pz_spec_verify(self.h, _ptr(d_target), _ptr(d_draft), B, K, V, ld,
                                      int(has_bonus), float(temperature), _np_ptr(di),
                                      _np_ptr(ua), _np_ptr(ur), _np_ptr(acc), _np_ptr(out))

@@ -149,6 +149,34 @@ def test_device_softmax_and_temperature(torch_cuda):
         assert (bits(d_t.cpu().numpy()) == bits(want)).all()
 
 
+def test_nan_temperature_is_not_clamped(lib, torch_cuda):
+    """temperature.c:10 clamps with T < 1e-6, which a NaN fails: the row
+    becomes NaN (x * (1/NaN) or x / NaN), and so does its softmax."""
+    o = po.oracle()
+    nan = ctypes.c_float(float("nan"))
+    for mode in (pz.PZ_TEMP_MUL_RECIP, pz.PZ_TEMP_DIV):
+        lib.pz_compat_set_temp_mode(mode)
+        x = rows(1, 4099, 8)[0]
+        y = x.copy()
+        lib.apply_temperature(ptr(x), x.size, nan)
+        o.orc_apply_temperature(ptr(y), y.size, nan, mode)
+        assert np.isnan(y).all() and np.isnan(x).all(), mode
+    lib.pz_compat_set_temp_mode(pz.PZ_TEMP_MUL_RECIP)
+    B, V = 3, 5003
+    x = pz.synth_normal(B, V, 2.0, 77)
+    d_in = to_dev(torch_cuda, x)
+    d_out = torch_cuda.empty_like(d_in)
+    with pz.Sampler(B, V) as s:
+        s.softmax(d_in, d_out, B, V, V, V, temperature=float("nan"))
+        s.sync()
+        got = d_out.cpu().numpy()
+    want = x.copy()
+    for b in range(B):
+        o.orc_apply_temperature(ptr(want[b]), V, nan, 0)
+        o.orc_softmax(ptr(want[b]), V)
+    assert np.isnan(want).all() and np.isnan(got).all()
+
+
 def test_against_reference_binary(lib):
     r = po.ref(True)
     if r is None:

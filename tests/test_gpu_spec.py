@@ -87,3 +87,12 @@ def test_sizes_and_temperature_forms(torch_cuda, V):
     for mode in (pz.PZ_TEMP_MUL_RECIP, pz.PZ_TEMP_DIV):
         run(torch_cuda, w["target"], w["draft"], w["draft_ids"], w["u_acc"], w["u_res"], 0.7,
             True, temp_mode=mode, label=f"V={V} mode={mode}")
+
+
+def test_nan_temperature(torch_cuda):
+    """A NaN temperature is not clamped (temperature.c:10 tests T < 1e-6):
+    every p and q is NaN, so each draft is rejected and the token falls back
+    exactly as the oracle's does."""
+    w = wl.build_c5(B=4, K=2, V=3000, seed=0xC5 + 21)
+    run(torch_cuda, w["target"], w["draft"], w["draft_ids"], w["u_acc"], w["u_res"],
+        float("nan"), True, label="nan tau")
