@@ -130,18 +130,22 @@ __device__ __forceinline__ float pz_unkey(uint32_t k) {
 typedef __attribute__((address_space(3))) uint32_t pz_lds_u32;
 typedef __attribute__((address_space(3))) int32_t pz_lds_i32;
 
+// The tables cover the ids [base, lim): the whole row (base 0, lim V) for a
+// workgroup that owns a row, or its slice for one of several workgroups that
+// share a row (base a multiple of 32).
 struct PzPenalty {
-  const pz_lds_u32* bitmap;  // ceil(V/32) words, bit i set <=> id i in history
+  const pz_lds_u32* bitmap;  // ceil((lim-base)/32) words, bit i-base set <=> id i in history
   const pz_lds_i32* hkey;    // hash keys (-1 = empty), hcap entries
   const pz_lds_i32* hcnt;    // counts
   int hcap;           // power of two, 0 when counts are not needed
+  int base, lim;      // ids held: [base, lim)
   float rep, pres, freq;
   bool active;
 };
 
-// Bytes of LDS the penalty context needs.
-__host__ __device__ inline size_t pz_penalty_lds_bytes(int V, int hcap) {
-  size_t words = ((size_t)V + 31) / 32;
+// Bytes of LDS the penalty context needs (for n ids).
+__host__ __device__ inline size_t pz_penalty_lds_bytes(int n, int hcap) {
+  size_t words = ((size_t)n + 31) / 32;
   return words * 4 + (size_t)hcap * 8;
 }
 
@@ -149,17 +153,21 @@ __device__ __forceinline__ uint32_t pz_hash(uint32_t id) {
   return (id * 0x9E3779B1u) >> 7;
 }
 
-// Set-up half of the build: fills P and clears the tables (no barrier).
+// Set-up half of the build for the ids [base, lim): fills P and clears the
+// tables (no barrier).
 template <int BLOCK>
-__device__ __forceinline__ void pz_penalty_setup(PzPenalty& P, char* lds, int V, int hcap,
-                                                 bool has_hist, const pz_row_params_dev& prm) {
+__device__ __forceinline__ void pz_penalty_setup_range(PzPenalty& P, char* lds, int base, int lim,
+                                                       int hcap, bool has_hist,
+                                                       const pz_row_params_dev& prm) {
   const int tid = threadIdx.x;
   P.active = has_hist && (prm.rep_penalty != 1.0f || prm.presence_penalty != 0.0f ||
                           prm.frequency_penalty != 0.0f);
   P.rep = prm.rep_penalty;
   P.pres = prm.presence_penalty;
   P.freq = prm.frequency_penalty;
-  const int words = (V + 31) >> 5;
+  P.base = base;
+  P.lim = lim;
+  const int words = (lim - base + 31) >> 5;
   uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds);
   int32_t* hkey = reinterpret_cast<int32_t*>(lds + (size_t)words * 4);
   int32_t* hcnt = hkey + hcap;
@@ -172,18 +180,26 @@ __device__ __forceinline__ void pz_penalty_setup(PzPenalty& P, char* lds, int V,
   for (int j = tid; j < P.hcap; j += BLOCK) { hkey[j] = -1; hcnt[j] = 0; }
 }
 
+template <int BLOCK>
+__device__ __forceinline__ void pz_penalty_setup(PzPenalty& P, char* lds, int V, int hcap,
+                                                 bool has_hist, const pz_row_params_dev& prm) {
+  pz_penalty_setup_range<BLOCK>(P, lds, 0, V, hcap, has_hist, prm);
+}
+
 // Inserts one history id (after the set-up and a barrier).  With dlist !=
 // nullptr every distinct valid id is also appended once to dlist, *dcount
-// counting them (zeroed by the caller before the set-up barrier).
+// counting them (zeroed by the caller before the set-up barrier).  Ids
+// outside [0, V) are ignored (the penalty's definition), and so are ids
+// outside the tables' [base, lim).
 __device__ __forceinline__ void pz_penalty_insert(const PzPenalty& P, char* lds, int V, int id,
                                                   int32_t* dlist, int* dcount) {
-  if (id < 0 || id >= V) return;  // ids outside [0,V) are ignored
-  const int words = (V + 31) >> 5;
+  if (id < 0 || id >= V || id < P.base || id >= P.lim) return;
+  const int words = (P.lim - P.base + 31) >> 5;
   uint32_t* bitmap = reinterpret_cast<uint32_t*>(lds);
   int32_t* hkey = reinterpret_cast<int32_t*>(lds + (size_t)words * 4);
   int32_t* hcnt = hkey + P.hcap;
   const uint32_t bit = 1u << (id & 31);
-  const uint32_t before = atomicOr(&bitmap[id >> 5], bit);
+  const uint32_t before = atomicOr(&bitmap[(id - P.base) >> 5], bit);
   if (dlist && !(before & bit)) dlist[atomicAdd(dcount, 1)] = id;
   if (P.hcap) {
     const uint32_t mask = (uint32_t)P.hcap - 1u;
@@ -196,16 +212,25 @@ __device__ __forceinline__ void pz_penalty_insert(const PzPenalty& P, char* lds,
   }
 }
 
+// Builds the tables of the ids [base, lim) of a row of V from its history.
 template <int BLOCK>
-__device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V, int hcap,
-                                                 const int32_t* hist_row, int H,
-                                                 const pz_row_params_dev& prm) {
-  pz_penalty_setup<BLOCK>(P, lds, V, hcap, hist_row != nullptr && H > 0, prm);
+__device__ __forceinline__ void pz_penalty_build_range(PzPenalty& P, char* lds, int V, int base,
+                                                       int lim, int hcap,
+                                                       const int32_t* hist_row, int H,
+                                                       const pz_row_params_dev& prm) {
+  pz_penalty_setup_range<BLOCK>(P, lds, base, lim, hcap, hist_row != nullptr && H > 0, prm);
   if (!P.active) return;
   __syncthreads();
   for (int j = threadIdx.x; j < H; j += BLOCK)
     pz_penalty_insert(P, lds, V, hist_row[j], nullptr, nullptr);
   __syncthreads();
+}
+
+template <int BLOCK>
+__device__ __forceinline__ void pz_penalty_build(PzPenalty& P, char* lds, int V, int hcap,
+                                                 const int32_t* hist_row, int H,
+                                                 const pz_row_params_dev& prm) {
+  pz_penalty_build_range<BLOCK>(P, lds, V, 0, V, hcap, hist_row, H, prm);
 }
 
 // Penalised value of a history member (caller checked the bitmap bit).
@@ -240,13 +265,14 @@ __device__ __forceinline__ float pz_penalize(const PzPenalty& P, float x, int id
   return pz_penalize_v(x, id, P.rep, P.pres, P.freq, P.hcap, P.hkey, P.hcnt);
 }
 
-// 4-bit membership nibble for the aligned group of 4 ids starting at i4*4.
+// 4-bit membership nibble for the aligned group of 4 ids starting at i
+// (i in [base, lim), base a multiple of 32).
 __device__ __forceinline__ uint32_t pz_pen_nibble(const PzPenalty& P, int i) {
-  return (P.bitmap[i >> 5] >> (i & 31)) & 0xfu;
+  return (P.bitmap[(i - P.base) >> 5] >> (i & 31)) & 0xfu;
 }
 
 __device__ __forceinline__ bool pz_pen_member(const PzPenalty& P, int i) {
-  return (P.bitmap[i >> 5] >> (i & 31)) & 1u;
+  return (P.bitmap[(i - P.base) >> 5] >> (i & 31)) & 1u;
 }
 
 // Temperature (temperature.c:8-25): x*(1/T) for the AVX-512 build, x/T for

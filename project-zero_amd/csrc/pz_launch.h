@@ -5,10 +5,12 @@
 #include <stdint.h>
 
 #include "pz_params.h"
+#include "pz_split.h"
 
 // Device scratch owned by a sampler (carved from one allocation).
 constexpr int PZ_FB_SLOTS = 32;        // rows the top-p fallback kernel sorts at once
 constexpr int PZ_TOPP_MAX_V = 200000;  // top_p.c:27 (larger rows take argmax)
+constexpr int PZ_TOPP_CAPG = 8192;     // top-p candidates a row can gather for the LDS sort
 
 struct pz_scratch {
   float* row_stat;    // [max_batch][4] per-row values handed between kernels
@@ -40,6 +42,7 @@ struct pz_launch {
   int32_t* ids;         // device [B] sampled ids
   float* p_out;         // device [B] p(chosen) or nullptr
   pz_scratch sc;         // device scratch owned by the sampler
+  PzSplitWs ws;          // workspace of the row-split passes
   int max_lds;          // max dynamic LDS per workgroup on this device
   hipStream_t stream;
 };

@@ -111,6 +111,12 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   // queue counters start at zero; the fallback kernel re-zeroes them after
   // each launch that read them
   if (hipMemset(s->sc.counters, 0, 16 * sizeof(int32_t)) != hipSuccess) return bail(PZ_EDEVICE);
+  s->split_bytes = pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, nullptr, nullptr);
+  if (hipMalloc(&s->d_split, s->split_bytes) != hipSuccess) return bail(PZ_ENOMEM);
+  pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, s->d_split, &s->ws);
+  // arrival counters start at zero; every pass's last workgroup re-zeroes
+  // its row's
+  if (hipMemset(s->d_split, 0, s->split_bytes) != hipSuccess) return bail(PZ_EDEVICE);
   *out = s;
   return rc;
 }
@@ -122,6 +128,7 @@ extern "C" void pz_sampler_destroy(pz_sampler* s) {
   (void)hipFree(s->d_params);
   (void)hipFree(s->d_rows);
   (void)hipFree(s->d_scratch);
+  (void)hipFree(s->d_split);
   (void)hipFree(s->spec_dev);
   (void)hipHostFree(s->spec_host);
   (void)hipHostFree(s->h_params);
@@ -281,6 +288,7 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
   L.ids = d_ids;
   L.p_out = d_p;
   L.sc = s->sc;
+  L.ws = s->ws;
   L.max_lds = s->max_lds;
   L.stream = s->stream;
 

@@ -35,6 +35,11 @@ struct pz_sampler {
   void* d_scratch = nullptr;
   size_t scratch_bytes = 0;
   pz_scratch sc{};
+  // workspace of the row-split passes (rows up to max_batch, ids up to
+  // max_vocab, top-p candidate lists)
+  void* d_split = nullptr;
+  size_t split_bytes = 0;
+  PzSplitWs ws{};
 
   pz_row_params_dev* res_params = nullptr;  // host work area (max_batch)
   int staged_n = -1, staged_B = -1;         // what d_params / d_rows hold

@@ -12,21 +12,23 @@
 //     trunc_sum = the same sequential sum (:91-93); r = u * trunc_sum;
 //     first i < cut-off with r < cdf, else slot 0 (:96-105).
 //
-// Design (one 1024-thread workgroup per row):
-//   pass 1  (HBM)   row maximum + per-segment estimates of the normaliser;
-//   pass 2  (L2)    exact e = expf(x - max) (glibc-identical pz_expf) of every
-//                   candidate -> integer segment records at the predicted
-//                   binade (pz_exact.h) + an LDS histogram of e (1/128
-//                   binade bins);
-//   walk    (wave 0) the exact sequential normaliser; meanwhile wave 1 picks,
-//                   from the histogram, the smallest set of top bins whose
-//                   estimated mass clears top_p with margin;
-//   pass 3  (L2)    gathers the candidates with p >= p(threshold) into LDS as
-//                   (p, ~id) keys -- a prefix of the reference's sort order;
-//   sort + exact cumulative walk + draw (binary search over the stored sums).
-// A row whose selected set does not fit in LDS, or whose exact cumulative
-// does not reach top_p inside it, is queued for the fallback kernel, which
-// sorts every candidate of the row in its global scratch slot.
+// Design: every row is split over S workgroups (pz_split.h), launches
+//   k_topp_stat    (HBM) row maximum, segment mass estimates, predicted
+//                  binades of the running sum;
+//   k_topp_rec     (L2)  exact e = expf(x - max) (glibc-identical pz_expf)
+//                  of every candidate -> integer segment records + a mass
+//                  histogram of e per workgroup; the row's last workgroup
+//                  walks the records (the exact normaliser) while a second
+//                  wave picks, from the merged histogram, the smallest set of
+//                  top bins whose estimated mass clears top_p with margin;
+//   k_topp_gather  (L2)  candidates with p >= the lowest selected bin -- a
+//                  prefix of the reference's sort order -- appended as
+//                  (p, ~id) keys; the row's last workgroup sorts them in LDS
+//                  (counting sort by p bin, rank inside a bin) and walks the
+//                  exact cumulative to the cut-off and the draw;
+//   k_topp_fallback rows whose selected set does not fit in LDS, or whose
+//                  cumulative does not reach top_p inside it: every
+//                  candidate sorted in a global scratch slot.
 #include <limits.h>
 
 #include "pz_device.h"
@@ -34,15 +36,11 @@
 #include "pz_launch.h"
 #include "pz_rowpass.h"
 #include "pz_sort.h"
+#include "pz_split.h"
 
 namespace {
 
-// Histogram of e in (0, 1]: bins of 1/128 binade, e >= 2^-29 (candidates are
-// >= expf(-20) ~ 2.06e-9); smaller values fall in bin 0.
-constexpr int EBIN_BASE = 98 << 7;
-constexpr int EBINS = (127 << 7) - EBIN_BASE + 1;
 constexpr int TOPP_CAP_MAX = 8192;
-constexpr int EBINS_BYTES = ((EBINS * 4 + 15) / 16) * 16;
 // Gathered lists of at least TOPP_BINSORT_MIN keys are ordered by a counting
 // sort over PBINS bins of p (1/128 binade each, 32 binades below 1.0) and a
 // rank count inside each bin; smaller ones by a bitonic sort.
@@ -50,15 +48,21 @@ constexpr int PBINS = 4 * PZ_RB;
 constexpr int TOPP_BINSORT_MIN = 1024;
 constexpr int TOPP_BIN_MAX = 256;  // larger bins: bitonic sort
 
+// Row states (PzRowState::i[0]).
+constexpr int TP_OPEN = 0, TP_DONE = 1;
+// PzRowState fields used here: f[0] p threshold, f[1] gate on y - M,
+// i[1] every candidate gathered, i[2] gathered count, i[3] overflow,
+// i[4] candidates in the selected bins.
+
 __device__ __forceinline__ int ebin(float e) {
-  const int b = (int)(__float_as_uint(e) >> 16) - EBIN_BASE;
-  return b < 0 ? 0 : (b >= EBINS ? EBINS - 1 : b);
+  const int b = (int)(__float_as_uint(e) >> 17) - PZ_TOPP_NB_BASE;
+  return b < 0 ? 0 : (b >= PZ_TOPP_NB ? PZ_TOPP_NB - 1 : b);
 }
 __device__ __forceinline__ float ebin_lo(int b) {
-  return __uint_as_float((uint32_t)(b + EBIN_BASE) << 16);
+  return __uint_as_float((uint32_t)(b + PZ_TOPP_NB_BASE) << 17);
 }
 __device__ __forceinline__ float ebin_mid(int b) {
-  return __uint_as_float(((uint32_t)(b + EBIN_BASE) << 16) | 0x8000u);
+  return __uint_as_float(((uint32_t)(b + PZ_TOPP_NB_BASE) << 17) | 0x10000u);
 }
 
 __device__ __forceinline__ uint64_t topp_key(float p, int id) {
@@ -68,20 +72,19 @@ __device__ __forceinline__ int key_id(uint64_t k) { return (int)(0xffffffffu - (
 __device__ __forceinline__ float key_p(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
 
 struct ToppShared {
-  PzPass1Shared p1;
+  int merged;  // waves done merging the histograms
   uint32_t wtot[PZ_RB / 64];
   uint32_t bmax;
   float sum;
   int bsel;
   uint32_t nsel;
-  int count;
-  int over;
   int cutoff;
   int first;
 };
 
 // Wave-aggregated append of up to one key per lane into buf (capacity cap).
-__device__ __forceinline__ void append_key(int* count, int* over, uint64_t* buf, int cap,
+template <class CountPtr>
+__device__ __forceinline__ void append_key(CountPtr count, int* over, uint64_t* buf, int cap,
                                            bool want, uint64_t key) {
   const uint64_t ball = __ballot(want);
   if (!ball) return;
@@ -103,7 +106,7 @@ __device__ __forceinline__ void append_key(int* count, int* over, uint64_t* buf,
 // keeps all of them, top_p.c:81).  Returns the cut-off, or -1 when the
 // list is a strict prefix whose cumulative stays below top_p.
 __device__ __forceinline__ int nucleus_cutoff(const uint64_t* keys, float* cum, int m, float top_p,
-                              bool all_gathered, int* cutoff_sh) {
+                                              bool all_gathered, int* cutoff_sh) {
   const int tid = threadIdx.x, lane = tid & 63;
   if (tid < 64) {
     PzAcc st;
@@ -132,8 +135,8 @@ __device__ __forceinline__ int nucleus_cutoff(const uint64_t* keys, float* cum, 
   return *cutoff_sh;
 }
 
-__device__ __forceinline__ void nucleus_draw(const uint64_t* keys, const float* cum, int cutoff, float uu,
-                             int32_t* id_out, float* p_out) {
+__device__ __forceinline__ void nucleus_draw(const uint64_t* keys, const float* cum, int cutoff,
+                                             float uu, int32_t* id_out, float* p_out) {
   const float trunc_sum = cum[cutoff - 1];
   const float r = uu * trunc_sum;
   int lo = 0, hi = cutoff;
@@ -157,387 +160,523 @@ __device__ __forceinline__ int pbin(uint64_t key) {
   return q < PBINS - 1 ? q : PBINS - 1;
 }
 
-// The (p desc, id asc) order of keys[0..m) without moving them: a counting
-// sort by p bin into perm1 (any order inside a bin), then each key's rank
-// inside its bin puts its slot at its sorted position in perm2.  Returns
-// false, having done nothing usable, when a bin holds more than
-// TOPP_BIN_MAX keys.  Every thread calls it.
-__device__ __forceinline__ bool binned_order(const pz_lds_u64* keys, int m, pz_lds_u16* perm1,
-                                             pz_lds_u16* perm2, pz_lds_u32b* bcnt,
-                                             pz_lds_u32b* bstart, ToppShared& S) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int i = tid; i < PBINS; i += PZ_RB) bcnt[i] = 0u;
-  if (tid == 0) S.bmax = 0u;
-  __syncthreads();
-  for (int i = tid; i < m; i += PZ_RB) atomicAdd((uint32_t*)&bcnt[pbin(keys[i])], 1u);
-  __syncthreads();
-  // exclusive scan over the bins; thread t owns bins 4t .. 4t+3
-  uint32_t c[4], local = 0, mx = 0;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    c[j] = bcnt[4 * tid + j];
-    local += c[j];
-    mx = c[j] > mx ? c[j] : mx;
-  }
-  const uint32_t incl = pz_wave_scan_u32(local);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t o = __shfl_xor(mx, off, 64);
-    mx = o > mx ? o : mx;
-  }
-  if (lane == 63) S.wtot[w] = incl;
-  if (lane == 0) atomicMax(&S.bmax, mx);
-  __syncthreads();
-  uint32_t run = incl - local;
-  for (int j = 0; j < w; j++) run += S.wtot[j];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    bstart[4 * tid + j] = run;
-    bcnt[4 * tid + j] = run;  // cursor
-    run += c[j];
-  }
-  __syncthreads();
-  if (S.bmax > (uint32_t)TOPP_BIN_MAX) return false;
-  for (int i = tid; i < m; i += PZ_RB) {
-    const uint32_t pos = atomicAdd((uint32_t*)&bcnt[pbin(keys[i])], 1u);
-    perm1[pos] = (uint16_t)i;
-  }
-  __syncthreads();
-  for (int j = tid; j < m; j += PZ_RB) {
-    const int i = perm1[j];
-    const uint64_t key = keys[i];
-    const int q = pbin(key);
-    const uint32_t b0 = bstart[q], b1 = bcnt[q];
-    uint32_t r = 0;
-    for (uint32_t x = b0; x < b1; x++) r += keys[perm1[x]] > key ? 1u : 0u;
-    perm2[b0 + r] = (uint16_t)i;
-  }
-  __syncthreads();
-  return true;
-}
-
-// The sorted probabilities (p of keys[perm[j]], j < m) as the terms of an
-// exact-sum records pass: the values are exact, so every increment is too.
-struct SortedTerms {
-  typedef float Raw[4];
-  const pz_lds_u64* keys;
-  const pz_lds_u16* perm;
-  int m;
-  __device__ __forceinline__ int load(int e0, Raw& r) const {
-#pragma unroll
-    for (int c = 0; c < 4; c++) r[c] = e0 + c < m ? key_p(keys[perm[e0 + c]]) : 0.0f;
-    const int n = m - e0;
-    return n < 0 ? 0 : (n > 4 ? 4 : n);
-  }
-  __device__ __forceinline__ void prep(int, int, Raw& r, float (&a)[4]) const {
-#pragma unroll
-    for (int c = 0; c < 4; c++) a[c] = r[c];
-  }
-  __device__ __forceinline__ void observe(int, const Raw&, const float (&)[4]) {}
-  __device__ __forceinline__ uint32_t inc(const Raw&, const float (&a)[4], int c, uint32_t g,
-                                          uint32_t* cls) const {
-    return pz_inc(a[c], g, cls);
-  }
-  __device__ __forceinline__ void cache_put(pz_lds_f32* base, const Raw& r,
-                                            const float (&)[4]) const {
-    pz_f4 q;
-    q.x = r[0];
-    q.y = r[1];
-    q.z = r[2];
-    q.w = r[3];
-    ((pz_lds_f4*)base)[threadIdx.x & 63] = q;
-  }
-  __device__ __forceinline__ void cache_terms(const pz_lds_f32* base, float (&v)[4]) const {
-    const pz_f4 q = ((const pz_lds_f4*)base)[threadIdx.x & 63];
-    v[0] = q.x;
-    v[1] = q.y;
-    v[2] = q.z;
-    v[3] = q.w;
-  }
-  __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
-    Raw r;
-    load(pz_seg_e0(k), r);
-#pragma unroll
-    for (int c = 0; c < 4; c++) v[c] = r[c];
-  }
-};
-
-// Cut-off and draw over the order in perm2 (top_p.c:80-105) with exact-sum
-// records of the sorted probabilities: the cumulative walk stops at the
-// first running sum >= top_p (the cut-off; its sum is the truncated mass),
-// a second walk over the same records at the first running sum > r.
-// Returns the picked sorted position, or -1 when the list is a strict prefix
-// whose cumulative stays below top_p.  Every thread calls it; rec is LDS of
-// pz_rec_bytes(m) bytes.
-__device__ __forceinline__ int binned_pick(const pz_lds_u64* keys, const pz_lds_u16* perm2, int m,
-                                           float top_p, bool all_gathered, float uu, char* rec,
-                                           PzRecShared& RS, int* sh) {
-  SortedTerms X;
-  X.keys = keys;
-  X.perm = perm2;
-  X.m = m;
-  const int ntiles = pz_tiles(m), nseg = ntiles * PZ_SEGS_PER_TILE;
-  const PzRec REC = pz_rec_at(rec, nseg);
-  pz_record_pass(X, ntiles, REC, RS, __builtin_inff());
-  if (threadIdx.x < 64) {
-    PzAcc st;
-    st.n = 0;
-    st.g = 1;
-    const int hit = pz_rec_walk(st, REC, nseg, top_p, PZ_STOP_GE, X);
-    int pick = -1;
-    int cutoff = hit >= 0 && hit < m ? hit + 1 : -1;
-    if (cutoff < 0 && all_gathered) cutoff = m;  // st then holds the whole sum
-    if (cutoff > 0) {
-      const float r = uu * pz_acc_value(st);  // trunc_sum: the cumulative at the cut-off
-      PzAcc s2;
-      s2.n = 0;
-      s2.g = 1;
-      const int d = pz_rec_walk(s2, REC, nseg, r, PZ_STOP_GT, X);
-      pick = d >= 0 && d < cutoff ? d : 0;
-    }
-    if (threadIdx.x == 0) *sh = pick;
-  }
-  __syncthreads();
-  return *sh;
-}
-
-// Candidate terms with the e histogram as observer.
+// Candidate terms with the e histogram (LDS, PZ_TOPP_NB bins) as observer.
 template <bool VEC>
 struct ToppTerms : PzExpTerms<PzRow<VEC>> {
-  uint32_t* ehist;
+  pz_lds_u32b* ehist;
   __device__ __forceinline__ void observe(int, const float (&)[4], const float (&a)[4]) {
 #pragma unroll
     for (int c = 0; c < 4; c++)
-      if (a[c] > 0.0f) atomicAdd(&ehist[ebin(a[c])], 1u);
+      if (a[c] > 0.0f) atomicAdd((uint32_t*)&ehist[ebin(a[c])], 1u);
   }
 };
 
+// The row's chain with penalty tables for the ids [lo, hi).
 template <bool VEC>
-__global__ __launch_bounds__(PZ_RB) void k_topp(
-    const float* __restrict__ logits, long ld, int V, const int32_t* __restrict__ rows,
-    const pz_row_params_dev* __restrict__ params, int n_params,
-    const int32_t* __restrict__ hist, int H, int hcap, int pen_bytes, int cap,
-    const float* __restrict__ u, int32_t* __restrict__ ids_out, float* __restrict__ p_out,
-    pz_scratch sc) {
-  extern __shared__ __align__(16) char lds[];
-  __shared__ ToppShared S;
-  __shared__ PzRecShared RS;
-  __shared__ uint64_t etab[32];
-  const pz_lds_u64* et = (const pz_lds_u64*)etab;
-  pz_etab_fill((pz_lds_u64*)etab);  // ordered by pz_pass1's barriers
-  const int row = pz_row_of(rows, blockIdx.x);
-  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-
+__device__ __forceinline__ PzRow<VEC> topp_row(const float* logits, long ld, int row, int V,
+                                              const pz_row_params_dev& prm, char* lds, int lo,
+                                              int hi, int hcap, const int32_t* hist, int H) {
   PzRow<VEC> R;
   R.x = logits + (long)row * ld;
   R.V = V;
   R.T = PzTemp::of(prm);
-  pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
+  pz_penalty_build_range<PZ_SP_BLOCK>(R.P, lds, V, lo, hi, hcap,
+                                      hist ? hist + (long)row * H : nullptr, H, prm);
+  return R;
+}
 
-  const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
-  char* reg = lds + pen_bytes;
-  // phase A: records + e histogram; phase B (overlaid): gathered keys + sums
-  uint32_t* ehist = reinterpret_cast<uint32_t*>(reg);
-  const PzRec REC = pz_rec_at(reg + EBINS_BYTES, nseg);
-  uint64_t* keys = reinterpret_cast<uint64_t*>(reg);
-  float* cum = reinterpret_cast<float*>(keys + cap);
+#define TOPP_ARGS                                                                            \
+  const float *__restrict__ logits, long ld, int V, const int32_t *__restrict__ rows,        \
+      const pz_row_params_dev *__restrict__ params, int n_params,                            \
+      const int32_t *__restrict__ hist, int H, int hcap, int nseg, int spw, int S,           \
+      PzSplitWs ws, const float *__restrict__ u, int32_t *__restrict__ ids_out,             \
+      float *__restrict__ p_out, pz_scratch sc
 
-  for (int i = tid; i < EBINS; i += PZ_RB) ehist[i] = 0u;
+// Rows the stat pass settles: y[0] NaN (the reference's maximum is NaN, no
+// candidate passes, argmax of a row starting with NaN -> 0) and an infinite
+// or absent maximum (every e is expf(NaN): the first y == max).
+__device__ __forceinline__ bool topp_degenerate(uint32_t flags) {
+  return (flags & (PZ_RS_Y0NAN | PZ_RS_NONFIN)) != 0;
+}
 
-  // ---- pass 1: maximum
-  const float M = pz_pass1<8>(R, ntiles, S.p1);
-  const float y0 = S.p1.y0;
-  if (y0 != y0) {
-    // max_val = NaN: no candidate passes, argmax of a row starting with NaN -> 0
-    if (tid == 0) {
-      ids_out[row] = 0;
-      if (p_out) p_out[row] = 1.0f;
-    }
-    return;
+// ---- pass 1: slice maxima (HBM) -------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_max(TOPP_ARGS) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  const int row = pz_row_of(rows, blockIdx.y);
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const PzSlice sl = pz_sp_slice(nseg, spw);
+  if (threadIdx.x == 0) SS.any = 0u;
+  const PzRow<VEC> R =
+      topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
+  __syncthreads();
+  pz_sp_stat_slice(R, row, sl, ws, SS, false);
+}
+
+// ---- pass 2: estimated mass of the candidates per segment -----------------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_est(TOPP_ARGS) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  const int row = pz_row_of(rows, blockIdx.y);
+  pz_sp_row_stat(row, S, ws, SS);
+  if (topp_degenerate(SS.any)) return;
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const PzSlice sl = pz_sp_slice(nseg, spw);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const PzRow<VEC> R =
+      topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
+  const float M = SS.M, thr = M - 20.0f;
+  float* seg_s = ws.seg_s + (size_t)row * ws.nsc;
+  for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
+    float y[4];
+    const int n = R.get(k * PZ_SP_SEG + 4 * lane, y);
+    float t = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (c < n && y[c] >= thr) t += pz_fast_exp(y[c] - M);
+    t = pz_wave_sum(t);
+    if (lane == 0) seg_s[k] = t;
   }
-  if (!(M > -__builtin_inff() && M < __builtin_inff())) {
-    // every e is expf(NaN): the sort leaves candidates in id order and no
-    // comparison succeeds -> the first candidate, i.e. the first y == max
-    if (tid == 0) S.first = INT_MAX;
-    __syncthreads();
-    int mine = INT_MAX;
-    for (int t = 0; t < ntiles; t++) {
-      float y[4];
-      const int e0 = pz_tile_e0(t);
-      const int n = R.get(e0, y);
-      for (int c = 0; c < n; c++)
-        if (y[c] == M && e0 + c < mine) mine = e0 + c;
-    }
-    atomicMin(&S.first, mine);
-    __syncthreads();
-    if (tid == 0) {
-      ids_out[row] = S.first;
-      if (p_out) p_out[row] = __builtin_nanf("");
-    }
-    return;
-  }
-  const float thr = M - 20.0f;
+}
 
-  // ---- records of the exact candidate terms (+ e histogram)
+// ---- pass 3: records of the exact candidate terms + mass histogram -------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_rec(TOPP_ARGS, int pen_bytes) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = pz_row_of(rows, blockIdx.y);
+  pz_sp_row_stat(row, S, ws, SS);
+  if (topp_degenerate(SS.any)) return;
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x;
+  const PzSlice sl = pz_sp_slice(nseg, spw);
+  const float M = SS.M;
+  pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
+  for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) ehist[i] = 0u;
+  const PzEstAbs est{ws.seg_s + (size_t)row * ws.nsc};
+  const float carry = pz_sp_prefix(est, sl.k0, SS);
+  pz_sp_predict(est, carry, row, sl, ws, SS);
   ToppTerms<VEC> X;
-  X.R = R;
+  X.R = topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
   X.M = M;
-  X.thr = thr;
+  X.thr = M - 20.0f;
   X.inv = 1.0f;
   X.as_p = false;
   X.et = et;
   X.ehist = ehist;
-  pz_record_pass(X, ntiles, REC, RS, __builtin_inff());
+  __syncthreads();
+  pz_sp_records(X, row, sl, ws);
+  __syncthreads();
+  uint32_t* gh = ws.hist + ((size_t)blockIdx.y * S + blockIdx.x) * PZ_TOPP_NB;
+  for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) gh[i] = ehist[i];
+}
 
-  // ---- exact normaliser (wave 0) || nucleus bin selection (wave 1)
-  if (w == 0) {
-    PzAcc st;
-    st.n = 0;
-    st.g = 1;
-    pz_rec_walk(st, REC, nseg, 0.0f, PZ_STOP_NONE, X);
-    if (lane == 0) S.sum = pz_acc_value(st);
-  } else if (w == 1) {
-    float tot = 0.0f;
-    uint32_t ncand = 0;
-    for (int b = lane; b < EBINS; b += 64) {
-      const uint32_t c = ehist[b];
-      tot += (float)c * ebin_mid(b);
-      ncand += c;
+// ---- pass 4 (one workgroup per row): exact normaliser and nucleus bins ----
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walk(TOPP_ARGS, int pen_bytes, int nc) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ ToppShared T;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = pz_row_of(rows, blockIdx.x);
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  pz_sp_row_stat(row, S, ws, SS);
+  const float M = SS.M;
+  const uint32_t flags = SS.any;
+  PzRowState& rs = ws.rs[row];
+  const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
+  __syncthreads();  // the expf table
+  if (flags & PZ_RS_Y0NAN) {
+    if (tid == 0) {
+      ids_out[row] = 0;
+      if (p_out) p_out[row] = 1.0f;
+      rs.i[0] = TP_DONE;
     }
-    tot = pz_wave_sum(tot);
-    ncand = pz_wave_sum_u32(ncand);
-    const float goal = (prm.top_p * 1.006f + 2e-4f) * tot;
-    float carry = 0.0f;
-    uint32_t ccarry = 0;
-    int bsel = 0;
-    uint32_t nsel = ncand;
-    for (int b0 = EBINS - 1; b0 >= 0; b0 -= 64) {
-      const int b = b0 - lane;
-      float m = 0.0f;
-      uint32_t c = 0;
-      if (b >= 0) {
-        c = ehist[b];
-        m = (float)c * ebin_mid(b);
-      }
-      const float incl = pz_wave_scan_f32(m);
-      const uint32_t cincl = pz_wave_scan_u32(c);
-      const uint64_t ball = __ballot(b >= 0 && carry + incl >= goal);
-      if (ball) {
-        const int L = (int)__builtin_ctzll(ball);
-        bsel = b0 - L;
-        nsel = ccarry + pz_readlane_u32(cincl, L);
-        break;
-      }
-      carry += pz_readlane_f32(incl, 63);
-      ccarry += pz_readlane_u32(cincl, 63);
-    }
-    if (lane == 0) {
-      S.bsel = bsel;
-      S.nsel = nsel;
-    }
+    return;
   }
-  if (tid == 0) {
-    S.count = 0;
-    S.over = 0;
+  if (flags & PZ_RS_NONFIN) {
+    if (tid == 0) T.first = INT_MAX;
+    __syncthreads();
+    int mine = INT_MAX;
+    for (int e0 = 4 * tid; e0 < V; e0 += 4 * PZ_SP_BLOCK) {
+      float y[4];
+      const int n = R.get(e0, y);
+      for (int c = 0; c < n; c++)
+        if (y[c] == M && e0 + c < mine) mine = e0 + c;
+    }
+    atomicMin(&T.first, mine);
+    __syncthreads();
+    if (tid == 0) {
+      ids_out[row] = T.first;
+      if (p_out) p_out[row] = __builtin_nanf("");
+      rs.i[0] = TP_DONE;
+    }
+    return;
+  }
+  pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
+  PzExpTerms<PzRow<VEC>> X;
+  X.R = R;
+  X.M = M;
+  X.thr = M - 20.0f;
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = et;
+  const size_t walk_off = ((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15;
+  if (tid == 0) T.merged = 0;
+  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, lds + walk_off, SS);
+
+  if (w == 0) {
+    // the exact normaliser
+    PzAcc st;
+    pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+    if (lane == 0) T.sum = pz_acc_value(st);
+  } else {
+    // meanwhile: merge the row's histograms (waves 1..15), then wave 1 picks
+    // the nucleus bins once every merging wave has signalled
+    for (int i = tid - 64; i < PZ_TOPP_NB; i += PZ_SP_BLOCK - 64) {
+      uint32_t c = 0;
+      for (int s2 = 0; s2 < S; s2++) c += ws.hist[((size_t)blockIdx.x * S + s2) * PZ_TOPP_NB + i];
+      ehist[i] = c;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) __hip_atomic_fetch_add(&T.merged, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (w == 1) {
+      while (__hip_atomic_load(&T.merged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
+             PZ_SP_WAVES - 1)
+        __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      float tot = 0.0f;
+      uint32_t ncand = 0;
+      for (int b = lane; b < PZ_TOPP_NB; b += 64) {
+        const uint32_t c = ehist[b];
+        tot += (float)c * ebin_mid(b);
+        ncand += c;
+      }
+      tot = pz_wave_sum(tot);
+      ncand = pz_wave_sum_u32(ncand);
+      // a bin's mass is known to within half its width (0.55 %): the
+      // selected set's estimate must clear top_p by more than that
+      const float goal = (prm.top_p * 1.012f + 3e-4f) * tot;
+      float carry = 0.0f;
+      uint32_t ccarry = 0;
+      int bsel = 0;
+      uint32_t nsel = ncand;
+      for (int b0 = PZ_TOPP_NB - 1; b0 >= 0; b0 -= 64) {
+        const int b = b0 - lane;
+        float m = 0.0f;
+        uint32_t c = 0;
+        if (b >= 0) {
+          c = ehist[b];
+          m = (float)c * ebin_mid(b);
+        }
+        const float incl = pz_wave_scan_f32(m);
+        const uint32_t cincl = pz_wave_scan_u32(c);
+        const uint64_t ball = __ballot(b >= 0 && carry + incl >= goal);
+        if (ball) {
+          const int L = (int)__builtin_ctzll(ball);
+          bsel = b0 - L;
+          nsel = ccarry + pz_readlane_u32(cincl, L);
+          break;
+        }
+        carry += pz_readlane_f32(incl, 63);
+        ccarry += pz_readlane_u32(cincl, 63);
+      }
+      if (lane == 0) {
+        T.bsel = bsel;
+        T.nsel = nsel;
+      }
+    }
   }
   __syncthreads();
+  if (tid == 0) {
+    const float inv = 1.0f / T.sum;  // top_p.c:72
+    const bool all = T.bsel == 0;
+    const float e_lo = ebin_lo(T.bsel);
+    rs.M = M;
+    rs.sum = T.sum;
+    rs.inv = inv;
+    rs.f[0] = all ? 0.0f : e_lo * inv;
+    rs.f[1] = all ? -__builtin_inff() : __logf(e_lo) - 0.01f;
+    rs.i[0] = TP_OPEN;
+    rs.i[1] = all ? 1 : 0;
+    rs.i[2] = 0;
+    rs.i[3] = 0;
+    rs.i[4] = (int)T.nsel;
+    if (T.nsel > (uint32_t)ws.capg) {
+      // the selected set cannot fit: straight to the fallback
+      const int q = atomicAdd(&sc.counters[0], 1);
+      sc.fb_list[q] = row;
+      rs.i[0] = TP_DONE;
+    }
+  }
+}
 
-  const float inv = 1.0f / S.sum;  // top_p.c:72
-  const bool all = S.bsel == 0;
-  bool fallback = S.nsel > (uint32_t)cap;
-  if (!fallback) {
-    // ---- pass 3: gather every candidate with p >= p_thr (a prefix of the
-    // (p desc, id asc) order) into LDS.  A cheap gate on y - M picks the
-    // lanes' possible candidates (a superset: 0.01 below the bin edge); the
-    // exact p of those is evaluated one candidate per lane per trip, and the
-    // survivors are appended with one LDS atomic per wave per trip.
-    const float e_lo = ebin_lo(S.bsel);
-    const float p_thr = all ? 0.0f : e_lo * inv;
-    const float dgate = all ? -__builtin_inff() : __logf(e_lo) - 0.01f;
-    constexpr int U2 = 8;
-    for (int t0 = 0; t0 < ntiles; t0 += U2) {
-      float y[U2][4];
-      int nv[U2];
-#pragma unroll
-      for (int uu = 0; uu < U2; uu++) {
-        const int t = t0 + uu < ntiles ? t0 + uu : ntiles - 1;  // unconditional loads
-        const int nl = R.load(pz_tile_e0(t), y[uu]);
-        nv[uu] = t0 + uu < ntiles ? nl : 0;
-      }
+// ---- pass 5: gather the selected candidates; sort, cut-off and draw ------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_gather(TOPP_ARGS) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = pz_row_of(rows, blockIdx.y);
+  const PzRowState rs0 = ws.rs[row];
+  if (rs0.i[0] == TP_DONE) return;
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const PzSlice sl = pz_sp_slice(nseg, spw);
+  const float M = rs0.M, thr = M - 20.0f, inv = rs0.inv;
+  const float p_thr = rs0.f[0], dgate = rs0.f[1];
+  PzRowState& rs = ws.rs[row];
+  uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
+  {
+    const PzRow<VEC> R =
+        topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
+    __syncthreads();  // the expf table
+    // A cheap gate on y - M picks each lane's possible candidates (a
+    // superset: 0.01 below the bin edge); their exact p is evaluated one per
+    // lane per trip and the survivors appended with one atomic per wave.
+    for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      float y[4];
+      const int n = R.get(e0, y);
       uint32_t want = 0;
 #pragma unroll
-      for (int uu = 0; uu < U2; uu++) {
-        const int e0 = pz_tile_e0(t0 + uu);
-        R.apply(e0, nv[uu], y[uu]);
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          const float yy = y[uu][c];
-          const bool w = (c < nv[uu]) & (yy >= thr) & ((yy - M) >= dgate);
-          want |= (w ? 1u : 0u) << (4 * uu + c);
-        }
+      for (int c = 0; c < 4; c++) {
+        const bool wnt = (c < n) & (y[c] >= thr) & ((y[c] - M) >= dgate);
+        want |= (wnt ? 1u : 0u) << c;
       }
-      const int e00 = pz_tile_e0(t0);
       while (__ballot(want != 0u)) {
         bool take = false;
         uint64_t key = 0;
         if (want) {
           const uint32_t j = (uint32_t)__builtin_ctz(want);
           want &= want - 1u;
-          float yy = y[0][0];
-#pragma unroll
-          for (int uu = 0; uu < U2; uu++)
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-              if (j == (uint32_t)(4 * uu + c)) yy = y[uu][c];
+          const float yy = j == 0 ? y[0] : (j == 1 ? y[1] : (j == 2 ? y[2] : y[3]));
           const float p = pz_expf_l(yy - M, et) * inv;
           take = p >= p_thr;
-          key = topp_key(p, e00 + (int)(j >> 2) * PZ_TILE + (int)(j & 3u));
+          key = topp_key(p, e0 + (int)j);
         }
-        append_key(&S.count, &S.over, keys, cap, take, key);
+        append_key(&rs.i[2], &rs.i[3], gkeys, ws.capg, take, key);
       }
     }
-    __syncthreads();
-    fallback = S.over != 0;
   }
-  if (!fallback) {
-    const int m = S.count;
-    pz_lds_u64* lkeys = (pz_lds_u64*)keys;
-    pz_lds_u16* perm1 = (pz_lds_u16*)cum;  // the running-sum area holds two u16 orders
-    pz_lds_u16* perm2 = perm1 + cap;
-    pz_lds_u32b* bcnt = (pz_lds_u32b*)(cum + cap);
+}
+
+// The sorted probabilities (p of bkeys[perm[j]], j < m, 0 past m) for the
+// walk over the sorted list.
+struct SortedSeg {
+  const pz_lds_u64* bkeys;
+  const pz_lds_u16* perm;
+  int m;
+  __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
+    const int j0 = k * PZ_SP_SEG + 4 * ((int)threadIdx.x & 63);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = j0 + c < m ? key_p(bkeys[perm[j0 + c]]) : 0.0f;
+  }
+};
+
+// ---- pass 6 (one workgroup per row): order, cut-off and draw ------------
+// The gathered keys are counted into bins of p (1/128 binade) straight from
+// global memory and scattered into LDS in bin order; each key's rank inside
+// its bin (independent reads, no chains) gives the (p desc, id asc) order;
+// the cumulative over that order is an exact-sum walk (records of the
+// sorted list, pz_sp_walk): first running sum >= top_p is the cut-off and
+// its sum the truncated mass (top_p.c:80-93); a second walk over the same
+// records stops at the first running sum > r (:96-105).
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap, int nc) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ ToppShared T;
+  const int row = pz_row_of(rows, blockIdx.x);
+  const PzRowState rs0 = ws.rs[row];
+  if (rs0.i[0] == TP_DONE) return;
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int m = rs0.i[2];
+  const bool all = rs0.i[1] != 0;
+  const uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
+  bool done = false;
+  if (rs0.i[3] == 0 && m <= cap && m > 0) {
+    pz_lds_u64* bkeys = (pz_lds_u64*)lds;                          // [cap]
+    pz_lds_u16* perm = (pz_lds_u16*)(lds + (size_t)cap * 8);       // [cap]
+    char* region = lds + (((size_t)cap * 10 + 15) & ~(size_t)15);  // bins, then the walk
+    pz_lds_u32b* bcnt = (pz_lds_u32b*)region;
     pz_lds_u32b* bstart = bcnt + PBINS;
-    if (m >= TOPP_BINSORT_MIN && binned_order(lkeys, m, perm1, perm2, bcnt, bstart, S)) {
-      // the bin arrays are free again: they hold the records of the sorted list
-      const int pick = binned_pick(lkeys, perm2, m, prm.top_p, all, u[row], (char*)bcnt, RS,
-                                   &S.cutoff);
-      if (pick >= 0) {
-        if (tid == 0) {
-          const uint64_t k = lkeys[perm2[pick]];
-          ids_out[row] = key_id(k);
-          if (p_out) p_out[row] = key_p(k);
-        }
-        return;
-      }
-    } else {
+    if (m < TOPP_BINSORT_MIN) {
+      // small lists: bitonic sort of the keys, then the lane-ordered walks
       int N = 1;
       while (N < m) N <<= 1;
-      for (int i = m + tid; i < N; i += PZ_RB) keys[i] = 0ull;
+      for (int i = tid; i < N; i += PZ_SP_BLOCK) bkeys[i] = i < m ? gkeys[i] : 0ull;
       __syncthreads();
-      pz_bitonic_desc<PZ_RB>(lkeys, N);
-      const int cutoff = nucleus_cutoff(keys, cum, m, prm.top_p, all, &S.cutoff);
+      pz_bitonic_desc<PZ_SP_BLOCK>(bkeys, N);
+      uint64_t* kk = reinterpret_cast<uint64_t*>(lds);
+      float* cum = reinterpret_cast<float*>(region);
+      const int cutoff = nucleus_cutoff(kk, cum, m, prm.top_p, all, &T.cutoff);
       if (cutoff > 0) {
         if (tid == 0)
-          nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
-        return;
+          nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
+        done = true;
+      }
+    } else {
+      for (int i = tid; i < PBINS; i += PZ_SP_BLOCK) bcnt[i] = 0u;
+      if (tid == 0) T.bmax = 0u;
+      __syncthreads();
+      for (int i = tid; i < m; i += PZ_SP_BLOCK)
+        atomicAdd((uint32_t*)&bcnt[pbin(gkeys[i])], 1u);
+      __syncthreads();
+      // exclusive scan over the bins; thread t owns bins 4t .. 4t+3
+      uint32_t c[4], local = 0, mx = 0;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        c[j] = bcnt[4 * tid + j];
+        local += c[j];
+        mx = c[j] > mx ? c[j] : mx;
+      }
+      const uint32_t incl = pz_wave_scan_u32(local);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = __shfl_xor(mx, off, 64);
+        mx = o > mx ? o : mx;
+      }
+      if (lane == 63) T.wtot[w] = incl;
+      if (lane == 0) atomicMax(&T.bmax, mx);
+      __syncthreads();
+      uint32_t run = incl - local;
+      for (int j = 0; j < w; j++) run += T.wtot[j];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        bstart[4 * tid + j] = run;
+        bcnt[4 * tid + j] = run;  // cursor
+        run += c[j];
+      }
+      __syncthreads();
+      const bool binned = T.bmax <= (uint32_t)TOPP_BIN_MAX;
+      if (binned) {
+        for (int i = tid; i < m; i += PZ_SP_BLOCK) {
+          const uint64_t key = gkeys[i];
+          const uint32_t pos = atomicAdd((uint32_t*)&bcnt[pbin(key)], 1u);
+          bkeys[pos] = key;
+        }
+        __syncthreads();
+        // rank inside the bin: every comparison independent of the others
+        for (int j = tid; j < m; j += PZ_SP_BLOCK) {
+          const uint64_t key = bkeys[j];
+          const int q = pbin(key);
+          const uint32_t b0 = bstart[q], b1 = bcnt[q];
+          uint32_t r = 0, x = b0;
+          for (; x + 4 <= b1; x += 4) {
+            const uint64_t k0 = bkeys[x], k1 = bkeys[x + 1], k2 = bkeys[x + 2], k3 = bkeys[x + 3];
+            r += (k0 > key ? 1u : 0u) + (k1 > key ? 1u : 0u) + (k2 > key ? 1u : 0u) +
+                 (k3 > key ? 1u : 0u);
+          }
+          for (; x < b1; x++) r += bkeys[x] > key ? 1u : 0u;
+          perm[b0 + r] = (uint16_t)j;
+        }
+        __syncthreads();
+        // records of the sorted list (this row's record area is free now)
+        const int nsl = (m + PZ_SP_SEG - 1) / PZ_SP_SEG;
+        SortedSeg X;
+        X.bkeys = bkeys;
+        X.perm = perm;
+        X.m = m;
+        float* est = ws.seg_s + (size_t)row * ws.nsc;
+        for (int k = w; k < nsl; k += PZ_SP_WAVES) {
+          float v[4];
+          X.seg(k, v);
+          const float t = pz_wave_sum((v[0] + v[1]) + (v[2] + v[3]));
+          if (lane == 0) est[k] = t;
+        }
+        __syncthreads();
+        PzSlice sl;
+        sl.k0 = 0;
+        sl.k1 = nsl;
+        pz_sp_predict(PzEstAbs{est}, 0.0f, row, sl, ws, SS);
+        {
+          uint32_t* rd = pz_sp_rec_d(ws, row);
+          uint32_t* rd2 = pz_sp_rec_d2(ws, row);
+          uint32_t* rgf = pz_sp_rec_gf(ws, row);
+          for (int k = w; k < nsl; k += PZ_SP_WAVES) {
+            float v[4];
+            X.seg(k, v);
+            const uint32_t gf = rgf[k];
+            const uint32_t g = gf & 0xffu;
+            const bool has2 = (gf & PZ_GF_HAS2) != 0;
+            uint32_t s1 = 0, s2 = 0;
+            bool d1 = false, d2 = false;
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+              uint32_t cls;
+              s1 += pz_inc(v[cc], g, &cls);
+              d1 |= cls != PZ_INC_PLAIN;
+              if (has2) {
+                s2 += pz_inc(v[cc], g - 1u, &cls);
+                d2 |= cls != PZ_INC_PLAIN;
+              }
+            }
+            s1 = pz_wave_sum_u32(s1);
+            s2 = pz_wave_sum_u32(s2);
+            const bool D1 = __ballot(d1) != 0, D2 = has2 && __ballot(d2) != 0;
+            if (lane == 0) {
+              rd[k] = s1;
+              rd2[k] = s2;
+              rgf[k] = gf | (D1 ? PZ_GF_DIRTY : 0u) | (D2 ? PZ_GF_DIRTY2 : 0u);
+            }
+          }
+        }
+        __syncthreads();
+        const PzWalk W = pz_sp_walk_setup(X, row, nsl, nc, ws, region, SS);
+        if (w == 0) {
+          PzAcc st;
+          const int hit = pz_sp_walk<PZ_STOP_GE>(st, W, prm.top_p, X);
+          int cutoff = hit >= 0 && hit < m ? hit + 1 : -1;
+          if (cutoff < 0 && all) cutoff = m;  // st then holds the whole sum
+          int pick = -1;
+          if (cutoff > 0) {
+            const float r = u[row] * pz_acc_value(st);  // trunc_sum: the cumulative at the cut-off
+            PzAcc s2;
+            const int d = pz_sp_walk<PZ_STOP_GT>(s2, W, r, X);
+            pick = d >= 0 && d < cutoff ? d : 0;
+          }
+          if (lane == 0) T.cutoff = pick;
+        }
+        __syncthreads();
+        if (T.cutoff >= 0) {
+          if (tid == 0) {
+            const uint64_t k = bkeys[perm[T.cutoff]];
+            ids_out[row] = key_id(k);
+            if (p_out) p_out[row] = key_p(k);
+          }
+          done = true;
+        }
+      } else {
+        // a bin too large for the rank count: bitonic sort of the whole list
+        __syncthreads();
+        int N = 1;
+        while (N < m) N <<= 1;
+        for (int i = tid; i < N; i += PZ_SP_BLOCK) bkeys[i] = i < m ? gkeys[i] : 0ull;
+        __syncthreads();
+        pz_bitonic_desc<PZ_SP_BLOCK>(bkeys, N);
+        uint64_t* kk = reinterpret_cast<uint64_t*>(lds);
+        float* cum = reinterpret_cast<float*>(region);
+        const int cutoff = nucleus_cutoff(kk, cum, m, prm.top_p, all, &T.cutoff);
+        if (cutoff > 0) {
+          if (tid == 0)
+            nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
+          done = true;
+        }
       }
     }
   }
-  // ---- queue the row for the fallback kernel
-  if (tid == 0) {
-    float* st = sc.row_stat + 4 * (long)row;
-    st[0] = M;
-    st[1] = inv;
+  if (!done && tid == 0) {
     const int q = atomicAdd(&sc.counters[0], 1);
     sc.fb_list[q] = row;
   }
@@ -549,7 +688,7 @@ template <bool VEC>
 __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
     const float* __restrict__ logits, long ld, int V,
     const pz_row_params_dev* __restrict__ params, int n_params,
-    const int32_t* __restrict__ hist, int H, int hcap, const float* __restrict__ u,
+    const int32_t* __restrict__ hist, int H, int hcap, PzSplitWs ws, const float* __restrict__ u,
     int32_t* __restrict__ ids_out, float* __restrict__ p_out, pz_scratch sc) {
   extern __shared__ __align__(16) char lds[];
   __shared__ int count, over, cutoff_sh;
@@ -569,8 +708,8 @@ __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
     R.V = V;
     R.T = PzTemp::of(prm);
     pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
-    const float M = sc.row_stat[4 * (long)row];
-    const float inv = sc.row_stat[4 * (long)row + 1];
+    const float M = ws.rs[row].M;
+    const float inv = ws.rs[row].inv;
     const float thr = M - 20.0f;
     if (tid == 0) {
       count = 0;
@@ -612,37 +751,72 @@ __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
   }
 }
 
-size_t topp_region_bytes(int V, int cap) {
-  const size_t a = (size_t)EBINS_BYTES + pz_rec_bytes(V);
-  // keys, running sums (or two u16 orders), then bin counts and starts or
-  // the records of the sorted list
-  const size_t bins = (size_t)PBINS * 8, recs = pz_rec_bytes(cap);
-  const size_t b = (size_t)cap * 12 + (bins > recs ? bins : recs);
-  return a > b ? a : b;
+
+size_t pen_region(const pz_launch& L, int n_ids) {
+  return L.pen_any ? (pz_penalty_lds_bytes(n_ids, L.hcap) + 15) & ~(size_t)15 : 0;
+}
+
+size_t max_sz(size_t a, size_t b) { return a > b ? a : b; }
+
+// LDS of the nucleus kernel for lists of up to cap keys with nc
+// pre-evaluated segments: keys and their order, then the bins / the running
+// sums of the small-list path / the walk over the sorted list.
+size_t topp_nucleus_bytes(int cap, int nc) {
+  const size_t head = ((size_t)cap * 10 + 15) & ~(size_t)15;
+  const size_t bins = (size_t)PBINS * 8, cum = (size_t)cap * 4;
+  const size_t walk = pz_sp_walk_lds((cap + PZ_SP_SEG - 1) / PZ_SP_SEG, nc);
+  return head + max_sz(max_sz(bins, cum), walk);
 }
 
 template <bool VEC>
 int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
-  const int pen = L.pen_any ? (int)((pz_penalty_lds_bytes(L.V, L.hcap) + 15) & ~(size_t)15) : 0;
-  const int fixed = (int)sizeof(ToppShared) + 64;
-  int cap = TOPP_CAP_MAX;
-  while (cap > 256 && pen + topp_region_bytes(L.V, cap) + fixed > (size_t)L.max_lds) cap >>= 1;
-  const size_t lds = pen + topp_region_bytes(L.V, cap);
-  if (lds + fixed > (size_t)L.max_lds) return -2;
-  auto kern = k_topp<VEC>;
+  const PzSplitWs& ws = L.ws;
+  const PzSplitPlan pl = pz_split_plan(L.V, n_rows, ws.smax);
+  if ((size_t)n_rows * pl.S > (size_t)ws.hslots || pl.nseg > ws.nsc) return -2;
+  const size_t fixed = 4096;  // static LDS of the kernels
+  const size_t pen_slice = pen_region(L, pl.spw * PZ_SP_SEG), pen_full = pen_region(L, L.V);
+  // slice passes: the slice's penalty tables (+ the histogram)
+  const size_t lds1 = pen_slice;
+  const size_t lds3 = pen_slice + PZ_TOPP_NB * 4;
+  // walk: the row's penalty tables, the merged histogram, the walk's arrays
+  const size_t walk_off = (pen_full + PZ_TOPP_NB * 4 + 15) & ~(size_t)15;
+  if (walk_off + fixed >= (size_t)L.max_lds) return -2;
+  const int nc = pz_sp_walk_nc(pl.nseg, (size_t)L.max_lds - walk_off - fixed);
+  if (nc < 1) return -2;
+  const size_t lds4 = walk_off + pz_sp_walk_lds(pl.nseg, nc);
+  // nucleus: the largest list (and its walk) that fits
+  int cap = TOPP_CAP_MAX < ws.capg ? TOPP_CAP_MAX : ws.capg;
+  const int nc6 = 16;
+  while (cap > 256 && topp_nucleus_bytes(cap, nc6) + fixed > (size_t)L.max_lds) cap >>= 1;
+  const size_t lds6 = topp_nucleus_bytes(cap, nc6);
+  if (lds6 + fixed > (size_t)L.max_lds || pen_full + fixed > (size_t)L.max_lds) return -2;
+  auto k1 = k_topp_max<VEC>;
+  auto k2 = k_topp_est<VEC>;
+  auto k3 = k_topp_rec<VEC>;
+  auto k4 = k_topp_walk<VEC>;
+  auto k5 = k_topp_gather<VEC>;
+  auto k6 = k_topp_nucleus<VEC>;
   auto fb = k_topp_fallback<VEC>;
-  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)lds) != hipSuccess)
-    return -1;
-  if (pen > 65536 && hipFuncSetAttribute((const void*)fb, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         pen) != hipSuccess)
-    return -1;
-  hipLaunchKernelGGL(kern, dim3(n_rows), dim3(PZ_RB), lds, L.stream, L.logits, L.ld, L.V, d_rows,
-                     L.params, L.n_params, L.hist, L.H, L.hcap, pen, cap, L.u, L.ids, L.p_out,
-                     L.sc);
+  const void* fns[7] = {(const void*)k1, (const void*)k2, (const void*)k3, (const void*)k4,
+                        (const void*)k5, (const void*)k6, (const void*)fb};
+  const size_t need[7] = {lds1, lds1, lds3, lds4, lds1, lds6, pen_full};
+  for (int i = 0; i < 7; i++)
+    if (need[i] > 65536 && hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)need[i]) != hipSuccess)
+      return -1;
+  const dim3 grid(pl.S, n_rows), block(PZ_SP_BLOCK);
+#define TOPP_PASS L.logits, L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, \
+                  pl.nseg, pl.spw, pl.S, ws, L.u, L.ids, L.p_out, L.sc
+  hipLaunchKernelGGL(k1, grid, block, lds1, L.stream, TOPP_PASS);
+  hipLaunchKernelGGL(k2, grid, block, lds1, L.stream, TOPP_PASS);
+  hipLaunchKernelGGL(k3, grid, block, lds3, L.stream, TOPP_PASS, (int)pen_slice);
+  hipLaunchKernelGGL(k4, dim3(n_rows), block, lds4, L.stream, TOPP_PASS, (int)pen_full, nc);
+  hipLaunchKernelGGL(k5, grid, block, lds1, L.stream, TOPP_PASS);
+  hipLaunchKernelGGL(k6, dim3(n_rows), block, lds6, L.stream, TOPP_PASS, cap, nc6);
+#undef TOPP_PASS
   const int fb_grid = n_rows < L.sc.fb_slots ? n_rows : L.sc.fb_slots;
-  hipLaunchKernelGGL(fb, dim3(fb_grid), dim3(PZ_RB), (size_t)pen, L.stream, L.logits, L.ld,
-                     L.V, L.params, L.n_params, L.hist, L.H, L.hcap, L.u, L.ids, L.p_out, L.sc);
+  hipLaunchKernelGGL(fb, dim3(fb_grid), dim3(PZ_RB), pen_full, L.stream, L.logits, L.ld, L.V,
+                     L.params, L.n_params, L.hist, L.H, L.hcap, ws, L.u, L.ids, L.p_out, L.sc);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
