@@ -119,6 +119,7 @@ PZ_API int pz_sampler_sync(pz_sampler *s);
  * CDF of r, threshold u_res[b] * sum(r)); when sum(r) == 0 it is drawn from p
  * with the categorical rule of generate.c:157-169.  If every draft is accepted
  * and has_bonus, a bonus token is drawn from p of target row K with u_res[b].
+ *   1 <= K <= 64 drafts per sequence.
  *   d_target: device [B, K + has_bonus, ld] fp32;  d_draft: device [B, K, ld]
  *   draft_ids, u_acc: host [B, K];  u_res: host [B]
  *   acc_len_out: host [B] accepted count;  ids_out: host [B, K+1] accepted

@@ -391,20 +391,26 @@ __device__ __forceinline__ int pz_rec_walk(PzAcc& st, const PzRec& R, int nseg, 
   return -1;
 }
 
-// Estimate of expf(d) with the hardware exp2: the fp32 product d*log2(e)
-// carries the error (relative < |d| * 2^-23.6 in the exponent, so the result
-// is within 2^-16.9 of expf(d) for d >= -104), plus v_exp_f32's own.  Only
-// used where pz_inc_from_estimate can prove the rounding it decides.
+// Estimate of expf(d) with the hardware exp2.  Its relative error grows with
+// |d|: the fp32 product d*log2(e) carries an absolute error of about
+// |d| * 2^-23 in the exponent, plus v_exp_f32's own.  The bound used below,
+// (|d| + 2) * 2^-23, is checked on every fp32 d in [-104, 0] where expf(d)
+// is normal.  Only used where pz_inc_from_estimate can prove the rounding it
+// decides.
 __device__ __forceinline__ float pz_fast_exp(float d) {
   return __builtin_amdgcn_exp2f(d * 1.44269504088896341f);
 }
 
-// Increment of a term at grid g from an estimate a (relative error below
-// 2^-16) when that settles the rounding; otherwise sets *exact (the caller
-// then evaluates the term exactly).  Grids below 2^-100 (only at the very
-// start of a row) always take the exact path, so estimates that underflow
-// cannot matter.
-__device__ __forceinline__ uint32_t pz_inc_from_estimate(float a, uint32_t g, bool* exact) {
+// Increment of a term at grid g from an estimate a of expf(d) (times a
+// factor rounded once more, for probabilities) when that settles the
+// rounding; otherwise sets *exact (the caller then evaluates the term
+// exactly).  The estimate's relative error is below (|d| + 3) * 2^-23; the
+// test uses twice that.  Grids below 2^-100 (only at the very start of a
+// row) always take the exact path, so estimates that underflow cannot
+// matter; so do terms of 2^20 grid steps or more, whose fraction fp32 no
+// longer resolves against the bound.
+__device__ __forceinline__ uint32_t pz_inc_from_estimate(float a, float d, uint32_t g,
+                                                         bool* exact) {
   *exact = false;
   if (g < 50u) {
     *exact = true;
@@ -412,13 +418,14 @@ __device__ __forceinline__ uint32_t pz_inc_from_estimate(float a, uint32_t g, bo
   }
   if (a == 0.0f) return 0u;
   const float t = a * __uint_as_float((277u - g) << 23);  // a / 2^(g - 150), exact
-  if (t >= 1024.0f) {
+  if (t >= 1048576.0f) {
     *exact = true;
     return 0u;
   }
   const float fl = floorf(t);
   const float fr = t - fl;
-  if (fabsf(fr - 0.5f) <= t * 0x1p-15f + 0x1p-20f) {
+  const float eps = (fabsf(d) + 3.0f) * 0x1p-22f;
+  if (fabsf(fr - 0.5f) <= t * eps + 0x1p-20f) {
     *exact = true;
     return 0u;
   }
@@ -453,7 +460,7 @@ struct PzExpTerms {
                                           uint32_t* cls) const {
     bool ex;
     *cls = PZ_INC_PLAIN;
-    const uint32_t i = pz_inc_from_estimate(a[c], g, &ex);
+    const uint32_t i = pz_inc_from_estimate(a[c], y[c] - M, g, &ex);
     return ex ? pz_inc(exact_term(y[c]), g, cls) : i;
   }
   // The cache keeps the exact terms, evaluated here by the segment's whole

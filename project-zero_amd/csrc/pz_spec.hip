@@ -14,13 +14,16 @@
 //   accepted and a bonus target row, the bonus token is drawn from p_K with
 //   u_res the same way.
 //
-// Kernels:
-//   k_spec_rows_*  one workgroup per logits row (all target rows, then all
-//                  draft rows): maximum, exact softmax normaliser, NaN/inf
-//                  degeneracy.
-//   k_spec_verify  one workgroup per sequence: acceptance tests (two logits
-//                  per draft), then the residual (exact Z and draw) or the
-//                  bonus / Z == 0 categorical draw.
+// Launches (rows split over several workgroups, pz_split.h):
+//   k_spec_stat   every target and draft row: maximum, segment estimates;
+//   k_spec_rec    their exact-term records;
+//   k_spec_walk   one workgroup per row: the exact softmax normaliser;
+//   k_spec_accept one wave per sequence: the acceptance tests (one draft per
+//                 lane), the row the token is drawn from;
+//   k_spec_vest   per sequence the estimated residual (or p) mass per segment;
+//   k_spec_vrec   its exact-term records;
+//   k_spec_vwalk  one workgroup per sequence: Z and the residual draw (or the
+//                 categorical draw from p), the output row.
 #include <string.h>
 
 #include "pz_device.h"
@@ -28,67 +31,44 @@
 #include "pz_launch.h"
 #include "pz_rowpass.h"
 #include "pz_sampler_impl.h"
+#include "pz_split.h"
 
 namespace {
 
-struct SpecRowsShared {
-  PzPass1Shared p1;
-  PzRecShared r;
+// Sequence outcomes after the acceptance tests.
+enum { SQ_DONE = 0, SQ_RES = 1, SQ_CAT = 2 };
+
+struct SpecSeq {
+  int mode;   // SQ_*
+  int js;     // accepted drafts
+  int qt, qd; // target / draft row of the draw (logits row indices)
+  int last;   // residual: the last x with r(x) > 0
+  int pad[3];
 };
 
-template <bool VEC>
-__device__ __forceinline__ void spec_rows_body(
-    const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
-    int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
-  extern __shared__ __align__(16) char lds[];
-  __shared__ SpecRowsShared S;
-  __shared__ uint64_t etab[32];
-  pz_etab_fill((pz_lds_u64*)etab);  // ordered by pz_pass1's barriers
-  const int q = blockIdx.x, tid = threadIdx.x;
-  const int NT = B * KT;
-  PzTempRow<VEC> R;
-  R.x = q < NT ? target + (long)q * ld : draft + (long)(q - NT) * ld;
-  R.V = V;
-  R.T = PzTemp::of(*prm);
-  const int ntiles = pz_tiles(V);
-  const PzRec REC = pz_rec_at(lds, ntiles * PZ_SEGS_PER_TILE);
-
-  const float M = pz_pass1<8>(R, ntiles, S.p1);
-  const bool bad = S.p1.any_nan || !(M > -__builtin_inff() && M < __builtin_inff());
-  float inv = __builtin_nanf("");
-  if (!bad) {
-    PzExpTerms<PzTempRow<VEC>> X;
-    X.R = R;
-    X.M = M;
-    X.thr = -__builtin_inff();
-    X.inv = 1.0f;
-    X.as_p = false;
-    X.et = (const pz_lds_u64*)etab;
-    inv = 1.0f / pz_exact_sum(X, ntiles, REC, S.r);
+struct SpecArgs {
+  const float* target;  // [B, KT, ld]
+  const float* draft;   // [B, K, ld]
+  long ld;
+  int V, B, K, KT, NT, NR, has_bonus;
+  PzTemp T;
+  const int32_t* draft_ids;  // [B, K]
+  const float* u_acc;        // [B, K]
+  const float* u_res;        // [B]
+  int32_t* acc_len;          // [B]
+  int32_t* ids_out;          // [B, K+1]
+  SpecSeq* seq;              // [B]
+  PzSplitWs ws;              // rows [0, NR): logits rows; [NR, NR + B): sequences
+  int nseg, spw, S, nc;
+  __device__ __forceinline__ const float* row(int q) const {
+    return q < NT ? target + (long)q * ld : draft + (long)(q - NT) * ld;
   }
-  if (tid == 0) {
-    stats[4 * (long)q] = M;
-    stats[4 * (long)q + 1] = inv;
-    stats[4 * (long)q + 2] = bad ? 1.0f : 0.0f;
-  }
-}
-
-__global__ __launch_bounds__(PZ_RB) void k_spec_rows_v(
-    const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
-    int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
-  spec_rows_body<true>(target, draft, ld, V, B, K, KT, prm, stats);
-}
-__global__ __launch_bounds__(PZ_RB) void k_spec_rows_s(
-    const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
-    int K, int KT, const pz_row_params_dev* __restrict__ prm, float* __restrict__ stats) {
-  spec_rows_body<false>(target, draft, ld, V, B, K, KT, prm, stats);
-}
+};
 
 // p(x) of one element of a row whose softmax statistics are (M, inv).
 template <bool VEC>
-__device__ __forceinline__ float prob_at(const PzTempRow<VEC>& R, int x, float M, float inv,
-                                        const pz_lds_u64* et) {
-  return pz_expf_l(R.T.apply(R.x[x]) - M, et) * inv;
+__device__ __forceinline__ float prob_at(const PzTempRow<VEC>& R, int x, float M, float inv) {
+  return pz_expf(R.T.apply(R.x[x]) - M) * inv;
 }
 
 // Residual terms r(x) = max(0, p(x) - q(x)) of a target/draft row pair,
@@ -134,22 +114,6 @@ struct ResidualTerms {
                                           uint32_t* cls) const {
     return pz_inc(a[c], g, cls);
   }
-  __device__ __forceinline__ void cache_put(pz_lds_f32* base, const Raw&,
-                                            const float (&a)[4]) const {
-    pz_f4 q;
-    q.x = a[0];
-    q.y = a[1];
-    q.z = a[2];
-    q.w = a[3];
-    ((pz_lds_f4*)base)[threadIdx.x & 63] = q;
-  }
-  __device__ __forceinline__ void cache_terms(const pz_lds_f32* base, float (&v)[4]) const {
-    const pz_f4 q = ((const pz_lds_f4*)base)[threadIdx.x & 63];
-    v[0] = q.x;
-    v[1] = q.y;
-    v[2] = q.z;
-    v[3] = q.w;
-  }
   __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
     Raw r;
     const int e0 = pz_seg_e0(k);
@@ -158,148 +122,372 @@ struct ResidualTerms {
   }
 };
 
-struct SpecVerifyShared {
-  PzRecShared r;
-  int jstar;
-  int last;
+template <bool VEC>
+__device__ __forceinline__ PzTempRow<VEC> temp_row(const SpecArgs& A, int q) {
+  PzTempRow<VEC> R;
+  R.x = A.row(q);
+  R.V = A.V;
+  R.T = A.T;
+  return R;
+}
+
+// Softmax of a row is degenerate (every p NaN) when any y is NaN or the
+// maximum is not finite (softmax.c:4-23 then sums a NaN).
+__device__ __forceinline__ bool spec_bad(uint32_t flags) {
+  return (flags & (PZ_RS_NAN | PZ_RS_NONFIN)) != 0;
+}
+
+// ---- every logits row: maximum and segment estimates (HBM) ----------------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_stat(SpecArgs A) {
+  __shared__ PzSpShared SS;
+  const int q = blockIdx.y;
+  if (threadIdx.x == 0) SS.any = 0u;
+  __syncthreads();
+  const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
+  pz_sp_stat_slice(temp_row<VEC>(A, q), q, sl, A.ws, SS, true);
+}
+
+// ---- their records ---------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_rec(SpecArgs A) {
+  __shared__ PzSpShared SS;
+  __shared__ uint64_t etab[32];
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int q = blockIdx.y;
+  pz_sp_row_stat(q, A.S, A.ws, SS);
+  if (spec_bad(SS.any)) return;
+  const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
+  const PzEstRel est{A.ws.seg_m + (size_t)q * A.ws.nsc, A.ws.seg_s + (size_t)q * A.ws.nsc, SS.M};
+  const float carry = pz_sp_prefix(est, sl.k0, SS);
+  pz_sp_predict(est, carry, q, sl, A.ws, SS);
+  PzExpTerms<PzTempRow<VEC>> X;
+  X.R = temp_row<VEC>(A, q);
+  X.M = SS.M;
+  X.thr = -__builtin_inff();
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = (const pz_lds_u64*)etab;
+  pz_sp_records(X, q, sl, A.ws);
+}
+
+// ---- one workgroup per row: the exact normaliser -----------------------------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_walk(SpecArgs A) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ uint64_t etab[32];
+  __shared__ float sum_sh;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int q = blockIdx.x;
+  pz_sp_row_stat(q, A.S, A.ws, SS);
+  PzRowState& rs = A.ws.rs[q];
+  if (spec_bad(SS.any)) {
+    if (threadIdx.x == 0) {
+      rs.M = SS.M;
+      rs.flags = SS.any;
+      rs.inv = __builtin_nanf("");
+    }
+    return;
+  }
+  PzExpTerms<PzTempRow<VEC>> X;
+  X.R = temp_row<VEC>(A, q);
+  X.M = SS.M;
+  X.thr = -__builtin_inff();
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = (const pz_lds_u64*)etab;
+  const PzWalk W = pz_sp_walk_setup(X, q, A.nseg, A.nc, A.ws, lds, SS);
+  if (threadIdx.x < 64) {
+    PzAcc st;
+    pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+    if (threadIdx.x == 0) sum_sh = pz_acc_value(st);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    rs.M = SS.M;
+    rs.flags = SS.any;
+    rs.sum = sum_sh;
+    rs.inv = 1.0f / sum_sh;  // softmax.c:19-22
+  }
+}
+
+// ---- one wave per sequence: acceptance tests ------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(64) void k_spec_accept(SpecArgs A) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  const PzRowState* rs = A.ws.rs;
+  bool accept = false;
+  if (lane < A.K) {
+    const int qt = b * A.KT + lane, qd = A.NT + b * A.K + lane;
+    const int d = A.draft_ids[b * A.K + lane];
+    if (d >= 0 && d < A.V) {
+      const float pd = prob_at(temp_row<VEC>(A, qt), d, rs[qt].M, rs[qt].inv);
+      const float qv = prob_at(temp_row<VEC>(A, qd), d, rs[qd].M, rs[qd].inv);
+      accept = qv > 0.0f && A.u_acc[b * A.K + lane] < pd / qv;
+    }
+  }
+  const uint64_t rej = __ballot(lane < A.K && !accept);
+  const int js = rej ? (int)__builtin_ctzll(rej) : A.K;
+  if (lane != 0) return;
+  SpecSeq s;
+  s.js = js;
+  s.last = -1;
+  s.qt = s.qd = -1;
+  int tok = -1;
+  s.mode = SQ_DONE;
+  if (js < A.K) {
+    const int qt = b * A.KT + js, qd = A.NT + b * A.K + js;
+    if (spec_bad(rs[qt].flags)) {
+      tok = A.V - 1;  // p is NaN everywhere: r == 0, and the p-draw falls back
+    } else if (spec_bad(rs[qd].flags)) {
+      s.mode = SQ_CAT;  // q is NaN: every p - q fails t > 0, Z == 0
+      s.qt = qt;
+    } else {
+      s.mode = SQ_RES;
+      s.qt = qt;
+      s.qd = qd;
+    }
+  } else if (A.has_bonus) {
+    const int qt = b * A.KT + A.K;
+    if (spec_bad(rs[qt].flags)) tok = A.V - 1;
+    else {
+      s.mode = SQ_CAT;
+      s.qt = qt;
+    }
+  }
+  A.seq[b] = s;
+  if (s.mode == SQ_DONE) {
+    A.acc_len[b] = js;
+    for (int j = 0; j <= A.K; j++)
+      A.ids_out[(long)b * (A.K + 1) + j] = j < js ? A.draft_ids[b * A.K + j] : (j == js ? tok : -1);
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ ResidualTerms<VEC> residual_terms(const SpecArgs& A, const SpecSeq& s,
+                                                             const pz_lds_u64* et) {
+  ResidualTerms<VEC> X;
+  X.T = temp_row<VEC>(A, s.qt);
+  X.D = temp_row<VEC>(A, s.qd);
+  X.MT = A.ws.rs[s.qt].M;
+  X.invT = A.ws.rs[s.qt].inv;
+  X.MD = A.ws.rs[s.qd].M;
+  X.invD = A.ws.rs[s.qd].inv;
+  X.lastpos = -1;
+  X.et = et;
+  return X;
+}
+
+template <bool VEC>
+__device__ __forceinline__ PzExpTerms<PzTempRow<VEC>> p_terms(const SpecArgs& A, int qt,
+                                                              const pz_lds_u64* et) {
+  PzExpTerms<PzTempRow<VEC>> X;
+  X.R = temp_row<VEC>(A, qt);
+  X.M = A.ws.rs[qt].M;
+  X.thr = -__builtin_inff();
+  X.inv = A.ws.rs[qt].inv;
+  X.as_p = true;
+  X.et = et;
+  return X;
+}
+
+// ---- per sequence: estimated mass of the draw's terms per segment ----------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vest(SpecArgs A) {
+  const int b = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const SpecSeq s = A.seq[b];
+  if (s.mode == SQ_DONE) return;
+  const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
+  const PzTempRow<VEC> T = temp_row<VEC>(A, s.qt);
+  const float MT = A.ws.rs[s.qt].M, invT = A.ws.rs[s.qt].inv;
+  float MD = 0.0f, invD = 0.0f;
+  PzTempRow<VEC> D = T;
+  if (s.mode == SQ_RES) {
+    D = temp_row<VEC>(A, s.qd);
+    MD = A.ws.rs[s.qd].M;
+    invD = A.ws.rs[s.qd].inv;
+  }
+  float* est = A.ws.seg_s + (size_t)(A.NR + b) * A.ws.nsc;
+  for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+    float yts[PZ_SP_U][4], yds[PZ_SP_U][4];
+    int ns[PZ_SP_U];
+#pragma unroll
+    for (int u = 0; u < PZ_SP_U; u++) {
+      const int e0 = (kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane;
+      ns[u] = T.load(e0, yts[u]);
+      if (s.mode == SQ_RES) D.load(e0, yds[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < PZ_SP_U; u++) {
+      const int k = kb + u * PZ_SP_WAVES;
+      if (k >= sl.k1) break;
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      const int n = ns[u];
+      float (&yt)[4] = yts[u];
+      float (&yd)[4] = yds[u];
+      T.apply(e0, n, yt);
+      float t = 0.0f;
+      if (s.mode == SQ_RES) {
+        D.apply(e0, n, yd);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          if (c >= n) continue;
+          const float r = pz_fast_exp(yt[c] - MT) * invT - pz_fast_exp(yd[c] - MD) * invD;
+          t += r > 0.0f ? r : 0.0f;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          if (c < n) t += pz_fast_exp(yt[c] - MT) * invT;
+      }
+      t = pz_wave_sum(t);
+      if (lane == 0) est[k] = t;
+    }
+  }
+}
+
+// ---- per sequence: records of the draw's terms ----------------------------
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vrec(SpecArgs A) {
+  __shared__ PzSpShared SS;
+  __shared__ uint64_t etab[32];
+  __shared__ int last_sh;
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int b = blockIdx.y;
+  const SpecSeq s = A.seq[b];
+  if (s.mode == SQ_DONE) return;
+  if (threadIdx.x == 0) last_sh = -1;
+  const int r = A.NR + b;
+  const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
+  const PzEstAbs est{A.ws.seg_s + (size_t)r * A.ws.nsc};
+  const float carry = pz_sp_prefix(est, sl.k0, SS);
+  pz_sp_predict(est, carry, r, sl, A.ws, SS);
+  if (s.mode == SQ_RES) {
+    ResidualTerms<VEC> X = residual_terms<VEC>(A, s, et);
+    pz_sp_records(X, r, sl, A.ws);
+    if (X.lastpos >= 0) atomicMax(&last_sh, X.lastpos);
+    __syncthreads();
+    if (threadIdx.x == 0 && last_sh >= 0) atomicMax(&A.seq[b].last, last_sh);
+  } else {
+    PzExpTerms<PzTempRow<VEC>> X = p_terms<VEC>(A, s.qt, et);
+    pz_sp_records(X, r, sl, A.ws);
+  }
+}
+
+// ---- one workgroup per sequence: Z and the draw -------------------------------
+struct VwalkShared {
   float Z;
   int hit;
 };
 
 template <bool VEC>
-__global__ __launch_bounds__(PZ_RB) void k_spec_verify(
-    const float* __restrict__ target, const float* __restrict__ draft, long ld, int V, int B,
-    int K, int KT, int has_bonus, const pz_row_params_dev* __restrict__ prm,
-    const float* __restrict__ stats, const int32_t* __restrict__ draft_ids,
-    const float* __restrict__ u_acc, const float* __restrict__ u_res,
-    int32_t* __restrict__ acc_len, int32_t* __restrict__ ids_out) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vwalk(SpecArgs A) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ SpecVerifyShared S;
+  __shared__ PzSpShared SS;
+  __shared__ PzRecShared RS;
+  __shared__ VwalkShared VS;
   __shared__ uint64_t etab[32];
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   pz_etab_fill((pz_lds_u64*)etab);
-  __syncthreads();
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const int NT = B * KT;
-  const int ntiles = pz_tiles(V), nseg = ntiles * PZ_SEGS_PER_TILE;
-  const PzRec REC = pz_rec_at(lds, nseg);
-  const PzTemp TT = PzTemp::of(*prm);
-
-  // ---- acceptance tests, in draft order, up to the first rejection
-  if (tid == 0) {
-    int j = 0;
-    for (; j < K; j++) {
-      const int qt = b * KT + j, qd = NT + b * K + j;
-      const int d = draft_ids[b * K + j];
-      bool accept = false;
-      if (d >= 0 && d < V) {
-        PzTempRow<VEC> RT{target + (long)qt * ld, V, TT};
-        PzTempRow<VEC> RD{draft + (long)(qd - NT) * ld, V, TT};
-        const float pd = prob_at(RT, d, stats[4 * qt], stats[4 * qt + 1], et);
-        const float qv = prob_at(RD, d, stats[4 * qd], stats[4 * qd + 1], et);
-        accept = qv > 0.0f && u_acc[b * K + j] < pd / qv;
+  const int b = blockIdx.x;
+  const SpecSeq s = A.seq[b];
+  if (s.mode == SQ_DONE) return;
+  const int r = A.NR + b;
+  const float ur = A.u_res[b];
+  int tok;
+  if (s.mode == SQ_RES) {
+    const ResidualTerms<VEC> X = residual_terms<VEC>(A, s, et);
+    const PzWalk W = pz_sp_walk_setup(X, r, A.nseg, A.nc, A.ws, lds, SS);
+    if (threadIdx.x < 64) {
+      PzAcc st;
+      pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+      const float Z = pz_acc_value(st);
+      int hit = -1;
+      if (Z > 0.0f) {
+        // the same sequence of adds: the CDF of r, stop at ur * Z < cdf
+        PzAcc s2;
+        hit = pz_sp_walk<PZ_STOP_GT>(s2, W, ur * Z, X);
+        if (hit >= A.V) hit = -1;
       }
-      if (!accept) break;
+      if (threadIdx.x == 0) {
+        VS.Z = Z;
+        VS.hit = hit;
+      }
     }
-    S.jstar = j;
-    S.last = 0;
-  }
-  __syncthreads();
-  const int js = S.jstar;
-  const float ur = u_res[b];
-  int tok = -1;
-  int cat_row = -1;  // target row to draw from with the categorical rule
-  if (js < K) {
-    const int qt = b * KT + js, qd = NT + b * K + js;
-    const bool badT = stats[4 * qt + 2] != 0.0f, badD = stats[4 * qd + 2] != 0.0f;
-    if (badT) {
-      tok = V - 1;  // p is NaN everywhere: r == 0, and the p-draw falls back
-    } else if (badD) {
-      cat_row = qt;  // q is NaN: every p - q fails t > 0, Z == 0
+    __syncthreads();
+    if (VS.Z > 0.0f) {
+      tok = VS.hit >= 0 ? VS.hit : A.seq[b].last;
     } else {
-      ResidualTerms<VEC> X;
-      X.T = PzTempRow<VEC>{target + (long)qt * ld, V, TT};
-      X.D = PzTempRow<VEC>{draft + (long)(qd - NT) * ld, V, TT};
-      X.MT = stats[4 * qt];
-      X.invT = stats[4 * qt + 1];
-      X.MD = stats[4 * qd];
-      X.invD = stats[4 * qd + 1];
-      X.lastpos = -1;
-      X.et = et;
-      pz_record_pass(X, ntiles, REC, S.r, __builtin_inff());
-      if (X.lastpos > 0) atomicMax(&S.last, X.lastpos);
-      if (tid < 64) {
-        PzAcc st;
-        st.n = 0;
-        st.g = 1;
-        pz_rec_walk(st, REC, nseg, 0.0f, PZ_STOP_NONE, X);
-        const float Z = pz_acc_value(st);
-        int hit = -1;
-        if (Z > 0.0f) {
-          // the same sequence of adds: the CDF of r, stop at ur * Z < cdf
-          PzAcc s2;
-          s2.n = 0;
-          s2.g = 1;
-          hit = pz_rec_walk(s2, REC, nseg, ur * Z, PZ_STOP_GT, X);
-          if (hit >= V) hit = -1;
-        }
-        if (tid == 0) {
-          S.Z = Z;
-          S.hit = hit;
-        }
-      }
-      __syncthreads();
-      if (S.Z > 0.0f) tok = S.hit >= 0 ? S.hit : S.last;
-      else cat_row = qt;
+      // Z == 0: categorical draw from p of the target row (generate.c:157-169),
+      // with records built by this workgroup alone (a rare path)
+      PzExpTerms<PzTempRow<VEC>> Xp = p_terms<VEC>(A, s.qt, et);
+      const int ntiles = pz_tiles(A.V);
+      const PzRec REC = pz_rec_at(lds, ntiles * PZ_SEGS_PER_TILE);
+      const int hit = pz_exact_draw(Xp, A.V, ntiles, ur, REC, RS);
+      tok = hit >= 0 ? hit : A.V - 1;
     }
-  } else if (has_bonus) {
-    const int qt = b * KT + K;
-    if (stats[4 * qt + 2] != 0.0f) tok = V - 1;
-    else cat_row = qt;
+  } else {
+    const PzExpTerms<PzTempRow<VEC>> X = p_terms<VEC>(A, s.qt, et);
+    const PzWalk W = pz_sp_walk_setup(X, r, A.nseg, A.nc, A.ws, lds, SS);
+    if (threadIdx.x < 64) {
+      PzAcc st;
+      int hit = pz_sp_walk<PZ_STOP_GT>(st, W, ur, X);
+      if (hit >= A.V) hit = -1;
+      if (threadIdx.x == 0) VS.hit = hit;
+    }
+    __syncthreads();
+    tok = VS.hit >= 0 ? VS.hit : A.V - 1;
   }
-  if (cat_row >= 0) {
-    // categorical draw from p of a target row (generate.c:157-169)
-    PzExpTerms<PzTempRow<VEC>> X;
-    X.R = PzTempRow<VEC>{target + (long)cat_row * ld, V, TT};
-    X.M = stats[4 * cat_row];
-    X.thr = -__builtin_inff();
-    X.inv = stats[4 * cat_row + 1];
-    X.as_p = true;
-    X.et = et;
-    const int hit = pz_exact_draw(X, V, ntiles, ur, REC, S.r);
-    tok = hit >= 0 ? hit : V - 1;
-  }
-  if (tid == 0) {
-    acc_len[b] = js;
-    for (int j = 0; j <= K; j++)
-      ids_out[(long)b * (K + 1) + j] = j < js ? draft_ids[b * K + j] : (j == js ? tok : -1);
+  if (threadIdx.x == 0) {
+    const int js = s.js;
+    A.acc_len[b] = js;
+    for (int j = 0; j <= A.K; j++)
+      A.ids_out[(long)b * (A.K + 1) + j] = j < js ? A.draft_ids[b * A.K + j] : (j == js ? tok : -1);
   }
 }
 
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 template <bool VEC>
-int launch_spec(pz_sampler* s, const float* d_target, const float* d_draft, long ld, int V,
-                int B, int K, int KT, int has_bonus, const pz_row_params_dev* d_prm,
-                float* d_stats, const int32_t* d_ids_in, const float* d_uacc,
-                const float* d_ures, int32_t* d_acc, int32_t* d_ids_out) {
-  const size_t lds = pz_rec_bytes(V);
-  if (lds + 256 > (size_t)s->max_lds) return -2;
-  auto k1 = VEC ? k_spec_rows_v : k_spec_rows_s;
-  auto k2 = k_spec_verify<VEC>;
-  if (lds > 65536) {
-    if (hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess ||
-        hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-      return -1;
-  }
-  const int NR = B * KT + B * K;
-  hipLaunchKernelGGL(k1, dim3(NR), dim3(PZ_RB), lds, s->stream, d_target, d_draft, ld, V, B, K,
-                     KT, d_prm, d_stats);
-  hipLaunchKernelGGL(k2, dim3(B), dim3(PZ_RB), lds, s->stream, d_target, d_draft, ld, V, B, K, KT,
-                     has_bonus, d_prm, d_stats, d_ids_in, d_uacc, d_ures, d_acc,
-                     d_ids_out);
+int launch_spec(pz_sampler* s, SpecArgs& A) {
+  const size_t fixed = 4096;
+  const PzSplitPlan pl = pz_split_plan(A.V, A.NR, A.ws.smax);
+  const PzSplitPlan pv = pz_split_plan(A.V, A.B, A.ws.smax);
+  if (pl.nseg > A.ws.nsc) return -2;
+  // two walking workgroups per CU fit when each takes at most half the LDS
+  int nc = pz_sp_walk_nc(pl.nseg, (size_t)s->max_lds / 2 - fixed);
+  if (nc < 12) nc = pz_sp_walk_nc(pl.nseg, (size_t)s->max_lds - fixed);
+  if (nc < 1) return -2;
+  const size_t walk = pz_sp_walk_lds(pl.nseg, nc);
+  const size_t rec = pz_rec_bytes(A.V);  // the Z == 0 path's records
+  const size_t lds_vw = walk > rec ? walk : rec;
+  if (lds_vw + fixed > (size_t)s->max_lds) return -2;
+  A.nseg = pl.nseg;
+  A.nc = nc;
+  auto kw = k_spec_walk<VEC>;
+  auto kv = k_spec_vwalk<VEC>;
+  if (walk > 65536 && hipFuncSetAttribute((const void*)kw,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (int)walk) != hipSuccess)
+    return -1;
+  if (lds_vw > 65536 && hipFuncSetAttribute((const void*)kv,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)lds_vw) != hipSuccess)
+    return -1;
+  const dim3 block(PZ_SP_BLOCK);
+  A.spw = pl.spw;
+  A.S = pl.S;
+  hipLaunchKernelGGL(k_spec_stat<VEC>, dim3(pl.S, A.NR), block, 0, s->stream, A);
+  hipLaunchKernelGGL(k_spec_rec<VEC>, dim3(pl.S, A.NR), block, 0, s->stream, A);
+  hipLaunchKernelGGL(kw, dim3(A.NR), block, walk, s->stream, A);
+  hipLaunchKernelGGL(k_spec_accept<VEC>, dim3(A.B), dim3(64), 0, s->stream, A);
+  A.spw = pv.spw;
+  A.S = pv.S;
+  hipLaunchKernelGGL(k_spec_vest<VEC>, dim3(pv.S, A.B), block, 0, s->stream, A);
+  hipLaunchKernelGGL(k_spec_vrec<VEC>, dim3(pv.S, A.B), block, 0, s->stream, A);
+  hipLaunchKernelGGL(kv, dim3(A.B), block, lds_vw, s->stream, A);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -310,7 +498,7 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
                               const int32_t* draft_ids, const float* u_acc, const float* u_res,
                               int32_t* acc_len_out, int32_t* ids_out) {
   if (!s) return PZ_EINVAL;
-  if (B < 0 || K < 1 || V < 1 || ld < V) return fail(s, PZ_EINVAL, "bad spec shape");
+  if (B < 0 || K < 1 || K > 64 || V < 1 || ld < V) return fail(s, PZ_EINVAL, "bad spec shape");
   if (B == 0) return PZ_OK;
   if (!d_target || !d_draft || !draft_ids || !u_acc || !u_res || !acc_len_out || !ids_out)
     return fail(s, PZ_EINVAL, "null spec argument");
@@ -320,17 +508,18 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   const int KT = K + (has_bonus ? 1 : 0);
   const int NR = B * KT + B * K;
 
-  // one input block and one output block, identical layout host and device
-  const size_t o_prm = 0;
-  const size_t o_ids = up256(o_prm + sizeof(pz_row_params_dev));
+  // one input block and one output block, identical layout host and device,
+  // then the sequences' state and the row-split workspace (device only)
+  const size_t o_ids = 0;
   const size_t o_uacc = up256(o_ids + (size_t)B * K * 4);
   const size_t o_ures = up256(o_uacc + (size_t)B * K * 4);
   const size_t in_bytes = up256(o_ures + (size_t)B * 4);
   const size_t o_acc = in_bytes;
   const size_t o_out = up256(o_acc + (size_t)B * 4);
   const size_t io_bytes = up256(o_out + (size_t)B * (K + 1) * 4);
-  const size_t o_stats = io_bytes;
-  const size_t dev_bytes = up256(o_stats + (size_t)NR * 16);
+  const size_t o_seq = io_bytes;
+  const size_t o_ws = up256(o_seq + (size_t)B * sizeof(SpecSeq));
+  const size_t dev_bytes = o_ws + pz_split_ws_layout(NR + B, V, 0, nullptr, nullptr);
 
   if (s->spec_dev_bytes < dev_bytes || s->spec_host_bytes < io_bytes) {
     PZ_HIP(s, hipStreamSynchronize(s->stream));
@@ -355,31 +544,38 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   PZ_HIP(s, hipStreamSynchronize(s->stream));
   char* h = static_cast<char*>(s->spec_host);
   char* d = static_cast<char*>(s->spec_dev);
-  pz_row_params_dev prm;
-  memset(&prm, 0, sizeof(prm));
-  float T = temperature;
-  if (T < 1e-6f) T = 1e-6f;  // temperature.c:10 (a NaN temperature stays NaN)
-  prm.temp = T;
-  prm.inv_temp = 1.0f / T;
-  prm.temp_div = s->temp_mode == PZ_TEMP_DIV;
-  prm.mode = PZ_MODE_CATEGORICAL;
-  prm.rep_penalty = 1.0f;
-  memcpy(h + o_prm, &prm, sizeof(prm));
   memcpy(h + o_ids, draft_ids, (size_t)B * K * 4);
   memcpy(h + o_uacc, u_acc, (size_t)B * K * 4);
   memcpy(h + o_ures, u_res, (size_t)B * 4);
   PZ_HIP(s, hipMemcpyAsync(d, h, in_bytes, hipMemcpyHostToDevice, s->stream));
+
+  float T = temperature;
+  if (T < 1e-6f) T = 1e-6f;  // temperature.c:10 (a NaN temperature stays NaN)
+  SpecArgs A;
+  memset(&A, 0, sizeof(A));
+  A.target = d_target;
+  A.draft = d_draft;
+  A.ld = ld;
+  A.V = V;
+  A.B = B;
+  A.K = K;
+  A.KT = KT;
+  A.NT = B * KT;
+  A.NR = NR;
+  A.has_bonus = has_bonus ? 1 : 0;
+  A.T.t = T;
+  A.T.inv = 1.0f / T;
+  A.T.div = s->temp_mode == PZ_TEMP_DIV;
+  A.draft_ids = reinterpret_cast<const int32_t*>(d + o_ids);
+  A.u_acc = reinterpret_cast<const float*>(d + o_uacc);
+  A.u_res = reinterpret_cast<const float*>(d + o_ures);
+  A.acc_len = reinterpret_cast<int32_t*>(d + o_acc);
+  A.ids_out = reinterpret_cast<int32_t*>(d + o_out);
+  A.seq = reinterpret_cast<SpecSeq*>(d + o_seq);
+  pz_split_ws_layout(NR + B, V, 0, d + o_ws, &A.ws);
   const bool vec = (ld % 4 == 0) && (((uintptr_t)d_target & 15) == 0) &&
                    (((uintptr_t)d_draft & 15) == 0);
-  auto launch = vec ? launch_spec<true> : launch_spec<false>;
-  const int rc = launch(s, d_target, d_draft, ld, V, B, K, KT, has_bonus ? 1 : 0,
-                        reinterpret_cast<const pz_row_params_dev*>(d + o_prm),
-                        reinterpret_cast<float*>(d + o_stats),
-                        reinterpret_cast<const int32_t*>(d + o_ids),
-                        reinterpret_cast<const float*>(d + o_uacc),
-                        reinterpret_cast<const float*>(d + o_ures),
-                        reinterpret_cast<int32_t*>(d + o_acc),
-                        reinterpret_cast<int32_t*>(d + o_out));
+  const int rc = vec ? launch_spec<true>(s, A) : launch_spec<false>(s, A);
   if (rc == -2) return fail(s, PZ_ENOTSUP, "V=%d needs more LDS than the device has", V);
   if (rc != 0) return fail(s, PZ_EDEVICE, "spec launch failed: %s",
                            hipGetErrorString(hipGetLastError()));

@@ -42,6 +42,7 @@ constexpr int PZ_SP_WAVES = PZ_SP_BLOCK / 64;  // 16
 constexpr int PZ_SP_SEG = 256;                 // ids per segment
 constexpr int PZ_SP_NC = 32;                   // special segments the walk pre-evaluates
 constexpr int PZ_SP_TARGET_WG = 512;           // workgroups a launch aims for (2 per CU)
+constexpr int PZ_SP_U = 4;                     // segments a wave loads per step
 
 // Row flags (from the slices' maxima and NaN flags).
 enum {
@@ -224,32 +225,43 @@ __device__ __forceinline__ void pz_sp_stat_slice(const Row& R, int row, const Pz
   bool nan = false;
   float* seg_m = ws.seg_m + (size_t)row * ws.nsc;
   float* seg_s = ws.seg_s + (size_t)row * ws.nsc;
-  for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
-    float y[4];
-    const int e0 = k * PZ_SP_SEG + 4 * lane;
-    const int n = R.get(e0, y);
-    float m = -__builtin_inff();
+  // PZ_SP_U segments per wave per step: their loads are all in flight
+  // before the first is used
+  for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+    float y[PZ_SP_U][4];
+    int n[PZ_SP_U];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      if (c >= n) continue;
-      if (y[c] != y[c]) nan = true;
-      else m = fmaxf(m, y[c]);
-    }
-    m = pz_wave_max(m);
-    if (est) {
-      float t = 0.0f;
-      if (m > -__builtin_inff() && m < __builtin_inff()) {
+    for (int u = 0; u < PZ_SP_U; u++)
+      n[u] = R.load((kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, y[u]);
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-          if (c < n && y[c] > -__builtin_inff()) t += pz_fast_exp(y[c] - m);  // NaN fails '>'
+    for (int u = 0; u < PZ_SP_U; u++) {
+      const int k = kb + u * PZ_SP_WAVES;
+      if (k >= sl.k1) break;
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      R.apply(e0, n[u], y[u]);
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if (c >= n[u]) continue;
+        if (y[u][c] != y[u][c]) nan = true;
+        else m = fmaxf(m, y[u][c]);
       }
-      t = pz_wave_sum(t);
-      if (lane == 0) {
-        seg_m[k] = m;
-        seg_s[k] = t;
+      m = pz_wave_max(m);
+      if (est) {
+        float t = 0.0f;
+        if (m > -__builtin_inff() && m < __builtin_inff()) {
+#pragma unroll
+          for (int c = 0; c < 4; c++)  // NaN fails '>'
+            if (c < n[u] && y[u][c] > -__builtin_inff()) t += pz_fast_exp(y[u][c] - m);
+        }
+        t = pz_wave_sum(t);
+        if (lane == 0) {
+          seg_m[k] = m;
+          seg_s[k] = t;
+        }
       }
+      smax = fmaxf(smax, m);
     }
-    smax = fmaxf(smax, m);
   }
   if (__ballot(nan) && lane == 0) atomicOr(&S.any, 1u);
   if (lane == 0) S.red[w] = smax;
@@ -370,12 +382,21 @@ __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
   uint32_t* rd = pz_sp_rec_d(ws, row);
   uint32_t* rd2 = pz_sp_rec_d2(ws, row);
   uint32_t* rgf = pz_sp_rec_gf(ws, row);
-  for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
+  for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+  typename X::Raw raws[PZ_SP_U];
+  int ns[PZ_SP_U];
+#pragma unroll
+  for (int u = 0; u < PZ_SP_U; u++)
+    ns[u] = x.load((kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, raws[u]);
+#pragma unroll
+  for (int u = 0; u < PZ_SP_U; u++) {
+    const int k = kb + u * PZ_SP_WAVES;
+    if (k >= sl.k1) break;
     const uint32_t gf = rgf[k];
     if (gf == PZ_NO_RECORD) continue;
     const int e0 = k * PZ_SP_SEG + 4 * lane;
-    typename X::Raw raw;
-    const int n = x.load(e0, raw);
+    typename X::Raw& raw = raws[u];
+    const int n = ns[u];
     float a[4];
     x.prep(e0, n, raw, a);
     x.observe(e0, raw, a);
@@ -407,6 +428,7 @@ __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
       rgf[k] = (gf & (0xffu | PZ_GF_HAS2 | PZ_GF_XING)) | (D1 ? PZ_GF_DIRTY : 0u) |
                (D2 ? PZ_GF_DIRTY2 : 0u);
     }
+  }
   }
 }
 
@@ -445,6 +467,13 @@ inline int pz_sp_walk_nc(int nseg, size_t max_lds) {
   for (int nc = PZ_SP_NC; nc >= 1; nc--)
     if (pz_sp_walk_lds(nseg, nc) <= max_lds) return nc;
   return 0;
+}
+
+// The walk's state is wave-uniform; saying so lets the compiler keep it in
+// scalar registers and branch on it with scalar instructions.
+__device__ __forceinline__ void pz_sp_uni(PzAcc& st) {
+  st.n = (uint32_t)__builtin_amdgcn_readfirstlane((int)st.n);
+  st.g = (uint32_t)__builtin_amdgcn_readfirstlane((int)st.g);
 }
 
 __device__ __forceinline__ bool pz_sp_clean(uint32_t gf) {
@@ -650,6 +679,8 @@ __device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint
                                             uint32_t fQ, float thr) {
   const int lane = threadIdx.x & 63;
   int pos = 0;
+  pz_sp_uni(st);
+  g0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)g0);
   for (int nev = 0; pos < PZ_SP_SEG; nev++) {
     if (nev >= 8 || (st.n == 0u && st.g == 1u)) return pz_sp_serial<MODE>(st, v, pos, thr);
     if (st.g != g0 && st.g != g0 + 1u) {
@@ -710,6 +741,7 @@ __device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint
     // a plain term that leaves the binade: one real add; a tie or a term as
     // large as the sum: the exact step
     st = kd == 1 ? pz_acc_of(pz_acc_value(st) + t) : pz_acc_add(st, t);
+    pz_sp_uni(st);
     if (MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value(st), thr, MODE)) return i;
     pos = i + 1;
   }
@@ -743,6 +775,7 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
       const int L = ball ? (int)__builtin_ctzll(ball) : 64;
       const int kb = k + L;
       st.n += W.pd[kb < nseg ? kb : nseg] - W.pd[k];
+      pz_sp_uni(st);
       if (kb >= nseg) break;
       k = kb;
       if (L == 64) continue;
@@ -755,6 +788,7 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
       if (d2 < (1u << 24) - st.n &&
           !(MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(st.n + d2, st.g), thr, MODE))) {
         st.n += d2;
+        pz_sp_uni(st);
         k++;
         continue;
       }

@@ -229,15 +229,24 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_est(TOPP_ARGS) {
       topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
   const float M = SS.M, thr = M - 20.0f;
   float* seg_s = ws.seg_s + (size_t)row * ws.nsc;
-  for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
-    float y[4];
-    const int n = R.get(k * PZ_SP_SEG + 4 * lane, y);
-    float t = 0.0f;
+  for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+    float y[PZ_SP_U][4];
+    int n[PZ_SP_U];
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (c < n && y[c] >= thr) t += pz_fast_exp(y[c] - M);
-    t = pz_wave_sum(t);
-    if (lane == 0) seg_s[k] = t;
+    for (int u = 0; u < PZ_SP_U; u++)
+      n[u] = R.load((kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, y[u]);
+#pragma unroll
+    for (int u = 0; u < PZ_SP_U; u++) {
+      const int k = kb + u * PZ_SP_WAVES;
+      if (k >= sl.k1) break;
+      R.apply(k * PZ_SP_SEG + 4 * lane, n[u], y[u]);
+      float t = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        if (c < n[u] && y[u][c] >= thr) t += pz_fast_exp(y[u][c] - M);
+      t = pz_wave_sum(t);
+      if (lane == 0) seg_s[k] = t;
+    }
   }
 }
 
@@ -443,10 +452,20 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_gather(TOPP_ARGS) {
     // A cheap gate on y - M picks each lane's possible candidates (a
     // superset: 0.01 below the bin edge); their exact p is evaluated one per
     // lane per trip and the survivors appended with one atomic per wave.
-    for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
+    for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+    float ys[PZ_SP_U][4];
+    int ns[PZ_SP_U];
+#pragma unroll
+    for (int u = 0; u < PZ_SP_U; u++)
+      ns[u] = R.load((kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, ys[u]);
+#pragma unroll
+    for (int u = 0; u < PZ_SP_U; u++) {
+      const int k = kb + u * PZ_SP_WAVES;
+      if (k >= sl.k1) break;
       const int e0 = k * PZ_SP_SEG + 4 * lane;
-      float y[4];
-      const int n = R.get(e0, y);
+      float (&y)[4] = ys[u];
+      const int n = ns[u];
+      R.apply(e0, n, y);
       uint32_t want = 0;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
@@ -466,6 +485,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_gather(TOPP_ARGS) {
         }
         append_key(&rs.i[2], &rs.i[3], gkeys, ws.capg, take, key);
       }
+    }
     }
   }
 }

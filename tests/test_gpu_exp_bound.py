@@ -1,7 +1,8 @@
 """The hardware-exp estimate used by the records pass (pz_fast_exp) stays
-within the relative error bound the exact-increment test assumes (2^-16),
-checked on every fp32 input in [-104, 0] against the glibc-identical pz_expf.
-A larger error would let an increment be decided from a wrong estimate."""
+within the relative error bound the exact-increment test assumes,
+(|d| + 2) * 2^-23 for exp(d), checked on every fp32 input in [-104, 0]
+against the glibc-identical pz_expf.  A larger error would let an increment
+be decided from a wrong estimate."""
 import ctypes
 import os
 
@@ -16,10 +17,13 @@ def test_fast_exp_error_bound(torch_cuda):
     lib = ctypes.CDLL(LIB)
     rel = ctypes.c_float()
     bad = ctypes.c_uint()
-    assert lib.pzcheck_exp_bound(ctypes.byref(rel), ctypes.byref(bad)) == 0
+    ratio = ctypes.c_float()
+    assert lib.pzcheck_exp_bound(ctypes.byref(rel), ctypes.byref(bad), ctypes.byref(ratio)) == 0
     print(f"max relative error {rel.value:.3e} (2^{__import__('math').log2(max(rel.value, 1e-45)):.2f}),"
+          f" max error / ((|d| + 2) 2^-23) = {ratio.value:.3f},"
           f" subnormal-range violations {bad.value}")
     assert rel.value < 2.0 ** -16
+    assert ratio.value <= 1.0
     assert bad.value == 0
 
 
