@@ -109,6 +109,30 @@ PZ_API int pz_sample_batch_async(pz_sampler *s, const float *d_logits, int B, in
 
 PZ_API int pz_sampler_sync(pz_sampler *s);
 
+/* Allocation-free form of pz_sample_batch_async.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops that forbid hipMalloc).  It takes no
+ * sampler: the kernels' scratch (row parameters, row lists, the top-p
+ * workspace) is one static device array per GPU, about 24 MiB, held until the
+ * process ends; its address is looked up on the first call on a device.
+ * Arguments as pz_sample_batch_async (device pointers for uniforms, ids and
+ * p), plus the device, the hipStream_t as void* (NULL: the null stream) and
+ * the temperature form (PZ_TEMP_MUL_RECIP or PZ_TEMP_DIV).  Limits:
+ * B <= PZ_NOALLOC_MAX_BATCH, V <= PZ_NOALLOC_MAX_VOCAB,
+ * H <= PZ_NOALLOC_MAX_HIST (PZ_ERANGE beyond, before anything is enqueued).
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * contents: calls that overlap on one GPU (other streams, other host threads)
+ * race, so order them on one stream.  Errors are reported by return code
+ * only.  Asynchronous on `stream`. */
+#define PZ_NOALLOC_MAX_BATCH 64
+#define PZ_NOALLOC_MAX_VOCAB 262144
+#define PZ_NOALLOC_MAX_HIST 2048
+PZ_API int pz_sample_batch_noalloc(int device, void *stream, int temp_mode,
+                                   const float *d_logits, int B, int V, long ld,
+                                   const pz_row_params *params, int n_params,
+                                   const int32_t *d_hist, int H, const float *d_u,
+                                   int32_t *d_ids_out, float *d_p_out);
+
 /* Speculative-draft verification (Leviathan et al. 2023, Alg. 1; absent from
  * the reference, whose plan is docs/architecture/IMPLEMENTATION_PLAN.md:
  * 1664-1693).  For each sequence b and draft position j < K:

@@ -23,9 +23,11 @@ struct pz_scratch {
   int fb_slots;       // min(PZ_FB_SLOTS, max_batch) sort slots
 };
 
-// Bytes of scratch for a sampler of this size; with base != nullptr also
-// fills *out with the carved pointers.
-size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* out);
+// Bytes of scratch for max_batch rows of up to max_vocab ids with at most
+// max_slots fallback sort slots; with base != nullptr also fills *out with
+// the carved pointers.
+size_t pz_scratch_layout(int max_batch, int max_vocab, int max_slots, void* base,
+                         pz_scratch* out);
 
 struct pz_launch {
   const float* logits;  // device [B, ld] fp32, caller-owned, read-only

@@ -32,7 +32,8 @@ int next_pow2(int v) {
 }  // namespace
 
 
-size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* out) {
+size_t pz_scratch_layout(int max_batch, int max_vocab, int max_slots, void* base,
+                         pz_scratch* out) {
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   int vt = max_vocab < PZ_TOPP_MAX_V ? max_vocab : PZ_TOPP_MAX_V;
   int slot = 256;  // >= one call of the cut-off walk (64 lanes x 4 running sums)
@@ -40,7 +41,7 @@ size_t pz_scratch_layout(int max_batch, int max_vocab, void* base, pz_scratch* o
   const size_t B = (size_t)max_batch;
   // the fallback sorts at most one queued row per slot at a time: a sampler
   // for max_batch rows never needs more than max_batch slots
-  const size_t slots = (size_t)(max_batch < PZ_FB_SLOTS ? max_batch : PZ_FB_SLOTS);
+  const size_t slots = (size_t)(max_batch < max_slots ? max_batch : max_slots);
   size_t off = 0;
   const size_t o_stat = off; off = up(off + B * 4 * sizeof(float));
   const size_t o_list = off; off = up(off + B * sizeof(int32_t));
@@ -105,9 +106,9 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
     return bail(PZ_ENOMEM);
   s->res_params = new (std::nothrow) pz_row_params_dev[B];
   if (!s->res_params) return bail(PZ_ENOMEM);
-  s->scratch_bytes = pz_scratch_layout(max_batch, max_vocab, nullptr, nullptr);
+  s->scratch_bytes = pz_scratch_layout(max_batch, max_vocab, PZ_FB_SLOTS, nullptr, nullptr);
   if (hipMalloc(&s->d_scratch, s->scratch_bytes) != hipSuccess) return bail(PZ_ENOMEM);
-  pz_scratch_layout(max_batch, max_vocab, s->d_scratch, &s->sc);
+  pz_scratch_layout(max_batch, max_vocab, PZ_FB_SLOTS, s->d_scratch, &s->sc);
   // queue counters start at zero; the fallback kernel re-zeroes them after
   // each launch that read them
   if (hipMemset(s->sc.counters, 0, 16 * sizeof(int32_t)) != hipSuccess) return bail(PZ_EDEVICE);
@@ -162,7 +163,7 @@ extern "C" int pz_sampler_sync(pz_sampler* s) {
 
 // Resolves one row's host parameters into the kernel form (mode decided as
 // generate.c:151-169; clamps of temperature.c:10 and top_k.c:11-17).
-static pz_row_params_dev resolve(const pz_row_params& p, int V, int temp_mode) {
+pz_row_params_dev pz_resolve_row(const pz_row_params& p, int V, int temp_mode) {
   pz_row_params_dev d;
   memset(&d, 0, sizeof(d));
   d.rep_penalty = p.rep_penalty;
@@ -192,15 +193,56 @@ static pz_row_params_dev resolve(const pz_row_params& p, int V, int temp_mode) {
   return d;
 }
 
-static bool penalty_active(const pz_row_params& p) {
+bool pz_penalty_active(const pz_row_params& p) {
   return p.rep_penalty != 1.0f || p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f;
 }
 
-static bool needs_counts(const pz_row_params& p) {
+bool pz_needs_counts(const pz_row_params& p) {
   return p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f;
 }
 
+int pz_hash_capacity(bool counts_any, int H) {
+  return counts_any ? next_pow2(2 * (H > 0 ? H : 1)) : 0;
+}
+
+void pz_group_rows(const pz_row_params_dev* res, int B, int n_params, int count[PZ_MODE_COUNT],
+                   int offset[PZ_MODE_COUNT], int* modes_present) {
+  for (int m = 0; m < PZ_MODE_COUNT; m++) count[m] = 0;
+  for (int b = 0; b < B; b++) count[res[n_params == 1 ? 0 : b].mode]++;
+  int acc = 0, present = 0;
+  for (int m = 0; m < PZ_MODE_COUNT; m++) {
+    offset[m] = acc;
+    acc += count[m];
+    present += count[m] > 0;
+  }
+  *modes_present = present;
+}
+
+void pz_fill_rows(const pz_row_params_dev* res, int B, int n_params,
+                  const int offset[PZ_MODE_COUNT], int32_t* rows) {
+  int fill[PZ_MODE_COUNT];
+  memcpy(fill, offset, sizeof(fill));
+  for (int b = 0; b < B; b++) rows[fill[res[n_params == 1 ? 0 : b].mode]++] = b;
+}
+
 typedef int (*pz_launcher)(const pz_launch&, int, const int32_t*);
+
+int pz_launch_modes(const pz_launch& L, const int count[PZ_MODE_COUNT],
+                    const int offset[PZ_MODE_COUNT], int modes_present, const int32_t* d_rows,
+                    int* failed_mode) {
+  static const pz_launcher launchers[PZ_MODE_COUNT] = {
+      pz_launch_greedy, pz_launch_categorical, pz_launch_topk, pz_launch_topp};
+  for (int m = 0; m < PZ_MODE_COUNT; m++) {
+    if (!count[m]) continue;
+    const int32_t* rows = modes_present > 1 ? d_rows + offset[m] : nullptr;
+    const int rc = launchers[m](L, count[m], rows);
+    if (rc != 0) {
+      *failed_mode = m;
+      return rc;
+    }
+  }
+  return 0;
+}
 
 // Common body of the sync and async entry points.  Stages params (and, when
 // the batch mixes modes, a mode-grouped row list) through pinned memory and
@@ -221,10 +263,10 @@ static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
   bool pen_any = false, counts_any = false;
   pz_row_params_dev* res = s->res_params;
   for (int i = 0; i < n_params; i++) {
-    res[i] = resolve(params[i], V, s->temp_mode);
-    if (H > 0 && penalty_active(params[i])) {
+    res[i] = pz_resolve_row(params[i], V, s->temp_mode);
+    if (H > 0 && pz_penalty_active(params[i])) {
       pen_any = true;
-      counts_any |= needs_counts(params[i]);
+      counts_any |= pz_needs_counts(params[i]);
     }
   }
   return pz_dispatch_resolved(s, d_logits, B, V, ld, n_params, d_hist, H, pen_any, counts_any,
@@ -234,20 +276,13 @@ static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
 int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, long ld,
                          int n_params, const int32_t* d_hist, int H, bool pen_any,
                          bool counts_any, const float* d_u, int32_t* d_ids, float* d_p) {
-  int count[PZ_MODE_COUNT] = {0, 0, 0, 0};
+  int count[PZ_MODE_COUNT], offset[PZ_MODE_COUNT], modes_present = 0;
   pz_row_params_dev* res = s->res_params;
-  for (int b = 0; b < B; b++) count[res[n_params == 1 ? 0 : b].mode]++;
+  pz_group_rows(res, B, n_params, count, offset, &modes_present);
   if (!d_u) {
     for (int b = 0; b < B; b++)
       if (res[n_params == 1 ? 0 : b].mode != PZ_MODE_GREEDY)
         return fail(s, PZ_EINVAL, "sampling rows need uniforms");
-  }
-  int modes_present = 0;
-  for (int m = 0; m < PZ_MODE_COUNT; m++) modes_present += count[m] > 0;
-  int offset[PZ_MODE_COUNT] = {0, 0, 0, 0};
-  {
-    int acc = 0;
-    for (int m = 0; m < PZ_MODE_COUNT; m++) { offset[m] = acc; acc += count[m]; }
   }
   // Parameters (and the row grouping they imply) usually repeat from step to
   // step: upload only when they changed, so back-to-back calls queue their
@@ -259,9 +294,7 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
     PZ_HIP(s, hipEventSynchronize(s->staged));
     memcpy(s->h_params, res, (size_t)n_params * sizeof(pz_row_params_dev));
     if (modes_present > 1) {
-      int fill[PZ_MODE_COUNT];
-      memcpy(fill, offset, sizeof(fill));
-      for (int b = 0; b < B; b++) s->h_rows[fill[res[n_params == 1 ? 0 : b].mode]++] = b;
+      pz_fill_rows(res, B, n_params, offset, s->h_rows);
       PZ_HIP(s, hipMemcpyAsync(s->d_rows, s->h_rows, (size_t)B * sizeof(int32_t),
                                hipMemcpyHostToDevice, s->stream));
     }
@@ -283,7 +316,7 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
   L.H = H;
   L.pen_any = pen_any;
   L.temp_div = s->temp_mode == PZ_TEMP_DIV;
-  L.hcap = counts_any ? next_pow2(2 * (H > 0 ? H : 1)) : 0;
+  L.hcap = pz_hash_capacity(counts_any, H);
   L.u = d_u;
   L.ids = d_ids;
   L.p_out = d_p;
@@ -292,16 +325,11 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
   L.max_lds = s->max_lds;
   L.stream = s->stream;
 
-  static const pz_launcher launchers[PZ_MODE_COUNT] = {
-      pz_launch_greedy, pz_launch_categorical, pz_launch_topk, pz_launch_topp};
-  for (int m = 0; m < PZ_MODE_COUNT; m++) {
-    if (!count[m]) continue;
-    const int32_t* rows = modes_present > 1 ? s->d_rows + offset[m] : nullptr;
-    const int rc = launchers[m](L, count[m], rows);
-    if (rc == -2) return fail(s, PZ_ENOTSUP, "sampling mode %d not supported for V=%d", m, V);
-    if (rc != 0) return fail(s, PZ_EDEVICE, "launch of mode %d failed: %s", m,
-                             hipGetErrorString(hipGetLastError()));
-  }
+  int m = -1;
+  const int rc = pz_launch_modes(L, count, offset, modes_present, s->d_rows, &m);
+  if (rc == -2) return fail(s, PZ_ENOTSUP, "sampling mode %d not supported for V=%d", m, V);
+  if (rc != 0) return fail(s, PZ_EDEVICE, "launch of mode %d failed: %s", m,
+                           hipGetErrorString(hipGetLastError()));
   return PZ_OK;
 }
 

@@ -71,6 +71,25 @@ static inline int fail(pz_sampler* s, int code, const char* fmt, ...) {
       return fail((s), PZ_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
 
+// Kernel form of one row's parameters (mode, clamps, reciprocal temperature).
+pz_row_params_dev pz_resolve_row(const pz_row_params& p, int V, int temp_mode);
+bool pz_penalty_active(const pz_row_params& p);
+bool pz_needs_counts(const pz_row_params& p);
+// LDS hash capacity for presence / frequency counts over H history ids.
+int pz_hash_capacity(bool counts_any, int H);
+// Rows per mode and each mode's offset in a mode-grouped row list.
+void pz_group_rows(const pz_row_params_dev* res, int B, int n_params, int count[PZ_MODE_COUNT],
+                   int offset[PZ_MODE_COUNT], int* modes_present);
+// The mode-grouped row list (B entries).
+void pz_fill_rows(const pz_row_params_dev* res, int B, int n_params,
+                  const int offset[PZ_MODE_COUNT], int32_t* rows);
+// One launch per mode present; d_rows (device, the grouped list) is read only
+// when more than one mode is present.  Returns 0, or the failing launcher's
+// code with *failed_mode set.
+int pz_launch_modes(const pz_launch& L, const int count[PZ_MODE_COUNT],
+                    const int offset[PZ_MODE_COUNT], int modes_present, const int32_t* d_rows,
+                    int* failed_mode);
+
 // Launches the kernels for B rows whose kernel parameters are already in
 // s->res_params (n_params entries).  Used by the public entry points after
 // resolving pz_row_params, and by the reference-compatible calls, which set

@@ -24,7 +24,7 @@ ABI_SYMBOLS = (
     "pz_sampler_last_error", "pz_sampler_stream", "pz_sample_batch",
     "pz_sample_batch_async", "pz_sampler_sync", "pz_spec_verify",
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
-    "pz_temperature_batch", "pz_softmax_batch",
+    "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
     # include/pz_sampling_compat.h: the reference sampler's own symbols
     "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
     "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
@@ -84,6 +84,8 @@ def load():
     lib.pz_sample_batch.argtypes = [_P, _P, _I, _I, _L, _P, _I, _P, _I, _P, _P, _P]
     lib.pz_sample_batch_async.argtypes = [_P, _P, _I, _I, _L, _P, _I, _P, _I, _P, _P, _P]
     lib.pz_sampler_sync.argtypes = [_P]
+    lib.pz_sample_batch_noalloc.argtypes = [_I, _P, _I, _P, _I, _I, _L, _P, _I, _P, _I, _P,
+                                            _P, _P]
     lib.pz_spec_verify.argtypes = [_P, _P, _P, _I, _I, _I, _L, _I, _F, _P, _P, _P, _P, _P]
     lib.pz_device_alloc.argtypes = [ctypes.POINTER(_P), ctypes.c_size_t, _I]
     lib.pz_device_free.argtypes = [_P]
@@ -317,3 +319,18 @@ def synth_draft_ids(draft, tau, seed):
     synth().pz_synth_draft_ids(_np_ptr(out), _np_ptr(np.ascontiguousarray(draft)), rows, V,
                                V, tau, seed)
     return out
+
+
+PZ_NOALLOC_MAX_BATCH, PZ_NOALLOC_MAX_VOCAB, PZ_NOALLOC_MAX_HIST = 64, 262144, 2048
+
+
+def sample_noalloc(d_logits, B, V, ld, params, d_u, d_ids, d_p=None, d_hist=None, H=0,
+                   device=0, stream=None, temp_mode=PZ_TEMP_MUL_RECIP):
+    """pz_sample_batch_noalloc: enqueues the batch on `stream` (a hipStream_t
+    address, None for the null stream) without a sampler object; uniforms,
+    ids and p are device buffers.  Returns the status code (PZ_OK or PZ_E*)."""
+    lib = load()
+    parr, n = _params_array(params, B)
+    return lib.pz_sample_batch_noalloc(device, stream, temp_mode, _ptr(d_logits), B, V, ld,
+                                       parr, n, _ptr(d_hist), H, _ptr(d_u), _ptr(d_ids),
+                                       _ptr(d_p))
