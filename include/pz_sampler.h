@@ -109,6 +109,32 @@ PZ_API int pz_sample_batch_async(pz_sampler *s, const float *d_logits, int B, in
 
 PZ_API int pz_sampler_sync(pz_sampler *s);
 
+/* One decode step with the RNG and the EOS check on the device, replacing
+ * the per-generation state of generate.c:125-126 (rng_seed / rng_float,
+ * src/sampling/rng.c:3-17), the sampling block of generate.c:145-169 and the
+ * EOS test of generate.c:198-211 for B rows at once.
+ *   d_state: device [B] xorshift64* states, one per row, caller-owned and
+ *   seeded as rng_seed does (seed 0 becomes 1).  Row b draws
+ *   u = rng_float(&d_state[b]) exactly when the reference would: never for a
+ *   greedy row, never for a top-p row that returns argmax before drawing
+ *   (V > 200000, top_p.c:33-34; a NaN first value after penalties and
+ *   temperature, top_p.c:68-69), once for every other row.  The state
+ *   advances only when the row draws.
+ *   d_eos_out: device [B] uint8 or NULL; 1 when the sampled id is in the
+ *   sampler's EOS list (pz_sampler_set_eos), else 0.
+ * Other arguments as pz_sample_batch_async.  Asynchronous on the sampler's
+ * stream. */
+PZ_API int pz_sample_step(pz_sampler *s, const float *d_logits, int B, int V, long ld,
+                          const pz_row_params *params, int n_params,
+                          const int32_t *d_hist, int H, uint64_t *d_state,
+                          int32_t *d_ids_out, float *d_p_out, uint8_t *d_eos_out);
+
+/* The EOS ids pz_sample_step checks (host list, copied; at most PZ_MAX_EOS):
+ * the model's eos_token_id when it is > 0 plus the tokenizer's eos_list,
+ * as generate.c:201-205 tests them.  Waits for the sampler's stream. */
+#define PZ_MAX_EOS 64
+PZ_API int pz_sampler_set_eos(pz_sampler *s, const int32_t *eos_ids, int n_eos);
+
 /* Allocation-free form of pz_sample_batch_async.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops that forbid hipMalloc).  It takes no

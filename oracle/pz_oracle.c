@@ -216,8 +216,8 @@ static int cmp_pi(const void *a, const void *b) {
   return (x->index > y->index) - (x->index < y->index);
 }
 
-static orc_pi *g_cand = NULL;   /* grows on demand; single-threaded like the reference */
-static int g_cand_cap = 0;
+static __thread orc_pi *g_cand = NULL;  /* grows on demand; one per thread */
+static __thread int g_cand_cap = 0;
 
 static orc_pi *cand_buf(int n) {
   if (n > g_cand_cap) {
@@ -358,8 +358,8 @@ int orc_chain(const float *x, int n, int k, float top_p, float u,
 }
 
 /* ---- per-row dispatch: generate.c:145-169 plus the extensions ---------- */
-static float *g_row = NULL;
-static int g_row_cap = 0;
+static __thread float *g_row = NULL;  /* one per thread */
+static __thread int g_row_cap = 0;
 
 int orc_sample_row(const float *x, int n, const orc_params *prm,
                    const int32_t *hist, int h, float u, int temp_mode,
@@ -407,6 +407,34 @@ void orc_sample_batch(const float *x, int rows, int n, long ld,
     if (p_chosen) p_chosen[b] = info.p_chosen;
     if (dist_draw) dist_draw[b] = info.dist_draw;
     if (dist_cut) dist_cut[b] = info.dist_cut;
+  }
+}
+
+/* One decode step.  The uniform is drawn from a copy of the row's state and
+ * the copy is kept only when the path taken is one where the reference
+ * consumes it: rng_float sits after sample_top_p's two argmax returns
+ * (top_p.c:33-34, 68-69, draw at :96), unconditionally in sample_top_k
+ * (top_k.c:62) and in the categorical block (generate.c:159); greedy rows
+ * never reach a sampler (generate.c:151-152).  EOS as generate.c:201-205
+ * (the caller's list holds eos_token_id when it is > 0). */
+void orc_sample_step(const float *x, int rows, int n, long ld,
+                     const orc_params *params, int n_params,
+                     const int32_t *hist, int h, unsigned long long *state,
+                     int temp_mode, const int32_t *eos, int n_eos,
+                     int32_t *ids, uint8_t *eos_flag, int32_t *drew) {
+  for (int b = 0; b < rows; b++) {
+    orc_info info;
+    const orc_params *prm = &params[n_params == 1 ? 0 : b];
+    unsigned long long s = state[b];
+    const float u = orc_rng_float(&s);
+    ids[b] = orc_sample_row(x + (long)b * ld, n, prm, hist ? hist + (long)b * h : NULL, h, u,
+                            temp_mode, &info);
+    const int draws = info.path != ORC_PATH_ARGMAX && info.path != ORC_PATH_TOPP_ARGMAX;
+    if (draws) state[b] = s;
+    if (drew) drew[b] = draws;
+    int f = 0;
+    for (int e = 0; e < n_eos; e++) f |= eos[e] == ids[b];
+    if (eos_flag) eos_flag[b] = (uint8_t)f;
   }
 }
 

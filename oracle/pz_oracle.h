@@ -120,6 +120,18 @@ void orc_sample_batch(const float *x, int rows, int n, long ld,
                       int32_t *ids, float *p_chosen, float *dist_draw,
                       float *dist_cut);
 
+/* One decode step with per-row RNG states and the EOS check
+ * (generate.c:125-126 state, :145-169 dispatch, :198-211 EOS).  Row b draws
+ * orc_rng_float(&state[b]) only where the reference's sampler consumes a
+ * uniform: not for argmax (:151-152), not when top-p returns argmax first
+ * (top_p.c:33-34, 68-69); once otherwise (top_k.c:62, top_p.c:96,
+ * generate.c:159).  eos_flag[b] = ids[b] is in eos[0..n_eos). */
+void orc_sample_step(const float *x, int rows, int n, long ld,
+                     const orc_params *params, int n_params,
+                     const int32_t *hist, int h, unsigned long long *state,
+                     int temp_mode, const int32_t *eos, int n_eos,
+                     int32_t *ids, uint8_t *eos_flag, int32_t *drew);
+
 /* ---- a11: speculative verification (build-defined) ---------------------
  * target [B, K+has_bonus, n], draft [B, K, n] logits; draft_ids [B, K];
  * u_acc [B, K]; u_res [B].  Outputs acc_len[B] and out_ids[B, K+1]

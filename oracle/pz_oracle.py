@@ -88,6 +88,8 @@ def oracle():
                                  ctypes.POINTER(OrcInfo)]
     o.orc_sample_batch.argtypes = [_P, _I, _I, _L, _P, _I, _P, _I, _P, _I, _P, _P, _P, _P]
     o.orc_sample_batch.restype = None
+    o.orc_sample_step.argtypes = [_P, _I, _I, _L, _P, _I, _P, _I, _P, _I, _P, _I, _P, _P, _P]
+    o.orc_sample_step.restype = None
     o.orc_spec_verify.argtypes = [_P, _P, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _P]
     o.orc_spec_verify.restype = None
     o.orc_expf.argtypes = [_F]
@@ -117,6 +119,46 @@ def sample_batch(x, params_list, u=None, hist=None, temp_mode=TEMP_MUL_RECIP):
     oracle().orc_sample_batch(_np(x), B, V, V, parr, len(params_list), _np(hist), H, _np(u),
                               temp_mode, _np(ids), _np(pc), _np(dd), _np(dc))
     return ids, pc, dd, dc
+
+
+def sample_step(x, params_list, state, hist=None, eos=(), temp_mode=TEMP_MUL_RECIP,
+                workers=1):
+    """One decode step over [B, V] with per-row RNG states (uint64[B],
+    advanced in place).  Returns ids, EOS flags (uint8) and whether each row
+    drew.  workers > 1 runs row blocks on that many threads (the oracle's
+    work buffers are per thread; ctypes releases the GIL)."""
+    x = np.ascontiguousarray(x, np.float32)
+    B, V = x.shape
+    if isinstance(params_list, OrcParams):
+        params_list = [params_list]
+    assert state.dtype == np.uint64 and state.flags.c_contiguous and state.size == B
+    H = 0
+    if hist is not None:
+        hist = np.ascontiguousarray(hist, np.int32)
+        H = hist.shape[1]
+    eos = np.ascontiguousarray(eos, np.int32).ravel()
+    ids = np.empty(B, np.int32)
+    flags = np.empty(B, np.uint8)
+    drew = np.empty(B, np.int32)
+    o = oracle()
+
+    def run(lo, hi):
+        pl = params_list if len(params_list) == 1 else params_list[lo:hi]
+        parr = (OrcParams * len(pl))(*pl)
+        o.orc_sample_step(_np(x[lo:hi]), hi - lo, V, V, parr, len(pl),
+                          _np(hist[lo:hi]) if hist is not None else None, H,
+                          _np(state[lo:hi]), temp_mode, _np(eos) if eos.size else None,
+                          int(eos.size), _np(ids[lo:hi]), _np(flags[lo:hi]), _np(drew[lo:hi]))
+
+    if workers <= 1 or B < 2:
+        run(0, B)
+    else:
+        from concurrent.futures import ThreadPoolExecutor
+        n = min(workers, B)
+        cuts = [B * i // n for i in range(n + 1)]
+        with ThreadPoolExecutor(n) as ex:
+            list(ex.map(lambda i: run(cuts[i], cuts[i + 1]), range(n)))
+    return ids, flags, drew.astype(bool)
 
 
 def sample_row(x, prm, u=0.0, hist=None, temp_mode=TEMP_MUL_RECIP):

@@ -102,7 +102,9 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   s->z_ids = static_cast<int32_t*>(zi);
   s->z_p = static_cast<float*>(zp);
   if (hipMalloc((void**)&s->d_params, B * sizeof(pz_row_params_dev)) != hipSuccess ||
-      hipMalloc((void**)&s->d_rows, B * sizeof(int32_t)) != hipSuccess)
+      hipMalloc((void**)&s->d_rows, B * sizeof(int32_t)) != hipSuccess ||
+      hipMalloc((void**)&s->d_u_step, B * sizeof(float)) != hipSuccess ||
+      hipMalloc((void**)&s->d_eos, PZ_MAX_EOS * sizeof(int32_t)) != hipSuccess)
     return bail(PZ_ENOMEM);
   s->res_params = new (std::nothrow) pz_row_params_dev[B];
   if (!s->res_params) return bail(PZ_ENOMEM);
@@ -128,6 +130,8 @@ extern "C" void pz_sampler_destroy(pz_sampler* s) {
   if (s->stream) (void)hipStreamSynchronize(s->stream);
   (void)hipFree(s->d_params);
   (void)hipFree(s->d_rows);
+  (void)hipFree(s->d_u_step);
+  (void)hipFree(s->d_eos);
   (void)hipFree(s->d_scratch);
   (void)hipFree(s->d_split);
   (void)hipFree(s->spec_dev);
@@ -244,12 +248,13 @@ int pz_launch_modes(const pz_launch& L, const int count[PZ_MODE_COUNT],
   return 0;
 }
 
-// Common body of the sync and async entry points.  Stages params (and, when
-// the batch mixes modes, a mode-grouped row list) through pinned memory and
-// launches one kernel per mode present.
-static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
-                    const pz_row_params* params, int n_params, const int32_t* d_hist,
-                    int H, const float* d_u, int32_t* d_ids, float* d_p) {
+// Common body of the sync, async and step entry points.  Stages params (and,
+// when the batch mixes modes, a mode-grouped row list) through pinned memory
+// and launches one kernel per mode present.
+int pz_dispatch_params(pz_sampler* s, const float* d_logits, int B, int V, long ld,
+                       const pz_row_params* params, int n_params, const int32_t* d_hist,
+                       int H, const float* d_u, int32_t* d_ids, float* d_p,
+                       const PzStepHooks* hooks) {
   if (!s) return PZ_EINVAL;
   if (!d_logits || !params || B < 0 || V <= 0 || ld < V) return fail(s, PZ_EINVAL, "bad logits/shape");
   if (n_params != 1 && n_params != B) return fail(s, PZ_EINVAL, "n_params must be 1 or B");
@@ -270,15 +275,17 @@ static int dispatch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
     }
   }
   return pz_dispatch_resolved(s, d_logits, B, V, ld, n_params, d_hist, H, pen_any, counts_any,
-                              d_u, d_ids, d_p);
+                              d_u, d_ids, d_p, hooks);
 }
 
 int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, long ld,
                          int n_params, const int32_t* d_hist, int H, bool pen_any,
-                         bool counts_any, const float* d_u, int32_t* d_ids, float* d_p) {
+                         bool counts_any, const float* d_u, int32_t* d_ids, float* d_p,
+                         const PzStepHooks* hooks) {
   int count[PZ_MODE_COUNT], offset[PZ_MODE_COUNT], modes_present = 0;
   pz_row_params_dev* res = s->res_params;
   pz_group_rows(res, B, n_params, count, offset, &modes_present);
+  if (hooks) d_u = s->d_u_step;  // written by the step's draw kernel
   if (!d_u) {
     for (int b = 0; b < B; b++)
       if (res[n_params == 1 ? 0 : b].mode != PZ_MODE_GREEDY)
@@ -325,11 +332,16 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
   L.max_lds = s->max_lds;
   L.stream = s->stream;
 
+  if (hooks && pz_launch_step_draw(L, B, hooks->state, s->d_u_step) != 0)
+    return fail(s, PZ_EDEVICE, "launch of the step draw failed");
   int m = -1;
   const int rc = pz_launch_modes(L, count, offset, modes_present, s->d_rows, &m);
   if (rc == -2) return fail(s, PZ_ENOTSUP, "sampling mode %d not supported for V=%d", m, V);
   if (rc != 0) return fail(s, PZ_EDEVICE, "launch of mode %d failed: %s", m,
                            hipGetErrorString(hipGetLastError()));
+  if (hooks && hooks->eos_out &&
+      pz_launch_step_eos(s->stream, d_ids, B, s->d_eos, s->n_eos, hooks->eos_out) != 0)
+    return fail(s, PZ_EDEVICE, "launch of the EOS check failed");
   return PZ_OK;
 }
 
@@ -339,7 +351,8 @@ extern "C" int pz_sample_batch_async(pz_sampler* s, const float* d_logits, int B
                                      int32_t* d_ids_out, float* d_p_out) {
   if (!s) return PZ_EINVAL;
   PZ_HIP(s, hipSetDevice(s->device));
-  return dispatch(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u, d_ids_out, d_p_out);
+  return pz_dispatch_params(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u, d_ids_out,
+                            d_p_out, nullptr);
 }
 
 extern "C" int pz_sample_batch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
@@ -358,8 +371,8 @@ extern "C" int pz_sample_batch(pz_sampler* s, const float* d_logits, int B, int 
     memcpy(s->h_u, u, (size_t)B * sizeof(float));
     d_u = s->z_u;
   }
-  int rc = dispatch(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u, s->z_ids,
-                    p_out ? s->z_p : nullptr);
+  int rc = pz_dispatch_params(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u,
+                              s->z_ids, p_out ? s->z_p : nullptr, nullptr);
   if (rc != PZ_OK) {
     (void)hipStreamSynchronize(s->stream);  // kernels already queued may use the buffers
     return rc;

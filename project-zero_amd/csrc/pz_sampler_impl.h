@@ -41,6 +41,12 @@ struct pz_sampler {
   size_t split_bytes = 0;
   PzSplitWs ws{};
 
+  // decode steps with device-side draws: the uniforms the draw kernel
+  // writes (max_batch) and the EOS ids (PZ_MAX_EOS, n_eos in use)
+  float* d_u_step = nullptr;
+  int32_t* d_eos = nullptr;
+  int n_eos = 0;
+
   pz_row_params_dev* res_params = nullptr;  // host work area (max_batch)
   int staged_n = -1, staged_B = -1;         // what d_params / d_rows hold
 
@@ -90,10 +96,28 @@ int pz_launch_modes(const pz_launch& L, const int count[PZ_MODE_COUNT],
                     const int offset[PZ_MODE_COUNT], int modes_present, const int32_t* d_rows,
                     int* failed_mode);
 
+// Extra work of a decode step (pz_sample_step): the per-row draws from
+// device RNG states before sampling, the EOS flags after.
+struct PzStepHooks {
+  uint64_t* state;   // device [B] xorshift64* states
+  uint8_t* eos_out;  // device [B] flags, or nullptr
+};
+int pz_launch_step_draw(const pz_launch& L, int B, uint64_t* d_state, float* d_u);
+int pz_launch_step_eos(hipStream_t st, const int32_t* d_ids, int B, const int32_t* d_eos,
+                       int n_eos, uint8_t* d_flags);
+
+// Resolves host parameters and samples (the body of the pz_sample_* entry
+// points); hooks != nullptr makes it a decode step (d_u is then ignored).
+int pz_dispatch_params(pz_sampler* s, const float* d_logits, int B, int V, long ld,
+                       const pz_row_params* params, int n_params, const int32_t* d_hist,
+                       int H, const float* d_u, int32_t* d_ids, float* d_p,
+                       const PzStepHooks* hooks);
+
 // Launches the kernels for B rows whose kernel parameters are already in
 // s->res_params (n_params entries).  Used by the public entry points after
 // resolving pz_row_params, and by the reference-compatible calls, which set
 // a row's mode directly.
 int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, long ld,
                          int n_params, const int32_t* d_hist, int H, bool pen_any,
-                         bool counts_any, const float* d_u, int32_t* d_ids, float* d_p);
+                         bool counts_any, const float* d_u, int32_t* d_ids, float* d_p,
+                         const PzStepHooks* hooks = nullptr);

@@ -25,6 +25,7 @@ ABI_SYMBOLS = (
     "pz_sample_batch_async", "pz_sampler_sync", "pz_spec_verify",
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
     "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
+    "pz_sample_step", "pz_sampler_set_eos",
     # include/pz_sampling_compat.h: the reference sampler's own symbols
     "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
     "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
@@ -84,6 +85,8 @@ def load():
     lib.pz_sample_batch.argtypes = [_P, _P, _I, _I, _L, _P, _I, _P, _I, _P, _P, _P]
     lib.pz_sample_batch_async.argtypes = [_P, _P, _I, _I, _L, _P, _I, _P, _I, _P, _P, _P]
     lib.pz_sampler_sync.argtypes = [_P]
+    lib.pz_sample_step.argtypes = [_P, _P, _I, _I, _L, _P, _I, _P, _I, _P, _P, _P, _P]
+    lib.pz_sampler_set_eos.argtypes = [_P, _P, _I]
     lib.pz_sample_batch_noalloc.argtypes = [_I, _P, _I, _P, _I, _I, _L, _P, _I, _P, _I, _P,
                                             _P, _P]
     lib.pz_spec_verify.argtypes = [_P, _P, _P, _I, _I, _I, _L, _I, _F, _P, _P, _P, _P, _P]
@@ -213,6 +216,20 @@ class Sampler:
 
     def sync(self):
         self._check(self.lib.pz_sampler_sync(self.h))
+
+    def set_eos(self, eos_ids):
+        """EOS ids that sample_step flags (host list, copied)."""
+        arr = np.ascontiguousarray(eos_ids, np.int32).ravel()
+        self._check(self.lib.pz_sampler_set_eos(self.h, _np_ptr(arr), arr.size))
+
+    def sample_step(self, d_logits, B, V, ld, params, d_state, d_ids, d_p=None, d_eos=None,
+                    d_hist=None, H=0):
+        """One decode step with device RNG states (u64[B]) and EOS flags
+        (u8[B]); asynchronous on the sampler's stream."""
+        parr, n = _params_array(params, B)
+        rc = self.lib.pz_sample_step(self.h, _ptr(d_logits), B, V, ld, parr, n, _ptr(d_hist), H,
+                                     _ptr(d_state), _ptr(d_ids), _ptr(d_p), _ptr(d_eos))
+        self._check(rc)
 
     def temperature(self, d_x, B, V, ld, temperature):
         """In-place apply_temperature over device rows (asynchronous)."""
