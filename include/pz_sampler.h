@@ -192,6 +192,19 @@ PZ_API int pz_temperature_batch(pz_sampler *s, float *d_x, long ld, int B, int V
 PZ_API int pz_softmax_batch(pz_sampler *s, const float *d_in, long ld_in, float *d_out,
                             long ld_out, int B, int V, float temperature);
 
+/* The reference softmax (src/math/softmax.c:4-23) over attention scores,
+ * the tn_softmax(att, valid_ctx) of src/transformer/attention.c:210,
+ * mla_attention.c:282, qwen35_attention.c:156 and qwen3moe_attention.c:136,
+ * for many rows at once (one per sequence and head).  Row r of d_in
+ * [n_rows, ld_in] holds len_r = min(d_len[r], n) scores (d_len: device
+ * int32 [n_rows], or NULL for len_r = n); d_out[r, 0 .. len_r) receives the
+ * probabilities, bit-identical to the reference, and entries from len_r on
+ * are not written (a row with len_r <= 0 is left alone).  d_in and d_out may
+ * be the same buffer.  Rows of up to 4096 scores run one wave each, longer
+ * ones one workgroup each.  Asynchronous on the sampler's stream. */
+PZ_API int pz_attn_softmax(pz_sampler *s, const float *d_in, long ld_in, float *d_out,
+                           long ld_out, int n_rows, int n, const int32_t *d_len);
+
 /* Device memory helpers for C hosts (hipMalloc / hipFree / hipMemcpy). */
 PZ_API int pz_device_alloc(void **ptr, size_t bytes, int device);
 PZ_API int pz_device_free(void *ptr);

@@ -113,6 +113,12 @@ int pz_dispatch_params(pz_sampler* s, const float* d_logits, int B, int V, long 
                        int H, const float* d_u, int32_t* d_ids, float* d_p,
                        const PzStepHooks* hooks);
 
+// The reference softmax of B device rows, one workgroup per row, after the
+// temperature T; row r holds min(d_len[r], V) entries (all V when d_len is
+// nullptr).
+int pz_launch_softmax_rows(pz_sampler* s, const float* d_in, long ld_in, float* d_out,
+                           long ld_out, int B, int V, PzTemp T, const int32_t* d_len);
+
 // Launches the kernels for B rows whose kernel parameters are already in
 // s->res_params (n_params entries).  Used by the public entry points after
 // resolving pz_row_params, and by the reference-compatible calls, which set

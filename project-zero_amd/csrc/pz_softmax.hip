@@ -8,7 +8,8 @@
 //     max) with a sequential fp32 sum in ascending order, x *= 1/sum.  Any
 //     NaN, or an infinite maximum, makes the sum NaN and every output NaN.
 // The softmax runs one 1024-thread workgroup per row: pass 1 (max), the
-// exact-sum records and walk (pz_rowpass.h), then one write pass.
+// exact-sum records and walk (pz_rowpass.h), then one write pass.  Rows may
+// have their own lengths (attention scores, pz_attn.hip).
 #include "pz_device.h"
 #include "pz_exact.h"
 #include "pz_launch.h"
@@ -34,13 +35,18 @@ struct SoftmaxShared {
 
 template <bool VEC>
 __global__ __launch_bounds__(PZ_RB) void k_softmax(const float* in, long ld_in, float* out,
-                                                   long ld_out, int V, PzTemp T) {
+                                                   long ld_out, int Vmax, PzTemp T,
+                                                   const int32_t* lens) {
   extern __shared__ __align__(16) char lds[];
   __shared__ SoftmaxShared S;
   __shared__ uint64_t etab[32];
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   pz_etab_fill((pz_lds_u64*)etab);  // ordered by pz_pass1's barriers
   const int row = blockIdx.x, tid = threadIdx.x;
+  // the row's length: every thread reads the same value, so the early return
+  // below is uniform over the workgroup
+  const int V = lens ? (lens[row] < Vmax ? lens[row] : Vmax) : Vmax;
+  if (V <= 0) return;
   PzTempRow<VEC> R;
   R.x = in + (long)row * ld_in;
   R.V = V;
@@ -85,6 +91,22 @@ PzTemp temp_of(pz_sampler* s, float temperature) {
 
 }  // namespace
 
+int pz_launch_softmax_rows(pz_sampler* s, const float* d_in, long ld_in, float* d_out,
+                           long ld_out, int B, int V, PzTemp T, const int32_t* d_len) {
+  const size_t lds = pz_rec_bytes(V);
+  if (lds + sizeof(SoftmaxShared) + 64 > (size_t)s->max_lds)
+    return fail(s, PZ_ENOTSUP, "V=%d needs more LDS than the device has", V);
+  const bool vec = (ld_in % 4 == 0) && (((uintptr_t)d_in & 15) == 0);
+  auto kern = vec ? k_softmax<true> : k_softmax<false>;
+  if (lds > 65536)
+    PZ_HIP(s, hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds));
+  hipLaunchKernelGGL(kern, dim3(B), dim3(PZ_RB), lds, s->stream, d_in, ld_in, d_out, ld_out, V,
+                     T, d_len);
+  PZ_HIP(s, hipGetLastError());
+  return PZ_OK;
+}
+
 extern "C" int pz_temperature_batch(pz_sampler* s, float* d_x, long ld, int B, int V,
                                     float temperature) {
   if (!s) return PZ_EINVAL;
@@ -106,16 +128,6 @@ extern "C" int pz_softmax_batch(pz_sampler* s, const float* d_in, long ld_in, fl
     return fail(s, PZ_EINVAL, "bad softmax shape");
   if (B == 0) return PZ_OK;
   PZ_HIP(s, hipSetDevice(s->device));
-  const size_t lds = pz_rec_bytes(V);
-  if (lds + sizeof(SoftmaxShared) + 64 > (size_t)s->max_lds)
-    return fail(s, PZ_ENOTSUP, "V=%d needs more LDS than the device has", V);
-  const bool vec = (ld_in % 4 == 0) && (((uintptr_t)d_in & 15) == 0);
-  auto kern = vec ? k_softmax<true> : k_softmax<false>;
-  if (lds > 65536)
-    PZ_HIP(s, hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)lds));
-  hipLaunchKernelGGL(kern, dim3(B), dim3(PZ_RB), lds, s->stream, d_in, ld_in, d_out, ld_out, V,
-                     temp_of(s, temperature));
-  PZ_HIP(s, hipGetLastError());
-  return PZ_OK;
+  return pz_launch_softmax_rows(s, d_in, ld_in, d_out, ld_out, B, V, temp_of(s, temperature),
+                                nullptr);
 }

@@ -25,7 +25,7 @@ ABI_SYMBOLS = (
     "pz_sample_batch_async", "pz_sampler_sync", "pz_spec_verify",
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
     "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
-    "pz_sample_step", "pz_sampler_set_eos",
+    "pz_sample_step", "pz_sampler_set_eos", "pz_attn_softmax",
     # include/pz_sampling_compat.h: the reference sampler's own symbols
     "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
     "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
@@ -96,6 +96,7 @@ def load():
     lib.pz_memcpy_d2h.argtypes = [_P, _P, ctypes.c_size_t]
     lib.pz_temperature_batch.argtypes = [_P, _P, _L, _I, _I, _F]
     lib.pz_softmax_batch.argtypes = [_P, _P, _L, _P, _L, _I, _I, _F]
+    lib.pz_attn_softmax.argtypes = [_P, _P, _L, _P, _L, _I, _I, _P]
     pull = ctypes.POINTER(ctypes.c_ulonglong)
     lib.sample_argmax.argtypes = [_P, _I]
     lib.apply_temperature.argtypes = [_P, _I, _F]
@@ -241,6 +242,13 @@ class Sampler:
         _sync_torch(d_in, d_out)
         self._check(self.lib.pz_softmax_batch(self.h, _ptr(d_in), ld_in, _ptr(d_out), ld_out, B,
                                               V, temperature))
+
+    def attn_softmax(self, d_in, d_out, n_rows, n, ld_in, ld_out, d_len=None):
+        """Reference softmax of attention-score rows, row r over its first
+        min(d_len[r], n) entries (asynchronous)."""
+        _sync_torch(d_in, d_out, d_len)
+        self._check(self.lib.pz_attn_softmax(self.h, _ptr(d_in), ld_in, _ptr(d_out), ld_out,
+                                             n_rows, n, _ptr(d_len)))
 
     def spec_verify(self, d_target, d_draft, B, K, V, ld, has_bonus, temperature,
                     draft_ids, u_acc, u_res):
