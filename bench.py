@@ -1,36 +1,48 @@
-"""Benchmark of the batched token sampler on one MI355X.
+"""Benchmark of the batched token sampler on one MI355X: ONE JSON line.
 
-Default workload (the one the headline metric is quoted on): batch 1024 x
-vocab 128256 fp32 logits ~ N(0, 3^2), repetition penalty 1.15 over a per-row
-history of 256 uniform ids, greedy argmax with lowest-id tie-break.  Logits and
-histories are resident in HBM before timing starts; a step is one
-pz_sample_batch call (the kernel plus the copy of the 1024 int32 ids to the
-host), timed over --steps steps after --warmup untimed ones.
+Headline (`value`): batch 1024 x vocab 128256 fp32 logits ~ N(0, 3^2),
+repetition penalty 1.15 over a per-row history of 256 uniform ids, greedy
+argmax with lowest-id tie-break.  A step is one synchronous pz_sample_batch
+call (the kernels plus the ids' return to the host); logits and histories are
+resident in HBM before timing starts.
 
-Printed: ONE JSON line with the throughput (rows/s), the roofline of the
-sampling kernels (algorithmic bytes / kernel time from HIP events on the
-sampler's own stream, against the 8 TB/s HBM peak), the measured HBM traffic
-per launch when a counter summary for the workload is committed
-(profiles/traffic.json), the CPU baseline (the oracle, one thread, on a
-bounded sample of the same workload) and the id parity of the timed batch.
+The same line carries
+  workloads    c1 one sequence x 49152, repetition + top-k 40 + top-p 0.95,
+                  one row per call (the reference's loop), 500 fresh rows
+               c2 64 x 128256, temperature 0.7 + top-p 0.9, 5 spikes per row
+               c3 256 x 151936, presence/frequency + top-k 20 + top-p 0.8
+               c5 speculative verification, 32 sequences x 4 drafts x 128256
+  batch_sweep  greedy (as the headline) and top-p (as c2) at vocab 128256,
+               batch 1, 8, 64, 256, 1024
+each with rows/s (wall clock of synchronous calls), the kernels' time per
+launch from HIP events on the sampler's own stream, algorithmic GB/s and the
+fraction of the 8 TB/s HBM peak, and parity with the oracle (ids; draws
+within 1e-5 of a CDF boundary counted apart).  The timed loops rotate over
+enough distinct batches that one pass reads more than the 256 MB Infinity
+Cache holds, so the GB/s figures are HBM figures.
 
-Other workloads, measured as parity cases with the same fields:
-  --workload c2   64 x 128256, temperature 0.7 + top-p 0.9 (5 spikes per row)
-  --workload c3   256 x 151936, presence/frequency + top-k 20 + top-p 0.8
-  --workload c1   one sequence x 49152, repetition + top-k 40 + top-p 0.95
-                  (500 steps of fresh logits, one row per call)
-  --workload c5   speculative verification, 32 sequences x 4 drafts x 128256
+CPU baseline: the oracle (oracle/pz_oracle.c, the clean-room restatement of
+the reference sampler) built on this host with the reference's release flags
+(-O3 -march=native), on a bounded sample of each workload: one thread
+(`cpu_baseline`, the reference's own threading) and N threads
+(`cpu_baseline_ncore`, N stated).  The temperature form follows the host:
+x * (1/T) where the CPU has AVX-512 (the reference's build there), else x / T;
+the GPU sampler uses the same form.
 """
 import argparse
 import json
 import os
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "project-zero_amd"))
 
 HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 << 20
+BOUNDARY = 1e-5
 METRIC = "sampled rows/s at vocab 128256, batch 1-1024; achieved HBM GB/s vs peak"
 
 WORKLOAD_TEXT = {
@@ -44,19 +56,32 @@ WORKLOAD_TEXT = {
     "c5": "speculative verification, 32 sequences x 4 drafts x vocab 128256 (+ bonus row), "
           "tau 0.8",
 }
-KERNELS = {"c4": "k_greedy", "c2": "k_topp", "c3": "k_topk", "c1": "k_topk",
-           "c5": "k_spec_rows + k_spec_verify"}
+KERNELS = {
+    "c4": "k_greedy",
+    "c2": "k_topp_max + k_topp_est + k_topp_rec + k_topp_walk + k_topp_gather + "
+          "k_topp_nucleus + k_topp_fallback",
+    "c3": "k_topk",
+    "c1": "k_topk",
+    "c5": "k_spec_stat + k_spec_rec + k_spec_walk + k_spec_accept + k_spec_vest + "
+          "k_spec_vrec + k_spec_vwalk",
+}
+SWEEP_B = (1, 8, 64, 256, 1024)
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=sorted(WORKLOAD_TEXT))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="target CPU time of the baseline sample")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "sweep"] + sorted(WORKLOAD_TEXT),
+                    help="all (default): the headline, every workload and the sweep; "
+                         "one name: that workload alone (profiling runs)")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline and the parity checks")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0,
+                    help="CPU time of each baseline sample (per thread count)")
     return ap.parse_args()
 
 
@@ -64,224 +89,446 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def orc_params(po, p):
-    return po.params(p.temperature, p.top_k, p.top_p, p.rep_penalty, p.presence_penalty,
-                     p.frequency_penalty)
+# ---------------------------------------------------------------------------
+# the oracle: CPU baseline and checker
+# ---------------------------------------------------------------------------
+class Cpu:
+    """The oracle built for this host, its thread count and temperature form."""
+
+    def __init__(self, enabled):
+        self.enabled = enabled
+        self.build = "not built"
+        self.po = None
+        self.threads = max(1, min(16, os.cpu_count() or 1))
+        if not enabled:
+            return
+        out = os.path.join(tempfile.mkdtemp(prefix="pzorc_"), "libpzoracle.so")
+        r = subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "native",
+                            f"NATIVE_OUT={out}"], capture_output=True, text=True)
+        if r.returncode == 0 and os.path.exists(out):
+            os.environ["PZ_ORACLE_LIB"] = out
+            self.build = "gcc -std=c99 -O3 -march=native -ffp-contract=off (built on this host)"
+        else:
+            log(f"native oracle build failed, using the shipped x86-64-v3 build: {r.stderr[-300:]}")
+            self.build = "gcc -std=c99 -O3 -march=x86-64-v3 -ffp-contract=off (shipped build)"
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pz_oracle as po
+        self.po = po
+        self.avx512 = po.host_has_avx512()
+
+    def temp_mode(self):
+        import pzsample as pz
+        if self.po is None:
+            return pz.PZ_TEMP_MUL_RECIP
+        return pz.PZ_TEMP_MUL_RECIP if self.avx512 else pz.PZ_TEMP_DIV
+
+    def oparams(self, params):
+        po = self.po
+        return [po.params(p.temperature, p.top_k, p.top_p, p.rep_penalty, p.presence_penalty,
+                          p.frequency_penalty) for p in params]
+
+    def rows(self, x, params, u, hist, lo, hi):
+        return self.po.sample_batch(x[lo:hi], self.oparams(params),
+                                    u=None if u is None else u[lo:hi],
+                                    hist=None if hist is None else hist[lo:hi],
+                                    temp_mode=self.temp_mode())
+
+    def parity(self, x, params, u, hist, gpu_ids, n_rows=None):
+        """Oracle ids of the first n_rows rows (threads over row blocks) and
+        the comparison, boundary rows apart."""
+        import numpy as np
+        from concurrent.futures import ThreadPoolExecutor
+        B = x.shape[0] if n_rows is None else n_rows
+        n = min(self.threads, B)
+        cuts = [B * i // n for i in range(n + 1)]
+        with ThreadPoolExecutor(n) as ex:
+            parts = list(ex.map(lambda i: self.rows(x, params, u, hist, cuts[i], cuts[i + 1]),
+                                range(n)))
+        ids = np.concatenate([p[0] for p in parts])
+        dd = np.concatenate([p[2] for p in parts])
+        dc = np.concatenate([p[3] for p in parts])
+        bnd = np.minimum(dd, dc) < BOUNDARY
+        bad = ids != np.asarray(gpu_ids[:B])
+        return {"rows": int(B), "boundary_rows": int(bnd.sum()),
+                "mismatches_nonboundary": int((bad & ~bnd).sum()),
+                "mismatches_boundary": int((bad & bnd).sum())}
+
+    def baseline(self, x, params, u, hist, budget, unit="rows/s"):
+        """Rows/s of the oracle on a bounded sample of the batch: one
+        thread, then self.threads threads each sampling the same rows."""
+        from concurrent.futures import ThreadPoolExecutor
+        B = x.shape[0]
+        probe = min(B, 4)
+        t0 = time.perf_counter()
+        self.rows(x, params, u, hist, 0, probe)
+        per_row = (time.perf_counter() - t0) / probe
+        rows = int(max(1, min(B, budget / max(per_row, 1e-9))))
+        reps = max(1, int(budget / max(per_row * rows, 1e-9))) if rows == B else 1
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            self.rows(x, params, u, hist, 0, rows)
+        dt1 = time.perf_counter() - t0
+        what = f"{reps} x the full {B}-row batch" if rows == B else f"the first {rows} of {B} rows"
+        one = {"value": rows * reps / dt1, "unit": unit, "cores": 1, "kind": "port",
+               "sample": f"{what} ({rows * reps} rows, {dt1:.1f} s)", "build": self.build}
+        N = self.threads
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(N) as ex:
+            list(ex.map(lambda _: self.rows(x, params, u, hist, 0, rows), range(N)))
+        dtn = time.perf_counter() - t0
+        ncore = {"value": N * rows / dtn, "unit": unit, "cores": N, "kind": "port",
+                 "sample": f"{N} threads x the first {rows} rows ({N * rows} rows, {dtn:.1f} s)",
+                 "build": self.build}
+        return one, ncore
 
 
-def cpu_baseline_rows(w, budget_s):
-    """The oracle (one thread) on whole batches, or on a prefix of the batch
-    when one batch exceeds the budget; returns (baseline, ids of the rows it
-    sampled)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import numpy as np
-    import pz_oracle as po
-    x, u, hist = w["logits"], w["u"], w["hist"]
-    prm = [orc_params(po, p) for p in w["params"]]
-    B = x.shape[0]
-    probe = min(B, 8)
-    t0 = time.perf_counter()
-    po.sample_batch(x[:probe], prm, u=None if u is None else u[:probe],
-                    hist=None if hist is None else hist[:probe])
-    per_row = (time.perf_counter() - t0) / probe
-    rows = int(max(1, min(B, budget_s / max(per_row, 1e-9))))
-    reps = 1
-    if rows == B:
-        reps = max(1, int(budget_s / max(per_row * B, 1e-9)))
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        ids, _, _, _ = po.sample_batch(x[:rows], prm, u=None if u is None else u[:rows],
-                                       hist=None if hist is None else hist[:rows])
-    dt = time.perf_counter() - t0
-    n = rows * reps
-    what = (f"{reps} x the full {B}-row batch" if rows == B else f"the first {rows} of {B} rows")
-    return {"value": n / dt, "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{what} ({n} rows, {dt:.1f} s; oracle/pz_oracle.c, 1 thread)"}, ids
+# ---------------------------------------------------------------------------
+# GPU timing
+# ---------------------------------------------------------------------------
+def events_ms(torch, stream_ptr, launches, per_call=False):
+    """Average time per launch of the kernels the callables in `launches`
+    enqueue (one launch each), from HIP events on the sampler's stream: one
+    pair around the whole back-to-back sequence, or with per_call (calls that
+    wait for their own results) one pair around each call's kernels."""
+    ext = torch.cuda.ExternalStream(stream_ptr)
+    launches[0]()
+    torch.cuda.synchronize()
+    if not per_call:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(ext)
+        for f in launches:
+            f()
+        e1.record(ext)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / len(launches)
+    total = 0.0
+    for f in launches:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(ext)
+        f()
+        e1.record(ext)
+        e1.synchronize()
+        total += e0.elapsed_time(e1)
+    return total / len(launches)
+
+
+def rotation(batch_bytes):
+    """Distinct batches the timed loop cycles through: more than the
+    Infinity Cache holds."""
+    return max(1, -(-int(1.2 * MALL_BYTES) // int(batch_bytes)))
+
+
+def roofline(bytes_per_launch, kern_ms, traffic, kernel):
+    achieved = bytes_per_launch / (kern_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": kernel,
+            "kernel_us": kern_ms * 1e3, "algorithmic_bytes_per_launch": int(bytes_per_launch)}
 
 
 def traffic_for(workload):
-    path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
             t = json.load(f)
         return t.get(workload, {}).get("hbm_bytes_per_launch")
     except (OSError, ValueError):
         return None
 
 
-def kernel_time_ms(torch, stream_ptr, fn, steps):
-    """Average time of fn()'s kernels per call from HIP events on the
-    sampler's own stream."""
-    ext = torch.cuda.ExternalStream(stream_ptr)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    fn()
-    torch.cuda.synchronize()
-    e0.record(ext)
-    for _ in range(steps):
-        fn()
-    e1.record(ext)
-    e1.synchronize()
-    return e0.elapsed_time(e1) / steps
-
-
-def bench_rows(args, torch, w):
+def run_batched(args, torch, cpu, name):
+    """c2, c3, c4: one synchronous call per step over rotating batches."""
     import numpy as np
     import pzsample as pz
-    x = w["logits"]
-    B, V = x.shape
-    hist = w["hist"]
-    H = hist.shape[1] if hist is not None else 0
+    import workloads as wl
+    build = wl.BUILDERS[name]
+    w0 = build()
+    B, V = w0["logits"].shape
+    nrot = rotation(B * w0["bytes_per_row"])
+    log(f"{name}: {nrot} distinct batches of {B} x {V}")
+    ws = [w0] + [build(seed=wl.SEEDS[name] + 977 * k) for k in range(1, nrot)]
+    H = w0["hist"].shape[1] if w0["hist"] is not None else 0
     dev = torch.device("cuda:0")
-    t_x = torch.from_numpy(x).to(dev)
-    t_h = torch.from_numpy(hist).to(dev) if hist is not None else None
-    u = w["u"]
-    t_u = torch.from_numpy(u).to(dev) if u is not None else None
+    t_x = [torch.from_numpy(w["logits"]).to(dev) for w in ws]
+    t_h = [torch.from_numpy(w["hist"]).to(dev) if H else None for w in ws]
+    t_u = [torch.from_numpy(w["u"]).to(dev) if w["u"] is not None else None for w in ws]
     t_ids = torch.empty(B, dtype=torch.int32, device=dev)
     torch.cuda.synchronize()
-    d_x, d_ids = t_x.data_ptr(), t_ids.data_ptr()
-    d_h = t_h.data_ptr() if t_h is not None else None
-    d_u = t_u.data_ptr() if t_u is not None else None
-    params = w["params"]
-    s = pz.Sampler(B, V, max_hist=max(H, 1))
-    per_call = 1 if args.workload == "c1" else B  # c1: one row per call, like the reference loop
-    ids = np.empty(B, np.int32)
+    params = w0["params"]
+    s = pz.Sampler(B, V, max_hist=max(H, 1), temp_mode=cpu.temp_mode())
 
-    def step():
-        if per_call == B:
-            return s.sample(d_x, B, V, V, params, u=u, d_hist=d_h, H=H)[0]
-        for r in range(B):
-            ids[r] = s.sample(d_x + 4 * V * r, 1, V, V, params,
-                              u=None if u is None else u[r:r + 1],
-                              d_hist=None if d_h is None else d_h + 4 * H * r, H=H)[0][0]
-        return ids
+    def step(k):
+        w = ws[k]
+        return s.sample(t_x[k], B, V, V, params, u=w["u"], d_hist=t_h[k], H=H)[0]
 
-    log("warmup")
-    for _ in range(args.warmup):
-        out = step()
+    for t in range(args.warmup):
+        step(t % nrot)
     torch.cuda.synchronize()
-    steps = args.steps if per_call == B else max(1, args.steps // 10)
-    log(f"timing {steps} steps")
     t0 = time.perf_counter()
-    for _ in range(steps):
-        out = step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / steps
-    gpu_ids = out.copy()
-
-    if per_call == B:
-        def launch():
-            s.sample_async(d_x, B, V, V, params, d_u, d_ids, d_hist=d_h, H=H)
-    else:
-        def launch():
-            s.sample_async(d_x, 1, V, V, params, d_u, d_ids, d_hist=d_h, H=H)
-    kern_ms = kernel_time_ms(torch, s.stream, launch, max(steps, 20))
-    rows_per_launch = per_call
-    s.close()
-    return dict(B=B, V=V, H=H, ms_per_step=ms_per_step, rows_per_step=B,
-                kern_ms=kern_ms, bytes_per_launch=w["bytes_per_row"] * rows_per_launch,
-                gpu_ids=gpu_ids)
-
-
-def bench_spec(args, torch, w):
-    import pzsample as pz
-    B, K, V = w["B"], w["K"], w["V"]
-    dev = torch.device("cuda:0")
-    t_t = torch.from_numpy(w["target"]).to(dev)
-    t_d = torch.from_numpy(w["draft"]).to(dev)
-    torch.cuda.synchronize()
-    s = pz.Sampler(B, V)
-
-    def call():
-        return s.spec_verify(t_t.data_ptr(), t_d.data_ptr(), B, K, V, V, w["has_bonus"],
-                             w["tau"], w["draft_ids"], w["u_acc"], w["u_res"])
-
-    for _ in range(args.warmup):
-        acc, out = call()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        acc, out = call()
+    for t in range(args.steps):
+        step(t % nrot)
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    kern_ms = kernel_time_ms(torch, s.stream, call, max(args.steps, 20))
+    ids0 = step(0).copy()
+
+    def launch(k):
+        return lambda: s.sample_async(t_x[k], B, V, V, params, t_u[k], t_ids, d_hist=t_h[k], H=H)
+    kern = events_ms(torch, s.stream, [launch(t % nrot) for t in range(max(args.steps, 20))])
     s.close()
-    return dict(B=B, V=V, K=K, ms_per_step=ms, rows_per_step=B, kern_ms=kern_ms,
-                bytes_per_launch=w["bytes_per_seq"] * B, acc=acc, out=out)
+    bpl = w0["bytes_per_row"] * B
+    r = {"workload": WORKLOAD_TEXT[name], "batch": B, "vocab": V, "hist": H,
+         "distinct_batches": nrot, "ms_per_step": ms, "value": B / (ms * 1e-3), "unit": "rows/s",
+         "roofline": roofline(bpl, kern, traffic_for(name), KERNELS[name])}
+    if cpu.enabled:
+        log(f"{name}: parity and cpu baseline")
+        r["parity"] = cpu.parity(w0["logits"], params, w0["u"], w0["hist"], ids0)
+        r["cpu_baseline"], r["cpu_baseline_ncore"] = cpu.baseline(
+            w0["logits"], params, w0["u"], w0["hist"], args.cpu_seconds)
+    del t_x, t_h, t_u
+    torch.cuda.empty_cache()
+    return r
+
+
+def run_c1(args, torch, cpu):
+    """One row per call, the reference's loop: 500 fresh rows, each call
+    synchronous (the id returns to the host before the next)."""
+    import numpy as np
+    import pzsample as pz
+    import workloads as wl
+    w = wl.build_c1()
+    x, hist, u = w["logits"], w["hist"], w["u"]
+    R, V = x.shape
+    H = hist.shape[1]
+    dev = torch.device("cuda:0")
+    t_x = torch.from_numpy(x).to(dev)
+    t_h = torch.from_numpy(hist).to(dev)
+    t_u = torch.from_numpy(u).to(dev)
+    t_ids = torch.empty(R, dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+    params = w["params"]
+    s = pz.Sampler(1, V, max_hist=H, temp_mode=cpu.temp_mode())
+    dx, dh, du, di = t_x.data_ptr(), t_h.data_ptr(), t_u.data_ptr(), t_ids.data_ptr()
+    ids = np.empty(R, np.int32)
+
+    def call(r):
+        return s.sample(dx + 4 * V * r, 1, V, V, params, u=u[r:r + 1], d_hist=dh + 4 * H * r,
+                        H=H)[0][0]
+
+    for r in range(min(args.warmup * 10, R)):
+        call(r)
+    t0 = time.perf_counter()
+    for r in range(R):
+        ids[r] = call(r)
+    ms = (time.perf_counter() - t0) * 1e3 / R
+
+    def launch(r):
+        return lambda: s.sample_async(dx + 4 * V * r, 1, V, V, params, du + 4 * r, di + 4 * r,
+                                      d_hist=dh + 4 * H * r, H=H)
+    kern = events_ms(torch, s.stream, [launch(r) for r in range(R)])
+    s.close()
+    r = {"workload": WORKLOAD_TEXT["c1"], "batch": 1, "vocab": V, "hist": H, "calls": R,
+         "ms_per_step": ms, "value": 1.0 / (ms * 1e-3), "unit": "rows/s",
+         "roofline": roofline(w["bytes_per_row"], kern, traffic_for("c1"), KERNELS["c1"])}
+    if cpu.enabled:
+        log("c1: parity and cpu baseline")
+        r["parity"] = cpu.parity(x, params, u, hist, ids)
+        r["cpu_baseline"], r["cpu_baseline_ncore"] = cpu.baseline(x, params, u, hist,
+                                                                  args.cpu_seconds)
+        r["gpu_call_over_cpu_row"] = r["cpu_baseline"]["value"] / r["value"]
+    return r
+
+
+def run_c5(args, torch, cpu):
+    import numpy as np
+    import pzsample as pz
+    import workloads as wl
+    w0 = wl.build_c5()
+    B, K, V = w0["B"], w0["K"], w0["V"]
+    nrot = rotation(w0["bytes_per_seq"] * B)
+    log(f"c5: {nrot} distinct batches")
+    ws = [w0] + [wl.build_c5(seed=wl.SEEDS["c5"] + 977 * k) for k in range(1, nrot)]
+    dev = torch.device("cuda:0")
+    t_t = [torch.from_numpy(w["target"]).to(dev) for w in ws]
+    t_d = [torch.from_numpy(w["draft"]).to(dev) for w in ws]
+    torch.cuda.synchronize()
+    s = pz.Sampler(B, V, temp_mode=cpu.temp_mode())
+
+    def call(k):
+        w = ws[k]
+        return s.spec_verify(t_t[k], t_d[k], B, K, V, V, w["has_bonus"], w["tau"],
+                             w["draft_ids"], w["u_acc"], w["u_res"])
+
+    for t in range(args.warmup):
+        call(t % nrot)
+    t0 = time.perf_counter()
+    for t in range(args.steps):
+        call(t % nrot)
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    acc0, out0 = call(0)
+    kern = events_ms(torch, s.stream,
+                     [(lambda k=t % nrot: call(k)) for t in range(max(args.steps, 20))],
+                     per_call=True)
+    s.close()
+    bpl = w0["bytes_per_seq"] * B
+    r = {"workload": WORKLOAD_TEXT["c5"], "batch": B, "drafts": K, "vocab": V,
+         "distinct_batches": nrot, "ms_per_step": ms, "value": B / (ms * 1e-3),
+         "unit": "sequences/s", "roofline": roofline(bpl, kern, traffic_for("c5"), KERNELS["c5"])}
+    if cpu.enabled:
+        log("c5: parity and cpu baseline")
+        po = cpu.po
+        tm = cpu.temp_mode()
+        acc, out, dist = po.spec_verify(w0["target"], w0["draft"], K, w0["has_bonus"],
+                                        w0["tau"], w0["draft_ids"], w0["u_acc"], w0["u_res"],
+                                        temp_mode=tm)
+        bnd = dist < BOUNDARY
+        bad = (acc != acc0) | (out != out0).any(axis=1)
+        r["parity"] = {"sequences": B, "boundary_sequences": int(bnd.sum()),
+                       "mismatches_nonboundary": int((bad & ~bnd).sum()),
+                       "mismatches_boundary": int((bad & bnd).sum())}
+        from concurrent.futures import ThreadPoolExecutor
+
+        def verify(lo, hi):
+            return po.spec_verify(w0["target"][lo:hi], w0["draft"][lo:hi], K, w0["has_bonus"],
+                                  w0["tau"], w0["draft_ids"][lo:hi], w0["u_acc"][lo:hi],
+                                  w0["u_res"][lo:hi], temp_mode=tm)
+        t1 = time.perf_counter()
+        verify(0, 1)
+        per_seq = time.perf_counter() - t1
+        nseq = int(max(1, min(B, args.cpu_seconds / max(per_seq, 1e-9))))
+        t0 = time.perf_counter()
+        verify(0, nseq)
+        dt1 = time.perf_counter() - t0
+        N = cpu.threads
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(N) as ex:
+            list(ex.map(lambda _: verify(0, nseq), range(N)))
+        dtn = time.perf_counter() - t0
+        r["cpu_baseline"] = {"value": nseq / dt1, "unit": "sequences/s", "cores": 1,
+                             "kind": "port", "sample": f"the first {nseq} of {B} sequences "
+                             f"({dt1:.1f} s)", "build": cpu.build}
+        r["cpu_baseline_ncore"] = {"value": N * nseq / dtn, "unit": "sequences/s", "cores": N,
+                                   "kind": "port", "sample": f"{N} threads x the first {nseq} "
+                                   f"sequences ({dtn:.1f} s)", "build": cpu.build}
+    del t_t, t_d
+    torch.cuda.empty_cache()
+    return r
+
+
+def run_sweep(args, torch, cpu):
+    """Greedy (headline chain) and top-p (c2 chain) at vocab 128256 over a
+    1024-row pool (525 MB, beyond the Infinity Cache): step t of batch B
+    reads rows [tB mod 1024, +B)."""
+    import numpy as np
+    import pzsample as pz
+    import workloads as wl
+    V, P = 128256, 1024
+    out = {"vocab": V, "pool_rows": P, "greedy": [], "top_p": []}
+    dev = torch.device("cuda:0")
+    for kind, build in (("greedy", wl.build_c4), ("top_p", wl.build_c2)):
+        w = build(B=P, V=V)
+        x, hist, u = w["logits"], w["hist"], w["u"]
+        H = hist.shape[1] if hist is not None else 0
+        t_x = torch.from_numpy(x).to(dev)
+        t_h = torch.from_numpy(hist).to(dev) if H else None
+        t_u = torch.from_numpy(u).to(dev) if u is not None else None
+        t_ids = torch.empty(P, dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        params = w["params"]
+        for B in SWEEP_B:
+            s = pz.Sampler(B, V, max_hist=max(H, 1), temp_mode=cpu.temp_mode())
+            steps = 100 if B <= 64 else (40 if B <= 256 else 20)
+            dx = t_x.data_ptr()
+            dh = t_h.data_ptr() if H else None
+            du = t_u.data_ptr() if t_u is not None else None
+
+            def off(t):
+                return (t * B) % P
+
+            def call(t):
+                o = off(t)
+                return s.sample(dx + 4 * V * o, B, V, V, params,
+                                u=None if u is None else u[o:o + B],
+                                d_hist=None if dh is None else dh + 4 * H * o, H=H)[0]
+            for t in range(3):
+                call(t)
+            t0 = time.perf_counter()
+            for t in range(steps):
+                call(t)
+            ms = (time.perf_counter() - t0) * 1e3 / steps
+            ids0 = call(0).copy()
+
+            def launch(t):
+                o = off(t)
+                return lambda: s.sample_async(dx + 4 * V * o, B, V, V, params,
+                                              None if du is None else du + 4 * o,
+                                              t_ids.data_ptr(),
+                                              d_hist=None if dh is None else dh + 4 * H * o, H=H)
+            kern = events_ms(torch, s.stream, [launch(t) for t in range(steps)])
+            s.close()
+            gbs = B * w["bytes_per_row"] / (kern * 1e-3) / 1e9
+            e = {"batch": B, "rows_per_s": B / (ms * 1e-3), "ms_per_step": ms,
+                 "kernel_us": kern * 1e3, "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS}
+            if cpu.enabled:
+                e["parity"] = cpu.parity(x, params, u, hist, ids0, n_rows=min(B, 64))
+            out[kind].append(e)
+            log(f"sweep {kind} B={B}: {e['rows_per_s']:.0f} rows/s, kernels {kern * 1e3:.1f} us, "
+                f"{gbs:.0f} GB/s")
+        del t_x, t_h, t_u
+        torch.cuda.empty_cache()
+    return out
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU (one process, one device); "
-                                   "rows shard across GPUs with no exchange, so multi-GPU "
-                                   "figures are not produced: run --gpus 1"}))
+                                   "rows shard across GPUs with no exchange, so no multi-GPU "
+                                   "figure is produced: run --gpus 1"}))
         sys.exit(2)
-    import numpy as np
     import torch
 
-    import workloads as wl
-
-    log(f"building workload {args.workload}")
-    w = wl.BUILDERS[args.workload]()
-    if args.workload == "c5":
-        r = bench_spec(args, torch, w)
-        unit = "sequences/s"
-    else:
-        r = bench_rows(args, torch, w)
-        unit = "rows/s"
-    log(f"step {r['ms_per_step'] * 1e3:.1f} us, kernels {r['kern_ms'] * 1e3:.1f} us per launch")
-    achieved = r["bytes_per_launch"] / (r["kern_ms"] * 1e-3) / 1e9
-    config = {"workload": WORKLOAD_TEXT[args.workload], "batch": r["B"], "vocab": r["V"]}
-    if "H" in r:
-        config["hist"] = r["H"]
-    if "K" in r:
-        config["drafts"] = r["K"]
+    cpu = Cpu(not args.no_cpu)
+    head = "c4" if args.workload in ("all", "sweep") else args.workload
+    runners = {"c1": run_c1, "c5": run_c5}
+    log(f"headline {head}")
+    h = runners.get(head, lambda a, t, c: run_batched(a, t, c, head))(args, torch, cpu)
+    log(f"{head}: step {h['ms_per_step'] * 1e3:.1f} us, kernels "
+        f"{h['roofline']['kernel_us']:.1f} us, frac {h['roofline']['frac']:.3f}")
+    config = {"workload": h["workload"], "batch": h["batch"], "vocab": h["vocab"]}
+    for k in ("hist", "drafts", "distinct_batches", "calls"):
+        if k in h:
+            config[k] = h[k]
     line = {
         "metric": METRIC,
-        "value": r["rows_per_step"] / (r["ms_per_step"] * 1e-3),
-        "unit": unit,
+        "value": h["value"],
+        "unit": h["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": r["ms_per_step"],
+        "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded generators in project-zero_amd/synth)",
         "config": config,
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_for(args.workload),
-                     "kernel": KERNELS[args.workload], "kernel_us": r["kern_ms"] * 1e3,
-                     "algorithmic_bytes_per_launch": r["bytes_per_launch"]},
+        "roofline": h["roofline"],
     }
-    if not args.no_cpu:
-        log("cpu baseline")
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import pz_oracle as po
-        if args.workload == "c5":
-            t0 = time.perf_counter()
-            reps = 0
-            while True:
-                acc, out, _ = po.spec_verify(w["target"], w["draft"], w["K"], w["has_bonus"],
-                                             w["tau"], w["draft_ids"], w["u_acc"], w["u_res"])
-                reps += 1
-                if time.perf_counter() - t0 >= args.cpu_seconds:
-                    break
-            dt = time.perf_counter() - t0
-            line["cpu_baseline"] = {"value": reps * w["B"] / dt, "unit": "sequences/s",
-                                    "cores": 1, "kind": "port",
-                                    "sample": f"{reps} x the full {w['B']}-sequence batch "
-                                              f"({dt:.1f} s; oracle/pz_oracle.c, 1 thread)"}
-            line["parity"] = {"sequences": w["B"],
-                              "acc_len_mismatches": int((acc != r["acc"]).sum()),
-                              "id_mismatches": int((out != r["out"]).any(axis=1).sum())}
-        else:
-            cb, cpu_ids = cpu_baseline_rows(w, args.cpu_seconds)
-            line["cpu_baseline"] = cb
-            n = len(cpu_ids)
-            line["parity"] = {"rows_checked": n,
-                              "id_mismatches_vs_oracle": int((cpu_ids != r["gpu_ids"][:n]).sum())}
+    for k in ("cpu_baseline", "cpu_baseline_ncore", "parity"):
+        if k in h:
+            line[k] = h[k]
+    if cpu.enabled:
+        line["temperature_form"] = "x*(1/T)" if cpu.avx512 else "x/T"
+    if args.workload == "all":
+        line["workloads"] = {}
+        for name in ("c1", "c2", "c3", "c5"):
+            log(f"workload {name}")
+            r = runners.get(name, lambda a, t, c, n=name: run_batched(a, t, c, n))(args, torch,
+                                                                                   cpu)
+            line["workloads"][name] = r
+            log(f"{name}: step {r['ms_per_step'] * 1e3:.1f} us, kernels "
+                f"{r['roofline']['kernel_us']:.1f} us, frac {r['roofline']['frac']:.3f}")
+    if args.workload in ("all", "sweep") and not args.no_sweep:
+        line["batch_sweep"] = run_sweep(args, torch, cpu)
     print(json.dumps(line), flush=True)
 
 

@@ -10,7 +10,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_LIB = os.path.join(HERE, "libpzoracle.so")
+# PZ_ORACLE_LIB selects another build of the same source (bench.py's
+# -march=native build on the timing host)
+ORACLE_LIB = os.environ.get("PZ_ORACLE_LIB") or os.path.join(HERE, "libpzoracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 
 TEMP_MUL_RECIP, TEMP_DIV = 0, 1
