@@ -14,6 +14,8 @@ The same line carries
                c5 speculative verification, 32 sequences x 4 drafts x 128256
   batch_sweep  greedy (as the headline) and top-p (as c2) at vocab 128256,
                batch 1, 8, 64, 256, 1024
+  attention    the reference softmax over attention scores (the tn_softmax of
+               attention.c:210), 32 heads x valid context 128, 4096, 32768
 each with rows/s (wall clock of synchronous calls), the kernels' time per
 launch from HIP events on the sampler's own stream, algorithmic GB/s and the
 fraction of the 8 TB/s HBM peak, and parity with the oracle (ids; draws
@@ -74,7 +76,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "sweep"] + sorted(WORKLOAD_TEXT),
+                    choices=["all", "sweep", "attn"] + sorted(WORKLOAD_TEXT),
                     help="all (default): the headline, every workload and the sweep; "
                          "one name: that workload alone (profiling runs)")
     ap.add_argument("--no-cpu", action="store_true",
@@ -477,6 +479,54 @@ def run_sweep(args, torch, cpu):
     return out
 
 
+def run_attention(args, torch, cpu):
+    """pz_attn_softmax over [32 heads, ctx] N(0, 3^2) scores, ctx rotating
+    over distinct score blocks past the Infinity Cache; bytes per launch =
+    one read and one write of every score."""
+    import ctypes
+    import numpy as np
+    import pzsample as pz
+    heads = 32
+    out = {"heads": heads, "entries": []}
+    dev = torch.device("cuda:0")
+    s = pz.Sampler(1, 16)
+    for ctx in (128, 4096, 32768):
+        blk = heads * ctx * 4
+        nrot = rotation(2 * blk)
+        rng = np.random.default_rng(ctx)
+        x = (rng.standard_normal((nrot * heads, ctx)) * 3.0).astype(np.float32)
+        t_x = torch.from_numpy(x).to(dev)
+        t_o = torch.empty_like(t_x)
+        torch.cuda.synchronize()
+        dx, do = t_x.data_ptr(), t_o.data_ptr()
+
+        def launch(t):
+            k = (t % nrot) * heads
+            return lambda: s.lib.pz_attn_softmax(s.h, dx + 4 * ctx * k, ctx, do + 4 * ctx * k,
+                                                 ctx, heads, ctx, None)
+        steps = 200 if ctx <= 4096 else 50
+        kern = events_ms(torch, s.stream, [launch(t) for t in range(steps)])
+        gbs = 2 * blk / (kern * 1e-3) / 1e9
+        e = {"ctx": ctx, "kernel_us": kern * 1e3, "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS,
+             "distinct_blocks": nrot,
+             "kernel": "k_attn_wave" if ctx <= 4096 else "k_softmax (one workgroup per row)"}
+        if cpu.enabled:
+            s.sync()
+            got = t_o[:heads].cpu().numpy()
+            want = x[:heads].copy()
+            o = cpu.po.oracle()
+            for r in range(heads):
+                o.orc_softmax(want[r].ctypes.data_as(ctypes.c_void_p), ctx)
+            e["parity"] = {"rows": heads, "rows_not_bit_identical":
+                           int((got.view(np.uint32) != want.view(np.uint32)).any(axis=1).sum())}
+        out["entries"].append(e)
+        log(f"attention ctx={ctx}: {kern * 1e3:.1f} us, {gbs:.0f} GB/s")
+        del t_x, t_o
+        torch.cuda.empty_cache()
+    s.close()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -487,6 +537,9 @@ def main():
     import torch
 
     cpu = Cpu(not args.no_cpu)
+    if args.workload == "attn":
+        print(json.dumps({"attention": run_attention(args, torch, cpu)}), flush=True)
+        return
     head = "c4" if args.workload in ("all", "sweep") else args.workload
     runners = {"c1": run_c1, "c5": run_c5}
     log(f"headline {head}")
@@ -529,6 +582,8 @@ def main():
                 f"{r['roofline']['kernel_us']:.1f} us, frac {r['roofline']['frac']:.3f}")
     if args.workload in ("all", "sweep") and not args.no_sweep:
         line["batch_sweep"] = run_sweep(args, torch, cpu)
+    if args.workload == "all":
+        line["attention"] = run_attention(args, torch, cpu)
     print(json.dumps(line), flush=True)
 
 
