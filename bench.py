@@ -16,6 +16,9 @@ The same line carries
                batch 1, 8, 64, 256, 1024
   attention    the reference softmax over attention scores (the tn_softmax of
                attention.c:210), 32 heads x valid context 128, 4096, 32768
+  lm_head      the bf16 LM head producing the logits (parallel_matmul_bf16,
+               vocab 128256 x hidden 2560), alone and with greedy argmax fused
+               into its epilogue, batch 1, 8, 32
 each with rows/s (wall clock of synchronous calls), the kernels' time per
 launch from HIP events on the sampler's own stream, algorithmic GB/s and the
 fraction of the 8 TB/s HBM peak, and parity with the oracle (ids; draws
@@ -76,7 +79,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "sweep", "attn"] + sorted(WORKLOAD_TEXT),
+                    choices=["all", "sweep", "attn", "lmhead"] + sorted(WORKLOAD_TEXT),
                     help="all (default): the headline, every workload and the sweep; "
                          "one name: that workload alone (profiling runs)")
     ap.add_argument("--no-cpu", action="store_true",
@@ -527,6 +530,56 @@ def run_attention(args, torch, cpu):
     return out
 
 
+def run_lm_head(args, torch, cpu):
+    """pz_lm_head_bf16 and pz_lm_head_argmax_bf16 at vocab 128256 x hidden
+    2560 (656 MB of bf16 weights: every launch streams them from HBM).
+    Bytes per launch: the weights once per batch tile, the activations, and
+    (unfused) the logits written."""
+    import numpy as np
+    import pzsample as pz
+    V, n = 128256, 2560
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0x1E0)
+    # bf16 bit patterns of small positive weights
+    w = torch.from_numpy(rng.integers(0x3c00, 0x3d00, (V, n), dtype=np.uint16).view(np.int16)).to(dev)
+    out = {"vocab": V, "hidden": n, "weight_bytes": V * n * 2, "entries": []}
+    s = pz.Sampler(32, V)
+    for B in (1, 8, 32):
+        x = torch.from_numpy(rng.standard_normal((B, n), dtype=np.float32)).to(dev)
+        logits = torch.empty((B, V), dtype=torch.float32, device=dev)
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        torch.cuda.synchronize()
+        dw, dx, dl, di = w.data_ptr(), x.data_ptr(), logits.data_ptr(), ids.data_ptr()
+        steps = 30
+        t_un = events_ms(torch, s.stream, [lambda: s.lib.pz_lm_head_bf16(
+            s.h, dw, V, n, dx, B, n, dl, V)] * steps)
+        t_fu = events_ms(torch, s.stream, [lambda: s.lib.pz_lm_head_argmax_bf16(
+            s.h, dw, V, n, dx, B, n, di)] * steps)
+        passes = -(-B // 8)  # batch tiles of 8 rows re-read the weights
+        b_un = passes * V * n * 2 + B * n * 4 + B * V * 4
+        b_fu = passes * V * n * 2 + B * n * 4 + B * 4
+        e = {"batch": B, "weight_passes": passes,
+             "unfused_us": t_un * 1e3, "unfused_gbs": b_un / (t_un * 1e-3) / 1e9,
+             "fused_us": t_fu * 1e3, "fused_gbs": b_fu / (t_fu * 1e-3) / 1e9}
+        e["unfused_frac"] = e["unfused_gbs"] / HBM_PEAK_GBS
+        e["fused_frac"] = e["fused_gbs"] / HBM_PEAK_GBS
+        if cpu.enabled:
+            s.sync()
+            lg = logits.cpu().numpy()
+            o = cpu.po.oracle()
+            want = [o.orc_argmax(np.ascontiguousarray(r).ctypes.data_as(cpu.po._P), V) for r in lg]
+            e["fused_ids_equal_argmax_of_unfused_logits"] = bool(
+                (ids.cpu().numpy() == np.array(want)).all())
+        out["entries"].append(e)
+        log(f"lm head B={B}: unfused {t_un * 1e3:.1f} us ({e['unfused_gbs']:.0f} GB/s), fused "
+            f"{t_fu * 1e3:.1f} us ({e['fused_gbs']:.0f} GB/s)")
+        del x, logits, ids
+    s.close()
+    del w
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -539,6 +592,9 @@ def main():
     cpu = Cpu(not args.no_cpu)
     if args.workload == "attn":
         print(json.dumps({"attention": run_attention(args, torch, cpu)}), flush=True)
+        return
+    if args.workload == "lmhead":
+        print(json.dumps({"lm_head": run_lm_head(args, torch, cpu)}), flush=True)
         return
     head = "c4" if args.workload in ("all", "sweep") else args.workload
     runners = {"c1": run_c1, "c5": run_c5}
@@ -584,6 +640,7 @@ def main():
         line["batch_sweep"] = run_sweep(args, torch, cpu)
     if args.workload == "all":
         line["attention"] = run_attention(args, torch, cpu)
+        line["lm_head"] = run_lm_head(args, torch, cpu)
     print(json.dumps(line), flush=True)
 
 

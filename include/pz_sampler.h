@@ -205,6 +205,26 @@ PZ_API int pz_softmax_batch(pz_sampler *s, const float *d_in, long ld_in, float 
 PZ_API int pz_attn_softmax(pz_sampler *s, const float *d_in, long ld_in, float *d_out,
                            long ld_out, int n_rows, int n, const int32_t *d_len);
 
+/* The LM head on the device: the classifier product of
+ * src/transformer/forward.c:102-168 as parallel_matmul_bf16 computes it
+ * (src/math/parallel_matmul.c:283-414), for B activation rows at once:
+ *   d_logits[b, i] = sum_j bf16(d_w[i, j]) * d_x[b, j]
+ * d_w: device [V, n] bf16 bit patterns (uint16), row-major as the model's
+ * wcls; d_x: device [B, ldx] fp32 final-norm activations; fp32
+ * accumulation.  The summation order is not the reference's SIMD order, so
+ * logits equal the exact product to fp32 rounding (|error| <= n * 2^-24 *
+ * sum_j |w_ij x_bj|), not bit for bit.  B <= max_batch; n * 4 bytes must fit
+ * in 96 KiB (n <= 24576).  Asynchronous on the sampler's stream. */
+PZ_API int pz_lm_head_bf16(pz_sampler *s, const uint16_t *d_w, int V, int n,
+                           const float *d_x, int B, long ldx, float *d_logits, long ld);
+
+/* The same product with greedy sampling (sample_argmax, argmax.c:3-13: the
+ * first maximum, a NaN logit 0 giving 0) fused into its epilogue: d_ids[b]
+ * is the argmax of exactly the logits pz_lm_head_bf16 writes, and no logits
+ * are written.  Asynchronous on the sampler's stream. */
+PZ_API int pz_lm_head_argmax_bf16(pz_sampler *s, const uint16_t *d_w, int V, int n,
+                                  const float *d_x, int B, long ldx, int32_t *d_ids);
+
 /* Device memory helpers for C hosts (hipMalloc / hipFree / hipMemcpy). */
 PZ_API int pz_device_alloc(void **ptr, size_t bytes, int device);
 PZ_API int pz_device_free(void *ptr);

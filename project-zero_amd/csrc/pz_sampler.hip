@@ -104,8 +104,12 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   if (hipMalloc((void**)&s->d_params, B * sizeof(pz_row_params_dev)) != hipSuccess ||
       hipMalloc((void**)&s->d_rows, B * sizeof(int32_t)) != hipSuccess ||
       hipMalloc((void**)&s->d_u_step, B * sizeof(float)) != hipSuccess ||
-      hipMalloc((void**)&s->d_eos, PZ_MAX_EOS * sizeof(int32_t)) != hipSuccess)
+      hipMalloc((void**)&s->d_eos, PZ_MAX_EOS * sizeof(int32_t)) != hipSuccess ||
+      hipMalloc((void**)&s->d_lmh_keys, B * sizeof(unsigned long long)) != hipSuccess ||
+      hipMalloc((void**)&s->d_lmh_nan, B) != hipSuccess)
     return bail(PZ_ENOMEM);
+  if (hipMemset(s->d_lmh_keys, 0, B * sizeof(unsigned long long)) != hipSuccess)
+    return bail(PZ_EDEVICE);
   s->res_params = new (std::nothrow) pz_row_params_dev[B];
   if (!s->res_params) return bail(PZ_ENOMEM);
   s->scratch_bytes = pz_scratch_layout(max_batch, max_vocab, PZ_FB_SLOTS, nullptr, nullptr);
@@ -132,6 +136,8 @@ extern "C" void pz_sampler_destroy(pz_sampler* s) {
   (void)hipFree(s->d_rows);
   (void)hipFree(s->d_u_step);
   (void)hipFree(s->d_eos);
+  (void)hipFree(s->d_lmh_keys);
+  (void)hipFree(s->d_lmh_nan);
   (void)hipFree(s->d_scratch);
   (void)hipFree(s->d_split);
   (void)hipFree(s->spec_dev);

@@ -47,6 +47,11 @@ struct pz_sampler {
   int32_t* d_eos = nullptr;
   int n_eos = 0;
 
+  // fused LM head + argmax: per-row argmax keys (zero between calls) and
+  // the NaN flag of logit 0 (max_batch each)
+  unsigned long long* d_lmh_keys = nullptr;
+  uint8_t* d_lmh_nan = nullptr;
+
   pz_row_params_dev* res_params = nullptr;  // host work area (max_batch)
   int staged_n = -1, staged_B = -1;         // what d_params / d_rows hold
 

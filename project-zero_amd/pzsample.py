@@ -25,7 +25,8 @@ ABI_SYMBOLS = (
     "pz_sample_batch_async", "pz_sampler_sync", "pz_spec_verify",
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
     "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
-    "pz_sample_step", "pz_sampler_set_eos", "pz_attn_softmax",
+    "pz_sample_step", "pz_sampler_set_eos", "pz_attn_softmax", "pz_lm_head_bf16",
+    "pz_lm_head_argmax_bf16",
     # include/pz_sampling_compat.h: the reference sampler's own symbols
     "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
     "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
@@ -97,6 +98,8 @@ def load():
     lib.pz_temperature_batch.argtypes = [_P, _P, _L, _I, _I, _F]
     lib.pz_softmax_batch.argtypes = [_P, _P, _L, _P, _L, _I, _I, _F]
     lib.pz_attn_softmax.argtypes = [_P, _P, _L, _P, _L, _I, _I, _P]
+    lib.pz_lm_head_bf16.argtypes = [_P, _P, _I, _I, _P, _I, _L, _P, _L]
+    lib.pz_lm_head_argmax_bf16.argtypes = [_P, _P, _I, _I, _P, _I, _L, _P]
     pull = ctypes.POINTER(ctypes.c_ulonglong)
     lib.sample_argmax.argtypes = [_P, _I]
     lib.apply_temperature.argtypes = [_P, _I, _F]
@@ -249,6 +252,18 @@ class Sampler:
         _sync_torch(d_in, d_out, d_len)
         self._check(self.lib.pz_attn_softmax(self.h, _ptr(d_in), ld_in, _ptr(d_out), ld_out,
                                              n_rows, n, _ptr(d_len)))
+
+    def lm_head(self, d_w, V, n, d_x, B, ldx, d_logits, ld):
+        """logits[b, i] = bf16 W[i, :] . x[b, :] (asynchronous)."""
+        _sync_torch(d_w, d_x, d_logits)
+        self._check(self.lib.pz_lm_head_bf16(self.h, _ptr(d_w), V, n, _ptr(d_x), B, ldx,
+                                             _ptr(d_logits), ld))
+
+    def lm_head_argmax(self, d_w, V, n, d_x, B, ldx, d_ids):
+        """Greedy ids of the LM head's logits, argmax fused (asynchronous)."""
+        _sync_torch(d_w, d_x, d_ids)
+        self._check(self.lib.pz_lm_head_argmax_bf16(self.h, _ptr(d_w), V, n, _ptr(d_x), B, ldx,
+                                                    _ptr(d_ids)))
 
     def spec_verify(self, d_target, d_draft, B, K, V, ld, has_bonus, temperature,
                     draft_ids, u_acc, u_res):
