@@ -180,6 +180,49 @@ PZ_API int pz_spec_verify(pz_sampler *s, const float *d_target, const float *d_d
                    const float *u_acc, const float *u_res,
                    int32_t *acc_len_out, int32_t *ids_out);
 
+/* The models of a speculative decode (docs/architecture/
+ * IMPLEMENTATION_PLAN.md:1675-1693), supplied by the caller, who owns their
+ * weights and KV caches.  Every call gets the sampler's stream (as void*)
+ * and returns 0 on success.
+ *   draft_step:     one token per sequence: d_tokens device [B], pos host [B]
+ *                   (the position each token takes); writes the draft
+ *                   model's logits of row b at d_logits + b * ld (device).
+ *   target_forward: n tokens per sequence: d_tokens device [B, n] at
+ *                   positions pos[b] .. pos[b] + n - 1; writes logits
+ *                   [B, n, V] (row j of sequence b at d_logits + (b*n+j)*ld).
+ *   kv_rollback:    kv_cache_rollback (plan 18.3): model 0 (draft) or 1
+ *                   (target) keeps, for each sequence b, only the cache
+ *                   positions < pos[b] (host [B]); later forwards overwrite
+ *                   the rest. */
+typedef struct {
+  void *ctx;
+  int (*draft_step)(void *ctx, const int32_t *d_tokens, const int32_t *pos, int B,
+                    float *d_logits, long ld, void *stream);
+  int (*target_forward)(void *ctx, const int32_t *d_tokens, const int32_t *pos, int B, int n,
+                        float *d_logits, long ld, void *stream);
+  int (*kv_rollback)(void *ctx, int model, const int32_t *pos, int B);
+} pz_spec_models;
+
+/* The speculative decode loop (plan 18.2) for B sequences, `rounds` rounds.
+ * tokens: host [B, max_len], sequence b holding len[b] >= 1 committed tokens
+ * (its caches cover positions < len[b] - 1: the last token is the next
+ * round's input).  Per round and sequence: K draft steps, each draft drawn
+ * on the device from q = softmax(draft / tau) with the categorical rule of
+ * generate.c:157-169 and the sequence's draft RNG state (d_draft_state,
+ * device [B], as pz_sample_step); one draft step more so the draft cache
+ * covers the last draft; one target forward over the input and the K drafts;
+ * pz_spec_verify with K + 1 uniforms drawn on the host from the sequence's
+ * verification state (verify_state, host [B]: K acceptance uniforms, then
+ * the residual one); the accepted drafts and the resampled or bonus token
+ * appended to tokens (len[b] grows by accepted + 1); both caches rolled back
+ * to the new length - 1.  accepted_out: host [rounds, B] accepted counts, or
+ * NULL.  1 <= K <= 64; every sequence must have room for rounds * (K + 1)
+ * more tokens.  Synchronous. */
+PZ_API int pz_spec_decode(pz_sampler *s, const pz_spec_models *m, int B, int K, int V,
+                          float tau, int32_t *tokens, int32_t *len, int max_len, int rounds,
+                          uint64_t *d_draft_state, uint64_t *verify_state,
+                          int32_t *accepted_out);
+
 /* The reference's temperature (src/sampling/temperature.c:8-25) over device
  * rows [B, ld], in place, on the sampler's stream (asynchronous). */
 PZ_API int pz_temperature_batch(pz_sampler *s, float *d_x, long ld, int B, int V,

@@ -233,3 +233,52 @@ def ref(avx512=None):
     r.softmax.restype = None
     _refs[path] = r
     return r
+
+
+# ---------------------------------------------------------------------------
+# The speculative decode loop (docs/architecture/IMPLEMENTATION_PLAN.md:
+# 1675-1693, plan 18.2 / 18.3; not implemented in the reference): the round
+# pz_spec_decode runs, restated over the oracle's own step and verification.
+# ---------------------------------------------------------------------------
+def spec_decode(models, B, K, V, tau, tokens, lens, rounds, draft_state, verify_state,
+                temp_mode=TEMP_MUL_RECIP):
+    """models: object with draft(tokens[B], pos[B]) -> [B, V] logits,
+    target(tokens[B, n], pos[B]) -> [B, n, V] logits and rollback(model,
+    pos[B]).  tokens [B, max_len] and lens [B] are advanced in place,
+    draft_state (uint64 [B]) and verify_state (uint64 [B]) too.  Returns the
+    accepted counts [rounds, B]."""
+    o = oracle()
+    acc_all = np.zeros((rounds, B), np.int32)
+    q = np.empty((B, K, V), np.float32)
+    prm = params(temperature=tau, top_k=0, top_p=1.0)
+    for r in range(rounds):
+        p0 = lens - 1
+        x = tokens[np.arange(B), p0].copy()
+        drafts = np.empty((B, K), np.int32)
+        cur = x
+        for j in range(K + 1):
+            lg = models.draft(cur, p0 + j)
+            if j < K:
+                q[:, j, :] = lg
+                ids, _, _ = sample_step(lg, [prm], draft_state, temp_mode=temp_mode)
+                drafts[:, j] = ids
+                cur = ids
+        tt = np.concatenate([x[:, None], drafts], axis=1)
+        p = models.target(tt, p0)
+        u_acc = np.empty((B, K), np.float32)
+        u_res = np.empty(B, np.float32)
+        for b in range(B):
+            s = ctypes.c_ulonglong(int(verify_state[b]))
+            for j in range(K):
+                u_acc[b, j] = o.orc_rng_float(ctypes.byref(s))
+            u_res[b] = o.orc_rng_float(ctypes.byref(s))
+            verify_state[b] = s.value
+        acc, out, _ = spec_verify(p, q, K, True, tau, drafts, u_acc, u_res, temp_mode=temp_mode)
+        for b in range(B):
+            a = int(acc[b])
+            tokens[b, lens[b]:lens[b] + a + 1] = out[b, :a + 1]
+            lens[b] += a + 1
+        acc_all[r] = acc
+        models.rollback(0, p0 + acc + 1)
+        models.rollback(1, p0 + acc + 1)
+    return acc_all

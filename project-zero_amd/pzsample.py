@@ -26,7 +26,7 @@ ABI_SYMBOLS = (
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
     "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
     "pz_sample_step", "pz_sampler_set_eos", "pz_attn_softmax", "pz_lm_head_bf16",
-    "pz_lm_head_argmax_bf16",
+    "pz_lm_head_argmax_bf16", "pz_spec_decode",
     # include/pz_sampling_compat.h: the reference sampler's own symbols
     "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
     "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
@@ -100,6 +100,7 @@ def load():
     lib.pz_attn_softmax.argtypes = [_P, _P, _L, _P, _L, _I, _I, _P]
     lib.pz_lm_head_bf16.argtypes = [_P, _P, _I, _I, _P, _I, _L, _P, _L]
     lib.pz_lm_head_argmax_bf16.argtypes = [_P, _P, _I, _I, _P, _I, _L, _P]
+    lib.pz_spec_decode.argtypes = [_P, _P, _I, _I, _I, _F, _P, _P, _I, _I, _P, _P, _P]
     pull = ctypes.POINTER(ctypes.c_ulonglong)
     lib.sample_argmax.argtypes = [_P, _I]
     lib.apply_temperature.argtypes = [_P, _I, _F]
