@@ -295,7 +295,10 @@ def run_batched(args, torch, cpu, name):
 
 def run_c1(args, torch, cpu):
     """One row per call, the reference's loop: 500 fresh rows, each call
-    synchronous (the id returns to the host before the next)."""
+    synchronous (the id returns to the host before the next).  The calls go
+    through a caller with its arguments marshalled once (pzsample
+    Sampler.caller), so the time is the library's, as a C loop would see
+    it."""
     import numpy as np
     import pzsample as pz
     import workloads as wl
@@ -314,9 +317,10 @@ def run_c1(args, torch, cpu):
     dx, dh, du, di = t_x.data_ptr(), t_h.data_ptr(), t_u.data_ptr(), t_ids.data_ptr()
     ids = np.empty(R, np.int32)
 
+    fast = s.caller(1, V, V, params, H=H)
+
     def call(r):
-        return s.sample(dx + 4 * V * r, 1, V, V, params, u=u[r:r + 1], d_hist=dh + 4 * H * r,
-                        H=H)[0][0]
+        return fast(dx + 4 * V * r, u[r:r + 1], dh + 4 * H * r)[0]
 
     for r in range(min(args.warmup * 10, R)):
         call(r)

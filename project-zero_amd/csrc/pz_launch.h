@@ -41,10 +41,13 @@ struct pz_launch {
   bool pen_any;         // any row has an active penalty
   bool temp_div;        // temperature as x / T (scalar build) rather than x * (1/T)
   const float* u;       // device [B] uniforms
+  const float* h_u = nullptr;  // host copy of the same uniforms, when the caller has one
+  int B = 0;            // rows of the call
   int32_t* ids;         // device [B] sampled ids
   float* p_out;         // device [B] p(chosen) or nullptr
   pz_scratch sc;         // device scratch owned by the sampler
   PzSplitWs ws;          // workspace of the row-split passes
+  int kmax = 0;         // largest top_k among the launch's top-k rows (0: unknown)
   int max_lds;          // max dynamic LDS per workgroup on this device
   hipStream_t stream;
 };

@@ -94,9 +94,11 @@ int device_setup(int device, const DeviceState** out) {
 }
 
 // One staging launch: up to kStageWords words copied to dst[first..], and
-// with zero_counters the fallback's queue counters cleared (they must read
-// zero when its kernel starts; it re-zeroes them when it ends, but a call
-// interrupted before then would leave them set).
+// with zero_counters the fallback's queue counters and the rows' arrival
+// counters cleared (they must read zero when a launch starts; the kernels
+// re-zero them when they end, but a call interrupted before then would leave
+// them set, and the array's first use must not depend on its initial
+// contents).
 constexpr int kStageWords = 480;
 struct StageChunk {
   uint32_t first;
@@ -106,14 +108,18 @@ struct StageChunk {
   uint32_t w[kStageWords];
 };
 
-__global__ void k_noalloc_stage(StageChunk c, uint32_t* dst, int32_t* counters) {
+__global__ void k_noalloc_stage(StageChunk c, uint32_t* dst, int32_t* counters,
+                                uint32_t* arrive) {
   for (uint32_t i = threadIdx.x; i < c.n; i += blockDim.x) dst[c.first + i] = c.w[i];
-  if (c.zero_counters && threadIdx.x < 16) counters[threadIdx.x] = 0;
+  if (c.zero_counters) {
+    if (threadIdx.x < 16) counters[threadIdx.x] = 0;
+    for (uint32_t i = threadIdx.x; i < PZ_NOALLOC_MAX_BATCH; i += blockDim.x) arrive[i] = 0u;
+  }
 }
 
 // Copies `words` words from host src to device dst through staging launches.
-int stage(const uint32_t* src, uint32_t words, uint32_t* dst, int32_t* counters, bool zero,
-          hipStream_t st) {
+int stage(const uint32_t* src, uint32_t words, uint32_t* dst, int32_t* counters,
+          uint32_t* arrive, bool zero, hipStream_t st) {
   StageChunk c;
   c.pad_ = 0;
   uint32_t first = 0;
@@ -123,7 +129,7 @@ int stage(const uint32_t* src, uint32_t words, uint32_t* dst, int32_t* counters,
     c.n = n;
     c.zero_counters = zero ? 1u : 0u;
     memcpy(c.w, src + first, n * sizeof(uint32_t));
-    hipLaunchKernelGGL(k_noalloc_stage, dim3(1), dim3(256), 0, st, c, dst, counters);
+    hipLaunchKernelGGL(k_noalloc_stage, dim3(1), dim3(256), 0, st, c, dst, counters, arrive);
     if (hipGetLastError() != hipSuccess) return PZ_EDEVICE;
     zero = false;
     first += n;
@@ -175,11 +181,13 @@ extern "C" int pz_sample_batch_noalloc(int device, void* stream, int temp_mode,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint32_t pwords = (uint32_t)(n_params * sizeof(pz_row_params_dev) / 4);
   int rc = stage(reinterpret_cast<const uint32_t*>(img.res), pwords,
-                 reinterpret_cast<uint32_t*>(lay.params), lay.sc.counters, true, st);
+                 reinterpret_cast<uint32_t*>(lay.params), lay.sc.counters, lay.ws.arrive, true,
+                 st);
   if (rc == PZ_OK && modes_present > 1) {
     pz_fill_rows(img.res, B, n_params, offset, img.rows);
     rc = stage(reinterpret_cast<const uint32_t*>(img.rows), (uint32_t)B,
-               reinterpret_cast<uint32_t*>(lay.rows), lay.sc.counters, false, st);
+               reinterpret_cast<uint32_t*>(lay.rows), lay.sc.counters, lay.ws.arrive, false,
+               st);
   }
   if (rc != PZ_OK) return rc;
 
@@ -199,6 +207,7 @@ extern "C" int pz_sample_batch_noalloc(int device, void* stream, int temp_mode,
   L.p_out = d_p_out;
   L.sc = lay.sc;
   L.ws = lay.ws;
+  L.kmax = pz_max_top_k(img.res, B, n_params);
   L.max_lds = ds->max_lds;
   L.stream = st;
   int m = -1;

@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <chrono>
 #include <new>
 
 #include "../../include/pz_sampler.h"
@@ -22,6 +23,8 @@ namespace {
 
 constexpr int kTopKMax = 1024;  // top_k.c:6
 constexpr int kMaxHist = 2048;
+// An id no kernel writes (ids are -1 .. V-1): marks rows still pending.
+constexpr int32_t kIdPending = INT32_MIN;
 
 int next_pow2(int v) {
   int p = 1;
@@ -228,6 +231,13 @@ void pz_group_rows(const pz_row_params_dev* res, int B, int n_params, int count[
   *modes_present = present;
 }
 
+int pz_max_top_k(const pz_row_params_dev* res, int B, int n_params) {
+  int kmax = 0;
+  for (int b = 0; b < (n_params == 1 ? 1 : B); b++)
+    if (res[b].mode == PZ_MODE_TOPK && res[b].top_k > kmax) kmax = res[b].top_k;
+  return kmax;
+}
+
 void pz_fill_rows(const pz_row_params_dev* res, int B, int n_params,
                   const int offset[PZ_MODE_COUNT], int32_t* rows) {
   int fill[PZ_MODE_COUNT];
@@ -331,10 +341,13 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
   L.temp_div = s->temp_mode == PZ_TEMP_DIV;
   L.hcap = pz_hash_capacity(counts_any, H);
   L.u = d_u;
+  L.h_u = hooks ? nullptr : s->call_u;
+  L.B = B;
   L.ids = d_ids;
   L.p_out = d_p;
   L.sc = s->sc;
   L.ws = s->ws;
+  L.kmax = pz_max_top_k(res, B, n_params);
   L.max_lds = s->max_lds;
   L.stream = s->stream;
 
@@ -361,6 +374,26 @@ extern "C" int pz_sample_batch_async(pz_sampler* s, const float* d_logits, int B
                             d_p_out, nullptr);
 }
 
+// Waits until the kernels have written all B ids into the coherent pinned
+// buffer (true), or gives up after two seconds (false).  Every sampling
+// kernel writes each row's id exactly once, after its last read of the row's
+// inputs (the uniform included), so once every id is back the call's host
+// buffers are free again, and later launches queue behind this call's in
+// stream order.  Watching the ids return is several microseconds quicker
+// than a stream synchronisation.
+static bool wait_ids(pz_sampler* s, int B) {
+  volatile const int32_t* h = s->h_ids;
+  const auto t0 = std::chrono::steady_clock::now();
+  for (int b = 0; b < B; b++) {
+    unsigned spins = 0;
+    while (h[b] == kIdPending)
+      if ((++spins & 0xffffu) == 0 &&
+          std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2))
+        return false;
+  }
+  return true;
+}
+
 extern "C" int pz_sample_batch(pz_sampler* s, const float* d_logits, int B, int V, long ld,
                                const pz_row_params* params, int n_params,
                                const int32_t* d_hist, int H, const float* u,
@@ -370,20 +403,29 @@ extern "C" int pz_sample_batch(pz_sampler* s, const float* d_logits, int B, int 
   if (B > s->max_batch) return fail(s, PZ_ERANGE, "B=%d > max_batch=%d", B, s->max_batch);
   if (B <= 0) return B == 0 ? PZ_OK : fail(s, PZ_EINVAL, "B<0");
   PZ_HIP(s, hipSetDevice(s->device));
-  // Every synchronous call ends with the stream drained, and asynchronous
-  // calls never touch h_u / h_ids / h_p: the buffers are free here.
+  // A synchronous call returns once its kernels have read h_u and written
+  // h_ids (see wait_ids), and asynchronous calls never touch h_u / h_ids /
+  // h_p: the buffers are free here.
   const float* d_u = nullptr;
   if (u) {
     memcpy(s->h_u, u, (size_t)B * sizeof(float));
     d_u = s->z_u;
   }
+  for (int b = 0; b < B; b++) s->h_ids[b] = kIdPending;
+  s->call_u = u ? s->h_u : nullptr;
   int rc = pz_dispatch_params(s, d_logits, B, V, ld, params, n_params, d_hist, H, d_u,
                               s->z_ids, p_out ? s->z_p : nullptr, nullptr);
+  s->call_u = nullptr;
   if (rc != PZ_OK) {
     (void)hipStreamSynchronize(s->stream);  // kernels already queued may use the buffers
     return rc;
   }
-  PZ_HIP(s, hipStreamSynchronize(s->stream));
+  // p(chosen) is written after the id: with it requested, wait for the stream
+  if (p_out || !wait_ids(s, B)) {
+    PZ_HIP(s, hipStreamSynchronize(s->stream));
+    for (int b = 0; b < B; b++)
+      if (s->h_ids[b] == kIdPending) return fail(s, PZ_EDEVICE, "row %d returned no id", b);
+  }
   memcpy(ids_out, s->h_ids, (size_t)B * sizeof(int32_t));
   if (p_out) memcpy(p_out, s->h_p, (size_t)B * sizeof(float));
   return PZ_OK;

@@ -52,6 +52,8 @@ struct pz_sampler {
   unsigned long long* d_lmh_keys = nullptr;
   uint8_t* d_lmh_nan = nullptr;
 
+  const float* call_u = nullptr;  // the synchronous call's host uniforms, during the call
+
   pz_row_params_dev* res_params = nullptr;  // host work area (max_batch)
   int staged_n = -1, staged_B = -1;         // what d_params / d_rows hold
 
@@ -91,6 +93,8 @@ int pz_hash_capacity(bool counts_any, int H);
 // Rows per mode and each mode's offset in a mode-grouped row list.
 void pz_group_rows(const pz_row_params_dev* res, int B, int n_params, int count[PZ_MODE_COUNT],
                    int offset[PZ_MODE_COUNT], int* modes_present);
+// Largest top_k among the top-k rows (0 when there are none).
+int pz_max_top_k(const pz_row_params_dev* res, int B, int n_params);
 // The mode-grouped row list (B entries).
 void pz_fill_rows(const pz_row_params_dev* res, int B, int n_params,
                   const int offset[PZ_MODE_COUNT], int32_t* rows);

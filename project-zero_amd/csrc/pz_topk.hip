@@ -32,12 +32,21 @@
 //   5. Wave 0 evaluates the k-slot softmax (expf from an LDS copy of its
 //      table), cut-off and draw with the exact sequential fp32 sums of the
 //      reference (lane-ordered scans).
+//
+// Small batches (a few rows: one sequence per call, as the reference's loop
+// runs) split each row over workgroups instead (k_topk_split): workgroup s
+// takes ids [4096 s, 4096 s + 4096), keys every valid element of that range
+// into LDS (penalty tables built for the range only) and selects the range's
+// own k largest (key, id); the row's top k are among the union of these.
+// The ranges' candidates meet in the row's workspace and the workgroup that
+// arrives last merges them and runs steps 4-5.
 #include "pz_device.h"
 #include "pz_exact.h"
 #include "pz_launch.h"
 #include "pz_rowpass.h"
 #include "pz_seq.h"
 #include "pz_sort.h"
+#include "pz_split.h"
 
 namespace {
 
@@ -61,6 +70,8 @@ struct TopkShared {
   int done;
   int count;  // candidates appended (may exceed TOPK_CAP)
   int ntop;   // survivors
+  int nbin;   // entries of the k-th bin (tk_select_bin)
+  uint32_t bin;
 };
 
 typedef __attribute__((address_space(3))) uint32_t tk_lds_u32;
@@ -177,9 +188,11 @@ __device__ __forceinline__ bool tk_find_bin(tk_lds_u32* hist, uint32_t need, uin
                                             uint32_t& above, uint32_t& cnt) {
   const int lane = threadIdx.x & 63;
   tk_lds_u32* h = hist + 32 * lane;  // lane l owns bins [32l, 32l+32)
+  // each lane walks its bins from a rotated start, so the 64 lanes' reads
+  // of one step fall in different LDS banks
   uint32_t own = 0;
 #pragma unroll
-  for (int j = 0; j < 32; j++) own += h[j];
+  for (int j = 0; j < 32; j++) own += h[(j + lane) & 31];
   const uint32_t incl = pz_wave_scan_u32(own);
   const uint32_t total = pz_readlane_u32(incl, 63);
   bool found = false;
@@ -199,7 +212,7 @@ __device__ __forceinline__ bool tk_find_bin(tk_lds_u32* hist, uint32_t need, uin
     found = true;
   }
 #pragma unroll
-  for (int j = 0; j < 32; j++) h[j] = 0u;
+  for (int j = 0; j < 32; j++) h[(j + lane) & 31] = 0u;
   return found;
 }
 
@@ -239,6 +252,84 @@ __device__ uint64_t tk_select(TopkShared& S, const pz_lds_u64* buf, int n, int k
     w = sh;
     if (S.done) return base;
   }
+}
+
+// Number of the n entries of a[] greater than c: eight independent LDS
+// reads per step (a sequential loop would wait for each read in turn).
+__device__ __forceinline__ int tk_rank(const pz_lds_u64* a, int n, uint64_t c) {
+  int r0 = 0, r1 = 0, r2 = 0, r3 = 0, j = 0;
+  for (; j + 8 <= n; j += 8) {
+    const uint64_t x0 = a[j], x1 = a[j + 1], x2 = a[j + 2], x3 = a[j + 3];
+    const uint64_t x4 = a[j + 4], x5 = a[j + 5], x6 = a[j + 6], x7 = a[j + 7];
+    r0 += (x0 > c) + (x4 > c);
+    r1 += (x1 > c) + (x5 > c);
+    r2 += (x2 > c) + (x6 > c);
+    r3 += (x3 > c) + (x7 > c);
+  }
+  for (; j < n; j++) r0 += a[j] > c ? 1 : 0;
+  return (r0 + r1) + (r2 + r3);
+}
+
+// The same contract as tk_select (exactly k entries of buf[0..n) are >=
+// the result; n > k >= 1, entries distinct; base == ~0 when the entries'
+// range is not known) in one histogram pass: the bin
+// of the top 11 key bits holding the k-th largest is found, and the entries
+// of that bin are ranked against each other (one per thread, every
+// comparison independent).  A bin of more than BLOCK entries (long runs of
+// equal values) takes the radix select.  S.hist is zero on entry and exit.
+template <int BLOCK>
+__device__ uint64_t tk_select_bin(TopkShared& S, const pz_lds_u64* buf, int n, int k,
+                                  uint64_t base, uint64_t maxc) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < n; i += BLOCK) atomicAdd(&S.hist[(uint32_t)(buf[i] >> 53)], 1u);
+  __syncthreads();
+  if (tid < PZ_WAVE) {
+    uint32_t bin = 0, above = 0, cnt = 0;
+    tk_find_bin((tk_lds_u32*)S.hist, (uint32_t)k, bin, above, cnt);  // zeroes S.hist
+    if (tid == 0) {
+      S.bin = bin;
+      S.need = k - (int)above;
+      S.nbin = (int)cnt;
+      S.ntop = 0;
+    }
+  }
+  __syncthreads();
+  const uint32_t bin = S.bin;
+  const int need = S.need, cnt = S.nbin;
+  if (cnt > BLOCK || cnt > HBINS / 2) {
+    if (base == ~0ull) {  // range not known: the entries' smallest and largest
+      if (tid == 0) {
+        S.base = ~0ull;
+        S.maxc = 0ull;
+      }
+      __syncthreads();
+      for (int i = tid; i < n; i += BLOCK) {
+        atomicMin(&S.base, buf[i]);
+        atomicMax(&S.maxc, buf[i]);
+      }
+      __syncthreads();
+      base = S.base;
+      maxc = S.maxc;
+    }
+    return tk_select<BLOCK>(S, buf, n, k, base, maxc);
+  }
+  // the bin's entries, listed in the (zero) histogram's words
+  pz_lds_u64* list = (pz_lds_u64*)S.hist;
+  for (int i = tid; i < n; i += BLOCK) {
+    const uint64_t c = buf[i];
+    if ((uint32_t)(c >> 53) == bin) list[atomicAdd(&S.ntop, 1)] = c;
+  }
+  __syncthreads();
+  if (tid < cnt) {
+    const uint64_t c = list[tid];
+    const int r = tk_rank(list, cnt, c);
+    if (r == need - 1) S.base = c;
+  }
+  __syncthreads();
+  const uint64_t thr = S.base;
+  for (int j = tid; j < 2 * cnt; j += BLOCK) S.hist[j] = 0u;
+  __syncthreads();
+  return thr;
 }
 
 // Element j (0..15) of a group's registers: a[j >> 2][j & 3] by selects
@@ -352,6 +443,11 @@ __device__ __forceinline__ void tk_pass(TopkShared& S, pz_lds_u64* buf, const Pz
   tk_drain(b);
 }
 
+__device__ __forceinline__ void tk_draw(TopkShared& S, const pz_lds_u64* res, int m, int k,
+                                        const pz_row_params_dev& prm, float uu, int row,
+                                        int32_t* __restrict__ ids_out,
+                                        float* __restrict__ p_out);
+
 // The k survivors of buf[0..n) (distinct candidates in [base, maxc]) in
 // order, then the k-slot softmax, top-p cut-off and draw of row `row` (wave
 // 0; uu is the row's uniform in thread 0).  Every thread calls it.
@@ -362,8 +458,7 @@ __device__ __forceinline__ void tk_finish(TopkShared& S, pz_lds_u64* buf, int n,
                                           int32_t* __restrict__ ids_out,
                                           float* __restrict__ p_out) {
   const int tid = threadIdx.x;
-  const int lane = tid & (PZ_WAVE - 1);
-  const uint64_t thr = n > k ? tk_select<BLOCK>(S, buf, n, k, base, maxc) : 0ull;
+  const uint64_t thr = n > k ? tk_select_bin<BLOCK>(S, buf, n, k, base, maxc) : 0ull;
   if (tid == 0) S.ntop = 0;
   __syncthreads();
   for (int i = tid; i < n; i += BLOCK) {
@@ -378,9 +473,7 @@ __device__ __forceinline__ void tk_finish(TopkShared& S, pz_lds_u64* buf, int n,
     const pz_lds_u64* top = (const pz_lds_u64*)S.top;
     if (tid < m) {
       const uint64_t c = top[tid];
-      int rank = 0;
-      for (int j = 0; j < m; j++) rank += top[j] > c ? 1 : 0;
-      buf[rank] = c;
+      buf[tk_rank(top, m, c)] = c;
     }
     res = buf;
   } else {
@@ -393,8 +486,18 @@ __device__ __forceinline__ void tk_finish(TopkShared& S, pz_lds_u64* buf, int n,
     res = top;
   }
   __syncthreads();
+  tk_draw(S, res, m, k, prm, uu, row, ids_out, p_out);
+}
 
-  // ---- 5. softmax over k slots, cut-off and draw (wave 0).  pv holds the
+// ---- 5. softmax over k slots, cut-off and draw (wave 0) of the m <= k
+// survivors res[0..m) in order (unfilled slots are (-1e30, -1)).
+__device__ __forceinline__ void tk_draw(TopkShared& S, const pz_lds_u64* res, int m, int k,
+                                        const pz_row_params_dev& prm, float uu, int row,
+                                        int32_t* __restrict__ ids_out,
+                                        float* __restrict__ p_out) {
+  const int tid = threadIdx.x;
+  const int lane = tid & (PZ_WAVE - 1);
+  // pv holds the
   // probabilities, cv their sequential cumulative sums (the cut-off scan of
   // top_p.c:80-88 and the draw's cdf add the same terms in the same order).
   // Lane l owns slots l, l+64, ... of pv; cv is read across lanes only after
@@ -550,7 +653,7 @@ __global__ __launch_bounds__(BLOCK) void k_topk(
     if (S.count <= TOPK_CAP) break;
     // the buffer holds TOPK_CAP >= k candidates of the row: its k-th largest
     // (key, id) bounds the row's k-th largest from below
-    const uint64_t thr = tk_select<BLOCK>(S, buf, TOPK_CAP, k, bd, S.maxc);
+    const uint64_t thr = tk_select_bin<BLOCK>(S, buf, TOPK_CAP, k, bd, S.maxc);
     if (tid < PZ_WAVE) tk_publish<DIV>(S, thr, T);
     if (tid == 0) {
       S.count = 0;
@@ -566,7 +669,188 @@ __global__ __launch_bounds__(BLOCK) void k_topk(
 
 
 
+// Uniforms of a small batch passed by value.
+struct PzUArg {
+  float v[8];
+  int n;  // rows 0..n-1 take v[row]
+};
+
+// One row split over gridDim.x workgroups of 4096 ids (one tile) each.
+// cand: the row's candidate area (`room` entries per workgroup, room >= k),
+// counts: entries each workgroup wrote ([rows][gridDim.x]); arrive: the
+// rows' arrival counters (zero between launches).
+template <int BLOCK, bool VEC, bool DIV>
+__global__ __launch_bounds__(BLOCK) void k_topk_split(
+    const float* __restrict__ logits, long ld, int V, const int32_t* __restrict__ rows,
+    const pz_row_params_dev* __restrict__ params, int n_params,
+    const int32_t* __restrict__ hist, int H, int hcap, size_t pen_bytes,
+    const float* __restrict__ u, int32_t* __restrict__ ids_out, float* __restrict__ p_out,
+    uint64_t* __restrict__ cand, int capg, int room, uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ arrive, PzUArg ua) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ TopkShared S;
+  __shared__ int last_sh;
+  const int sl = blockIdx.x, S_row = gridDim.x;
+  const int row = pz_row_of(rows, blockIdx.y);
+  const int tid = threadIdx.x;
+  const int lane = tid & (PZ_WAVE - 1);
+  const float* x = logits + (long)row * ld;
+  const int32_t* hrow = hist ? hist + (long)row * H : nullptr;
+  const int lo = sl * PZ_TILE;
+  const int hi = lo + PZ_TILE < V ? lo + PZ_TILE : V;
+  const int e0 = lo + 4 * tid;
+  float a[4];
+  const int n = pz_load4<VEC, false>(x, hi, e0, a);
+  const uint64_t tab = tid < 32 ? pz_exp2_tab[tid] : 0ull;
+  // the uniform: from the launch's arguments for the first rows of a small
+  // batch (no memory read on the merge's path), else from u
+  float uu = 0.0f;
+  if (tid == 0) uu = row < ua.n ? ua.v[row] : u[row];
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  pz_lds_u64* buf = (pz_lds_u64*)(lds + pen_bytes);
+  PzPenalty P;
+  pz_penalty_setup_range<BLOCK>(P, lds, lo, hi, hcap, hrow != nullptr && H > 0, prm);
+  for (int j = tid; j < HBINS; j += BLOCK) S.hist[j] = 0u;
+  if (tid == 0) {
+    S.count = 0;
+    S.maxc = 0ull;
+    S.base = ~0ull;
+  }
+  if (tid < 32) S.etab[tid] = tab;
+  __syncthreads();
+  if (P.active) {
+    for (int j = tid; j < H; j += BLOCK) pz_penalty_insert(P, lds, V, hrow[j], nullptr, nullptr);
+    __syncthreads();
+  }
+  const PzTemp T = PzTemp::of(prm);
+  const int k = prm.top_k;
+  // every valid element of the range (y > -1e30, NaN never), keyed
+  uint64_t cc[4];
+  uint32_t want = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    float y = a[c];
+    if (c < n && P.active && pz_pen_member(P, e0 + c)) y = pz_penalize(P, y, e0 + c);
+    y = tk_temper<DIV>(y, T);
+    cc[c] = comp_of(tk_key(y + 0.0f), e0 + c);
+    if (c < n && y > -1e30f) want |= 1u << c;
+  }
+  {
+    const uint32_t cnt = (uint32_t)__builtin_popcount(want);
+    const uint32_t incl = pz_wave_scan_u32(cnt);
+    const uint32_t total = pz_readlane_u32(incl, 63);
+    int base = 0;
+    if (lane == 0 && total) base = atomicAdd(&S.count, (int)total);
+    base = __builtin_amdgcn_readfirstlane(base);
+    int slot = base + (int)(incl - cnt);
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if ((want >> c) & 1u) buf[slot++] = cc[c];
+  }
+  __syncthreads();
+  // a superset of this range's k largest: every key in the bins (top 11 key
+  // bits) from the one holding the k-th largest up, when that fits the
+  // range's room, else exactly the k largest
+  const int nc = S.count;
+  uint64_t thr = 0ull;
+  if (nc > k) {
+    for (int i = tid; i < nc; i += BLOCK) atomicAdd(&S.hist[(uint32_t)(buf[i] >> 53)], 1u);
+    __syncthreads();
+    if (tid < PZ_WAVE) {
+      uint32_t bin = 0, above = 0, cnt = 0;
+      tk_find_bin((tk_lds_u32*)S.hist, (uint32_t)k, bin, above, cnt);  // zeroes S.hist
+      if (tid == 0) {
+        S.bin = bin;
+        S.nbin = (int)(above + cnt);
+      }
+    }
+    __syncthreads();
+    thr = S.nbin <= room ? (uint64_t)S.bin << 53
+                         : tk_select_bin<BLOCK>(S, buf, nc, k, ~0ull, 0ull);
+  }
+  uint64_t* out = cand + (size_t)row * capg + (size_t)sl * room;
+  if (tid == 0) S.ntop = 0;
+  __syncthreads();
+  for (int i = tid; i < nc; i += BLOCK) {
+    const uint64_t c = buf[i];
+    if (c >= thr) out[atomicAdd(&S.ntop, 1)] = c;
+  }
+  __syncthreads();
+  if (tid == 0) counts[(size_t)row * S_row + sl] = (uint32_t)S.ntop;
+  // the last workgroup of the row merges the ranges' candidates
+  if (!pz_sp_arrive(arrive, row, S_row, &last_sh)) return;
+  if (tid == 0) {
+    S.count = 0;
+    S.maxc = 0ull;
+    S.base = ~0ull;
+  }
+  __syncthreads();
+  const uint64_t* all = cand + (size_t)row * capg;
+  // the ranges' counts and their prefix (at most 64 ranges: one wave)
+  __shared__ int off[65];
+  if (tid < PZ_WAVE) {
+    const int c = tid < S_row ? (int)counts[(size_t)row * S_row + tid] : 0;
+    off[tid + 1] = (int)pz_wave_scan_u32((uint32_t)c);
+    if (tid == 0) off[0] = 0;
+  }
+  __syncthreads();
+  const int total = off[S_row];  // at most TOPK_CAP: S * room entries
+  // up to four entries per thread, their loads issued together
+  uint64_t got[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int f = tid + q * BLOCK;
+    got[q] = 0ull;
+    if (f < total) {
+      int si = 0;
+      while (off[si + 1] <= f) si++;
+      got[q] = all[(size_t)si * room + (f - off[si])];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int f = tid + q * BLOCK;
+    if (f < total) buf[f] = got[q];
+  }
+  __syncthreads();
+  pz_sp_rearm(arrive, row);
+  tk_finish<BLOCK>(S, buf, total, k, ~0ull, 0ull, prm, uu, row, ids_out, p_out);
+}
+
 }  // namespace
+
+// Rows split over workgroups when the launch would otherwise occupy few CUs
+// and the ranges' candidates fit one merge buffer.
+constexpr int TOPK_SPLIT_MAX_WG = 256;
+
+template <bool VEC, bool DIV>
+static int launch_topk_split_t(const pz_launch& L, int n_rows, const int32_t* d_rows, int S,
+                               int kmax) {
+  const size_t pen =
+      L.pen_any ? (pz_penalty_lds_bytes(PZ_TILE, L.hcap) + 15) & ~(size_t)15 : 0;
+  const size_t lds = pen + (size_t)TOPK_CAP * 8;
+  if ((int)(lds + sizeof(TopkShared) + 16) > L.max_lds) return -2;
+  auto kern = k_topk_split<TOPK_BLOCK, VEC, DIV>;
+  if (lds > 65536 &&
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) != hipSuccess)
+    return -1;
+  // each range's room in the candidate area: the merge buffer (and the
+  // row's area) split evenly, at least kmax (the caller checked S * kmax)
+  int room = TOPK_CAP / S;
+  if (room > L.ws.capg / S) room = L.ws.capg / S;
+  if (room < kmax) return -2;
+  PzUArg ua;
+  ua.n = 0;
+  if (L.h_u && L.B <= 8) {
+    for (int b = 0; b < L.B; b++) ua.v[b] = L.h_u[b];
+    ua.n = L.B;
+  }
+  hipLaunchKernelGGL(kern, dim3(S, n_rows), dim3(TOPK_BLOCK), lds, L.stream, L.logits, L.ld,
+                     L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pen, L.u, L.ids,
+                     L.p_out, L.ws.keys, L.ws.capg, room, L.ws.slice_f, L.ws.arrive, ua);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 template <bool VEC, bool DIV>
 static int launch_topk_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
@@ -587,6 +871,17 @@ static int launch_topk_t(const pz_launch& L, int n_rows, const int32_t* d_rows) 
 int pz_launch_topk(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (n_rows <= 0) return 0;
   const bool vec = (L.ld % 4 == 0) && (((uintptr_t)L.logits & 15) == 0);
+  // the largest k among the rows decides whether the split's merge fits
+  // (k is resolved per row on the host: the host passes it as kmax)
+  const int S = pz_tiles(L.V);
+  if (S >= 2 && (long)S * n_rows <= TOPK_SPLIT_MAX_WG && L.kmax > 0 &&
+      (long)S * L.kmax <= TOPK_CAP && (long)S * L.kmax <= L.ws.capg && L.ws.keys) {
+    if (L.temp_div)
+      return vec ? launch_topk_split_t<true, true>(L, n_rows, d_rows, S, L.kmax)
+                 : launch_topk_split_t<false, true>(L, n_rows, d_rows, S, L.kmax);
+    return vec ? launch_topk_split_t<true, false>(L, n_rows, d_rows, S, L.kmax)
+               : launch_topk_split_t<false, false>(L, n_rows, d_rows, S, L.kmax);
+  }
   if (L.temp_div)
     return vec ? launch_topk_t<true, true>(L, n_rows, d_rows)
                : launch_topk_t<false, true>(L, n_rows, d_rows);

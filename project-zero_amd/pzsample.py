@@ -211,6 +211,30 @@ class Sampler:
         self._check(rc)
         return ids, p
 
+    def caller(self, B, V, ld, params, H=0):
+        """A function f(d_logits, u, d_hist) -> ids for repeated synchronous
+        calls of one shape: the arguments are marshalled once, so a call
+        costs the library call itself (as a C caller pays), not the
+        wrapper's per-call conversions.  d_logits / d_hist: device addresses
+        (int); u: float32 array of B uniforms or None.  The returned ids
+        array is reused by the next call."""
+        parr, n = _params_array(params, B)
+        ids = np.empty(B, np.int32)
+        ub = np.empty(B, np.float32)
+        pids, pu = _np_ptr(ids), _np_ptr(ub)
+        f, h = self.lib.pz_sample_batch, self.h
+        check = self._check
+
+        def call(d_logits, u=None, d_hist=None):
+            if u is not None:
+                ub[:] = u
+            rc = f(h, d_logits, B, V, ld, parr, n, d_hist, H, pu if u is not None else None,
+                   pids, None)
+            if rc:
+                check(rc)
+            return ids
+        return call
+
     def sample_async(self, d_logits, B, V, ld, params, d_u, d_ids, d_p=None,
                      d_hist=None, H=0):
         parr, n = _params_array(params, B)

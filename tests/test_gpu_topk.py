@@ -120,3 +120,26 @@ def test_uniform_one_and_zero(torch_cuda):
         check(torch_cuda, x, [pz.row_params(temperature=1.0, top_k=30, top_p=0.9)], u,
               label=f"u={uval}")
         check(torch_cuda, x, [pz.row_params(temperature=1.0, top_k=30)], u, label=f"u={uval} k")
+
+
+@pytest.mark.parametrize("B,V", [(1, 49152), (3, 128256), (8, 4097), (1, 4096), (2, 151936)])
+@pytest.mark.parametrize("k,top_p", [(1, 1.0), (40, 0.95), (100, 1.0), (300, 0.8)])
+def test_small_batch_rows_split_over_workgroups(torch_cuda, B, V, k, top_p):
+    """Small batches take the split kernel (each 4096-id range selects its own
+    top k, the last workgroup of the row merges) whenever the ranges' k
+    candidates fit its merge buffer; penalties, ties across range boundaries
+    and rows with fewer than k valid values included."""
+    rng = np.random.default_rng(V + k)
+    x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
+    x[0, 4090:4102] = 9.0                      # a tie straddling a range boundary
+    if B > 1:
+        x[1, :] = -np.inf                      # no valid value: every slot stays -1
+        x[1, ::997] = 1.0                      # ... but a few valid ones, fewer than k
+    if B > 2:
+        x[2, 5] = np.nan
+    H = 64
+    hist = rng.integers(0, V, (B, H)).astype(np.int32)
+    hist[0, :4] = [4090, 4095, 4096, 4101]     # penalised members of the tie
+    params = [pz.row_params(temperature=0.8, top_k=k, top_p=top_p, rep_penalty=1.3)]
+    check(torch_cuda, x, params, pz.synth_draws(B, V * 7 + k), hist=hist,
+          label=f"split B={B} V={V} k={k}")
