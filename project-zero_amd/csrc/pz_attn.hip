@@ -11,8 +11,9 @@
 // exponentials, the exact sum and the write need no LDS beyond the exp
 // table.  The sum is the exact sequential one (pz_exact.h): the first
 // segment by serial fp32 adds, every later one through the integer state --
-// one ballot finds the next binade exit or tie in the segment's increment
-// prefix, which is taken with one exact add (pz_sp_events).  Longer rows use
+// a segment with at most one binade exit and no tie in one step
+// (pz_sp_fast), else one ballot per event over the segment's increment
+// prefix, each taken with one exact add (pz_sp_events).  Longer rows use
 // the one-workgroup-per-row softmax (pz_softmax.hip).
 #include <hip/hip_runtime.h>
 
@@ -40,7 +41,8 @@ __device__ __noinline__ PzAcc attn_seg_sum(PzAcc st, float a, float b, float c, 
     const uint32_t g0 = st.g;
     pz_sp_prefix4(v, g0, P, fP);
     pz_sp_prefix4(v, g0 + 1u, Q, fQ);
-    pz_sp_events<PZ_STOP_NONE>(st, v, g0, P, fP, Q, fQ, 0.0f);
+    if (!pz_sp_fast<PZ_STOP_NONE>(st, v, P, fP, Q, fQ, 0.0f))
+      pz_sp_events<PZ_STOP_NONE>(st, v, g0, P, fP, g0 + 1u, Q, fQ, 0.0f);
   }
   pz_sp_uni(st);
   return st;

@@ -139,7 +139,7 @@ __device__ __forceinline__ bool spec_bad(uint32_t flags) {
 
 // ---- every logits row: maximum and segment estimates (HBM) ----------------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_stat(SpecArgs A) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_stat(SpecArgs A) {
   __shared__ PzSpShared SS;
   const int q = blockIdx.y;
   if (threadIdx.x == 0) SS.any = 0u;
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_stat(SpecArgs A) {
 
 // ---- their records ---------------------------------------------------------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_rec(SpecArgs A) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_rec(SpecArgs A) {
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
   pz_etab_fill((pz_lds_u64*)etab);
@@ -294,7 +294,7 @@ __device__ __forceinline__ PzExpTerms<PzTempRow<VEC>> p_terms(const SpecArgs& A,
 
 // ---- per sequence: estimated mass of the draw's terms per segment ----------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vest(SpecArgs A) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vest(SpecArgs A) {
   const int b = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const SpecSeq s = A.seq[b];
   if (s.mode == SQ_DONE) return;
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vest(SpecArgs A) {
 
 // ---- per sequence: records of the draw's terms ----------------------------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vrec(SpecArgs A) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vrec(SpecArgs A) {
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
   __shared__ int last_sh;

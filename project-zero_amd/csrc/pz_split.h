@@ -44,6 +44,11 @@ constexpr int PZ_SP_NC = 32;                   // special segments the walk pre-
 constexpr int PZ_SP_TARGET_WG = 512;           // workgroups a launch aims for (2 per CU)
 constexpr int PZ_SP_U = 4;                     // segments a wave loads per step
 
+// Slice kernels run PZ_SP_TARGET_WG workgroups of PZ_SP_BLOCK threads: two
+// per CU only if a wave keeps to 64 VGPRs (8 waves per SIMD); past that the
+// launch runs in two rounds.
+#define PZ_SP_TWO_PER_CU __attribute__((amdgpu_waves_per_eu(8)))
+
 // Row flags (from the slices' maxima and NaN flags).
 enum {
   PZ_RS_NAN = 1,      // some y is NaN
@@ -203,10 +208,12 @@ __device__ __forceinline__ void pz_sp_rearm(uint32_t* arrive, int row) {
 
 struct PzSpShared {
   float red[PZ_SP_WAVES];
+  uint32_t red2[PZ_SP_WAVES];
   float M;
   uint32_t any;
   int flag;
   int cnt;
+  int tail_end;
   float carry;
   int list[PZ_SP_NC];
 };
@@ -444,21 +451,36 @@ struct PzWalk {
   pz_lds_u32* d2;     // [nseg] increments at the grid below (HAS2)
   pz_lds_u32* gf;     // [nseg] grid and flags
   pz_lds_u32* pd;     // [nseg + 1] exclusive prefix of d (mod 2^32)
+  pz_lds_u32* chp;    // [nseg + 1] exclusive prefix count of grid changes between
+                      //            neighbouring clean segments
   pz_lds_i32* slot;   // [nseg] pre-evaluated slot, or -1
   pz_lds_f32* terms;  // [nc][256] exact terms
   pz_lds_u32* pa;     // [nc][256] inclusive increment prefix at the slot's grid g0
-  pz_lds_u32* pb;     // [nc][256] the same at g0 + 1
-  pz_lds_u8* fa;      // [nc][64] per lane: flagged (tie / big) terms at g0, one bit each
-  pz_lds_u8* fb;      // [nc][64] the same at g0 + 1
-  pz_lds_i32* g0;     // [nc]
-  int nseg, nc;
+  pz_lds_u32* pb;     // [nc][256] the same at g1 (the grid the segment is expected to end in)
+  pz_lds_u8* fa;      // [nc][64] per lane: flagged (tie / big) terms at g0 (low nibble)
+                      //          and the ties among them (high nibble)
+  pz_lds_u8* fb;      // [nc][64] the same at g1
+  pz_lds_i32* g0;     // [nc] the grid of pa (the record's grid)
+  pz_lds_u32* sinfo;  // [nc] g1 | first tie at g0 << 8 | (last flagged at g1 + 1) << 17
+  pz_lds_u32* spt1;   // [nc] pa at the first tie
+  pz_lds_u32* stc;    // [nc] parity corrections of the later ties at g0
+  // The run of clean segments before listed special j (j < n_pre), and the
+  // tail run after the last one (j = n_pre): its end (the special's segment,
+  // or where the tail stops), the sum of its records and their common grid
+  // (0: not one grid).
+  pz_lds_i32* rk;     // [nc + 1]
+  pz_lds_u32* rD;     // [nc + 1]
+  pz_lds_u32* rG;     // [nc + 1]
+  pz_lds_f32* tmp;    // [256] terms of a segment evaluated during the walk
+  int nseg, nc, n_pre;
 };
 
 // LDS of the walk for a row of nseg segments with nc pre-evaluated special
-// segments: six words per segment plus the prefix's extra word; per special
-// segment its terms, two increment prefixes, two flag masks and its grid.
+// segments: seven words per segment plus the prefixes' extra words and 1 KB
+// of staging; per special segment its terms, two increment prefixes, two
+// flag masks, four scalars and its run's three words.
 __host__ __device__ inline size_t pz_sp_walk_lds(int nseg, int nc) {
-  return (size_t)nseg * 24 + 32 + (size_t)nc * (3 * PZ_SP_SEG * 4 + 2 * 64 + 4);
+  return (size_t)nseg * 28 + 48 + PZ_SP_SEG * 4 + (size_t)nc * (3 * PZ_SP_SEG * 4 + 2 * 64 + 16 + 12);
 }
 
 // Special segments the walk can pre-evaluate within max_lds bytes (0 if the
@@ -502,16 +524,132 @@ __device__ __forceinline__ void pz_sp_prefix4(const float (&v)[4], uint32_t g, u
   }
 }
 
-// Element i of a lane-major 4-per-lane array (wave-uniform i).
+// Element i of a lane-major 4-per-lane array (wave-uniform i): the four
+// registers of lane i / 4 read into scalars, then scalar selects (a select
+// between registers on a uniform index compiles to branches).
 __device__ __forceinline__ uint32_t pz_sp_elem(const uint32_t (&a)[4], int i) {
-  const int c = i & 3;
-  const uint32_t x = c == 0 ? a[0] : (c == 1 ? a[1] : (c == 2 ? a[2] : a[3]));
-  return pz_readlane_u32(x, i >> 2);
+  const int l = i >> 2, c = i & 3;
+  const uint32_t x0 = pz_readlane_u32(a[0], l), x1 = pz_readlane_u32(a[1], l);
+  const uint32_t x2 = pz_readlane_u32(a[2], l), x3 = pz_readlane_u32(a[3], l);
+  const uint32_t lo = (c & 1) ? x1 : x0, hi = (c & 1) ? x3 : x2;
+  return (c & 2) ? hi : lo;
 }
 __device__ __forceinline__ float pz_sp_elemf(const float (&a)[4], int i) {
-  const int c = i & 3;
-  const float x = c == 0 ? a[0] : (c == 1 ? a[1] : (c == 2 ? a[2] : a[3]));
-  return pz_readlane_f32(x, i >> 2);
+  const uint32_t u[4] = {__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]),
+                         __float_as_uint(a[3])};
+  return __uint_as_float(pz_sp_elem(u, i));
+}
+
+// Index of the first element (lane-major, 4 per lane) whose predicate holds,
+// or PZ_SP_SEG: one ballot per register column and scalar minima.
+__device__ __forceinline__ int pz_sp_first4(bool p0, bool p1, bool p2, bool p3) {
+  const uint64_t b0 = __ballot(p0), b1 = __ballot(p1), b2 = __ballot(p2), b3 = __ballot(p3);
+  const int i0 = b0 ? 4 * (int)__builtin_ctzll(b0) : 1024;
+  const int i1 = b1 ? 4 * (int)__builtin_ctzll(b1) + 1 : 1024;
+  const int i2 = b2 ? 4 * (int)__builtin_ctzll(b2) + 2 : 1024;
+  const int i3 = b3 ? 4 * (int)__builtin_ctzll(b3) + 3 : 1024;
+  const int m01 = i0 < i1 ? i0 : i1, m23 = i2 < i3 ? i2 : i3;
+  const int m = m01 < m23 ? m01 : m23;
+  return m < PZ_SP_SEG ? m : PZ_SP_SEG;
+}
+
+// Inclusive prefix pv of the increments at grid g (as pz_sp_prefix4), with
+// this lane's flag bits (tie or big) and, apart, its tie bits.
+__device__ __forceinline__ void pz_sp_prefix4t(const float (&v)[4], uint32_t g, uint32_t (&pv)[4],
+                                               uint32_t& flags, uint32_t& ties) {
+  uint32_t inc[4], sum = 0;
+  flags = 0;
+  ties = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint32_t cls;
+    inc[c] = pz_inc(v[c], g, &cls);
+    flags |= (cls != PZ_INC_PLAIN ? 1u : 0u) << c;
+    ties |= (cls == PZ_INC_TIE ? 1u : 0u) << c;
+    sum += inc[c];
+  }
+  uint32_t run = pz_wave_scan_u32(sum) - sum;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    run += inc[c];
+    pv[c] = run;
+  }
+}
+
+// Exclusive maximum over the lanes below (0 for lane 0).
+__device__ __forceinline__ uint32_t pz_wave_excl_max_u32(uint32_t v) {
+#define PZ_MAXDPP_(x, ctrl, rmask)                                                      \
+  {                                                                                     \
+    const uint32_t o = PZ_DPP(x, ctrl, rmask);                                          \
+    x = o > x ? o : x;                                                                  \
+  }
+  PZ_MAXDPP_(v, 0x111, 0xf);  // row_shr:1
+  PZ_MAXDPP_(v, 0x112, 0xf);  // row_shr:2
+  PZ_MAXDPP_(v, 0x114, 0xf);  // row_shr:4
+  PZ_MAXDPP_(v, 0x118, 0xf);  // row_shr:8
+  PZ_MAXDPP_(v, 0x142, 0xa);  // row_bcast:15
+  PZ_MAXDPP_(v, 0x143, 0xc);  // row_bcast:31
+#undef PZ_MAXDPP_
+  // lane l takes lane l - 1's inclusive maximum (wave_shr:1; lane 0 gets 0)
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x138, 0xf, 0xf, true);
+}
+
+// A special segment in the walker's registers: its terms, the increment
+// prefixes at its two grids, and per lane the flag bits (tie or big; low
+// nibble) and tie bits (high nibble) at each.
+struct PzSpSeg {
+  float v[4];
+  uint32_t P[4], Q[4];
+  uint32_t fa, fb;
+};
+
+// Its scalars: the grids g0 (of P) and g1 (of Q), the first tie at g0 (256:
+// none), the last flagged term at g1 plus one (0: none), P at the first tie
+// and the parity corrections of the later ties at g0.  From a state n at
+// g0 with no term leaving the binade and no big term, the ties at g0 give
+// n + P[255] + ((n + pt1) & 1) + tc: round-half-even leaves the state even
+// after the first tie, so only that one depends on n.
+struct PzSpInfo {
+  uint32_t g0, sinfo, pt1, tc;
+};
+
+__device__ __forceinline__ void pz_sp_prep(const float (&v)[4], uint32_t g0, uint32_t g1,
+                                           PzSpSeg& d, PzSpInfo& inf) {
+  const int lane = threadIdx.x & 63;
+  uint32_t fP, tP, fQ, tQ;
+  pz_sp_prefix4t(v, g0, d.P, fP, tP);
+  pz_sp_prefix4t(v, g1, d.Q, fQ, tQ);
+#pragma unroll
+  for (int c = 0; c < 4; c++) d.v[c] = v[c];
+  d.fa = fP | (tP << 4);
+  d.fb = fQ | (tQ << 4);
+  const uint64_t bt = __ballot(tP != 0u), bq = __ballot(fQ != 0u);
+  uint32_t ft = PZ_SP_SEG, lq1 = 0;
+  if (bt) {
+    const int L = (int)__builtin_ctzll(bt);
+    ft = 4u * L + (uint32_t)__builtin_ctz(pz_readlane_u32(tP, L));
+  }
+  if (bq) {
+    const int L = 63 - (int)__builtin_clzll(bq);
+    lq1 = 4u * L + 32u - (uint32_t)__builtin_clz(pz_readlane_u32(fQ, L));
+  }
+  // each later tie's correction: the parity of the prefix since the tie
+  // before it (the previous tie's prefix + 1 by a max-scan: 0 = none yet)
+  uint32_t last = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) last = ((tP >> c) & 1u) ? d.P[c] + 1u : last;
+  uint32_t prev = pz_wave_excl_max_u32(last), corr = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    if ((tP >> c) & 1u) {
+      if (prev) corr += (d.P[c] - (prev - 1u)) & 1u;
+      prev = d.P[c] + 1u;
+    }
+  }
+  inf.g0 = g0;
+  inf.sinfo = g1 | (ft << 8) | (lq1 << 17);
+  inf.pt1 = ft < (uint32_t)PZ_SP_SEG ? pz_sp_elem(d.P, (int)ft) : 0u;
+  inf.tc = pz_wave_sum_u32(corr);
 }
 
 // Stages the row's records in LDS and pre-evaluates up to nc special
@@ -533,57 +671,84 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   W.fa = (pz_lds_u8*)p;        p += (size_t)nc * 64;
   W.fb = (pz_lds_u8*)p;        p += (size_t)nc * 64;
   W.g0 = (pz_lds_i32*)p;       p += (size_t)nc * 4;
+  W.sinfo = (pz_lds_u32*)p;    p += (size_t)nc * 4;
+  W.spt1 = (pz_lds_u32*)p;     p += (size_t)nc * 4;
+  W.stc = (pz_lds_u32*)p;      p += (size_t)nc * 4;
+  W.rk = (pz_lds_i32*)p;       p += (size_t)(nc + 1) * 4;
+  W.rD = (pz_lds_u32*)p;       p += (size_t)(nc + 1) * 4;
+  W.rG = (pz_lds_u32*)p;       p += (size_t)(nc + 1) * 4;
+  W.tmp = (pz_lds_f32*)p;      p += PZ_SP_SEG * 4;
   W.d = (pz_lds_u32*)p;        p += (size_t)nseg * 4;
   W.d2 = (pz_lds_u32*)p;       p += (size_t)nseg * 4;
   W.gf = (pz_lds_u32*)p;       p += (size_t)nseg * 4;
   W.pd = (pz_lds_u32*)p;       p += (size_t)(nseg + 1) * 4;
+  W.chp = (pz_lds_u32*)p;      p += (size_t)(nseg + 1) * 4;
   W.slot = (pz_lds_i32*)p;
   const uint32_t* rd = pz_sp_rec_d(ws, row);
   const uint32_t* rd2 = pz_sp_rec_d2(ws, row);
   const uint32_t* rgf = pz_sp_rec_gf(ws, row);
-  // records, their prefix, and the special segments in id order
+  if (tid == 0) S.tail_end = nseg;
+  // records, their prefix, the grid changes between clean neighbours, and
+  // the special segments in id order
   uint32_t base = 0;  // prefix carried over the chunks (thread-uniform)
   int sbase = 0;      // specials found in earlier chunks
+  uint32_t cbase = 0; // grid changes in earlier chunks
   for (int c0 = 0; c0 < nseg; c0 += PZ_SP_BLOCK) {
     const int k = c0 + tid;
-    uint32_t d = 0, gf = PZ_NO_RECORD;
+    uint32_t d = 0, gf = PZ_NO_RECORD, gfp = PZ_NO_RECORD;
     if (k < nseg) {
       d = rd[k];
       gf = rgf[k];
+      if (k > 0) gfp = rgf[k - 1];
       W.d[k] = d;
       W.d2[k] = rd2[k];
       W.gf[k] = gf;
     }
     const bool special = k < nseg && !pz_sp_clean(gf);
-    // exclusive prefix of d and rank of the special segments (workgroup scans)
+    const bool chg = k < nseg && pz_sp_clean(gf) && pz_sp_clean(gfp) && ((gf ^ gfp) & 0xffu) != 0u;
+    // exclusive prefixes of d and of the grid changes, and the rank of the
+    // special segments (workgroup scans)
     const uint32_t incl = pz_wave_scan_u32(d);
     const uint64_t sb = __ballot(special);
+    const uint64_t cb = __ballot(chg);
     __syncthreads();
     if (lane == 63) S.list[w] = (int)incl;  // wave totals (list[] is free until the end)
-    if (lane == 0) S.red[w] = __int_as_float(__popcll(sb));
+    if (lane == 0) {
+      S.red[w] = __int_as_float(__popcll(sb));
+      S.red2[w] = (uint32_t)__popcll(cb);
+    }
     __syncthreads();
-    uint32_t off = base;
+    uint32_t off = base, coff = cbase;
     int soff = sbase;
     for (int i = 0; i < w; i++) {
       off += (uint32_t)S.list[i];
       soff += __float_as_int(S.red[i]);
+      coff += S.red2[i];
     }
-    uint32_t tot = 0;
+    uint32_t tot = 0, ctot = 0;
     int stot = 0;
     for (int i = 0; i < PZ_SP_WAVES; i++) {
       tot += (uint32_t)S.list[i];
       stot += __float_as_int(S.red[i]);
+      ctot += S.red2[i];
     }
+    const uint64_t below = (1ull << lane) - 1ull;
     if (k < nseg) {
       W.pd[k] = off + incl - d;
-      const int rank = soff + __popcll(sb & ((1ull << lane) - 1ull));
+      W.chp[k] = coff + (uint32_t)__popcll(cb & below);
+      const int rank = soff + __popcll(sb & below);
       W.slot[k] = special && rank < nc ? rank : -1;
+      if (special && rank == nc) S.tail_end = k;  // the first special past the listed ones
     }
     base += tot;
     sbase += stot;
+    cbase += ctot;
     __syncthreads();
   }
-  if (tid == 0) W.pd[nseg] = base;
+  if (tid == 0) {
+    W.pd[nseg] = base;
+    W.chp[nseg] = cbase;
+  }
   __syncthreads();
   // the list of pre-evaluated segments
   for (int k = tid; k < nseg; k += PZ_SP_BLOCK) {
@@ -593,29 +758,56 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   if (tid == 0) S.cnt = sbase < nc ? sbase : nc;
   __syncthreads();
   const int n_pre = S.cnt;
+  W.n_pre = n_pre;
+  // the clean runs between the listed specials (every segment of a run is
+  // clean: the listed specials are all the specials up to the last one)
+  if (tid <= n_pre) {
+    const int a = tid == 0 ? 0 : S.list[tid - 1] + 1;
+    const int b = tid < n_pre ? S.list[tid] : S.tail_end;
+    uint32_t D = 0, G = 0;
+    if (b > a) {
+      D = W.pd[b] - W.pd[a];
+      const bool one_grid = b == a + 1 || W.chp[b] == W.chp[a + 1];
+      G = one_grid ? (W.gf[a] & 0xffu) : 0u;
+    }
+    W.rk[tid] = b;
+    W.rD[tid] = D;
+    W.rG[tid] = G;
+  }
   for (int j = w; j < n_pre; j += PZ_SP_WAVES) {
     const int k = S.list[j];
     float v[4];
     x.seg(k, v);
+    const uint32_t gf = W.gf[k];
+    const uint32_t g = gf == PZ_NO_RECORD ? 1u : (gf & 0xffu);
+    // the grid the segment is expected to end in: a mid-binade start plus
+    // the segment's terms (a term as large as the sum lifts it several
+    // binades at once)
+    const float sum = pz_wave_sum((v[0] + v[1]) + (v[2] + v[3]));
+    const float start = g > 1u ? 1.5f * __uint_as_float(g << 23) : 0.0f;  // 1.5 * 2^(g - 127)
+    const uint32_t ge = pz_grid_of(start + sum);
+    PzSpSeg d;
+    PzSpInfo inf;
+    pz_sp_prep(v, g, ge > g + 1u ? ge : g + 1u, d, inf);
     pz_f4 q;
     q.x = v[0];
     q.y = v[1];
     q.z = v[2];
     q.w = v[3];
     ((pz_lds_f4*)(W.terms + j * PZ_SP_SEG))[lane] = q;
-    const uint32_t gf = W.gf[k];
-    const uint32_t g = gf == PZ_NO_RECORD ? 1u : (gf & 0xffu);
-    uint32_t pa[4], pb[4], fa, fb;
-    pz_sp_prefix4(v, g, pa, fa);
-    pz_sp_prefix4(v, g + 1u, pb, fb);
     pz_u4 a4, b4;
-    a4.x = pa[0]; a4.y = pa[1]; a4.z = pa[2]; a4.w = pa[3];
-    b4.x = pb[0]; b4.y = pb[1]; b4.z = pb[2]; b4.w = pb[3];
+    a4.x = d.P[0]; a4.y = d.P[1]; a4.z = d.P[2]; a4.w = d.P[3];
+    b4.x = d.Q[0]; b4.y = d.Q[1]; b4.z = d.Q[2]; b4.w = d.Q[3];
     ((pz_lds_u4*)(W.pa + j * PZ_SP_SEG))[lane] = a4;
     ((pz_lds_u4*)(W.pb + j * PZ_SP_SEG))[lane] = b4;
-    W.fa[j * 64 + lane] = (uint8_t)fa;
-    W.fb[j * 64 + lane] = (uint8_t)fb;
-    if (lane == 0) W.g0[j] = (int)g;
+    W.fa[j * 64 + lane] = (uint8_t)d.fa;
+    W.fb[j * 64 + lane] = (uint8_t)d.fb;
+    if (lane == 0) {
+      W.g0[j] = (int)g;
+      W.sinfo[j] = inf.sinfo;
+      W.spt1[j] = inf.pt1;
+      W.stc[j] = inf.tc;
+    }
   }
   __syncthreads();
   return W;
@@ -667,80 +859,171 @@ __device__ __forceinline__ int pz_sp_serial(PzAcc& st, const float (&v)[4], int 
   return -1;
 }
 
-// One segment element by element from the state st: each event (a term that
-// leaves the binade, a tie, a term as large as the sum, a stop hit) is found
-// with one ballot over the increment prefix at the state's grid -- P at g0,
-// Q at g0 + 1, recomputed from the terms at any other grid -- and taken with
-// one exact add (pz_acc_add).  Dense events go to the serial loop.  Returns
-// the first hit index or -1.
+// pz_sp_serial over terms [start, end) in LDS (tl[i]; end a multiple of 16):
+// every lane reads the same addresses (broadcast), so the chain of fp32 adds
+// takes its operands from VGPRs; the next 16 terms load while the current
+// 16 are added, and a stop is tested once per 16 terms (sums only grow: when
+// the 16th running sum does not hit, none of the 16 does).
 template <int MODE>
-__device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint32_t g0,
-                                            uint32_t (&P)[4], uint32_t fP, uint32_t (&Q)[4],
-                                            uint32_t fQ, float thr) {
+__device__ __forceinline__ int pz_sp_serial_lds(PzAcc& st, const pz_lds_f32* tl, int start,
+                                                int end, float thr) {
+  float s = pz_acc_value(st);
+  int i = start;
+  for (; i < end && (i & 15); i++) {
+    const float sn = s + tl[i];
+    if (MODE != PZ_STOP_NONE && pz_stop_hit(sn, thr, MODE)) {
+      st = pz_acc_of(sn);
+      return i;
+    }
+    s = sn;
+  }
+  if (i < end) {
+    const pz_lds_f4* q = (const pz_lds_f4*)tl;
+    pz_f4 a = q[i / 4], b = q[i / 4 + 1], c = q[i / 4 + 2], d = q[i / 4 + 3];
+    for (; i < end; i += 16) {
+      const float x[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w,
+                           c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+      if (i + 16 < end) {
+        const int n4 = (i + 16) / 4;
+        a = q[n4];
+        b = q[n4 + 1];
+        c = q[n4 + 2];
+        d = q[n4 + 3];
+      }
+      float t = s;
+#pragma unroll
+      for (int j = 0; j < 16; j++) t = t + x[j];
+      if (MODE != PZ_STOP_NONE && pz_stop_hit(t, thr, MODE)) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+          const float sn = s + x[j];
+          if (pz_stop_hit(sn, thr, MODE)) {
+            st = pz_acc_of(sn);
+            return i + j;
+          }
+          s = sn;
+        }
+      }
+      s = t;
+    }
+  }
+  st = pz_acc_of(s);
+  return -1;
+}
+
+// The increment dd from the state (n, g) at which the running sum meets the
+// stop (value(n + dd) >= thr, or > thr): positive floats order as their
+// bits, so the test is one integer compare.  0xffffffff: never inside the
+// binade (no stop, or a NaN threshold).
+template <int MODE>
+__device__ __forceinline__ uint32_t pz_sp_hit_room(uint32_t n, uint32_t g, float thr) {
+  if (MODE == PZ_STOP_NONE || thr != thr) return 0xffffffffu;
+  int64_t tb;  // the least bit pattern that hits
+  if (thr > 0.0f) tb = (int64_t)__float_as_uint(thr) + (MODE == PZ_STOP_GT ? 1 : 0);
+  else tb = (MODE == PZ_STOP_GT && thr == 0.0f) ? 1 : 0;
+  const int64_t need = tb - (int64_t)((g - 1u) << 23) - (int64_t)n;
+  return need <= 0 ? 0u : (need >= (int64_t)0xffffffffu ? 0xffffffffu : (uint32_t)need);
+}
+
+// One segment element by element from the state st: the next event (a
+// term that leaves the binade, a tie, a term as large as the sum, a stop
+// hit) is found from the increment prefix at the state's grid -- P at gP, Q
+// at gQ, both recomputed from the terms at any other grid -- in integer
+// arithmetic per lane and one ballot; the terms before it are one integer
+// step and the event term is taken exactly (pz_acc_add; a plain term that
+// leaves the binade with one real fp32 add).  Dense events go to the serial
+// loop (from tl, an LDS copy of the terms, when there is one).  Returns the
+// first hit index or -1.
+template <int MODE>
+__device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint32_t gP,
+                                            uint32_t (&P)[4], uint32_t fP, uint32_t gQ,
+                                            uint32_t (&Q)[4], uint32_t fQ, float thr,
+                                            const pz_lds_f32* tl = nullptr) {
   const int lane = threadIdx.x & 63;
   int pos = 0;
   pz_sp_uni(st);
-  g0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)g0);
+  gP = (uint32_t)__builtin_amdgcn_readfirstlane((int)gP);
+  gQ = (uint32_t)__builtin_amdgcn_readfirstlane((int)gQ);
   for (int nev = 0; pos < PZ_SP_SEG; nev++) {
-    if (nev >= 8 || (st.n == 0u && st.g == 1u)) return pz_sp_serial<MODE>(st, v, pos, thr);
-    if (st.g != g0 && st.g != g0 + 1u) {
-      g0 = st.g;
-      pz_sp_prefix4(v, g0, P, fP);
-      pz_sp_prefix4(v, g0 + 1u, Q, fQ);
+    if (nev >= 8 || (st.n == 0u && st.g == 1u)) {
+      if (!tl) return pz_sp_serial<MODE>(st, v, pos, thr);
+      // dense events (a sum still comparable to its terms, e.g. at the start
+      // of a row): up to 64 terms by real adds, then events again.  From a
+      // zero sum the zero terms before the first nonzero one change nothing
+      // (unless a zero sum already meets the stop).
+      if (st.n == 0u && st.g == 1u &&
+          !(MODE != PZ_STOP_NONE && pz_stop_hit(0.0f, thr, MODE))) {
+        bool nz[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) nz[c] = 4 * lane + c >= pos && v[c] != 0.0f;
+        pos = pz_sp_first4(nz[0], nz[1], nz[2], nz[3]);
+        if (pos >= PZ_SP_SEG) return -1;
+      }
+      const int end = ((pos + 64) & ~15) < PZ_SP_SEG ? ((pos + 64) & ~15) : PZ_SP_SEG;
+      const int r = pz_sp_serial_lds<MODE>(st, tl, pos, end, thr);
+      pz_sp_uni(st);
+      if (r >= 0 || end >= PZ_SP_SEG) return r;
+      pos = end;
+      nev = -1;
+      continue;
     }
-    const bool hi = st.g != g0;
+    if (st.g != gP && st.g != gQ) {
+      gP = st.g;
+      gQ = st.g + 1u;
+      pz_sp_prefix4(v, gP, P, fP);
+      pz_sp_prefix4(v, gQ, Q, fQ);
+    }
+    const bool hi = st.g != gP;
     uint32_t a[4];
 #pragma unroll
     for (int c = 0; c < 4; c++) a[c] = hi ? Q[c] : P[c];
     const uint32_t fl4 = hi ? fQ : fP;
+    const uint32_t before = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a[3], 0x138, 0xf, 0xf, true);
     const uint32_t base = pos > 0 ? pz_sp_elem(a, pos - 1) : 0u;
-    if (pos > 0) {
-      // after an event: the rest of the segment in one step when it holds no
-      // flagged term, stays in the binade and (sums only grow) ends below
-      // the stop
-      const uint64_t fb =
-          __ballot(fl4 != 0u && 4 * lane + 31 - (int)__builtin_clz(fl4) >= pos);
-      const uint32_t rest = pz_sp_elem(a, PZ_SP_SEG - 1) - base;
-      if (!fb && rest < (1u << 24) - st.n &&
-          !(MODE != PZ_STOP_NONE &&
-            pz_stop_hit(pz_acc_value_ng(st.n + rest, st.g), thr, MODE))) {
-        st.n += rest;
-        return -1;
-      }
-    }
-    const uint32_t room = (1u << 24) - st.n;  // a prefix >= room leaves the binade
-    int ev = 4, kind = 0;
+    const uint32_t room = (1u << 24) - st.n;
+    const uint32_t hroom = pz_sp_hit_room<MODE>(st.n, st.g, thr);
+    const uint32_t rmin = room < hroom ? room : hroom;
+    // per lane, in integer arithmetic (no per-element booleans): bit c of m
+    // for a live element that is flagged or whose prefix reaches rmin (dd <
+    // 2^31 decides by the sign of dd - rmin; dd >= 2^31 always reaches it)
+    const int rel = 4 * lane - pos;
+    uint32_t m = 0;
 #pragma unroll
-    for (int c = 3; c >= 0; c--) {
-      const int i = 4 * lane + c;
-      const bool live = i >= pos;
-      const bool fl = live && ((fl4 >> c) & 1u);
+    for (int c = 0; c < 4; c++) {
       const uint32_t dd = a[c] - base;
-      const bool cross = live && !fl && dd >= room;
-      const bool hit = MODE != PZ_STOP_NONE && live && !fl && !cross &&
-                       pz_stop_hit(pz_acc_value_ng(st.n + dd, st.g), thr, MODE);
-      if (fl || cross || hit) {
-        ev = c;
-        kind = hit ? 2 : (cross ? 1 : 3);
-      }
+      const uint32_t reach = (dd >> 31) | (((dd - rmin) >> 31) ^ 1u);
+      const uint32_t live = ((uint32_t)(rel + c) >> 31) ^ 1u;
+      m |= ((((fl4 >> c) & 1u) | reach) & live) << c;
     }
-    const uint64_t ball = __ballot(ev < 4);
+    const uint64_t ball = __ballot(m != 0u);
     if (!ball) {
-      st.n += pz_sp_elem(a, PZ_SP_SEG - 1) - base;
+      st.n += pz_readlane_u32(a[3], 63) - base;
       return -1;
     }
+    // this lane's first event: the prefix before it, its own, its term, its flag
+    const int c = (int)__builtin_ctz(m | 16u);
+    const uint32_t prv = c == 0 ? before : (c == 1 ? a[0] : (c == 2 ? a[1] : a[2]));
+    const uint32_t cur = c == 0 ? a[0] : (c == 1 ? a[1] : (c == 2 ? a[2] : a[3]));
+    const float tv = c == 0 ? v[0] : (c == 1 ? v[1] : (c == 2 ? v[2] : v[3]));
+    const uint32_t flg = (fl4 >> c) & 1u;
     const int L = (int)__builtin_ctzll(ball);
-    const int i = 4 * L + __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(ev, L));
-    const int kd = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_readlane(kind, L));
-    if (kd == 2) {
-      st.n += pz_sp_elem(a, i) - base;
-      return i;
+    const int i = 4 * L + __builtin_amdgcn_readlane(c, L);
+    const uint32_t prev = i == pos ? base : pz_readlane_u32(prv, L);
+    const uint32_t curL = pz_readlane_u32(cur, L);
+    const float t = pz_readlane_f32(tv, L);
+    const bool flagged = pz_readlane_u32(flg, L) != 0u;
+    st.n += prev - base;
+    if (flagged) {
+      st = pz_acc_add(st, t);  // a tie or a term as large as the sum
+    } else {
+      const uint32_t inc = curL - prev;
+      if (inc < (1u << 24) - st.n) {  // neither flagged nor leaving the binade: a stop hit
+        st.n += inc;
+        pz_sp_uni(st);
+        return i;
+      }
+      st = pz_acc_of(pz_acc_value(st) + t);  // leaves the binade: one real add
     }
-    if (i > pos) st.n += pz_sp_elem(a, i - 1) - base;
-    const float t = pz_sp_elemf(v, i);
-    // a plain term that leaves the binade: one real add; a tie or a term as
-    // large as the sum: the exact step
-    st = kd == 1 ? pz_acc_of(pz_acc_value(st) + t) : pz_acc_add(st, t);
     pz_sp_uni(st);
     if (MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value(st), thr, MODE)) return i;
     pos = i + 1;
@@ -748,23 +1031,159 @@ __device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint
   return -1;
 }
 
-// The walk (one wave): the exact sequential sum of the row's terms in id
-// order, from state 0.  With a stop mode returns the element index of the
-// first hit (st = the sum including it), else -1 (st = the whole sum).  X
-// provides seg(k, v[4]) for segments evaluated during the walk.
-template <int MODE, class X>
-__device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr, const X& x) {
+// The common special segment in one step: at the state's grid no tie or big
+// term comes before the first term that leaves the binade, that term is
+// taken with one real fp32 add, and the rest of the segment fits the next
+// binade without a flagged term (the prefixes only grow, so the rest's
+// total decides).  Also a segment with no event at all.  Needs st.g == the
+// grid of P; Q is the prefix at the grid above.  Returns false, leaving st
+// alone, for anything else (and for a stop hit anywhere in the segment),
+// which the caller hands to pz_sp_events.
+template <int MODE>
+__device__ __forceinline__ bool pz_sp_fast(PzAcc& st, const float (&v)[4], const uint32_t (&P)[4],
+                                           uint32_t fP, const uint32_t (&Q)[4], uint32_t fQ,
+                                           float thr) {
   const int lane = threadIdx.x & 63;
-  st.n = 0;
-  st.g = 1;
-  int k = 0;
-  const int nseg = W.nseg;
-  while (k < nseg) {
-    // runs of clean records at the state's grid: 64 segments per step
+  const uint32_t room = (1u << 24) - st.n;
+  bool e[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) e[c] = ((fP >> c) & 1u) != 0u || P[c] >= room;
+  const int i = pz_sp_first4(e[0], e[1], e[2], e[3]);
+  PzAcc a;
+  if (i >= PZ_SP_SEG) {
+    a.n = st.n + pz_readlane_u32(P[3], 63);
+    a.g = st.g;
+  } else {
+    if ((pz_readlane_u32(fP, i >> 2) >> (i & 3)) & 1u) return false;  // a tie or a big term first
+    const uint32_t before = i > 0 ? pz_sp_elem(P, i - 1) : 0u;
+    a = pz_acc_of(pz_acc_value_ng(st.n + before, st.g) + pz_sp_elemf(v, i));
+    if (a.g != st.g + 1u) return false;
+    // the terms after i at the next grid: none flagged, their sum inside it
+    const uint32_t qi = pz_sp_elem(Q, i);
+    const uint64_t later = __ballot(fQ != 0u && 4 * lane + 31 - (int)__builtin_clz(fQ) > i);
+    const uint32_t rest = pz_readlane_u32(Q[3], 63) - qi;
+    if (later || rest >= (1u << 24) - a.n) return false;
+    a.n += rest;
+  }
+  if (MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value(a), thr, MODE)) return false;
+  st.n = (uint32_t)__builtin_amdgcn_readfirstlane((int)a.n);
+  st.g = (uint32_t)__builtin_amdgcn_readfirstlane((int)a.g);
+  return true;
+}
+
+// A pre-evaluated special segment in one step (sinfo, pt1, tc as in
+// PzSpInfo; the state at g0, the grid of P): with no term leaving the
+// binade and no big term, the segment's increments plus its ties' parity
+// corrections; else, when no tie comes first, the first term that leaves
+// the binade (or the big term) taken with one real fp32 add and the rest of
+// the segment at g1, which must hold no flagged term after it and fit the
+// binade.  Returns false, leaving st alone, for anything else (and for a
+// stop hit anywhere in the segment).
+template <int MODE>
+__device__ __forceinline__ bool pz_sp_fast_pre(PzAcc& st, const PzSpSeg& d, uint32_t sinfo,
+                                               uint32_t pt1, uint32_t tc, float thr) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t g1 = sinfo & 0xffu, ft = (sinfo >> 8) & 0x1ffu, lq1 = (sinfo >> 17) & 0x1ffu;
+  const uint32_t room = (1u << 24) - st.n;
+  const uint32_t big = (d.fa & ~(d.fa >> 4)) & 15u;  // flagged and not a tie
+  uint32_t m = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const uint32_t reach = (d.P[c] >> 31) | (((d.P[c] - room) >> 31) ^ 1u);
+    m |= (((big >> c) & 1u) | reach) << c;
+  }
+  const uint64_t ball = __ballot(m != 0u);
+  PzAcc a;
+  if (!ball) {
+    uint32_t nn = st.n + pz_readlane_u32(d.P[3], 63);
+    if (ft < (uint32_t)PZ_SP_SEG) {
+      nn += ((st.n + pt1) & 1u) + tc;
+      if (nn >= (1u << 24)) return false;
+    }
+    a.n = nn;
+    a.g = st.g;
+  } else {
+    const int c = (int)__builtin_ctz(m | 16u);
+    const uint32_t before = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.P[3], 0x138, 0xf, 0xf, true);
+    const uint32_t prv = c == 0 ? before : (c == 1 ? d.P[0] : (c == 2 ? d.P[1] : d.P[2]));
+    const float tv = c == 0 ? d.v[0] : (c == 1 ? d.v[1] : (c == 2 ? d.v[2] : d.v[3]));
+    const uint32_t qv = c == 0 ? d.Q[0] : (c == 1 ? d.Q[1] : (c == 2 ? d.Q[2] : d.Q[3]));
+    const int L = (int)__builtin_ctzll(ball);
+    const uint32_t i = 4u * L + (uint32_t)__builtin_amdgcn_readlane(c, L);
+    if (ft <= i) return false;  // a tie first
+    const uint32_t prev = pz_readlane_u32(prv, L), qi = pz_readlane_u32(qv, L);
+    a = pz_acc_of(pz_acc_value_ng(st.n + prev, st.g) + pz_readlane_f32(tv, L));
+    const uint32_t rest = pz_readlane_u32(d.Q[3], 63) - qi;
+    if (a.g != g1 || lq1 > i + 1u || rest >= (1u << 24) - a.n) return false;
+    a.n += rest;
+  }
+  if (MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value(a), thr, MODE)) return false;
+  st.n = (uint32_t)__builtin_amdgcn_readfirstlane((int)a.n);
+  st.g = (uint32_t)__builtin_amdgcn_readfirstlane((int)a.g);
+  return true;
+}
+
+// The pre-evaluated data of slot s (one round of LDS reads).
+__device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int s, PzSpSeg& d) {
+  const int lane = threadIdx.x & 63;
+  const pz_f4 q = ((const pz_lds_f4*)(W.terms + s * PZ_SP_SEG))[lane];
+  const pz_u4 a4 = ((const pz_lds_u4*)(W.pa + s * PZ_SP_SEG))[lane];
+  const pz_u4 b4 = ((const pz_lds_u4*)(W.pb + s * PZ_SP_SEG))[lane];
+  d.fa = W.fa[s * 64 + lane];
+  d.fb = W.fb[s * 64 + lane];
+  d.v[0] = q.x; d.v[1] = q.y; d.v[2] = q.z; d.v[3] = q.w;
+  d.P[0] = a4.x; d.P[1] = a4.y; d.P[2] = a4.z; d.P[3] = a4.w;
+  d.Q[0] = b4.x; d.Q[1] = b4.y; d.Q[2] = b4.z; d.Q[3] = b4.w;
+}
+
+// The record at the grid below (HAS2) when the state sits there: gf, d2 of
+// the segment.  Returns true when it served the segment.
+template <int MODE>
+__device__ __forceinline__ bool pz_sp_has2(PzAcc& st, uint32_t gf, uint32_t d2, float thr) {
+  if (gf != PZ_NO_RECORD && (gf & PZ_GF_HAS2) && !(gf & (PZ_GF_DIRTY2 | PZ_GF_XING)) &&
+      (gf & 0xffu) - 1u == st.g && d2 < (1u << 24) - st.n &&
+      !(MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(st.n + d2, st.g), thr, MODE))) {
+    st.n += d2;
+    pz_sp_uni(st);
+    return true;
+  }
+  return false;
+}
+
+// Segment k from the state st when its primary record cannot serve it and
+// it has no pre-evaluated slot: the record at the grid below (HAS2), else
+// its exact terms (X::seg) through pz_sp_fast or the events.  Returns the
+// index of a stop hit in the segment, or -1.
+template <int MODE, class X>
+__device__ __forceinline__ int pz_sp_special(PzAcc& st, const PzWalk& W, float thr, const X& x,
+                                             int k) {
+  const int lane = threadIdx.x & 63;
+  if (pz_sp_has2<MODE>(st, W.gf[k], W.d2[k], thr)) return -1;
+  float v[4];
+  uint32_t P[4], Q[4], fP, fQ;
+  x.seg(k, v);
+  const uint32_t g0 = st.g;
+  pz_sp_prefix4(v, g0, P, fP);
+  pz_sp_prefix4(v, g0 + 1u, Q, fQ);
+  pz_f4 q;
+  q.x = v[0]; q.y = v[1]; q.z = v[2]; q.w = v[3];
+  ((pz_lds_f4*)W.tmp)[lane] = q;
+  if (pz_sp_fast<MODE>(st, v, P, fP, Q, fQ, thr)) return -1;
+  return pz_sp_events<MODE>(st, v, g0, P, fP, g0 + 1u, Q, fQ, thr, W.tmp);
+}
+
+// Segments [k, kend) one record at a time: runs of clean records at the
+// state's grid advance 64 segments per step, any other segment goes through
+// pz_sp_special.  Returns the element index of a stop hit, or -1.
+template <int MODE, class X>
+__device__ __forceinline__ int pz_sp_walk_range(PzAcc& st, const PzWalk& W, float thr,
+                                                const X& x, int k, int kend) {
+  const int lane = threadIdx.x & 63;
+  while (k < kend) {
     {
       const int kk = k + lane;
       bool bad = true;
-      if (kk < nseg) {
+      if (kk < kend) {
         const uint32_t gf = W.gf[kk];
         const uint32_t upto = W.pd[kk + 1] - W.pd[k];  // d of [k, kk]
         bad = !pz_sp_clean(gf) || (gf & 0xffu) != st.g || upto >= (1u << 24) - st.n ||
@@ -774,50 +1193,93 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
       const uint64_t ball = __ballot(bad);
       const int L = ball ? (int)__builtin_ctzll(ball) : 64;
       const int kb = k + L;
-      st.n += W.pd[kb < nseg ? kb : nseg] - W.pd[k];
+      st.n += W.pd[kb < kend ? kb : kend] - W.pd[k];
       pz_sp_uni(st);
-      if (kb >= nseg) break;
+      if (kb >= kend) break;
       k = kb;
       if (L == 64) continue;
     }
-    // segment k cannot be taken from its primary record
-    const uint32_t gf = W.gf[k];
-    if (gf != PZ_NO_RECORD && (gf & PZ_GF_HAS2) && !(gf & (PZ_GF_DIRTY2 | PZ_GF_XING)) &&
-        (gf & 0xffu) - 1u == st.g) {
-      const uint32_t d2 = W.d2[k];
-      if (d2 < (1u << 24) - st.n &&
-          !(MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(st.n + d2, st.g), thr, MODE))) {
-        st.n += d2;
-        pz_sp_uni(st);
-        k++;
-        continue;
-      }
-    }
-    const int s = W.slot[k];
-    float v[4];
-    uint32_t P[4], Q[4], fP, fQ, g0;
-    if (s >= 0) {
-      // everything the segment needs, in one round of LDS reads
-      const pz_f4 q = ((const pz_lds_f4*)(W.terms + s * PZ_SP_SEG))[lane];
-      const pz_u4 a4 = ((const pz_lds_u4*)(W.pa + s * PZ_SP_SEG))[lane];
-      const pz_u4 b4 = ((const pz_lds_u4*)(W.pb + s * PZ_SP_SEG))[lane];
-      fP = W.fa[s * 64 + lane];
-      fQ = W.fb[s * 64 + lane];
-      g0 = (uint32_t)W.g0[s];
-      v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
-      P[0] = a4.x; P[1] = a4.y; P[2] = a4.z; P[3] = a4.w;
-      Q[0] = b4.x; Q[1] = b4.y; Q[2] = b4.z; Q[3] = b4.w;
-    } else {
-      x.seg(k, v);
-      g0 = st.g;
-      pz_sp_prefix4(v, g0, P, fP);
-      pz_sp_prefix4(v, g0 + 1u, Q, fQ);
-    }
-    const int r = pz_sp_events<MODE>(st, v, g0, P, fP, Q, fQ, thr);
+    const int r = pz_sp_special<MODE>(st, W, thr, x, k);
     if (r >= 0) return k * PZ_SP_SEG + r;
     k++;
   }
   return -1;
+}
+
+// The walk (one wave): the exact sequential sum of the row's terms in id
+// order, from state 0.  With a stop mode returns the element index of the
+// first hit (st = the sum including it), else -1 (st = the whole sum).  X
+// provides seg(k, v[4]) for segments evaluated during the walk.
+//
+// It goes from listed special to listed special: the clean run before each
+// one is a single step when its records share the state's grid and neither
+// leave the binade nor reach the stop (sums only grow, so the run's total
+// decides); otherwise that run goes record by record (pz_sp_walk_range).
+// The runs' and the specials' scalars sit in the wave's lanes (lane j: run
+// and special j), and each special's pre-evaluated data loads while the one
+// before is processed, so a step waits on no LDS read.
+template <int MODE, class X>
+__device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr, const X& x) {
+  const int lane = threadIdx.x & 63;
+  st.n = 0;
+  st.g = 1;
+  const int np = W.n_pre;
+  int mk = 0;
+  uint32_t mD = 0, mG = 0, mg0 = 0, msi = 0, mpt = 0, mtc = 0, mgf = PZ_NO_RECORD, md2 = 0;
+  if (lane <= np) {
+    mk = W.rk[lane];
+    mD = W.rD[lane];
+    mG = W.rG[lane];
+  }
+  if (lane < np) {
+    mg0 = (uint32_t)W.g0[lane];
+    msi = W.sinfo[lane];
+    mpt = W.spt1[lane];
+    mtc = W.stc[lane];
+    mgf = W.gf[mk];
+    md2 = W.d2[mk];
+  }
+  PzSpSeg nxt;
+  if (np > 0) pz_sp_load_slot(W, 0, nxt);
+  int k = 0;
+  for (int j = 0;; j++) {
+    const int b = __builtin_amdgcn_readlane(mk, j);
+    const PzSpSeg cur = nxt;
+    if (j + 1 < np) pz_sp_load_slot(W, j + 1, nxt);
+    if (k < b) {
+      const uint32_t D = pz_readlane_u32(mD, j), G = pz_readlane_u32(mG, j);
+      if (G == st.g && D < (1u << 24) - st.n &&
+          !(MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(st.n + D, st.g), thr, MODE))) {
+        st.n += D;
+      } else {
+        const int r = pz_sp_walk_range<MODE>(st, W, thr, x, k, b);
+        if (r >= 0) return r;
+      }
+      pz_sp_uni(st);
+    }
+    k = b;
+    if (j >= np) break;
+    // special b (slot j)
+    if (!pz_sp_has2<MODE>(st, pz_readlane_u32(mgf, j), pz_readlane_u32(md2, j), thr)) {
+      const uint32_t g0 = pz_readlane_u32(mg0, j), si = pz_readlane_u32(msi, j);
+      if (!(st.g == g0 &&
+            pz_sp_fast_pre<MODE>(st, cur, si, pz_readlane_u32(mpt, j), pz_readlane_u32(mtc, j),
+                                 thr))) {
+        uint32_t P[4], Q[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          P[c] = cur.P[c];
+          Q[c] = cur.Q[c];
+        }
+        const int r = pz_sp_events<MODE>(st, cur.v, g0, P, cur.fa & 15u, si & 0xffu, Q,
+                                         cur.fb & 15u, thr, W.terms + j * PZ_SP_SEG);
+        if (r >= 0) return b * PZ_SP_SEG + r;
+      }
+    }
+    k = b + 1;
+  }
+  // past the listed specials (more specials than slots): record by record
+  return k < W.nseg ? pz_sp_walk_range<MODE>(st, W, thr, x, k, W.nseg) : -1;
 }
 
 #endif

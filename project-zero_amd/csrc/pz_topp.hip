@@ -201,7 +201,7 @@ __device__ __forceinline__ bool topp_degenerate(uint32_t flags) {
 
 // ---- pass 1: slice maxima (HBM) -------------------------------------------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_max(TOPP_ARGS) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_max(TOPP_ARGS) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   const int row = pz_row_of(rows, blockIdx.y);
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_max(TOPP_ARGS) {
 
 // ---- pass 2: estimated mass of the candidates per segment -----------------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_est(TOPP_ARGS) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_est(TOPP_ARGS) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   const int row = pz_row_of(rows, blockIdx.y);
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_est(TOPP_ARGS) {
 
 // ---- pass 3: records of the exact candidate terms + mass histogram -------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_rec(TOPP_ARGS, int pen_bytes) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_ARGS, int pen_bytes) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
@@ -430,7 +430,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walk(TOPP_ARGS, int pen_by
 
 // ---- pass 5: gather the selected candidates; sort, cut-off and draw ------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_gather(TOPP_ARGS) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_gather(TOPP_ARGS) {
   extern __shared__ __align__(16) char lds[];
   __shared__ uint64_t etab[32];
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
