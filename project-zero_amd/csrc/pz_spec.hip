@@ -349,7 +349,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vest(Spec
 
 // ---- per sequence: records of the draw's terms ----------------------------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vrec(SpecArgs A) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vrec(SpecArgs A) {
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
   __shared__ int last_sh;

@@ -166,11 +166,14 @@ __device__ __forceinline__ uint32_t* pz_sp_rec_gf(const PzSplitWs& ws, int row) 
 struct PzSlice {
   int k0, k1;
 };
-__device__ __forceinline__ PzSlice pz_sp_slice(int nseg, int spw) {
+__device__ __forceinline__ PzSlice pz_sp_slice_at(int idx, int nseg, int spw) {
   PzSlice s;
-  s.k0 = (int)blockIdx.x * spw;
+  s.k0 = idx * spw;
   s.k1 = s.k0 + spw < nseg ? s.k0 + spw : nseg;
   return s;
+}
+__device__ __forceinline__ PzSlice pz_sp_slice(int nseg, int spw) {
+  return pz_sp_slice_at((int)blockIdx.x, nseg, spw);
 }
 
 // Ids [lo, hi) of a slice (for its penalty tables).
@@ -464,6 +467,7 @@ struct PzWalk {
   pz_lds_u32* sinfo;  // [nc] g1 | first tie at g0 << 8 | (last flagged at g1 + 1) << 17
   pz_lds_u32* spt1;   // [nc] pa at the first tie
   pz_lds_u32* stc;    // [nc] parity corrections of the later ties at g0
+  pz_lds_u32* rdy;    // [nc] slot written (set by the wave that pre-evaluates it)
   // The run of clean segments before listed special j (j < n_pre), and the
   // tail run after the last one (j = n_pre): its end (the special's segment,
   // or where the tail stops), the sum of its records and their common grid
@@ -478,9 +482,9 @@ struct PzWalk {
 // LDS of the walk for a row of nseg segments with nc pre-evaluated special
 // segments: seven words per segment plus the prefixes' extra words and 1 KB
 // of staging; per special segment its terms, two increment prefixes, two
-// flag masks, four scalars and its run's three words.
+// flag masks, five scalars and its run's three words.
 __host__ __device__ inline size_t pz_sp_walk_lds(int nseg, int nc) {
-  return (size_t)nseg * 28 + 48 + PZ_SP_SEG * 4 + (size_t)nc * (3 * PZ_SP_SEG * 4 + 2 * 64 + 16 + 12);
+  return (size_t)nseg * 28 + 48 + PZ_SP_SEG * 4 + (size_t)nc * (3 * PZ_SP_SEG * 4 + 2 * 64 + 20 + 12);
 }
 
 // Special segments the walk can pre-evaluate within max_lds bytes (0 if the
@@ -538,6 +542,20 @@ __device__ __forceinline__ float pz_sp_elemf(const float (&a)[4], int i) {
   const uint32_t u[4] = {__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]),
                          __float_as_uint(a[3])};
   return __uint_as_float(pz_sp_elem(u, i));
+}
+
+// x_c for a per-lane c in 0..3.  The values pass through an empty asm
+// first: a select between elements of one array would otherwise become a
+// load at a per-lane index, which puts the array in scratch memory.
+__device__ __forceinline__ uint32_t pz_sel4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                            int c) {
+  asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
+  const uint32_t lo = (c & 1) ? x1 : x0, hi = (c & 1) ? x3 : x2;
+  return (c & 2) ? hi : lo;
+}
+__device__ __forceinline__ float pz_sel4f(float x0, float x1, float x2, float x3, int c) {
+  return __uint_as_float(pz_sel4(__float_as_uint(x0), __float_as_uint(x1), __float_as_uint(x2),
+                                 __float_as_uint(x3), c));
 }
 
 // Index of the first element (lane-major, 4 per lane) whose predicate holds,
@@ -601,6 +619,7 @@ struct PzSpSeg {
   float v[4];
   uint32_t P[4], Q[4];
   uint32_t fa, fb;
+  uint32_t g0, sinfo, pt1, tc;  // as PzSpInfo (wave-uniform)
 };
 
 // Its scalars: the grids g0 (of P) and g1 (of Q), the first tie at g0 (256:
@@ -615,7 +634,6 @@ struct PzSpInfo {
 
 __device__ __forceinline__ void pz_sp_prep(const float (&v)[4], uint32_t g0, uint32_t g1,
                                            PzSpSeg& d, PzSpInfo& inf) {
-  const int lane = threadIdx.x & 63;
   uint32_t fP, tP, fQ, tQ;
   pz_sp_prefix4t(v, g0, d.P, fP, tP);
   pz_sp_prefix4t(v, g1, d.Q, fQ, tQ);
@@ -655,11 +673,14 @@ __device__ __forceinline__ void pz_sp_prep(const float (&v)[4], uint32_t g0, uin
 // Stages the row's records in LDS and pre-evaluates up to nc special
 // segments (dirty, crossing, or without a record) in id order: exact terms
 // (X::seg) and increment prefixes and flags at the record's grid and the
-// next.  Every thread calls it.
+// next.  Every thread calls it; it returns without a final barrier: the
+// walker (wave 0) waits per slot (pz_sp_load_slot), the other waves may go
+// on to other work.
 template <class X>
 __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg, int nc,
                                                    const PzSplitWs& ws, char* lds,
-                                                   PzSpShared& S) {
+                                                   PzSpShared& S,
+                                                   int n_producers = PZ_SP_WAVES - 1) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   PzWalk W;
   W.nseg = nseg;
@@ -674,6 +695,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   W.sinfo = (pz_lds_u32*)p;    p += (size_t)nc * 4;
   W.spt1 = (pz_lds_u32*)p;     p += (size_t)nc * 4;
   W.stc = (pz_lds_u32*)p;      p += (size_t)nc * 4;
+  W.rdy = (pz_lds_u32*)p;      p += (size_t)nc * 4;
   W.rk = (pz_lds_i32*)p;       p += (size_t)(nc + 1) * 4;
   W.rD = (pz_lds_u32*)p;       p += (size_t)(nc + 1) * 4;
   W.rG = (pz_lds_u32*)p;       p += (size_t)(nc + 1) * 4;
@@ -773,8 +795,14 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     W.rk[tid] = b;
     W.rD[tid] = D;
     W.rG[tid] = G;
+    if (tid < n_pre) W.rdy[tid] = 0u;
   }
-  for (int j = w; j < n_pre; j += PZ_SP_WAVES) {
+  __syncthreads();
+  // Waves 1 .. n_producers pre-evaluate the listed specials in id order,
+  // each slot flagged when written, while wave 0 (the walker) starts at once
+  // and waits only at a slot that is not ready yet.  The producers wait on
+  // nothing, so every such wait ends.
+  for (int j = w - 1; w > 0 && w <= n_producers && j < n_pre; j += n_producers) {
     const int k = S.list[j];
     float v[4];
     x.seg(k, v);
@@ -808,8 +836,10 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
       W.spt1[j] = inf.pt1;
       W.stc[j] = inf.tc;
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0)
+      __hip_atomic_store((uint32_t*)&W.rdy[j], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  __syncthreads();
   return W;
 }
 
@@ -1002,9 +1032,9 @@ __device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint
     }
     // this lane's first event: the prefix before it, its own, its term, its flag
     const int c = (int)__builtin_ctz(m | 16u);
-    const uint32_t prv = c == 0 ? before : (c == 1 ? a[0] : (c == 2 ? a[1] : a[2]));
-    const uint32_t cur = c == 0 ? a[0] : (c == 1 ? a[1] : (c == 2 ? a[2] : a[3]));
-    const float tv = c == 0 ? v[0] : (c == 1 ? v[1] : (c == 2 ? v[2] : v[3]));
+    const uint32_t prv = pz_sel4(before, a[0], a[1], a[2], c);
+    const uint32_t cur = pz_sel4(a[0], a[1], a[2], a[3], c & 3);
+    const float tv = pz_sel4f(v[0], v[1], v[2], v[3], c & 3);
     const uint32_t flg = (fl4 >> c) & 1u;
     const int L = (int)__builtin_ctzll(ball);
     const int i = 4 * L + __builtin_amdgcn_readlane(c, L);
@@ -1082,7 +1112,6 @@ __device__ __forceinline__ bool pz_sp_fast(PzAcc& st, const float (&v)[4], const
 template <int MODE>
 __device__ __forceinline__ bool pz_sp_fast_pre(PzAcc& st, const PzSpSeg& d, uint32_t sinfo,
                                                uint32_t pt1, uint32_t tc, float thr) {
-  const int lane = threadIdx.x & 63;
   const uint32_t g1 = sinfo & 0xffu, ft = (sinfo >> 8) & 0x1ffu, lq1 = (sinfo >> 17) & 0x1ffu;
   const uint32_t room = (1u << 24) - st.n;
   const uint32_t big = (d.fa & ~(d.fa >> 4)) & 15u;  // flagged and not a tie
@@ -1105,9 +1134,9 @@ __device__ __forceinline__ bool pz_sp_fast_pre(PzAcc& st, const PzSpSeg& d, uint
   } else {
     const int c = (int)__builtin_ctz(m | 16u);
     const uint32_t before = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)d.P[3], 0x138, 0xf, 0xf, true);
-    const uint32_t prv = c == 0 ? before : (c == 1 ? d.P[0] : (c == 2 ? d.P[1] : d.P[2]));
-    const float tv = c == 0 ? d.v[0] : (c == 1 ? d.v[1] : (c == 2 ? d.v[2] : d.v[3]));
-    const uint32_t qv = c == 0 ? d.Q[0] : (c == 1 ? d.Q[1] : (c == 2 ? d.Q[2] : d.Q[3]));
+    const uint32_t prv = pz_sel4(before, d.P[0], d.P[1], d.P[2], c);
+    const float tv = pz_sel4f(d.v[0], d.v[1], d.v[2], d.v[3], c & 3);
+    const uint32_t qv = pz_sel4(d.Q[0], d.Q[1], d.Q[2], d.Q[3], c & 3);
     const int L = (int)__builtin_ctzll(ball);
     const uint32_t i = 4u * L + (uint32_t)__builtin_amdgcn_readlane(c, L);
     if (ft <= i) return false;  // a tie first
@@ -1123,9 +1152,19 @@ __device__ __forceinline__ bool pz_sp_fast_pre(PzAcc& st, const PzSpSeg& d, uint
   return true;
 }
 
-// The pre-evaluated data of slot s (one round of LDS reads).
+// Whether slot s has been written (acquire).
+__device__ __forceinline__ bool pz_sp_slot_ready(const PzWalk& W, int s) {
+  return __hip_atomic_load((uint32_t*)&W.rdy[s], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+}
+
+// The pre-evaluated data of slot s (one round of LDS reads), once written.
 __device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int s, PzSpSeg& d) {
   const int lane = threadIdx.x & 63;
+  while (!pz_sp_slot_ready(W, s)) __builtin_amdgcn_s_sleep(1);
+  d.g0 = (uint32_t)W.g0[s];
+  d.sinfo = W.sinfo[s];
+  d.pt1 = W.spt1[s];
+  d.tc = W.stc[s];
   const pz_f4 q = ((const pz_lds_f4*)(W.terms + s * PZ_SP_SEG))[lane];
   const pz_u4 a4 = ((const pz_lds_u4*)(W.pa + s * PZ_SP_SEG))[lane];
   const pz_u4 b4 = ((const pz_lds_u4*)(W.pb + s * PZ_SP_SEG))[lane];
@@ -1225,27 +1264,26 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
   st.g = 1;
   const int np = W.n_pre;
   int mk = 0;
-  uint32_t mD = 0, mG = 0, mg0 = 0, msi = 0, mpt = 0, mtc = 0, mgf = PZ_NO_RECORD, md2 = 0;
+  uint32_t mD = 0, mG = 0, mgf = PZ_NO_RECORD, md2 = 0;
   if (lane <= np) {
     mk = W.rk[lane];
     mD = W.rD[lane];
     mG = W.rG[lane];
   }
   if (lane < np) {
-    mg0 = (uint32_t)W.g0[lane];
-    msi = W.sinfo[lane];
-    mpt = W.spt1[lane];
-    mtc = W.stc[lane];
     mgf = W.gf[mk];
     md2 = W.d2[mk];
   }
   PzSpSeg nxt;
-  if (np > 0) pz_sp_load_slot(W, 0, nxt);
+  bool have = false;  // nxt holds slot j
   int k = 0;
   for (int j = 0;; j++) {
     const int b = __builtin_amdgcn_readlane(mk, j);
-    const PzSpSeg cur = nxt;
-    if (j + 1 < np) pz_sp_load_slot(W, j + 1, nxt);
+    PzSpSeg cur = nxt;
+    if (j < np && !have) pz_sp_load_slot(W, j, cur);
+    // the next slot's loads overlap this step when it is already written
+    have = j + 1 < np && pz_sp_slot_ready(W, j + 1);
+    if (have) pz_sp_load_slot(W, j + 1, nxt);
     if (k < b) {
       const uint32_t D = pz_readlane_u32(mD, j), G = pz_readlane_u32(mG, j);
       if (G == st.g && D < (1u << 24) - st.n &&
@@ -1261,10 +1299,8 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
     if (j >= np) break;
     // special b (slot j)
     if (!pz_sp_has2<MODE>(st, pz_readlane_u32(mgf, j), pz_readlane_u32(md2, j), thr)) {
-      const uint32_t g0 = pz_readlane_u32(mg0, j), si = pz_readlane_u32(msi, j);
-      if (!(st.g == g0 &&
-            pz_sp_fast_pre<MODE>(st, cur, si, pz_readlane_u32(mpt, j), pz_readlane_u32(mtc, j),
-                                 thr))) {
+      const uint32_t g0 = cur.g0, si = cur.sinfo;
+      if (!(st.g == g0 && pz_sp_fast_pre<MODE>(st, cur, si, cur.pt1, cur.tc, thr))) {
         uint32_t P[4], Q[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {

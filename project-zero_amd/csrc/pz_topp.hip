@@ -13,19 +13,22 @@
 //     first i < cut-off with r < cdf, else slot 0 (:96-105).
 //
 // Design: every row is split over S workgroups (pz_split.h), launches
-//   k_topp_stat    (HBM) row maximum, segment mass estimates, predicted
-//                  binades of the running sum;
+//   k_topp_stat    (HBM) slice maxima;
+//   k_topp_est     (L2)  estimated candidate mass per segment;
 //   k_topp_rec     (L2)  exact e = expf(x - max) (glibc-identical pz_expf)
-//                  of every candidate -> integer segment records + a mass
-//                  histogram of e per workgroup; the row's last workgroup
-//                  walks the records (the exact normaliser) while a second
-//                  wave picks, from the merged histogram, the smallest set of
-//                  top bins whose estimated mass clears top_p with margin;
-//   k_topp_gather  (L2)  candidates with p >= the lowest selected bin -- a
-//                  prefix of the reference's sort order -- appended as
-//                  (p, ~id) keys; the row's last workgroup sorts them in LDS
-//                  (counting sort by p bin, rank inside a bin) and walks the
-//                  exact cumulative to the cut-off and the draw;
+//                  of every candidate -> integer segment records at the
+//                  predicted binades + a mass histogram of e per workgroup;
+//   k_topp_walk    one workgroup per row walks the records (the exact
+//                  normaliser) while its spare waves merge the histograms
+//                  and pick the smallest set of top bins whose estimated
+//                  mass clears top_p with margin; in the same launch S
+//                  workgroups per row then gather the candidates of those
+//                  bins as (e, ~id) keys -- with p = e * (1/sum) a prefix of
+//                  the reference's sort order, so the gather does not wait
+//                  for the normaliser;
+//   k_topp_nucleus (one workgroup per row) keys to p, sorted in LDS
+//                  (counting sort by p bin, rank inside a bin), the exact
+//                  cumulative to the cut-off and the draw;
 //   k_topp_fallback rows whose selected set does not fit in LDS, or whose
 //                  cumulative does not reach top_p inside it: every
 //                  candidate sorted in a global scratch slot.
@@ -69,6 +72,11 @@ __device__ __forceinline__ uint64_t topp_key(float p, int id) {
   return ((uint64_t)__float_as_uint(p) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
 }
 __device__ __forceinline__ int key_id(uint64_t k) { return (int)(0xffffffffu - (uint32_t)k); }
+// A gathered (e, ~id) key as (p, ~id): p = e * (1 / sum), top_p.c:72-74.
+__device__ __forceinline__ uint64_t topp_pkey(uint64_t ekey, float inv) {
+  const float p = __uint_as_float((uint32_t)(ekey >> 32)) * inv;
+  return ((uint64_t)__float_as_uint(p) << 32) | (ekey & 0xffffffffull);
+}
 __device__ __forceinline__ float key_p(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
 
 struct ToppShared {
@@ -199,22 +207,26 @@ __device__ __forceinline__ bool topp_degenerate(uint32_t flags) {
   return (flags & (PZ_RS_Y0NAN | PZ_RS_NONFIN)) != 0;
 }
 
-// ---- pass 1: slice maxima (HBM) -------------------------------------------
+// ---- pass 1 (HBM): slice maxima -------------------------------------------
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_max(TOPP_ARGS) {
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_stat(TOPP_ARGS) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   const int row = pz_row_of(rows, blockIdx.y);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const PzSlice sl = pz_sp_slice(nseg, spw);
-  if (threadIdx.x == 0) SS.any = 0u;
+  if (threadIdx.x == 0) {
+    SS.any = 0u;
+    if (blockIdx.x == 0) ws.rs[row].i[5] = 0;  // the nucleus bins of this launch: not yet picked
+  }
   const PzRow<VEC> R =
       topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
   __syncthreads();
   pz_sp_stat_slice(R, row, sl, ws, SS, false);
 }
 
-// ---- pass 2: estimated mass of the candidates per segment -----------------
+// ---- pass 2 (L2): estimated mass of the candidates per segment, and each --
+// segment's maximum (the gather skips segments below its gate)
 template <bool VEC>
 __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_est(TOPP_ARGS) {
   extern __shared__ __align__(16) char lds[];
@@ -229,6 +241,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_est(TOPP_
       topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
   const float M = SS.M, thr = M - 20.0f;
   float* seg_s = ws.seg_s + (size_t)row * ws.nsc;
+  float* seg_m = ws.seg_m + (size_t)row * ws.nsc;
   for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
     float y[PZ_SP_U][4];
     int n[PZ_SP_U];
@@ -240,17 +253,62 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_est(TOPP_
       const int k = kb + u * PZ_SP_WAVES;
       if (k >= sl.k1) break;
       R.apply(k * PZ_SP_SEG + 4 * lane, n[u], y[u]);
-      float t = 0.0f;
+      float t = 0.0f, mx = -__builtin_inff();
 #pragma unroll
-      for (int c = 0; c < 4; c++)
+      for (int c = 0; c < 4; c++) {
         if (c < n[u] && y[u][c] >= thr) t += pz_fast_exp(y[u][c] - M);
+        if (c < n[u]) mx = fmaxf(mx, y[u][c]);  // NaN-free maximum (rows with NaN: fmaxf skips it)
+      }
       t = pz_wave_sum(t);
-      if (lane == 0) seg_s[k] = t;
+      mx = pz_wave_max(mx);
+      if (lane == 0) {
+        seg_s[k] = t;
+        seg_m[k] = mx;
+      }
     }
   }
 }
 
-// ---- pass 3: records of the exact candidate terms + mass histogram -------
+// Nucleus bins from the row's merged e histogram (one wave), given its
+// estimated total mass and count: the smallest set of top bins whose
+// estimated mass clears top_p by more than the histogram's resolution (a
+// bin's mass is known to within half its width, 0.55 %).  bsel 0 keeps every
+// candidate.  (Any choice gives the reference's result: the nucleus checks
+// that its cut-off lies inside the gathered set, else the fallback runs.)
+__device__ __forceinline__ void topp_select_bins(const pz_lds_u32b* ehist, float tot,
+                                                 uint32_t ncand, float top_p, int* bsel_out,
+                                                 uint32_t* nsel_out) {
+  const int lane = threadIdx.x & 63;
+  const float goal = (top_p * 1.012f + 3e-4f) * tot;
+  float carry = 0.0f;
+  uint32_t ccarry = 0;
+  int bsel = 0;
+  uint32_t nsel = ncand;
+  for (int b0 = PZ_TOPP_NB - 1; b0 >= 0; b0 -= 64) {
+    const int b = b0 - lane;
+    float m = 0.0f;
+    uint32_t c = 0;
+    if (b >= 0) {
+      c = ehist[b];
+      m = (float)c * ebin_mid(b);
+    }
+    const float incl = pz_wave_scan_f32(m);
+    const uint32_t cincl = pz_wave_scan_u32(c);
+    const uint64_t ball = __ballot(b >= 0 && carry + incl >= goal);
+    if (ball) {
+      const int L = (int)__builtin_ctzll(ball);
+      bsel = b0 - L;
+      nsel = ccarry + pz_readlane_u32(cincl, L);
+      break;
+    }
+    carry += pz_readlane_f32(incl, 63);
+    ccarry += pz_readlane_u32(cincl, 63);
+  }
+  *bsel_out = bsel;
+  *nsel_out = nsel;
+}
+
+// ---- pass 3 (L2): records of the exact candidate terms + mass histogram ---
 template <bool VEC>
 __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_ARGS, int pen_bytes) {
   extern __shared__ __align__(16) char lds[];
@@ -285,179 +343,57 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_
   for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) gh[i] = ehist[i];
 }
 
-// ---- pass 4 (one workgroup per row): exact normaliser and nucleus bins ----
+// Gather of one slice: candidates with e >= e_lo (1 - 2^-21) (a superset
+// gate on y - M first, 0.01 below the bin edge; each possible candidate's
+// exact e one per lane per trip), staged as (e, ~id) keys in LDS (lkeys,
+// capacity lcap; one LDS atomic per wave and trip) and appended to the row's
+// list with one global atomic per workgroup.  Any e below that bound has
+// fl(e * inv) < fl(e_lo * inv) (two roundings of 2^-24 cannot close a 2^-21
+// gap), so every candidate with p >= p_lo = fl(e_lo * inv) is gathered.
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walk(TOPP_ARGS, int pen_bytes, int nc) {
-  extern __shared__ __align__(16) char lds[];
-  __shared__ PzSpShared SS;
-  __shared__ ToppShared T;
-  __shared__ uint64_t etab[32];
-  const pz_lds_u64* et = (const pz_lds_u64*)etab;
-  pz_etab_fill((pz_lds_u64*)etab);
-  const int row = pz_row_of(rows, blockIdx.x);
-  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+__device__ __forceinline__ void topp_gather_slice(TOPP_ARGS, int row, int slice, int gspw,
+                                                  char* lds, pz_lds_u64* lkeys, int lcap,
+                                                  const pz_lds_u64* et, PzSpShared& SS) {
   pz_sp_row_stat(row, S, ws, SS);
-  const float M = SS.M;
-  const uint32_t flags = SS.any;
-  PzRowState& rs = ws.rs[row];
-  const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
-  __syncthreads();  // the expf table
-  if (flags & PZ_RS_Y0NAN) {
-    if (tid == 0) {
-      ids_out[row] = 0;
-      if (p_out) p_out[row] = 1.0f;
-      rs.i[0] = TP_DONE;
-    }
-    return;
-  }
-  if (flags & PZ_RS_NONFIN) {
-    if (tid == 0) T.first = INT_MAX;
-    __syncthreads();
-    int mine = INT_MAX;
-    for (int e0 = 4 * tid; e0 < V; e0 += 4 * PZ_SP_BLOCK) {
-      float y[4];
-      const int n = R.get(e0, y);
-      for (int c = 0; c < n; c++)
-        if (y[c] == M && e0 + c < mine) mine = e0 + c;
-    }
-    atomicMin(&T.first, mine);
-    __syncthreads();
-    if (tid == 0) {
-      ids_out[row] = T.first;
-      if (p_out) p_out[row] = __builtin_nanf("");
-      rs.i[0] = TP_DONE;
-    }
-    return;
-  }
-  pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
-  PzExpTerms<PzRow<VEC>> X;
-  X.R = R;
-  X.M = M;
-  X.thr = M - 20.0f;
-  X.inv = 1.0f;
-  X.as_p = false;
-  X.et = et;
-  const size_t walk_off = ((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15;
-  if (tid == 0) T.merged = 0;
-  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, lds + walk_off, SS);
-
-  if (w == 0) {
-    // the exact normaliser
-    PzAcc st;
-    pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
-    if (lane == 0) T.sum = pz_acc_value(st);
-  } else {
-    // meanwhile: merge the row's histograms (waves 1..15), then wave 1 picks
-    // the nucleus bins once every merging wave has signalled
-    for (int i = tid - 64; i < PZ_TOPP_NB; i += PZ_SP_BLOCK - 64) {
-      uint32_t c = 0;
-      for (int s2 = 0; s2 < S; s2++) c += ws.hist[((size_t)blockIdx.x * S + s2) * PZ_TOPP_NB + i];
-      ehist[i] = c;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    if (lane == 0) __hip_atomic_fetch_add(&T.merged, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    if (w == 1) {
-      while (__hip_atomic_load(&T.merged, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) <
-             PZ_SP_WAVES - 1)
-        __builtin_amdgcn_s_sleep(1);
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      float tot = 0.0f;
-      uint32_t ncand = 0;
-      for (int b = lane; b < PZ_TOPP_NB; b += 64) {
-        const uint32_t c = ehist[b];
-        tot += (float)c * ebin_mid(b);
-        ncand += c;
-      }
-      tot = pz_wave_sum(tot);
-      ncand = pz_wave_sum_u32(ncand);
-      // a bin's mass is known to within half its width (0.55 %): the
-      // selected set's estimate must clear top_p by more than that
-      const float goal = (prm.top_p * 1.012f + 3e-4f) * tot;
-      float carry = 0.0f;
-      uint32_t ccarry = 0;
-      int bsel = 0;
-      uint32_t nsel = ncand;
-      for (int b0 = PZ_TOPP_NB - 1; b0 >= 0; b0 -= 64) {
-        const int b = b0 - lane;
-        float m = 0.0f;
-        uint32_t c = 0;
-        if (b >= 0) {
-          c = ehist[b];
-          m = (float)c * ebin_mid(b);
-        }
-        const float incl = pz_wave_scan_f32(m);
-        const uint32_t cincl = pz_wave_scan_u32(c);
-        const uint64_t ball = __ballot(b >= 0 && carry + incl >= goal);
-        if (ball) {
-          const int L = (int)__builtin_ctzll(ball);
-          bsel = b0 - L;
-          nsel = ccarry + pz_readlane_u32(cincl, L);
-          break;
-        }
-        carry += pz_readlane_f32(incl, 63);
-        ccarry += pz_readlane_u32(cincl, 63);
-      }
-      if (lane == 0) {
-        T.bsel = bsel;
-        T.nsel = nsel;
-      }
-    }
+  if (topp_degenerate(SS.any)) return;
+  // the row's nucleus bins, picked by the walking workgroup of this launch
+  // (it has a lower block index, so it was dispatched first, and it waits on
+  // nothing here: the wait ends)
+  // (relaxed polls -- an acquire per poll would invalidate the L2 the walks
+  // read from -- then one acquire)
+  if (threadIdx.x == 0) {
+    while (__hip_atomic_load(&ws.rs[row].i[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+      __builtin_amdgcn_s_sleep(8);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  if (tid == 0) {
-    const float inv = 1.0f / T.sum;  // top_p.c:72
-    const bool all = T.bsel == 0;
-    const float e_lo = ebin_lo(T.bsel);
-    rs.M = M;
-    rs.sum = T.sum;
-    rs.inv = inv;
-    rs.f[0] = all ? 0.0f : e_lo * inv;
-    rs.f[1] = all ? -__builtin_inff() : __logf(e_lo) - 0.01f;
-    rs.i[0] = TP_OPEN;
-    rs.i[1] = all ? 1 : 0;
-    rs.i[2] = 0;
-    rs.i[3] = 0;
-    rs.i[4] = (int)T.nsel;
-    if (T.nsel > (uint32_t)ws.capg) {
-      // the selected set cannot fit: straight to the fallback
-      const int q = atomicAdd(&sc.counters[0], 1);
-      sc.fb_list[q] = row;
-      rs.i[0] = TP_DONE;
-    }
-  }
-}
-
-// ---- pass 5: gather the selected candidates; sort, cut-off and draw ------
-template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_gather(TOPP_ARGS) {
-  extern __shared__ __align__(16) char lds[];
-  __shared__ uint64_t etab[32];
-  const pz_lds_u64* et = (const pz_lds_u64*)etab;
-  pz_etab_fill((pz_lds_u64*)etab);
-  const int row = pz_row_of(rows, blockIdx.y);
   const PzRowState rs0 = ws.rs[row];
   if (rs0.i[0] == TP_DONE) return;
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const PzSlice sl = pz_sp_slice(nseg, spw);
-  const float M = rs0.M, thr = M - 20.0f, inv = rs0.inv;
-  const float p_thr = rs0.f[0], dgate = rs0.f[1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const PzSlice sl = pz_sp_slice_at(slice, nseg, gspw);
+  const float M = rs0.M, thr = M - 20.0f;
+  const float e_lo = rs0.f[0] * (1.0f - 0x1p-21f), dgate = rs0.f[1];
   PzRowState& rs = ws.rs[row];
   uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
-  {
-    const PzRow<VEC> R =
-        topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
-    __syncthreads();  // the expf table
-    // A cheap gate on y - M picks each lane's possible candidates (a
-    // superset: 0.01 below the bin edge); their exact p is evaluated one per
-    // lane per trip and the survivors appended with one atomic per wave.
-    for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+  const float* seg_m = ws.seg_m + (size_t)row * ws.nsc;
+  const PzRow<VEC> R =
+      topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
+  if (threadIdx.x == 0) {
+    SS.cnt = 0;
+    SS.flag = 0;
+  }
+  __syncthreads();  // the penalty tables, the staging count
+  for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
     float ys[PZ_SP_U][4];
     int ns[PZ_SP_U];
 #pragma unroll
-    for (int u = 0; u < PZ_SP_U; u++)
-      ns[u] = R.load((kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, ys[u]);
+    for (int u = 0; u < PZ_SP_U; u++) {
+      // a segment whose maximum is below the gate holds no candidate
+      const int k = kb + u * PZ_SP_WAVES;
+      ns[u] = k < sl.k1 && !(seg_m[k] - M < dgate)
+                  ? R.load(k * PZ_SP_SEG + 4 * lane, ys[u]) : 0;
+    }
 #pragma unroll
     for (int u = 0; u < PZ_SP_U; u++) {
       const int k = kb + u * PZ_SP_WAVES;
@@ -479,14 +415,189 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_gather(TO
           const uint32_t j = (uint32_t)__builtin_ctz(want);
           want &= want - 1u;
           const float yy = j == 0 ? y[0] : (j == 1 ? y[1] : (j == 2 ? y[2] : y[3]));
-          const float p = pz_expf_l(yy - M, et) * inv;
-          take = p >= p_thr;
-          key = topp_key(p, e0 + (int)j);
+          const float e = pz_expf_l(yy - M, et);
+          take = e >= e_lo;
+          key = topp_key(e, e0 + (int)j);
         }
-        append_key(&rs.i[2], &rs.i[3], gkeys, ws.capg, take, key);
+        const uint64_t ball = __ballot(take);
+        if (ball) {
+          const int leader = (int)__builtin_ctzll(ball);
+          int base = 0;
+          if (lane == leader) base = atomicAdd(&SS.cnt, __popcll(ball));
+          base = __builtin_amdgcn_readlane(base, leader);
+          if (take) {
+            const int slot = base + __popcll(ball & ((1ull << lane) - 1ull));
+            if (slot < lcap) lkeys[slot] = key;
+            else SS.flag = 1;
+          }
+        }
       }
     }
+  }
+  __syncthreads();
+  const int n = SS.cnt < lcap ? SS.cnt : lcap;
+  if (threadIdx.x == 0) {
+    SS.carry = __int_as_float(n > 0 ? atomicAdd(&rs.i[2], n) : 0);
+    if (SS.flag) rs.i[3] = 1;
+  }
+  __syncthreads();
+  const int base = __float_as_int(SS.carry);
+  bool over = false;
+  for (int i = threadIdx.x; i < n; i += PZ_SP_BLOCK) {
+    if (base + i < ws.capg) gkeys[base + i] = lkeys[i];
+    else over = true;
+  }
+  if (over) rs.i[3] = 1;
+}
+
+// ---- pass 4: the exact normaliser (one workgroup per row) beside the ------
+// gather (gS workgroups per row, slices of gspw segments), in one launch:
+// blocks [0, rows) walk, blocks [rows, rows + rows * gS) gather.  A gather
+// block waits only for its row's nucleus bins, which the walking block picks
+// early; the gather keys carry e, not p, so nothing waits for the
+// normaliser.  Each block takes a CU of its own (the walk's LDS), so gS is
+// sized for the gather to run in one round beside the walks.
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walk(TOPP_ARGS, int pen_bytes, int nc,
+                                                          int n_rows, int gS, int gspw,
+                                                          int goff, int lcap) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ int first_sh, merged_sh;
+  __shared__ float sum_sh, tot_sh;
+  __shared__ uint32_t ncand_sh;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  if ((int)blockIdx.x >= n_rows) {
+    const int g = (int)blockIdx.x - n_rows;
+    topp_gather_slice<VEC>(logits, ld, V, rows, params, n_params, hist, H, hcap, nseg, spw, S,
+                           ws, u, ids_out, p_out, sc, pz_row_of(rows, g / gS), g % gS, gspw,
+                           lds, (pz_lds_u64*)(lds + goff), lcap, et, SS);
+    return;
+  }
+  const int row = pz_row_of(rows, blockIdx.x);
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x;
+  pz_sp_row_stat(row, S, ws, SS);
+  const float M = SS.M;
+  const uint32_t flags = SS.any;
+  PzRowState& rs = ws.rs[row];
+  const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
+  __syncthreads();  // the expf table
+  if (flags & PZ_RS_Y0NAN) {
+    if (tid == 0) {
+      ids_out[row] = 0;
+      if (p_out) p_out[row] = 1.0f;
+      rs.i[0] = TP_DONE;
     }
+    return;
+  }
+  if (flags & PZ_RS_NONFIN) {
+    if (tid == 0) first_sh = INT_MAX;
+    __syncthreads();
+    int mine = INT_MAX;
+    for (int e0 = 4 * tid; e0 < V; e0 += 4 * PZ_SP_BLOCK) {
+      float y[4];
+      const int n = R.get(e0, y);
+      for (int c = 0; c < n; c++)
+        if (y[c] == M && e0 + c < mine) mine = e0 + c;
+    }
+    atomicMin(&first_sh, mine);
+    __syncthreads();
+    if (tid == 0) {
+      ids_out[row] = first_sh;
+      if (p_out) p_out[row] = __builtin_nanf("");
+      rs.i[0] = TP_DONE;
+    }
+    return;
+  }
+  PzExpTerms<PzRow<VEC>> X;
+  X.R = R;
+  X.M = M;
+  X.thr = M - 20.0f;
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = et;
+  pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
+  const size_t walk_off = ((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15;
+  const int w = tid >> 6;
+  if (tid == 0) {
+    merged_sh = 0;
+    tot_sh = 0.0f;
+    ncand_sh = 0u;
+  }
+  // waves 1..7 pre-evaluate the walk's specials while waves 8..15 merge the
+  // row's histograms and wave 8 picks the nucleus bins for this launch's
+  // gather
+  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, lds + walk_off, SS, 7);
+  if (w == 0) {
+    PzAcc st;
+    pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+    if (tid == 0) sum_sh = pz_acc_value(st);
+  } else if (w >= 8) {
+    // merged histogram (every load of a bin issued before its sum), with
+    // the estimated total mass and count on the side
+    const uint32_t* hrow = ws.hist + (size_t)blockIdx.x * S * PZ_TOPP_NB;
+    float tot = 0.0f;
+    uint32_t ncand = 0;
+    for (int i = tid - 512; i < PZ_TOPP_NB; i += PZ_SP_BLOCK - 512) {
+      uint32_t c = 0;
+      int s2 = 0;
+      for (; s2 + 4 <= S; s2 += 4) {
+        const uint32_t c0 = hrow[(size_t)s2 * PZ_TOPP_NB + i];
+        const uint32_t c1 = hrow[(size_t)(s2 + 1) * PZ_TOPP_NB + i];
+        const uint32_t c2 = hrow[(size_t)(s2 + 2) * PZ_TOPP_NB + i];
+        const uint32_t c3 = hrow[(size_t)(s2 + 3) * PZ_TOPP_NB + i];
+        c += (c0 + c1) + (c2 + c3);
+      }
+      for (; s2 < S; s2++) c += hrow[(size_t)s2 * PZ_TOPP_NB + i];
+      ehist[i] = c;
+      tot += (float)c * ebin_mid(i);
+      ncand += c;
+    }
+    tot = pz_wave_sum(tot);
+    ncand = pz_wave_sum_u32(ncand);
+    if ((tid & 63) == 0) {
+      atomicAdd(&tot_sh, tot);
+      atomicAdd(&ncand_sh, ncand);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((tid & 63) == 0)
+      __hip_atomic_fetch_add(&merged_sh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (w == 8) {
+      while (__hip_atomic_load(&merged_sh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8)
+        __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      int bsel;
+      uint32_t nsel;
+      topp_select_bins(ehist, tot_sh, ncand_sh, prm.top_p, &bsel, &nsel);
+      if (tid == 512) {
+        const bool all = bsel == 0;
+        const float e_lo = ebin_lo(bsel);
+        rs.M = M;
+        rs.f[0] = all ? 0.0f : e_lo;
+        rs.f[1] = all ? -__builtin_inff() : __logf(e_lo) - 0.01f;
+        rs.i[1] = all ? 1 : 0;
+        rs.i[2] = 0;
+        rs.i[3] = 0;
+        rs.i[4] = (int)nsel;
+        if (nsel > (uint32_t)ws.capg) {
+          // the selected set cannot fit: straight to the fallback
+          const int q = atomicAdd(&sc.counters[0], 1);
+          sc.fb_list[q] = row;
+          rs.i[0] = TP_DONE;
+        } else {
+          rs.i[0] = TP_OPEN;
+        }
+        __hip_atomic_store(&rs.i[5], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    rs.sum = sum_sh;
+    rs.inv = 1.0f / sum_sh;  // top_p.c:72
   }
 }
 
@@ -524,6 +635,12 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
   const int m = rs0.i[2];
   const bool all = rs0.i[1] != 0;
   const uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
+  const float inv = rs0.inv;
+  // Every candidate with p >= p_lo = fl(e_lo * inv) was gathered (p is
+  // monotone in e; the gather keeps a margin below e_lo), so the sorted list
+  // is the reference's order down to p_lo, and a cut-off whose last term
+  // lies at or above p_lo only ever saw reference terms (else: the fallback).
+  const float p_lo = rs0.f[0] * inv;
   bool done = false;
   if (rs0.i[3] == 0 && m <= cap && m > 0) {
     pz_lds_u64* bkeys = (pz_lds_u64*)lds;                          // [cap]
@@ -535,13 +652,13 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
       // small lists: bitonic sort of the keys, then the lane-ordered walks
       int N = 1;
       while (N < m) N <<= 1;
-      for (int i = tid; i < N; i += PZ_SP_BLOCK) bkeys[i] = i < m ? gkeys[i] : 0ull;
+      for (int i = tid; i < N; i += PZ_SP_BLOCK) bkeys[i] = i < m ? topp_pkey(gkeys[i], inv) : 0ull;
       __syncthreads();
       pz_bitonic_desc<PZ_SP_BLOCK>(bkeys, N);
       uint64_t* kk = reinterpret_cast<uint64_t*>(lds);
       float* cum = reinterpret_cast<float*>(region);
       const int cutoff = nucleus_cutoff(kk, cum, m, prm.top_p, all, &T.cutoff);
-      if (cutoff > 0) {
+      if (cutoff > 0 && (all || key_p(kk[cutoff - 1]) >= p_lo)) {
         if (tid == 0)
           nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
         done = true;
@@ -551,7 +668,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
       if (tid == 0) T.bmax = 0u;
       __syncthreads();
       for (int i = tid; i < m; i += PZ_SP_BLOCK)
-        atomicAdd((uint32_t*)&bcnt[pbin(gkeys[i])], 1u);
+        atomicAdd((uint32_t*)&bcnt[pbin(topp_pkey(gkeys[i], inv))], 1u);
       __syncthreads();
       // exclusive scan over the bins; thread t owns bins 4t .. 4t+3
       uint32_t c[4], local = 0, mx = 0;
@@ -582,7 +699,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
       const bool binned = T.bmax <= (uint32_t)TOPP_BIN_MAX;
       if (binned) {
         for (int i = tid; i < m; i += PZ_SP_BLOCK) {
-          const uint64_t key = gkeys[i];
+          const uint64_t key = topp_pkey(gkeys[i], inv);
           const uint32_t pos = atomicAdd((uint32_t*)&bcnt[pbin(key)], 1u);
           bkeys[pos] = key;
         }
@@ -659,6 +776,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
           const int hit = pz_sp_walk<PZ_STOP_GE>(st, W, prm.top_p, X);
           int cutoff = hit >= 0 && hit < m ? hit + 1 : -1;
           if (cutoff < 0 && all) cutoff = m;  // st then holds the whole sum
+          if (cutoff > 0 && !all && !(key_p(bkeys[perm[cutoff - 1]]) >= p_lo)) cutoff = -1;
           int pick = -1;
           if (cutoff > 0) {
             const float r = u[row] * pz_acc_value(st);  // trunc_sum: the cumulative at the cut-off
@@ -682,13 +800,13 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
         __syncthreads();
         int N = 1;
         while (N < m) N <<= 1;
-        for (int i = tid; i < N; i += PZ_SP_BLOCK) bkeys[i] = i < m ? gkeys[i] : 0ull;
+        for (int i = tid; i < N; i += PZ_SP_BLOCK) bkeys[i] = i < m ? topp_pkey(gkeys[i], inv) : 0ull;
         __syncthreads();
         pz_bitonic_desc<PZ_SP_BLOCK>(bkeys, N);
         uint64_t* kk = reinterpret_cast<uint64_t*>(lds);
         float* cum = reinterpret_cast<float*>(region);
         const int cutoff = nucleus_cutoff(kk, cum, m, prm.top_p, all, &T.cutoff);
-        if (cutoff > 0) {
+        if (cutoff > 0 && (all || key_p(kk[cutoff - 1]) >= p_lo)) {
           if (tid == 0)
             nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
           done = true;
@@ -797,42 +915,51 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   const size_t pen_slice = pen_region(L, pl.spw * PZ_SP_SEG), pen_full = pen_region(L, L.V);
   // slice passes: the slice's penalty tables (+ the histogram)
   const size_t lds1 = pen_slice;
-  const size_t lds3 = pen_slice + PZ_TOPP_NB * 4;
+  const size_t lds2 = pen_slice + PZ_TOPP_NB * 4;
   // walk: the row's penalty tables, the merged histogram, the walk's arrays
+  // (the gather blocks of the same launch use the first pen_slice bytes)
   const size_t walk_off = (pen_full + PZ_TOPP_NB * 4 + 15) & ~(size_t)15;
   if (walk_off + fixed >= (size_t)L.max_lds) return -2;
   const int nc = pz_sp_walk_nc(pl.nseg, (size_t)L.max_lds - walk_off - fixed);
   if (nc < 1) return -2;
-  const size_t lds4 = walk_off + pz_sp_walk_lds(pl.nseg, nc);
+  const size_t lds3 = walk_off + pz_sp_walk_lds(pl.nseg, nc);
   // nucleus: the largest list (and its walk) that fits
   int cap = TOPP_CAP_MAX < ws.capg ? TOPP_CAP_MAX : ws.capg;
   const int nc6 = 16;
   while (cap > 256 && topp_nucleus_bytes(cap, nc6) + fixed > (size_t)L.max_lds) cap >>= 1;
-  const size_t lds6 = topp_nucleus_bytes(cap, nc6);
-  if (lds6 + fixed > (size_t)L.max_lds || pen_full + fixed > (size_t)L.max_lds) return -2;
-  auto k1 = k_topp_max<VEC>;
-  auto k2 = k_topp_est<VEC>;
-  auto k3 = k_topp_rec<VEC>;
-  auto k4 = k_topp_walk<VEC>;
-  auto k5 = k_topp_gather<VEC>;
-  auto k6 = k_topp_nucleus<VEC>;
+  const size_t lds4 = topp_nucleus_bytes(cap, nc6);
+  if (lds4 + fixed > (size_t)L.max_lds || pen_full + fixed > (size_t)L.max_lds) return -2;
+  auto k1 = k_topp_stat<VEC>;
+  auto k1e = k_topp_est<VEC>;
+  auto k2 = k_topp_rec<VEC>;
+  auto k3 = k_topp_walk<VEC>;
+  auto k4 = k_topp_nucleus<VEC>;
   auto fb = k_topp_fallback<VEC>;
-  const void* fns[7] = {(const void*)k1, (const void*)k2, (const void*)k3, (const void*)k4,
-                        (const void*)k5, (const void*)k6, (const void*)fb};
-  const size_t need[7] = {lds1, lds1, lds3, lds4, lds1, lds6, pen_full};
-  for (int i = 0; i < 7; i++)
+  const void* fns[6] = {(const void*)k1, (const void*)k1e, (const void*)k2, (const void*)k3,
+                        (const void*)k4, (const void*)fb};
+  const size_t need[6] = {lds1, lds1, lds2, lds3, lds4, pen_full};
+  for (int i = 0; i < 6; i++)
     if (need[i] > 65536 && hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)need[i]) != hipSuccess)
       return -1;
   const dim3 grid(pl.S, n_rows), block(PZ_SP_BLOCK);
+  // gather blocks per row: the CUs the walks leave free, in one round
+  const int cus = PZ_SP_TARGET_WG / 2;
+  int gS = n_rows < cus ? (cus - n_rows) / n_rows : 1;
+  gS = gS < 1 ? 1 : (gS > pl.S ? pl.S : gS);
+  const int gspw = (pl.nseg + gS - 1) / gS;
+  // a gather block's LDS: its slice's penalty tables, then staged keys
+  const size_t goff = (pen_region(L, gspw * PZ_SP_SEG) + 15) & ~(size_t)15;
+  int lcap = (int)((lds3 - goff) / 8);
+  lcap = lcap < ws.capg ? lcap : ws.capg;
 #define TOPP_PASS L.logits, L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, \
                   pl.nseg, pl.spw, pl.S, ws, L.u, L.ids, L.p_out, L.sc
   hipLaunchKernelGGL(k1, grid, block, lds1, L.stream, TOPP_PASS);
-  hipLaunchKernelGGL(k2, grid, block, lds1, L.stream, TOPP_PASS);
-  hipLaunchKernelGGL(k3, grid, block, lds3, L.stream, TOPP_PASS, (int)pen_slice);
-  hipLaunchKernelGGL(k4, dim3(n_rows), block, lds4, L.stream, TOPP_PASS, (int)pen_full, nc);
-  hipLaunchKernelGGL(k5, grid, block, lds1, L.stream, TOPP_PASS);
-  hipLaunchKernelGGL(k6, dim3(n_rows), block, lds6, L.stream, TOPP_PASS, cap, nc6);
+  hipLaunchKernelGGL(k1e, grid, block, lds1, L.stream, TOPP_PASS);
+  hipLaunchKernelGGL(k2, grid, block, lds2, L.stream, TOPP_PASS, (int)pen_slice);
+  hipLaunchKernelGGL(k3, dim3(n_rows * (1 + gS)), block, lds3, L.stream, TOPP_PASS,
+                     (int)pen_full, nc, n_rows, gS, gspw, (int)goff, lcap);
+  hipLaunchKernelGGL(k4, dim3(n_rows), block, lds4, L.stream, TOPP_PASS, cap, nc6);
 #undef TOPP_PASS
   const int fb_grid = n_rows < L.sc.fb_slots ? n_rows : L.sc.fb_slots;
   hipLaunchKernelGGL(fb, dim3(fb_grid), dim3(PZ_RB), pen_full, L.stream, L.logits, L.ld, L.V,
