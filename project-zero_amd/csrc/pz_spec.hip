@@ -172,8 +172,11 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_rec(SpecA
 }
 
 // ---- one workgroup per row: the exact normaliser -----------------------------
+// 512 threads: one wave walks, the others stage and pre-evaluate, and two
+// workgroups share a CU with room for the walk's registers.
+constexpr int SPEC_WALK_BLOCK = 512;
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_walk(SpecArgs A) {
+__global__ __launch_bounds__(SPEC_WALK_BLOCK) void k_spec_walk(SpecArgs A) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
@@ -402,13 +405,15 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vwalk(SpecArgs A) {
     const PzWalk W = pz_sp_walk_setup(X, r, A.nseg, A.nc, A.ws, lds, SS);
     if (threadIdx.x < 64) {
       PzAcc st;
-      pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+      PzWalkCk ck;
+      pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X, &ck);
       const float Z = pz_acc_value(st);
       int hit = -1;
       if (Z > 0.0f) {
-        // the same sequence of adds: the CDF of r, stop at ur * Z < cdf
+        // the same sequence of adds: the CDF of r, stop at ur * Z < cdf,
+        // resumed from the last state of the first walk below the stop
         PzAcc s2;
-        hit = pz_sp_walk<PZ_STOP_GT>(s2, W, ur * Z, X);
+        hit = pz_sp_walk<PZ_STOP_GT>(s2, W, ur * Z, X, nullptr, &ck);
         if (hit >= A.V) hit = -1;
       }
       if (threadIdx.x == 0) {
@@ -481,7 +486,7 @@ int launch_spec(pz_sampler* s, SpecArgs& A) {
   A.S = pl.S;
   hipLaunchKernelGGL(k_spec_stat<VEC>, dim3(pl.S, A.NR), block, 0, s->stream, A);
   hipLaunchKernelGGL(k_spec_rec<VEC>, dim3(pl.S, A.NR), block, 0, s->stream, A);
-  hipLaunchKernelGGL(kw, dim3(A.NR), block, walk, s->stream, A);
+  hipLaunchKernelGGL(kw, dim3(A.NR), dim3(SPEC_WALK_BLOCK), walk, s->stream, A);
   hipLaunchKernelGGL(k_spec_accept<VEC>, dim3(A.B), dim3(64), 0, s->stream, A);
   A.spw = pv.spw;
   A.S = pv.S;

@@ -679,9 +679,11 @@ __device__ __forceinline__ void pz_sp_prep(const float (&v)[4], uint32_t g0, uin
 template <class X>
 __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg, int nc,
                                                    const PzSplitWs& ws, char* lds,
-                                                   PzSpShared& S,
-                                                   int n_producers = PZ_SP_WAVES - 1) {
+                                                   PzSpShared& S, int n_producers = -1) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // any multiple of 64 threads up to 1024
+  const int nt = (int)blockDim.x, nw = nt >> 6;
+  if (n_producers < 0) n_producers = nw - 1;
   PzWalk W;
   W.nseg = nseg;
   W.nc = nc;
@@ -715,7 +717,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   uint32_t base = 0;  // prefix carried over the chunks (thread-uniform)
   int sbase = 0;      // specials found in earlier chunks
   uint32_t cbase = 0; // grid changes in earlier chunks
-  for (int c0 = 0; c0 < nseg; c0 += PZ_SP_BLOCK) {
+  for (int c0 = 0; c0 < nseg; c0 += nt) {
     const int k = c0 + tid;
     uint32_t d = 0, gf = PZ_NO_RECORD, gfp = PZ_NO_RECORD;
     if (k < nseg) {
@@ -749,7 +751,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     }
     uint32_t tot = 0, ctot = 0;
     int stot = 0;
-    for (int i = 0; i < PZ_SP_WAVES; i++) {
+    for (int i = 0; i < nw; i++) {
       tot += (uint32_t)S.list[i];
       stot += __float_as_int(S.red[i]);
       ctot += S.red2[i];
@@ -773,7 +775,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   }
   __syncthreads();
   // the list of pre-evaluated segments
-  for (int k = tid; k < nseg; k += PZ_SP_BLOCK) {
+  for (int k = tid; k < nseg; k += nt) {
     const int s = W.slot[k];
     if (s >= 0) S.list[s] = k;
   }
@@ -1245,6 +1247,14 @@ __device__ __forceinline__ int pz_sp_walk_range(PzAcc& st, const PzWalk& W, floa
   return -1;
 }
 
+// States of a walk after each listed special (lane j: after special j), so
+// a later walk over the same terms with a higher stop can resume from the
+// last one below its stop instead of from state 0.
+struct PzWalkCk {
+  uint32_t n = 0, g = 0;  // per lane
+  int cnt = 0;            // specials recorded
+};
+
 // The walk (one wave): the exact sequential sum of the row's terms in id
 // order, from state 0.  With a stop mode returns the element index of the
 // first hit (st = the sum including it), else -1 (st = the whole sum).  X
@@ -1257,8 +1267,16 @@ __device__ __forceinline__ int pz_sp_walk_range(PzAcc& st, const PzWalk& W, floa
 // The runs' and the specials' scalars sit in the wave's lanes (lane j: run
 // and special j), and each special's pre-evaluated data loads while the one
 // before is processed, so a step waits on no LDS read.
+//
+// With rec, the state after each listed special is recorded there; with
+// from (a record of an earlier walk over the same terms whose sums never
+// met this walk's stop before the point it resumes from), the walk starts at
+// the last recorded state that does not meet the stop -- the sums only grow,
+// so no hit lies before it.
 template <int MODE, class X>
-__device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr, const X& x) {
+__device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr, const X& x,
+                                          PzWalkCk* rec = nullptr,
+                                          const PzWalkCk* from = nullptr) {
   const int lane = threadIdx.x & 63;
   st.n = 0;
   st.g = 1;
@@ -1276,8 +1294,21 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
   }
   PzSpSeg nxt;
   bool have = false;  // nxt holds slot j
-  int k = 0;
-  for (int j = 0;; j++) {
+  int k = 0, j0 = 0;
+  if (from && from->cnt > 0) {
+    const bool hit = lane < from->cnt &&
+                     (MODE == PZ_STOP_NONE ||
+                      pz_stop_hit(pz_acc_value_ng(from->n, from->g), thr, MODE));
+    const uint64_t hb = __ballot(hit);
+    const int h = hb ? (int)__builtin_ctzll(hb) : from->cnt;  // first record at or past the stop
+    if (h > 0) {
+      st.n = pz_readlane_u32(from->n, h - 1);
+      st.g = pz_readlane_u32(from->g, h - 1);
+      k = __builtin_amdgcn_readlane(mk, h - 1) + 1;
+      j0 = h;
+    }
+  }
+  for (int j = j0;; j++) {
     const int b = __builtin_amdgcn_readlane(mk, j);
     PzSpSeg cur = nxt;
     if (j < np && !have) pz_sp_load_slot(W, j, cur);
@@ -1313,6 +1344,11 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
       }
     }
     k = b + 1;
+    if (rec) {
+      rec->n = lane == j ? st.n : rec->n;
+      rec->g = lane == j ? st.g : rec->g;
+      rec->cnt = j + 1;
+    }
   }
   // past the listed specials (more specials than slots): record by record
   return k < W.nseg ? pz_sp_walk_range<MODE>(st, W, thr, x, k, W.nseg) : -1;

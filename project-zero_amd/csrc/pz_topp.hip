@@ -773,7 +773,8 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
         const PzWalk W = pz_sp_walk_setup(X, row, nsl, nc, ws, region, SS);
         if (w == 0) {
           PzAcc st;
-          const int hit = pz_sp_walk<PZ_STOP_GE>(st, W, prm.top_p, X);
+          PzWalkCk ck;
+          const int hit = pz_sp_walk<PZ_STOP_GE>(st, W, prm.top_p, X, &ck);
           int cutoff = hit >= 0 && hit < m ? hit + 1 : -1;
           if (cutoff < 0 && all) cutoff = m;  // st then holds the whole sum
           if (cutoff > 0 && !all && !(key_p(bkeys[perm[cutoff - 1]]) >= p_lo)) cutoff = -1;
@@ -781,7 +782,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
           if (cutoff > 0) {
             const float r = u[row] * pz_acc_value(st);  // trunc_sum: the cumulative at the cut-off
             PzAcc s2;
-            const int d = pz_sp_walk<PZ_STOP_GT>(s2, W, r, X);
+            const int d = pz_sp_walk<PZ_STOP_GT>(s2, W, r, X, nullptr, &ck);
             pick = d >= 0 && d < cutoff ? d : 0;
           }
           if (lane == 0) T.cutoff = pick;
