@@ -456,7 +456,10 @@ struct PzWalk {
   pz_lds_u32* pd;     // [nseg + 1] exclusive prefix of d (mod 2^32)
   pz_lds_u32* chp;    // [nseg + 1] exclusive prefix count of grid changes between
                       //            neighbouring clean segments
-  pz_lds_i32* slot;   // [nseg] pre-evaluated slot, or -1
+  pz_lds_i32* spk;    // [nseg] the special segments in id order
+  // Ring of nc pre-evaluated specials: special j sits in slot j % nc once
+  // rdy[slot] == j + 1; a producer rewrites a slot only after the walker has
+  // consumed the special before (consumed > j - nc).
   pz_lds_f32* terms;  // [nc][256] exact terms
   pz_lds_u32* pa;     // [nc][256] inclusive increment prefix at the slot's grid g0
   pz_lds_u32* pb;     // [nc][256] the same at g1 (the grid the segment is expected to end in)
@@ -467,30 +470,24 @@ struct PzWalk {
   pz_lds_u32* sinfo;  // [nc] g1 | first tie at g0 << 8 | (last flagged at g1 + 1) << 17
   pz_lds_u32* spt1;   // [nc] pa at the first tie
   pz_lds_u32* stc;    // [nc] parity corrections of the later ties at g0
-  pz_lds_u32* rdy;    // [nc] slot written (set by the wave that pre-evaluates it)
-  // The run of clean segments before listed special j (j < n_pre), and the
-  // tail run after the last one (j = n_pre): its end (the special's segment,
-  // or where the tail stops), the sum of its records and their common grid
-  // (0: not one grid).
-  pz_lds_i32* rk;     // [nc + 1]
-  pz_lds_u32* rD;     // [nc + 1]
-  pz_lds_u32* rG;     // [nc + 1]
+  pz_lds_u32* rdy;    // [nc] special + 1 held by the slot (0: none yet)
+  pz_lds_u32* consumed;  // specials the walker has read out of the ring
   pz_lds_f32* tmp;    // [256] terms of a segment evaluated during the walk
-  int nseg, nc, n_pre;
+  int nseg, nc, n_spec;
 };
 
-// LDS of the walk for a row of nseg segments with nc pre-evaluated special
-// segments: seven words per segment plus the prefixes' extra words and 1 KB
-// of staging; per special segment its terms, two increment prefixes, two
-// flag masks, five scalars and its run's three words.
+// LDS of the walk for a row of nseg segments with a ring of nc pre-evaluated
+// specials: six words per segment plus the prefixes' extra words, the ring's
+// counter and 1 KB of staging; per slot its terms, two increment prefixes,
+// two flag masks and five scalars.
 __host__ __device__ inline size_t pz_sp_walk_lds(int nseg, int nc) {
-  return (size_t)nseg * 28 + 48 + PZ_SP_SEG * 4 + (size_t)nc * (3 * PZ_SP_SEG * 4 + 2 * 64 + 20 + 12);
+  return (size_t)nseg * 24 + 64 + PZ_SP_SEG * 4 + (size_t)nc * (3 * PZ_SP_SEG * 4 + 2 * 64 + 20);
 }
 
-// Special segments the walk can pre-evaluate within max_lds bytes (0 if the
-// records alone do not fit).
+// Ring slots of the walk within max_lds bytes (0 when fewer than two fit:
+// the ring's hand-over needs two).
 inline int pz_sp_walk_nc(int nseg, size_t max_lds) {
-  for (int nc = PZ_SP_NC; nc >= 1; nc--)
+  for (int nc = PZ_SP_NC; nc >= 2; nc--)
     if (pz_sp_walk_lds(nseg, nc) <= max_lds) return nc;
   return 0;
 }
@@ -670,18 +667,19 @@ __device__ __forceinline__ void pz_sp_prep(const float (&v)[4], uint32_t g0, uin
   inf.tc = pz_wave_sum_u32(corr);
 }
 
-// Stages the row's records in LDS and pre-evaluates up to nc special
-// segments (dirty, crossing, or without a record) in id order: exact terms
-// (X::seg) and increment prefixes and flags at the record's grid and the
-// next.  Every thread calls it; it returns without a final barrier: the
-// walker (wave 0) waits per slot (pz_sp_load_slot), the other waves may go
-// on to other work.
+// Stages the row's records in LDS, lists every special segment (dirty,
+// crossing, or without a record) in id order, and starts the pre-evaluation
+// of the specials into the ring: exact terms (X::seg) and increment
+// prefixes and flags at the record's grid and the grid the segment is
+// expected to end in.  Every thread calls it; it returns without a final
+// barrier: waves 1 .. n_producers keep filling the ring while the walker
+// (wave 0) consumes it (pz_sp_load_slot), the other waves may go on to other
+// work.  Any block size that is a multiple of 64, up to 1024.
 template <class X>
 __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg, int nc,
                                                    const PzSplitWs& ws, char* lds,
                                                    PzSpShared& S, int n_producers = -1) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // any multiple of 64 threads up to 1024
   const int nt = (int)blockDim.x, nw = nt >> 6;
   if (n_producers < 0) n_producers = nw - 1;
   PzWalk W;
@@ -698,20 +696,17 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   W.spt1 = (pz_lds_u32*)p;     p += (size_t)nc * 4;
   W.stc = (pz_lds_u32*)p;      p += (size_t)nc * 4;
   W.rdy = (pz_lds_u32*)p;      p += (size_t)nc * 4;
-  W.rk = (pz_lds_i32*)p;       p += (size_t)(nc + 1) * 4;
-  W.rD = (pz_lds_u32*)p;       p += (size_t)(nc + 1) * 4;
-  W.rG = (pz_lds_u32*)p;       p += (size_t)(nc + 1) * 4;
+  W.consumed = (pz_lds_u32*)p; p += 16;
   W.tmp = (pz_lds_f32*)p;      p += PZ_SP_SEG * 4;
   W.d = (pz_lds_u32*)p;        p += (size_t)nseg * 4;
   W.d2 = (pz_lds_u32*)p;       p += (size_t)nseg * 4;
   W.gf = (pz_lds_u32*)p;       p += (size_t)nseg * 4;
   W.pd = (pz_lds_u32*)p;       p += (size_t)(nseg + 1) * 4;
   W.chp = (pz_lds_u32*)p;      p += (size_t)(nseg + 1) * 4;
-  W.slot = (pz_lds_i32*)p;
+  W.spk = (pz_lds_i32*)p;
   const uint32_t* rd = pz_sp_rec_d(ws, row);
   const uint32_t* rd2 = pz_sp_rec_d2(ws, row);
   const uint32_t* rgf = pz_sp_rec_gf(ws, row);
-  if (tid == 0) S.tail_end = nseg;
   // records, their prefix, the grid changes between clean neighbours, and
   // the special segments in id order
   uint32_t base = 0;  // prefix carried over the chunks (thread-uniform)
@@ -736,7 +731,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     const uint64_t sb = __ballot(special);
     const uint64_t cb = __ballot(chg);
     __syncthreads();
-    if (lane == 63) S.list[w] = (int)incl;  // wave totals (list[] is free until the end)
+    if (lane == 63) S.list[w] = (int)incl;  // wave totals
     if (lane == 0) {
       S.red[w] = __int_as_float(__popcll(sb));
       S.red2[w] = (uint32_t)__popcll(cb);
@@ -760,9 +755,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     if (k < nseg) {
       W.pd[k] = off + incl - d;
       W.chp[k] = coff + (uint32_t)__popcll(cb & below);
-      const int rank = soff + __popcll(sb & below);
-      W.slot[k] = special && rank < nc ? rank : -1;
-      if (special && rank == nc) S.tail_end = k;  // the first special past the listed ones
+      if (special) W.spk[soff + __popcll(sb & below)] = k;
     }
     base += tot;
     sbase += stot;
@@ -772,40 +765,23 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   if (tid == 0) {
     W.pd[nseg] = base;
     W.chp[nseg] = cbase;
+    *W.consumed = 0u;
   }
+  if (tid < nc) W.rdy[tid] = 0u;
+  W.n_spec = sbase;
   __syncthreads();
-  // the list of pre-evaluated segments
-  for (int k = tid; k < nseg; k += nt) {
-    const int s = W.slot[k];
-    if (s >= 0) S.list[s] = k;
-  }
-  if (tid == 0) S.cnt = sbase < nc ? sbase : nc;
-  __syncthreads();
-  const int n_pre = S.cnt;
-  W.n_pre = n_pre;
-  // the clean runs between the listed specials (every segment of a run is
-  // clean: the listed specials are all the specials up to the last one)
-  if (tid <= n_pre) {
-    const int a = tid == 0 ? 0 : S.list[tid - 1] + 1;
-    const int b = tid < n_pre ? S.list[tid] : S.tail_end;
-    uint32_t D = 0, G = 0;
-    if (b > a) {
-      D = W.pd[b] - W.pd[a];
-      const bool one_grid = b == a + 1 || W.chp[b] == W.chp[a + 1];
-      G = one_grid ? (W.gf[a] & 0xffu) : 0u;
-    }
-    W.rk[tid] = b;
-    W.rD[tid] = D;
-    W.rG[tid] = G;
-    if (tid < n_pre) W.rdy[tid] = 0u;
-  }
-  __syncthreads();
-  // Waves 1 .. n_producers pre-evaluate the listed specials in id order,
-  // each slot flagged when written, while wave 0 (the walker) starts at once
-  // and waits only at a slot that is not ready yet.  The producers wait on
-  // nothing, so every such wait ends.
-  for (int j = w - 1; w > 0 && w <= n_producers && j < n_pre; j += n_producers) {
-    const int k = S.list[j];
+  // Waves 1 .. n_producers pre-evaluate the specials in id order into the
+  // ring, while wave 0 (the walker) starts at once.  The walker waits only
+  // for the special it needs next; the producer of that special handles its
+  // specials in increasing order and waits only until special j - nc is
+  // consumed, which it is by then -- so every wait ends.
+  for (int j = w - 1; w > 0 && w <= n_producers && j < sbase; j += n_producers) {
+    if (j >= nc)
+      while (__hip_atomic_load((uint32_t*)W.consumed, __ATOMIC_ACQUIRE,
+                               __HIP_MEMORY_SCOPE_WORKGROUP) <= (uint32_t)(j - nc))
+        __builtin_amdgcn_s_sleep(1);
+    const int k = W.spk[j];
+    const int sl = j % nc;
     float v[4];
     x.seg(k, v);
     const uint32_t gf = W.gf[k];
@@ -824,23 +800,24 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     q.y = v[1];
     q.z = v[2];
     q.w = v[3];
-    ((pz_lds_f4*)(W.terms + j * PZ_SP_SEG))[lane] = q;
+    ((pz_lds_f4*)(W.terms + sl * PZ_SP_SEG))[lane] = q;
     pz_u4 a4, b4;
     a4.x = d.P[0]; a4.y = d.P[1]; a4.z = d.P[2]; a4.w = d.P[3];
     b4.x = d.Q[0]; b4.y = d.Q[1]; b4.z = d.Q[2]; b4.w = d.Q[3];
-    ((pz_lds_u4*)(W.pa + j * PZ_SP_SEG))[lane] = a4;
-    ((pz_lds_u4*)(W.pb + j * PZ_SP_SEG))[lane] = b4;
-    W.fa[j * 64 + lane] = (uint8_t)d.fa;
-    W.fb[j * 64 + lane] = (uint8_t)d.fb;
+    ((pz_lds_u4*)(W.pa + sl * PZ_SP_SEG))[lane] = a4;
+    ((pz_lds_u4*)(W.pb + sl * PZ_SP_SEG))[lane] = b4;
+    W.fa[sl * 64 + lane] = (uint8_t)d.fa;
+    W.fb[sl * 64 + lane] = (uint8_t)d.fb;
     if (lane == 0) {
-      W.g0[j] = (int)g;
-      W.sinfo[j] = inf.sinfo;
-      W.spt1[j] = inf.pt1;
-      W.stc[j] = inf.tc;
+      W.g0[sl] = (int)g;
+      W.sinfo[sl] = inf.sinfo;
+      W.spt1[sl] = inf.pt1;
+      W.stc[sl] = inf.tc;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0)
-      __hip_atomic_store((uint32_t*)&W.rdy[j], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store((uint32_t*)&W.rdy[sl], (uint32_t)(j + 1), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   return W;
 }
@@ -1154,15 +1131,18 @@ __device__ __forceinline__ bool pz_sp_fast_pre(PzAcc& st, const PzSpSeg& d, uint
   return true;
 }
 
-// Whether slot s has been written (acquire).
-__device__ __forceinline__ bool pz_sp_slot_ready(const PzWalk& W, int s) {
-  return __hip_atomic_load((uint32_t*)&W.rdy[s], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != 0u;
+// Whether special j is in the ring (acquire).
+__device__ __forceinline__ bool pz_sp_slot_ready(const PzWalk& W, int j) {
+  return __hip_atomic_load((uint32_t*)&W.rdy[j % W.nc], __ATOMIC_ACQUIRE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP) == (uint32_t)(j + 1);
 }
 
-// The pre-evaluated data of slot s (one round of LDS reads), once written.
-__device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int s, PzSpSeg& d) {
+// The pre-evaluated data of special j (one round of LDS reads), once in the
+// ring.
+__device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int j, PzSpSeg& d) {
   const int lane = threadIdx.x & 63;
-  while (!pz_sp_slot_ready(W, s)) __builtin_amdgcn_s_sleep(1);
+  while (!pz_sp_slot_ready(W, j)) __builtin_amdgcn_s_sleep(1);
+  const int s = j % W.nc;
   d.g0 = (uint32_t)W.g0[s];
   d.sinfo = W.sinfo[s];
   d.pt1 = W.spt1[s];
@@ -1175,6 +1155,39 @@ __device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int s, PzSpSeg&
   d.v[0] = q.x; d.v[1] = q.y; d.v[2] = q.z; d.v[3] = q.w;
   d.P[0] = a4.x; d.P[1] = a4.y; d.P[2] = a4.z; d.P[3] = a4.w;
   d.Q[0] = b4.x; d.Q[1] = b4.y; d.Q[2] = b4.z; d.Q[3] = b4.w;
+}
+
+// Lane i of the walker: the clean run before special j0 + i (its end, the
+// sum of its records, their common grid or 0) and the special's own record
+// (grid and flags, the increment at the grid below); the run after the last
+// special ends at nseg.
+struct PzRunLanes {
+  int k;
+  uint32_t D, G, gf, d2;
+};
+__device__ __forceinline__ PzRunLanes pz_sp_run_lanes(const PzWalk& W, int j0) {
+  const int j = j0 + (int)(threadIdx.x & 63);
+  PzRunLanes r;
+  r.k = 0;
+  r.D = 0;
+  r.G = 0;
+  r.gf = PZ_NO_RECORD;
+  r.d2 = 0;
+  if (j <= W.n_spec) {
+    const int a = j == 0 ? 0 : W.spk[j - 1] + 1;
+    const int b = j < W.n_spec ? W.spk[j] : W.nseg;
+    r.k = b;
+    if (b > a) {
+      r.D = W.pd[b] - W.pd[a];
+      const bool one_grid = b == a + 1 || W.chp[b] == W.chp[a + 1];
+      r.G = one_grid ? (W.gf[a] & 0xffu) : 0u;
+    }
+    if (j < W.n_spec) {
+      r.gf = W.gf[b];
+      r.d2 = W.d2[b];
+    }
+  }
+  return r;
 }
 
 // The record at the grid below (HAS2) when the state sits there: gf, d2 of
@@ -1280,20 +1293,7 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
   const int lane = threadIdx.x & 63;
   st.n = 0;
   st.g = 1;
-  const int np = W.n_pre;
-  int mk = 0;
-  uint32_t mD = 0, mG = 0, mgf = PZ_NO_RECORD, md2 = 0;
-  if (lane <= np) {
-    mk = W.rk[lane];
-    mD = W.rD[lane];
-    mG = W.rG[lane];
-  }
-  if (lane < np) {
-    mgf = W.gf[mk];
-    md2 = W.d2[mk];
-  }
-  PzSpSeg nxt;
-  bool have = false;  // nxt holds slot j
+  const int np = W.n_spec;
   int k = 0, j0 = 0;
   if (from && from->cnt > 0) {
     const bool hit = lane < from->cnt &&
@@ -1304,19 +1304,38 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
     if (h > 0) {
       st.n = pz_readlane_u32(from->n, h - 1);
       st.g = pz_readlane_u32(from->g, h - 1);
-      k = __builtin_amdgcn_readlane(mk, h - 1) + 1;
+      k = W.spk[h - 1] + 1;
       j0 = h;
     }
   }
+  int base = j0 & ~63;  // specials of the lanes
+  PzRunLanes m = pz_sp_run_lanes(W, base);
+  PzSpSeg nxt;
+  bool have = false;  // nxt holds special j
   for (int j = j0;; j++) {
-    const int b = __builtin_amdgcn_readlane(mk, j);
+    if (j - base == 64) {
+      base = j;
+      m = pz_sp_run_lanes(W, base);
+    }
+    const int jl = j - base;
+    const int b = __builtin_amdgcn_readlane(m.k, jl);
     PzSpSeg cur = nxt;
     if (j < np && !have) pz_sp_load_slot(W, j, cur);
-    // the next slot's loads overlap this step when it is already written
+    // the next special's loads overlap this step when it is already in the
+    // ring; the slots of the specials before j are released to the
+    // producers once their reads are done (special j's slot stays: the
+    // serial path reads its terms there).  The producer of special j + 1
+    // needs consumed > j + 1 - nc, which holds with nc >= 2.
     have = j + 1 < np && pz_sp_slot_ready(W, j + 1);
     if (have) pz_sp_load_slot(W, j + 1, nxt);
+    if (j < np) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0)
+        __hip_atomic_store((uint32_t*)W.consumed, (uint32_t)j, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     if (k < b) {
-      const uint32_t D = pz_readlane_u32(mD, j), G = pz_readlane_u32(mG, j);
+      const uint32_t D = pz_readlane_u32(m.D, jl), G = pz_readlane_u32(m.G, jl);
       if (G == st.g && D < (1u << 24) - st.n &&
           !(MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value_ng(st.n + D, st.g), thr, MODE))) {
         st.n += D;
@@ -1328,8 +1347,8 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
     }
     k = b;
     if (j >= np) break;
-    // special b (slot j)
-    if (!pz_sp_has2<MODE>(st, pz_readlane_u32(mgf, j), pz_readlane_u32(md2, j), thr)) {
+    // special b
+    if (!pz_sp_has2<MODE>(st, pz_readlane_u32(m.gf, jl), pz_readlane_u32(m.d2, jl), thr)) {
       const uint32_t g0 = cur.g0, si = cur.sinfo;
       if (!(st.g == g0 && pz_sp_fast_pre<MODE>(st, cur, si, cur.pt1, cur.tc, thr))) {
         uint32_t P[4], Q[4];
@@ -1339,19 +1358,18 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
           Q[c] = cur.Q[c];
         }
         const int r = pz_sp_events<MODE>(st, cur.v, g0, P, cur.fa & 15u, si & 0xffu, Q,
-                                         cur.fb & 15u, thr, W.terms + j * PZ_SP_SEG);
+                                         cur.fb & 15u, thr, W.terms + (j % W.nc) * PZ_SP_SEG);
         if (r >= 0) return b * PZ_SP_SEG + r;
       }
     }
     k = b + 1;
-    if (rec) {
+    if (rec && j < 64) {
       rec->n = lane == j ? st.n : rec->n;
       rec->g = lane == j ? st.g : rec->g;
       rec->cnt = j + 1;
     }
   }
-  // past the listed specials (more specials than slots): record by record
-  return k < W.nseg ? pz_sp_walk_range<MODE>(st, W, thr, x, k, W.nseg) : -1;
+  return -1;
 }
 
 #endif
