@@ -18,7 +18,7 @@ struct pz_scratch {
   int32_t* counters;  // [16] queue counters: [0] rows queued, [1] fallback
                       // workgroups done (both zero between calls)
   uint64_t* fb_keys;  // [fb_slots][slot_n] sort buffers of the fallback
-  float* fb_cum;      // [fb_slots][slot_n] running sums of the fallback
+  uint64_t* fb_keys2; // [fb_slots][slot_n] its second buffer (keys in bin order)
   int slot_n;         // power of two >= min(max_vocab, PZ_TOPP_MAX_V)
   int fb_slots;       // min(PZ_FB_SLOTS, max_batch) sort slots
 };

@@ -26,7 +26,7 @@
 
 namespace {
 
-constexpr int kFbSlots = 4;       // top-p fallback sort slots (rows sorted at once)
+constexpr int kFbSlots = 3;       // top-p fallback sort slots (rows sorted at once)
 constexpr int kMaxDevices = 64;
 constexpr size_t kScratchBytes = (size_t)24 << 20;
 

@@ -39,7 +39,7 @@ size_t pz_scratch_layout(int max_batch, int max_vocab, int max_slots, void* base
                          pz_scratch* out) {
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   int vt = max_vocab < PZ_TOPP_MAX_V ? max_vocab : PZ_TOPP_MAX_V;
-  int slot = 256;  // >= one call of the cut-off walk (64 lanes x 4 running sums)
+  int slot = 256;  // a power of two >= every candidate list (one segment at least)
   while (slot < vt) slot <<= 1;
   const size_t B = (size_t)max_batch;
   // the fallback sorts at most one queued row per slot at a time: a sampler
@@ -50,14 +50,14 @@ size_t pz_scratch_layout(int max_batch, int max_vocab, int max_slots, void* base
   const size_t o_list = off; off = up(off + B * sizeof(int32_t));
   const size_t o_cnt = off;  off = up(off + 16 * sizeof(int32_t));
   const size_t o_keys = off; off = up(off + slots * slot * sizeof(uint64_t));
-  const size_t o_cum = off;  off = up(off + slots * slot * sizeof(float));
+  const size_t o_keys2 = off; off = up(off + slots * slot * sizeof(uint64_t));
   if (base && out) {
     char* b = static_cast<char*>(base);
     out->row_stat = reinterpret_cast<float*>(b + o_stat);
     out->fb_list = reinterpret_cast<int32_t*>(b + o_list);
     out->counters = reinterpret_cast<int32_t*>(b + o_cnt);
     out->fb_keys = reinterpret_cast<uint64_t*>(b + o_keys);
-    out->fb_cum = reinterpret_cast<float*>(b + o_cum);
+    out->fb_keys2 = reinterpret_cast<uint64_t*>(b + o_keys2);
     out->slot_n = slot;
     out->fb_slots = (int)slots;
   }

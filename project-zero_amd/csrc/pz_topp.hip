@@ -168,6 +168,42 @@ __device__ __forceinline__ int pbin(uint64_t key) {
   return q < PBINS - 1 ? q : PBINS - 1;
 }
 
+// Exclusive starts of the PBINS bin counts in bcnt, by every thread of a
+// PZ_SP_BLOCK workgroup (thread t owns bins 4t .. 4t+3): bstart[b] = bcnt[b]
+// = the start of bin b (bcnt turns into the bins' cursors).  T.bmax must be
+// 0 on entry; returns the largest bin count.
+__device__ __forceinline__ uint32_t topp_bin_starts(pz_lds_u32b* bcnt, pz_lds_u32b* bstart,
+                                                    ToppShared& T) {
+  static_assert(PBINS == 4 * PZ_SP_BLOCK, "four bins per thread");
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  uint32_t c[4], local = 0, mx = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    c[j] = bcnt[4 * tid + j];
+    local += c[j];
+    mx = c[j] > mx ? c[j] : mx;
+  }
+  const uint32_t incl = pz_wave_scan_u32(local);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = __shfl_xor(mx, off, 64);
+    mx = o > mx ? o : mx;
+  }
+  if (lane == 63) T.wtot[w] = incl;
+  if (lane == 0) atomicMax(&T.bmax, mx);
+  __syncthreads();
+  uint32_t run = incl - local;
+  for (int j = 0; j < w; j++) run += T.wtot[j];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    bstart[4 * tid + j] = run;
+    bcnt[4 * tid + j] = run;  // cursor
+    run += c[j];
+  }
+  __syncthreads();
+  return T.bmax;
+}
+
 // Candidate terms with the e histogram (LDS, PZ_TOPP_NB bins) as observer.
 template <bool VEC>
 struct ToppTerms : PzExpTerms<PzRow<VEC>> {
@@ -607,12 +643,105 @@ struct SortedSeg {
   const pz_lds_u64* bkeys;
   const pz_lds_u16* perm;
   int m;
+  __device__ __forceinline__ uint64_t key(int j) const { return bkeys[perm[j]]; }
   __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
     const int j0 = k * PZ_SP_SEG + 4 * ((int)threadIdx.x & 63);
 #pragma unroll
     for (int c = 0; c < 4; c++) v[c] = j0 + c < m ? key_p(bkeys[perm[j0 + c]]) : 0.0f;
   }
 };
+// The same over a sorted key list in global memory.
+struct GSortedSeg {
+  const uint64_t* keys;
+  int m;
+  __device__ __forceinline__ uint64_t key(int j) const { return keys[j]; }
+  __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
+    const int j0 = k * PZ_SP_SEG + 4 * ((int)threadIdx.x & 63);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = j0 + c < m ? key_p(keys[j0 + c]) : 0.0f;
+  }
+};
+
+// The cut-off and the draw over a list X of m keys sorted by (p desc, id
+// asc), by every thread of the workgroup: records of the list (the row's
+// record area, free once the row's normaliser is known), an exact-sum walk
+// to the first running sum >= top_p -- the cut-off and the truncated mass
+// (top_p.c:80-93) -- and a second walk, resumed from the first one's
+// checkpoints, to the first running sum > u * trunc_sum (:96-105).  all: the
+// list holds every candidate (a cumulative that never reaches top_p keeps
+// all, :81); otherwise a cut-off term below p_lo, or none inside the list,
+// means the list is too short.  Returns the picked index or -1 (too short).
+template <class X>
+__device__ __forceinline__ int nucleus_pick(const X& xs, int m, int row, float top_p, float uu, bool all,
+                            float p_lo, int nc, char* region, const PzSplitWs& ws,
+                            PzSpShared& SS, int* pick_sh) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nsl = (m + PZ_SP_SEG - 1) / PZ_SP_SEG;
+  float* est = ws.seg_s + (size_t)row * ws.nsc;
+  for (int k = w; k < nsl; k += PZ_SP_WAVES) {
+    float v[4];
+    xs.seg(k, v);
+    const float t = pz_wave_sum((v[0] + v[1]) + (v[2] + v[3]));
+    if (lane == 0) est[k] = t;
+  }
+  __syncthreads();
+  PzSlice sl;
+  sl.k0 = 0;
+  sl.k1 = nsl;
+  pz_sp_predict(PzEstAbs{est}, 0.0f, row, sl, ws, SS);
+  {
+    uint32_t* rd = pz_sp_rec_d(ws, row);
+    uint32_t* rd2 = pz_sp_rec_d2(ws, row);
+    uint32_t* rgf = pz_sp_rec_gf(ws, row);
+    for (int k = w; k < nsl; k += PZ_SP_WAVES) {
+      float v[4];
+      xs.seg(k, v);
+      const uint32_t gf = rgf[k];
+      const uint32_t g = gf & 0xffu;
+      const bool has2 = (gf & PZ_GF_HAS2) != 0;
+      uint32_t s1 = 0, s2 = 0;
+      bool d1 = false, d2 = false;
+#pragma unroll
+      for (int cc = 0; cc < 4; cc++) {
+        uint32_t cls;
+        s1 += pz_inc(v[cc], g, &cls);
+        d1 |= cls != PZ_INC_PLAIN;
+        if (has2) {
+          s2 += pz_inc(v[cc], g - 1u, &cls);
+          d2 |= cls != PZ_INC_PLAIN;
+        }
+      }
+      s1 = pz_wave_sum_u32(s1);
+      s2 = pz_wave_sum_u32(s2);
+      const bool D1 = __ballot(d1) != 0, D2 = has2 && __ballot(d2) != 0;
+      if (lane == 0) {
+        rd[k] = s1;
+        rd2[k] = s2;
+        rgf[k] = gf | (D1 ? PZ_GF_DIRTY : 0u) | (D2 ? PZ_GF_DIRTY2 : 0u);
+      }
+    }
+  }
+  __syncthreads();
+  const PzWalk W = pz_sp_walk_setup(xs, row, nsl, nc, ws, region, SS);
+  if (w == 0) {
+    PzAcc st;
+    PzWalkCk ck;
+    const int hit = pz_sp_walk<PZ_STOP_GE>(st, W, top_p, xs, &ck);
+    int cutoff = hit >= 0 && hit < m ? hit + 1 : -1;
+    if (cutoff < 0 && all) cutoff = m;  // st then holds the whole sum
+    if (cutoff > 0 && !all && !(key_p(xs.key(cutoff - 1)) >= p_lo)) cutoff = -1;
+    int pick = -1;
+    if (cutoff > 0) {
+      const float r = uu * pz_acc_value(st);  // trunc_sum: the cumulative at the cut-off
+      PzAcc s2;
+      const int d = pz_sp_walk<PZ_STOP_GT>(s2, W, r, xs, nullptr, &ck);
+      pick = d >= 0 && d < cutoff ? d : 0;
+    }
+    if (lane == 0) *pick_sh = pick;
+  }
+  __syncthreads();
+  return *pick_sh;
+}
 
 // ---- pass 6 (one workgroup per row): order, cut-off and draw ------------
 // The gathered keys are counted into bins of p (1/128 binade) straight from
@@ -631,7 +760,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
   const PzRowState rs0 = ws.rs[row];
   if (rs0.i[0] == TP_DONE) return;
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x;
   const int m = rs0.i[2];
   const bool all = rs0.i[1] != 0;
   const uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
@@ -670,33 +799,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
       for (int i = tid; i < m; i += PZ_SP_BLOCK)
         atomicAdd((uint32_t*)&bcnt[pbin(topp_pkey(gkeys[i], inv))], 1u);
       __syncthreads();
-      // exclusive scan over the bins; thread t owns bins 4t .. 4t+3
-      uint32_t c[4], local = 0, mx = 0;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        c[j] = bcnt[4 * tid + j];
-        local += c[j];
-        mx = c[j] > mx ? c[j] : mx;
-      }
-      const uint32_t incl = pz_wave_scan_u32(local);
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t o = __shfl_xor(mx, off, 64);
-        mx = o > mx ? o : mx;
-      }
-      if (lane == 63) T.wtot[w] = incl;
-      if (lane == 0) atomicMax(&T.bmax, mx);
-      __syncthreads();
-      uint32_t run = incl - local;
-      for (int j = 0; j < w; j++) run += T.wtot[j];
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        bstart[4 * tid + j] = run;
-        bcnt[4 * tid + j] = run;  // cursor
-        run += c[j];
-      }
-      __syncthreads();
-      const bool binned = T.bmax <= (uint32_t)TOPP_BIN_MAX;
+      const bool binned = topp_bin_starts(bcnt, bstart, T) <= (uint32_t)TOPP_BIN_MAX;
       if (binned) {
         for (int i = tid; i < m; i += PZ_SP_BLOCK) {
           const uint64_t key = topp_pkey(gkeys[i], inv);
@@ -719,75 +822,11 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
           perm[b0 + r] = (uint16_t)j;
         }
         __syncthreads();
-        // records of the sorted list (this row's record area is free now)
-        const int nsl = (m + PZ_SP_SEG - 1) / PZ_SP_SEG;
         SortedSeg X;
         X.bkeys = bkeys;
         X.perm = perm;
         X.m = m;
-        float* est = ws.seg_s + (size_t)row * ws.nsc;
-        for (int k = w; k < nsl; k += PZ_SP_WAVES) {
-          float v[4];
-          X.seg(k, v);
-          const float t = pz_wave_sum((v[0] + v[1]) + (v[2] + v[3]));
-          if (lane == 0) est[k] = t;
-        }
-        __syncthreads();
-        PzSlice sl;
-        sl.k0 = 0;
-        sl.k1 = nsl;
-        pz_sp_predict(PzEstAbs{est}, 0.0f, row, sl, ws, SS);
-        {
-          uint32_t* rd = pz_sp_rec_d(ws, row);
-          uint32_t* rd2 = pz_sp_rec_d2(ws, row);
-          uint32_t* rgf = pz_sp_rec_gf(ws, row);
-          for (int k = w; k < nsl; k += PZ_SP_WAVES) {
-            float v[4];
-            X.seg(k, v);
-            const uint32_t gf = rgf[k];
-            const uint32_t g = gf & 0xffu;
-            const bool has2 = (gf & PZ_GF_HAS2) != 0;
-            uint32_t s1 = 0, s2 = 0;
-            bool d1 = false, d2 = false;
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-              uint32_t cls;
-              s1 += pz_inc(v[cc], g, &cls);
-              d1 |= cls != PZ_INC_PLAIN;
-              if (has2) {
-                s2 += pz_inc(v[cc], g - 1u, &cls);
-                d2 |= cls != PZ_INC_PLAIN;
-              }
-            }
-            s1 = pz_wave_sum_u32(s1);
-            s2 = pz_wave_sum_u32(s2);
-            const bool D1 = __ballot(d1) != 0, D2 = has2 && __ballot(d2) != 0;
-            if (lane == 0) {
-              rd[k] = s1;
-              rd2[k] = s2;
-              rgf[k] = gf | (D1 ? PZ_GF_DIRTY : 0u) | (D2 ? PZ_GF_DIRTY2 : 0u);
-            }
-          }
-        }
-        __syncthreads();
-        const PzWalk W = pz_sp_walk_setup(X, row, nsl, nc, ws, region, SS);
-        if (w == 0) {
-          PzAcc st;
-          PzWalkCk ck;
-          const int hit = pz_sp_walk<PZ_STOP_GE>(st, W, prm.top_p, X, &ck);
-          int cutoff = hit >= 0 && hit < m ? hit + 1 : -1;
-          if (cutoff < 0 && all) cutoff = m;  // st then holds the whole sum
-          if (cutoff > 0 && !all && !(key_p(bkeys[perm[cutoff - 1]]) >= p_lo)) cutoff = -1;
-          int pick = -1;
-          if (cutoff > 0) {
-            const float r = u[row] * pz_acc_value(st);  // trunc_sum: the cumulative at the cut-off
-            PzAcc s2;
-            const int d = pz_sp_walk<PZ_STOP_GT>(s2, W, r, X, nullptr, &ck);
-            pick = d >= 0 && d < cutoff ? d : 0;
-          }
-          if (lane == 0) T.cutoff = pick;
-        }
-        __syncthreads();
+        nucleus_pick(X, m, row, prm.top_p, u[row], all, p_lo, nc, region, ws, SS, &T.cutoff);
         if (T.cutoff >= 0) {
           if (tid == 0) {
             const uint64_t k = bkeys[perm[T.cutoff]];
@@ -816,72 +855,257 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
     }
   }
   if (!done && tid == 0) {
+    if (rs0.i[3] == 0 && m <= cap && m > 0) {
+      // the whole gathered list was sorted: the cut-off lies past it
+      ws.rs[row].f[0] = 0.0f;
+      ws.rs[row].i[1] = 1;
+    }
     const int q = atomicAdd(&sc.counters[0], 1);
     sc.fb_list[q] = row;
   }
 }
 
-// Fallback: every candidate of the row, sorted in the workgroup's global
-// scratch slot, then the same cumulative and draw.
+// Fallback, one workgroup per queued row at a time (rows whose selected set
+// overflowed the gather or the nucleus kernel's LDS, or whose cut-off lies
+// outside it): the candidates with e at or above the row's gate -- every
+// candidate when the gate is 0 -- as (p, ~id) keys in the workgroup's global
+// slot; a counting sort by p bin into the second slot, then each key's rank
+// inside its bin (bins above TOPP_BIN_MAX keys: a bitonic sort in LDS; a bin
+// beyond the LDS buffer: one global bitonic sort of the whole list) back into
+// the first, which then holds the reference's order; then nucleus_pick.  A
+// gated list too short for the cut-off is gathered again with gate 0.
+constexpr int FB_NC = 8;                                // pre-evaluated segments of its walk
+constexpr int FB_LBUF = 8192;                           // keys of its LDS bin sort
+constexpr int FB_BIG = 1024;  // bins above TOPP_BIN_MAX it lists (slot_n / 257 < FB_BIG)
+// bins, starts, the big-bin list and its chunk starts
+constexpr size_t FB_HEAD = (size_t)PBINS * 8 + (size_t)FB_BIG * 8 + 16;
+
+// One pass of the fallback over row with the given gate (the workgroup's
+// slot: blockIdx.x).  Returns false when the gated list is too short for the
+// cut-off.  (A function of its own: inlined into the kernel's loop over the
+// queue, the walk's registers spill.)
 template <bool VEC>
-__global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
-    const float* __restrict__ logits, long ld, int V,
-    const pz_row_params_dev* __restrict__ params, int n_params,
-    const int32_t* __restrict__ hist, int H, int hcap, PzSplitWs ws, const float* __restrict__ u,
-    int32_t* __restrict__ ids_out, float* __restrict__ p_out, pz_scratch sc) {
+__device__ __noinline__ bool fb_pass(const float* __restrict__ logits, long ld, int V,
+                                     const pz_row_params_dev* __restrict__ params, int n_params,
+                                     const int32_t* __restrict__ hist, int H, int hcap, int nseg,
+                                     const PzSplitWs& ws, const float* __restrict__ u,
+                                     int32_t* __restrict__ ids_out, float* __restrict__ p_out,
+                                     const pz_scratch& sc, int row, float gate) {
   extern __shared__ __align__(16) char lds[];
-  __shared__ int count, over, cutoff_sh;
+  __shared__ PzSpShared SS;
+  __shared__ ToppShared T;
   __shared__ uint64_t etab[32];
+  __shared__ int nbig, nchunks;
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
-  pz_etab_fill((pz_lds_u64*)etab);
-  __syncthreads();
-  const int tid = threadIdx.x;
-  const int n_fb = sc.counters[0];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint64_t* keys = sc.fb_keys + (size_t)blockIdx.x * sc.slot_n;
-  float* cum = sc.fb_cum + (size_t)blockIdx.x * sc.slot_n;
-  for (int q = blockIdx.x; q < n_fb; q += gridDim.x) {
-    const int row = sc.fb_list[q];
-    const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-    PzRow<VEC> R;
-    R.x = logits + (long)row * ld;
-    R.V = V;
-    R.T = PzTemp::of(prm);
-    pz_penalty_build<PZ_RB>(R.P, lds, V, hcap, hist ? hist + (long)row * H : nullptr, H, prm);
-    const float M = ws.rs[row].M;
-    const float inv = ws.rs[row].inv;
-    const float thr = M - 20.0f;
-    if (tid == 0) {
-      count = 0;
-      over = 0;
+  uint64_t* keys2 = sc.fb_keys2 + (size_t)blockIdx.x * sc.slot_n;
+  // after the gather: bin counts (then cursors, then ends), bin starts, the
+  // big-bin list, then the LDS sort buffer or the walk
+  pz_lds_u32b* bcnt = (pz_lds_u32b*)lds;
+  pz_lds_u32b* bstart = bcnt + PBINS;
+  pz_lds_u32b* big = bstart + PBINS;
+  pz_lds_u32b* chs = big + FB_BIG;
+  char* region = lds + FB_HEAD;
+  pz_lds_u64* sbuf = (pz_lds_u64*)region;
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const PzRowState rs0 = ws.rs[row];
+  const float M = rs0.M, inv = rs0.inv, thr = M - 20.0f;
+  const float* seg_m = ws.seg_m + (size_t)row * ws.nsc;
+  __syncthreads();  // the previous pass's LDS is free
+  pz_etab_fill((pz_lds_u64*)etab);
+  const bool all = gate == 0.0f;
+  // gathered: every e >= e_lo, so every p >= p_lo = fl(gate * inv) (p is
+  // monotone in e); dgate skips the expf of terms far below the gate
+  const float e_lo = gate * (1.0f - 0x1p-21f), p_lo = gate * inv;
+  const float dgate = all ? -__builtin_inff() : rs0.f[1];
+  const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
+  if (tid == 0) SS.cnt = 0;
+  __syncthreads();
+  for (int kb = w; kb < nseg; kb += PZ_SP_U * PZ_SP_WAVES) {
+    float ys[PZ_SP_U][4];
+    int ns[PZ_SP_U];
+#pragma unroll
+    for (int uu = 0; uu < PZ_SP_U; uu++) {
+      const int k = kb + uu * PZ_SP_WAVES;
+      ns[uu] = k < nseg && !(seg_m[k] - M < dgate) ? R.load(k * PZ_SP_SEG + 4 * lane, ys[uu])
+                                                   : 0;
     }
-    __syncthreads();
-    const int ntiles = pz_tiles(V);
-    for (int t = 0; t < ntiles; t++) {
-      float y[4];
-      const int e0 = pz_tile_e0(t);
-      const int n = R.get(e0, y);
+#pragma unroll
+    for (int uu = 0; uu < PZ_SP_U; uu++) {
+      const int k = kb + uu * PZ_SP_WAVES;
+      if (k >= nseg) break;
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      float (&y)[4] = ys[uu];
+      const int n = ns[uu];
+      R.apply(e0, n, y);
+      uint32_t want = 0;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        const bool want = c < n && y[c] >= thr;
+        const bool wnt = (c < n) & (y[c] >= thr) & ((y[c] - M) >= dgate);
+        want |= (wnt ? 1u : 0u) << c;
+      }
+      while (__ballot(want != 0u)) {
+        bool take = false;
         uint64_t key = 0;
-        if (want) key = topp_key(pz_expf_l(y[c] - M, et) * inv, e0 + c);
-        append_key(&count, &over, keys, sc.slot_n, want, key);
+        if (want) {
+          const uint32_t j = (uint32_t)__builtin_ctz(want);
+          want &= want - 1u;
+          const float yy = j == 0 ? y[0] : (j == 1 ? y[1] : (j == 2 ? y[2] : y[3]));
+          const float e = pz_expf_l(yy - M, et);
+          take = e >= e_lo;
+          key = topp_key(e * inv, e0 + (int)j);  // top_p.c:72-74
+        }
+        const uint64_t ball = __ballot(take);
+        if (ball) {
+          const int leader = (int)__builtin_ctzll(ball);
+          int base = 0;
+          if (lane == leader) base = atomicAdd(&SS.cnt, __popcll(ball));
+          base = __builtin_amdgcn_readlane(base, leader);
+          // (slot_n >= V: every candidate fits)
+          if (take) keys[base + __popcll(ball & ((1ull << lane) - 1ull))] = key;
+        }
       }
     }
-    __syncthreads();
-    const int m = count;
+  }
+  __syncthreads();  // the keys, their count; the penalty tables are free
+  const int m = SS.cnt;
+  for (int i = tid; i < PBINS; i += PZ_SP_BLOCK) bcnt[i] = 0u;
+  if (tid == 0) {
+    T.bmax = 0u;
+    nbig = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < m; i += PZ_SP_BLOCK) atomicAdd((uint32_t*)&bcnt[pbin(keys[i])], 1u);
+  __syncthreads();
+  const uint32_t bmax = topp_bin_starts(bcnt, bstart, T);
+  if (bmax > (uint32_t)FB_LBUF) {
+    // a bin beyond the LDS buffer: the whole list by one global bitonic sort
     int N = 1;
     while (N < m) N <<= 1;
-    for (int i = m + tid; i < N; i += PZ_RB) keys[i] = 0ull;
+    for (int i = m + tid; i < N; i += PZ_SP_BLOCK) keys[i] = 0ull;
     __syncthreads();
-    pz_bitonic_desc<PZ_RB>(keys, N);
-    const int cutoff = nucleus_cutoff(keys, cum, m, prm.top_p, true, &cutoff_sh);
-    if (tid == 0) nucleus_draw(keys, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
-    __syncthreads();
+    pz_bitonic_desc<PZ_SP_BLOCK>(keys, N);
+  } else {
+    for (int i = tid; i < m; i += PZ_SP_BLOCK) {
+      const uint64_t key = keys[i];
+      keys2[atomicAdd((uint32_t*)&bcnt[pbin(key)], 1u)] = key;
+    }
+    __syncthreads();  // bcnt[b]: the end of bin b
+    // rank inside the bin: every comparison independent of the others
+    for (int j = tid; j < m; j += PZ_SP_BLOCK) {
+      const uint64_t key = keys2[j];
+      const int b = pbin(key);
+      const uint32_t b0 = bstart[b], b1 = bcnt[b];
+      if (b1 - b0 > (uint32_t)TOPP_BIN_MAX) continue;
+      uint32_t r = 0, x = b0;
+      for (; x + 4 <= b1; x += 4) {
+        const uint64_t k0 = keys2[x], k1 = keys2[x + 1], k2 = keys2[x + 2], k3 = keys2[x + 3];
+        r += (k0 > key ? 1u : 0u) + (k1 > key ? 1u : 0u) + (k2 > key ? 1u : 0u) +
+             (k3 > key ? 1u : 0u);
+      }
+      for (; x < b1; x++) r += keys2[x] > key ? 1u : 0u;
+      keys[b0 + r] = key;
+    }
+    // the big bins (above TOPP_BIN_MAX keys, so fewer than FB_BIG of them),
+    // listed in bin order and sorted in LDS in chunks of consecutive big bins
+    // of up to FB_LBUF keys: keys are ordered between bins, so a chunk's
+    // sorted union is its bins' sorted lists one after the other
+    if (bmax > (uint32_t)TOPP_BIN_MAX) {
+      for (int r = 0; r < PBINS; r += PZ_SP_BLOCK) {
+        const int b = r + tid;
+        const bool isbig = bcnt[b] - bstart[b] > (uint32_t)TOPP_BIN_MAX;
+        const uint64_t ball = __ballot(isbig);
+        if (lane == 0) T.wtot[w] = (uint32_t)__popcll(ball);
+        __syncthreads();
+        uint32_t base = (uint32_t)nbig;
+        for (int j = 0; j < w; j++) base += T.wtot[j];
+        if (isbig) big[base + __popcll(ball & ((1ull << lane) - 1ull))] = (uint32_t)b;
+        __syncthreads();
+        if (tid == 0) {
+          uint32_t t = 0;
+          for (int j = 0; j < PZ_SP_WAVES; j++) t += T.wtot[j];
+          nbig += (int)t;
+        }
+        __syncthreads();
+      }
+      if (tid == 0) {
+        int nch = 0;
+        uint32_t acc = 0;
+        for (int i = 0; i < nbig; i++) {
+          const uint32_t c = bcnt[big[i]] - bstart[big[i]];
+          if (i == 0 || acc + c > (uint32_t)FB_LBUF) {
+            chs[nch++] = (uint32_t)i;
+            acc = 0;
+          }
+          acc += c;
+        }
+        chs[nch] = (uint32_t)nbig;
+        nchunks = nch;
+      }
+      __syncthreads();
+      for (int k = 0; k < nchunks; k++) {
+        const int i0 = (int)chs[k], i1 = (int)chs[k + 1];
+        int off = 0;
+        for (int i = i0; i < i1; i++) {
+          const uint32_t b0 = bstart[big[i]];
+          const int c = (int)(bcnt[big[i]] - b0);
+          for (int j = tid; j < c; j += PZ_SP_BLOCK) sbuf[off + j] = keys2[b0 + j];
+          off += c;
+        }
+        int N = 1;
+        while (N < off) N <<= 1;
+        for (int j = off + tid; j < N; j += PZ_SP_BLOCK) sbuf[j] = 0ull;
+        __syncthreads();
+        pz_bitonic_desc<PZ_SP_BLOCK>(sbuf, N);
+        off = 0;
+        for (int i = i0; i < i1; i++) {
+          const uint32_t b0 = bstart[big[i]];
+          const int c = (int)(bcnt[big[i]] - b0);
+          for (int j = tid; j < c; j += PZ_SP_BLOCK) keys[b0 + j] = sbuf[off + j];
+          off += c;
+        }
+        __syncthreads();
+      }
+    }
+  }
+  __syncthreads();  // keys: the sorted list
+  GSortedSeg X;
+  X.keys = keys;
+  X.m = m;
+  const int pick =
+      nucleus_pick(X, m, row, prm.top_p, u[row], all, p_lo, FB_NC, region, ws, SS, &T.cutoff);
+  if (pick >= 0 || all) {
+    if (tid == 0) {
+      const uint64_t k = keys[pick > 0 ? pick : 0];
+      ids_out[row] = key_id(k);
+      if (p_out) p_out[row] = key_p(k);
+    }
+    return true;
+  }
+  return false;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
+    const float* __restrict__ logits, long ld, int V,
+    const pz_row_params_dev* __restrict__ params, int n_params,
+    const int32_t* __restrict__ hist, int H, int hcap, int nseg, PzSplitWs ws,
+    const float* __restrict__ u, int32_t* __restrict__ ids_out, float* __restrict__ p_out,
+    pz_scratch sc) {
+  const int n_fb = sc.counters[0];
+  for (int q = blockIdx.x; q < n_fb; q += gridDim.x) {
+    const int row = sc.fb_list[q];
+    const PzRowState rs0 = ws.rs[row];
+    const float gate = rs0.i[1] ? 0.0f : rs0.f[0];
+    if (!fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out,
+                      p_out, sc, row, gate))
+      fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out, p_out,
+                   sc, row, 0.0f);  // the cut-off lies past the gated list
   }
   // the last workgroup out re-arms the queue for the next launch (every
   // workgroup has read counters[0] before it counts itself done)
-  if (tid == 0) {
+  if (threadIdx.x == 0) {
     __threadfence();
     if (atomicAdd(&sc.counters[1], 1) == (int)gridDim.x - 1) {
       atomicExch(&sc.counters[0], 0);
@@ -890,6 +1114,14 @@ __global__ __launch_bounds__(PZ_RB) void k_topp_fallback(
   }
 }
 
+// LDS of the fallback: the penalty tables during the gather, then the bins
+// and the sort buffer or the walk over up to slot_n keys.
+size_t topp_fallback_bytes(size_t pen_full, int slot_n) {
+  const size_t sortb = (size_t)FB_LBUF * 8;
+  const size_t walk = pz_sp_walk_lds((slot_n + PZ_SP_SEG - 1) / PZ_SP_SEG, FB_NC);
+  const size_t after = FB_HEAD + (sortb > walk ? sortb : walk);
+  return pen_full > after ? pen_full : after;
+}
 
 size_t pen_region(const pz_launch& L, int n_ids) {
   return L.pen_any ? (pz_penalty_lds_bytes(n_ids, L.hcap) + 15) & ~(size_t)15 : 0;
@@ -938,7 +1170,9 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   auto fb = k_topp_fallback<VEC>;
   const void* fns[6] = {(const void*)k1, (const void*)k1e, (const void*)k2, (const void*)k3,
                         (const void*)k4, (const void*)fb};
-  const size_t need[6] = {lds1, lds1, lds2, lds3, lds4, pen_full};
+  const size_t lds5 = topp_fallback_bytes(pen_full, L.sc.slot_n);
+  if (lds5 + fixed > (size_t)L.max_lds || L.sc.slot_n / (TOPP_BIN_MAX + 1) >= FB_BIG) return -2;
+  const size_t need[6] = {lds1, lds1, lds2, lds3, lds4, lds5};
   for (int i = 0; i < 6; i++)
     if (need[i] > 65536 && hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)need[i]) != hipSuccess)
@@ -963,8 +1197,8 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   hipLaunchKernelGGL(k4, dim3(n_rows), block, lds4, L.stream, TOPP_PASS, cap, nc6);
 #undef TOPP_PASS
   const int fb_grid = n_rows < L.sc.fb_slots ? n_rows : L.sc.fb_slots;
-  hipLaunchKernelGGL(fb, dim3(fb_grid), dim3(PZ_RB), pen_full, L.stream, L.logits, L.ld, L.V,
-                     L.params, L.n_params, L.hist, L.H, L.hcap, ws, L.u, L.ids, L.p_out, L.sc);
+  hipLaunchKernelGGL(fb, dim3(fb_grid), block, lds5, L.stream, L.logits, L.ld, L.V, L.params,
+                     L.n_params, L.hist, L.H, L.hcap, pl.nseg, ws, L.u, L.ids, L.p_out, L.sc);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

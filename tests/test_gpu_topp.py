@@ -88,6 +88,18 @@ def test_flat_and_broad_rows_use_the_fallback(torch_cuda):
     check(torch_cuda, x, [pz.row_params(temperature=1.0, top_p=0.9)], u, label="broad 0.9")
 
 
+def test_selected_bins_beyond_the_gather(torch_cuda):
+    """Rows 377, 796 and 977 of the 1024-row c2 pool: the nucleus bins picked
+    from the e histogram hold 8.3K-8.8K candidates (nuclei of 7.3K-7.7K),
+    past the 8192-key gather, so the fallback sorts the gated candidates;
+    two ordinary rows beside them."""
+    w = wl.build_c2(B=1024)
+    pick = [377, 796, 977, 0, 1]
+    x = np.ascontiguousarray(w["logits"][pick])
+    u = np.ascontiguousarray(w["u"][pick])
+    check(torch_cuda, x, w["params"], u, label="c2 pool rows past the gather")
+
+
 def test_degenerate_rows(torch_cuda):
     B, V = 8, 5000
     x = pz.synth_normal(B, V, 2.0, 51)
