@@ -10,7 +10,7 @@
 // Device scratch owned by a sampler (carved from one allocation).
 constexpr int PZ_FB_SLOTS = 32;        // rows the top-p fallback kernel sorts at once
 constexpr int PZ_TOPP_MAX_V = 200000;  // top_p.c:27 (larger rows take argmax)
-constexpr int PZ_TOPP_CAPG = 8192;     // top-p candidates a row can gather for the LDS sort
+constexpr int PZ_TOPP_CAPG = 12288;    // top-p candidates a row can gather for the LDS sort
 
 struct pz_scratch {
   float* row_stat;    // [max_batch][4] per-row values handed between kernels

@@ -94,11 +94,11 @@ int device_setup(int device, const DeviceState** out) {
 }
 
 // One staging launch: up to kStageWords words copied to dst[first..], and
-// with zero_counters the fallback's queue counters and the rows' arrival
-// counters cleared (they must read zero when a launch starts; the kernels
-// re-zero them when they end, but a call interrupted before then would leave
-// them set, and the array's first use must not depend on its initial
-// contents).
+// with zero_counters the fallback's queue counters, the rows' arrival
+// counters and the rows' meeting words cleared (they must read zero when a
+// launch starts; the kernels re-zero them when they end, but a call
+// interrupted before then would leave them set, and the array's first use
+// must not depend on its initial contents).
 constexpr int kStageWords = 480;
 struct StageChunk {
   uint32_t first;
@@ -109,17 +109,19 @@ struct StageChunk {
 };
 
 __global__ void k_noalloc_stage(StageChunk c, uint32_t* dst, int32_t* counters,
-                                uint32_t* arrive) {
+                                uint32_t* arrive, uint64_t* meet, uint32_t n_meet) {
   for (uint32_t i = threadIdx.x; i < c.n; i += blockDim.x) dst[c.first + i] = c.w[i];
   if (c.zero_counters) {
     if (threadIdx.x < 16) counters[threadIdx.x] = 0;
     for (uint32_t i = threadIdx.x; i < PZ_NOALLOC_MAX_BATCH; i += blockDim.x) arrive[i] = 0u;
+    for (uint32_t i = threadIdx.x; i < n_meet; i += blockDim.x) meet[i] = 0ull;
   }
 }
 
 // Copies `words` words from host src to device dst through staging launches.
 int stage(const uint32_t* src, uint32_t words, uint32_t* dst, int32_t* counters,
-          uint32_t* arrive, bool zero, hipStream_t st) {
+          const PzSplitWs& ws, bool zero, hipStream_t st) {
+  const uint32_t n_meet = (uint32_t)(PZ_NOALLOC_MAX_BATCH * 2 * ws.smax);
   StageChunk c;
   c.pad_ = 0;
   uint32_t first = 0;
@@ -129,7 +131,8 @@ int stage(const uint32_t* src, uint32_t words, uint32_t* dst, int32_t* counters,
     c.n = n;
     c.zero_counters = zero ? 1u : 0u;
     memcpy(c.w, src + first, n * sizeof(uint32_t));
-    hipLaunchKernelGGL(k_noalloc_stage, dim3(1), dim3(256), 0, st, c, dst, counters, arrive);
+    hipLaunchKernelGGL(k_noalloc_stage, dim3(1), dim3(256), 0, st, c, dst, counters, ws.arrive,
+                       ws.meet, n_meet);
     if (hipGetLastError() != hipSuccess) return PZ_EDEVICE;
     zero = false;
     first += n;
@@ -181,13 +184,11 @@ extern "C" int pz_sample_batch_noalloc(int device, void* stream, int temp_mode,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint32_t pwords = (uint32_t)(n_params * sizeof(pz_row_params_dev) / 4);
   int rc = stage(reinterpret_cast<const uint32_t*>(img.res), pwords,
-                 reinterpret_cast<uint32_t*>(lay.params), lay.sc.counters, lay.ws.arrive, true,
-                 st);
+                 reinterpret_cast<uint32_t*>(lay.params), lay.sc.counters, lay.ws, true, st);
   if (rc == PZ_OK && modes_present > 1) {
     pz_fill_rows(img.res, B, n_params, offset, img.rows);
     rc = stage(reinterpret_cast<const uint32_t*>(img.rows), (uint32_t)B,
-               reinterpret_cast<uint32_t*>(lay.rows), lay.sc.counters, lay.ws.arrive, false,
-               st);
+               reinterpret_cast<uint32_t*>(lay.rows), lay.sc.counters, lay.ws, false, st);
   }
   if (rc != PZ_OK) return rc;
 

@@ -70,6 +70,9 @@ struct PzRowState {
 struct PzSplitWs {
   PzRowState* rs;     // [rows]
   uint32_t* arrive;   // [rows] arrival counters, zero between launches
+  uint64_t* meet;     // [rows][2][smax] values the workgroups of a row hand each
+                      // other within a launch (bit 63: written), zero between
+                      // launches
   float* slice_m;     // [rows][smax] slice maxima (NaN-free)
   uint32_t* slice_f;  // [rows][smax] slice NaN flags
   float* seg_m;       // [rows][nsc] segment maxima (stat pass)
@@ -124,6 +127,7 @@ inline size_t pz_split_ws_layout(int rows, int V, int capg, void* base, PzSplitW
   size_t off = 0;
   const size_t o_rs = off;   off = up(off + R * sizeof(PzRowState));
   const size_t o_arr = off;  off = up(off + R * 4);
+  const size_t o_meet = off; off = up(off + R * 2 * smax * 8);
   const size_t o_sm = off;   off = up(off + R * smax * 4);
   const size_t o_sf = off;   off = up(off + R * smax * 4);
   const size_t o_segm = off; off = up(off + R * nsc * 4);
@@ -135,6 +139,7 @@ inline size_t pz_split_ws_layout(int rows, int V, int capg, void* base, PzSplitW
     char* b = static_cast<char*>(base);
     out->rs = reinterpret_cast<PzRowState*>(b + o_rs);
     out->arrive = reinterpret_cast<uint32_t*>(b + o_arr);
+    out->meet = reinterpret_cast<uint64_t*>(b + o_meet);
     out->slice_m = reinterpret_cast<float*>(b + o_sm);
     out->slice_f = reinterpret_cast<uint32_t*>(b + o_sf);
     out->seg_m = reinterpret_cast<float*>(b + o_segm);

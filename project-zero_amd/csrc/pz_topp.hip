@@ -43,7 +43,10 @@
 
 namespace {
 
-constexpr int TOPP_CAP_MAX = 8192;
+constexpr int TOPP_CAP_MAX = 12288;
+// Lists whose bins are too large for the rank count are bitonic-sorted whole
+// in LDS up to this many keys (beyond: the fallback).
+constexpr int TOPP_BITONIC_MAX = 8192;
 // Gathered lists of at least TOPP_BINSORT_MIN keys are ordered by a counting
 // sort over PBINS bins of p (1/128 binade each, 32 binades below 1.0) and a
 // rank count inside each bin; smaller ones by a bitonic sort.
@@ -205,14 +208,42 @@ __device__ __forceinline__ uint32_t topp_bin_starts(pz_lds_u32b* bcnt, pz_lds_u3
 }
 
 // Candidate terms with the e histogram (LDS, PZ_TOPP_NB bins) as observer.
-template <bool VEC>
-struct ToppTerms : PzExpTerms<PzRow<VEC>> {
+template <class Row>
+struct ToppTermsR : PzExpTerms<Row> {
   pz_lds_u32b* ehist;
   __device__ __forceinline__ void observe(int, const float (&)[4], const float (&a)[4]) {
 #pragma unroll
     for (int c = 0; c < 4; c++)
       if (a[c] > 0.0f) atomicAdd((uint32_t*)&ehist[ebin(a[c])], 1u);
   }
+};
+template <bool VEC>
+using ToppTerms = ToppTermsR<PzRow<VEC>>;
+
+// A workgroup's slice of the row with the chain already applied, in LDS
+// (ids from lo on): a row for the records pass that only reads LDS.
+struct ToppLdsRow {
+  const pz_lds_f32* y;
+  int lo, V;
+  __device__ __forceinline__ int load(int e0, float (&r)[4]) const {
+    int n = V - e0;
+    n = n < 0 ? 0 : (n > 4 ? 4 : n);
+    const pz_f4 q = *(const pz_lds_f4*)(y + (e0 - lo));
+    r[0] = q.x;
+    r[1] = q.y;
+    r[2] = q.z;
+    r[3] = q.w;
+    return n;
+  }
+  __device__ __forceinline__ void apply(int, int, float (&)[4]) const {}
+  __device__ __forceinline__ int get(int e0, float (&r)[4]) const { return load(e0, r); }
+};
+
+// Estimated mass of the slice's segments, from LDS (k from k0 on).
+struct ToppSliceEst {
+  const float* s;
+  int k0;
+  __device__ __forceinline__ float operator()(int k) const { return s[k - k0]; }
 };
 
 // The row's chain with penalty tables for the ids [lo, hi).
@@ -379,6 +410,175 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_
   for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) gh[i] = ehist[i];
 }
 
+// ---- passes 1-3 in one launch, for slices that fit in LDS ---------------
+// Each workgroup reads its slice once and keeps it, the chain applied, in
+// LDS; the row's S workgroups meet twice (for the row maximum, then for the
+// estimated mass before each slice), and the estimates, the records and the
+// mass histogram all come from LDS.  At a meeting each workgroup posts one
+// 64-bit word (value and a written bit, so no fence orders it: a fence at
+// agent scope writes back or invalidates the whole L2) and wave 0 polls the
+// row's S words.  A row's workgroups are consecutive in the launch order
+// and a CU holds two of them, so every workgroup a wait depends on has been
+// dispatched: the waits end.  (The walk launch, which follows, clears the
+// words.)
+constexpr int TOPP_FRONT_SEGS = 64;  // segments of a slice held in LDS (64 KiB)
+
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOPP_ARGS,
+                                                                             int pen_bytes) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ uint64_t etab[32];
+  __shared__ float sest[TOPP_FRONT_SEGS];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = pz_row_of(rows, blockIdx.y);
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const PzSlice sl = pz_sp_slice(nseg, spw);
+  const int lo = pz_sp_lo(sl);
+  pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
+  pz_lds_f32* ybuf = (pz_lds_f32*)(lds + (((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15));
+  uint64_t* meet = ws.meet + (size_t)row * 2 * ws.smax;
+  if (tid == 0) {
+    SS.any = 0u;
+    if (blockIdx.x == 0) ws.rs[row].i[5] = 0;  // the nucleus bins of this call: not yet picked
+  }
+  for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) ehist[i] = 0u;
+  const PzRow<VEC> R =
+      topp_row<VEC>(logits, ld, row, V, prm, lds, lo, pz_sp_hi(sl, V), hcap, hist, H);
+  __syncthreads();
+  // 1. the slice, once: chain applied, into LDS; segment and slice maxima
+  float* seg_m = ws.seg_m + (size_t)row * ws.nsc;
+  float smx = -__builtin_inff();
+  bool nan = false;
+  for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+    float y[PZ_SP_U][4];
+    int n[PZ_SP_U];
+#pragma unroll
+    for (int uu = 0; uu < PZ_SP_U; uu++)
+      n[uu] = R.load((kb + uu * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, y[uu]);
+#pragma unroll
+    for (int uu = 0; uu < PZ_SP_U; uu++) {
+      const int k = kb + uu * PZ_SP_WAVES;
+      if (k >= sl.k1) break;
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      R.apply(e0, n[uu], y[uu]);
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if (c >= n[uu]) continue;
+        if (y[uu][c] != y[uu][c]) nan = true;
+        else m = fmaxf(m, y[uu][c]);
+      }
+      pz_f4 q;
+      q.x = y[uu][0];
+      q.y = y[uu][1];
+      q.z = y[uu][2];
+      q.w = y[uu][3];
+      *(pz_lds_f4*)(ybuf + (e0 - lo)) = q;
+      m = pz_wave_max(m);
+      if (lane == 0) seg_m[k] = m;  // (NaN-free; the gather skips segments by it)
+      smx = fmaxf(smx, m);
+    }
+  }
+  if (__ballot(nan) && lane == 0) atomicOr(&SS.any, 1u);
+  if (lane == 0) SS.red[w] = smx;
+  __syncthreads();
+  if (tid == 0) {
+    float mm = SS.red[0];
+    for (int i = 1; i < PZ_SP_WAVES; i++) mm = fmaxf(mm, SS.red[i]);
+    uint32_t f = SS.any;
+    ws.slice_m[(size_t)row * ws.smax + blockIdx.x] = mm;
+    ws.slice_f[(size_t)row * ws.smax + blockIdx.x] = f;
+    if (blockIdx.x == 0) {
+      ws.rs[row].y0 = ybuf[0];
+      if (ybuf[0] != ybuf[0]) f |= PZ_RS_Y0NAN;
+    }
+    // meet 1: every slice's maximum and flags
+    __hip_atomic_store(&meet[blockIdx.x],
+                       (1ull << 63) | ((uint64_t)f << 32) | (uint64_t)__float_as_uint(mm),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (w == 0) {
+    uint64_t v = 1ull << 63;
+    for (;;) {
+      if (lane < S) v = __hip_atomic_load(&meet[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__ballot((v >> 63) == 0) == 0) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    const float M = pz_wave_max(lane < S ? __uint_as_float((uint32_t)v) : -__builtin_inff());
+    const bool anyf = __ballot(lane < S && (((uint32_t)(v >> 32) & PZ_RS_NAN) != 0)) != 0;
+    const bool y0nan = __ballot(lane < S && (((uint32_t)(v >> 32) & PZ_RS_Y0NAN) != 0)) != 0;
+    if (lane == 0) {
+      uint32_t flags = anyf ? PZ_RS_NAN : 0u;
+      if (y0nan) flags |= PZ_RS_Y0NAN;
+      if (!(M > -__builtin_inff() && M < __builtin_inff())) flags |= PZ_RS_NONFIN;
+      SS.M = M;
+      SS.any = flags;
+    }
+  }
+  __syncthreads();
+  const bool degen = topp_degenerate(SS.any);
+  const float M = SS.M, thr = M - 20.0f;
+  // 2. the estimated candidate mass of each segment (as k_topp_est), and the
+  // slice's total for the slices after it
+  if (!degen) {
+    for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      int n = V - e0;
+      n = n < 0 ? 0 : (n > 4 ? 4 : n);
+      const pz_f4 q = *(const pz_lds_f4*)(ybuf + (e0 - lo));
+      const float y[4] = {q.x, q.y, q.z, q.w};
+      float t = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        if (c < n && y[c] >= thr) t += pz_fast_exp(y[c] - M);
+      t = pz_wave_sum(t);
+      if (lane == 0) sest[k - sl.k0] = t;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float tot = 0.0f;
+    if (!degen)
+      for (int k = sl.k0; k < sl.k1; k++) tot += sest[k - sl.k0];
+    // meet 2: every slice's estimated mass
+    __hip_atomic_store(&meet[ws.smax + blockIdx.x], (1ull << 63) | (uint64_t)__float_as_uint(tot),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (degen) return;  // (every workgroup of the row; the words are cleared all the same)
+  if (w == 0) {
+    uint64_t v = 1ull << 63;
+    for (;;) {
+      if (lane < (int)blockIdx.x)
+        v = __hip_atomic_load(&meet[ws.smax + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__ballot((v >> 63) == 0) == 0) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    // the estimated mass before this slice
+    const float carry = pz_wave_sum(lane < (int)blockIdx.x ? __uint_as_float((uint32_t)v) : 0.0f);
+    if (lane == 0) SS.carry = carry;
+  }
+  __syncthreads();
+  pz_sp_predict(ToppSliceEst{sest, sl.k0}, SS.carry, row, sl, ws, SS);
+  // 3. records from LDS (as k_topp_rec)
+  ToppTermsR<ToppLdsRow> X;
+  X.R.y = ybuf;
+  X.R.lo = lo;
+  X.R.V = V;
+  X.M = M;
+  X.thr = thr;
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = et;
+  X.ehist = ehist;
+  pz_sp_records(X, row, sl, ws);
+  __syncthreads();
+  uint32_t* gh = ws.hist + ((size_t)blockIdx.y * S + blockIdx.x) * PZ_TOPP_NB;
+  for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) gh[i] = ehist[i];
+}
+
 // Gather of one slice: candidates with e >= e_lo (1 - 2^-21) (a superset
 // gate on y - M first, 0.01 below the bin edge; each possible candidate's
 // exact e one per lane per trip), staged as (e, ~id) keys in LDS (lkeys,
@@ -515,6 +715,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walk(TOPP_ARGS, int pen_by
   const int row = pz_row_of(rows, blockIdx.x);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const int tid = threadIdx.x;
+  // k_topp_front's meetings are over: clear the row's words
+  for (int i = tid; i < 2 * ws.smax; i += PZ_SP_BLOCK)
+    __hip_atomic_store(&ws.meet[(size_t)row * 2 * ws.smax + i], 0ull, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   pz_sp_row_stat(row, S, ws, SS);
   const float M = SS.M;
   const uint32_t flags = SS.any;
@@ -770,7 +974,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
   // is the reference's order down to p_lo, and a cut-off whose last term
   // lies at or above p_lo only ever saw reference terms (else: the fallback).
   const float p_lo = rs0.f[0] * inv;
-  bool done = false;
+  bool done = false, sorted = false;  // sorted: the whole list, cut-off checked
   if (rs0.i[3] == 0 && m <= cap && m > 0) {
     pz_lds_u64* bkeys = (pz_lds_u64*)lds;                          // [cap]
     pz_lds_u16* perm = (pz_lds_u16*)(lds + (size_t)cap * 8);       // [cap]
@@ -792,6 +996,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
           nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
         done = true;
       }
+      sorted = true;
     } else {
       for (int i = tid; i < PBINS; i += PZ_SP_BLOCK) bcnt[i] = 0u;
       if (tid == 0) T.bmax = 0u;
@@ -835,7 +1040,8 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
           }
           done = true;
         }
-      } else {
+        sorted = true;
+      } else if (m <= TOPP_BITONIC_MAX) {
         // a bin too large for the rank count: bitonic sort of the whole list
         __syncthreads();
         int N = 1;
@@ -851,11 +1057,12 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
             nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
           done = true;
         }
+        sorted = true;
       }
     }
   }
   if (!done && tid == 0) {
-    if (rs0.i[3] == 0 && m <= cap && m > 0) {
+    if (sorted) {
       // the whole gathered list was sorted: the cut-off lies past it
       ws.rs[row].f[0] = 0.0f;
       ws.rs[row].i[1] = 1;
@@ -875,6 +1082,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
 // the first, which then holds the reference's order; then nucleus_pick.  A
 // gated list too short for the cut-off is gathered again with gate 0.
 constexpr int FB_NC = 8;                                // pre-evaluated segments of its walk
+constexpr int FB_U = 8;                                 // segments a wave loads at once
 constexpr int FB_LBUF = 8192;                           // keys of its LDS bin sort
 constexpr int FB_BIG = 1024;  // bins above TOPP_BIN_MAX it lists (slot_n / 257 < FB_BIG)
 // bins, starts, the big-bin list and its chunk starts
@@ -882,10 +1090,10 @@ constexpr size_t FB_HEAD = (size_t)PBINS * 8 + (size_t)FB_BIG * 8 + 16;
 
 // One pass of the fallback over row with the given gate (the workgroup's
 // slot: blockIdx.x).  Returns false when the gated list is too short for the
-// cut-off.  (A function of its own: inlined into the kernel's loop over the
-// queue, the walk's registers spill.)
+// cut-off.  (Inlined: a kernel that calls a function launches slower, even
+// when the queue is empty.)
 template <bool VEC>
-__device__ __noinline__ bool fb_pass(const float* __restrict__ logits, long ld, int V,
+__device__ __forceinline__ bool fb_pass(const float* __restrict__ logits, long ld, int V,
                                      const pz_row_params_dev* __restrict__ params, int n_params,
                                      const int32_t* __restrict__ hist, int H, int hcap, int nseg,
                                      const PzSplitWs& ws, const float* __restrict__ u,
@@ -922,48 +1130,58 @@ __device__ __noinline__ bool fb_pass(const float* __restrict__ logits, long ld, 
   const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
   if (tid == 0) SS.cnt = 0;
   __syncthreads();
-  for (int kb = w; kb < nseg; kb += PZ_SP_U * PZ_SP_WAVES) {
-    float ys[PZ_SP_U][4];
-    int ns[PZ_SP_U];
+  // each wave: segments w + 16 j; which of its next 64 hold a term at or
+  // above the gate, from one load per lane, then FB_U row loads in flight
+  for (int kb = w; kb < nseg; kb += 64 * PZ_SP_WAVES) {
+    const int kl = kb + lane * PZ_SP_WAVES;
+    uint64_t todo = __ballot(kl < nseg && !(seg_m[kl < nseg ? kl : 0] - M < dgate));
+    while (todo) {
+      int ks[FB_U], ns[FB_U];
+      float ys[FB_U][4];
 #pragma unroll
-    for (int uu = 0; uu < PZ_SP_U; uu++) {
-      const int k = kb + uu * PZ_SP_WAVES;
-      ns[uu] = k < nseg && !(seg_m[k] - M < dgate) ? R.load(k * PZ_SP_SEG + 4 * lane, ys[uu])
-                                                   : 0;
-    }
-#pragma unroll
-    for (int uu = 0; uu < PZ_SP_U; uu++) {
-      const int k = kb + uu * PZ_SP_WAVES;
-      if (k >= nseg) break;
-      const int e0 = k * PZ_SP_SEG + 4 * lane;
-      float (&y)[4] = ys[uu];
-      const int n = ns[uu];
-      R.apply(e0, n, y);
-      uint32_t want = 0;
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const bool wnt = (c < n) & (y[c] >= thr) & ((y[c] - M) >= dgate);
-        want |= (wnt ? 1u : 0u) << c;
-      }
-      while (__ballot(want != 0u)) {
-        bool take = false;
-        uint64_t key = 0;
-        if (want) {
-          const uint32_t j = (uint32_t)__builtin_ctz(want);
-          want &= want - 1u;
-          const float yy = j == 0 ? y[0] : (j == 1 ? y[1] : (j == 2 ? y[2] : y[3]));
-          const float e = pz_expf_l(yy - M, et);
-          take = e >= e_lo;
-          key = topp_key(e * inv, e0 + (int)j);  // top_p.c:72-74
+      for (int uu = 0; uu < FB_U; uu++) {
+        ks[uu] = -1;
+        ns[uu] = 0;
+        if (todo) {
+          const int j = (int)__builtin_ctzll(todo);
+          todo &= todo - 1ull;
+          ks[uu] = kb + j * PZ_SP_WAVES;
+          ns[uu] = R.load(ks[uu] * PZ_SP_SEG + 4 * lane, ys[uu]);
         }
-        const uint64_t ball = __ballot(take);
-        if (ball) {
-          const int leader = (int)__builtin_ctzll(ball);
-          int base = 0;
-          if (lane == leader) base = atomicAdd(&SS.cnt, __popcll(ball));
-          base = __builtin_amdgcn_readlane(base, leader);
-          // (slot_n >= V: every candidate fits)
-          if (take) keys[base + __popcll(ball & ((1ull << lane) - 1ull))] = key;
+      }
+#pragma unroll
+      for (int uu = 0; uu < FB_U; uu++) {
+        if (ks[uu] < 0) break;
+        const int e0 = ks[uu] * PZ_SP_SEG + 4 * lane;
+        float (&y)[4] = ys[uu];
+        const int n = ns[uu];
+        R.apply(e0, n, y);
+        uint32_t want = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const bool wnt = (c < n) & (y[c] >= thr) & ((y[c] - M) >= dgate);
+          want |= (wnt ? 1u : 0u) << c;
+        }
+        while (__ballot(want != 0u)) {
+          bool take = false;
+          uint64_t key = 0;
+          if (want) {
+            const uint32_t j = (uint32_t)__builtin_ctz(want);
+            want &= want - 1u;
+            const float yy = j == 0 ? y[0] : (j == 1 ? y[1] : (j == 2 ? y[2] : y[3]));
+            const float e = pz_expf_l(yy - M, et);
+            take = e >= e_lo;
+            key = topp_key(e * inv, e0 + (int)j);  // top_p.c:72-74
+          }
+          const uint64_t ball = __ballot(take);
+          if (ball) {
+            const int leader = (int)__builtin_ctzll(ball);
+            int base = 0;
+            if (lane == leader) base = atomicAdd(&SS.cnt, __popcll(ball));
+            base = __builtin_amdgcn_readlane(base, leader);
+            // (slot_n >= V: every candidate fits)
+            if (take) keys[base + __popcll(ball & ((1ull << lane) - 1ull))] = key;
+          }
         }
       }
     }
@@ -1134,7 +1352,8 @@ size_t max_sz(size_t a, size_t b) { return a > b ? a : b; }
 // sums of the small-list path / the walk over the sorted list.
 size_t topp_nucleus_bytes(int cap, int nc) {
   const size_t head = ((size_t)cap * 10 + 15) & ~(size_t)15;
-  const size_t bins = (size_t)PBINS * 8, cum = (size_t)cap * 4;
+  const size_t bins = (size_t)PBINS * 8;
+  const size_t cum = (size_t)(cap < TOPP_BITONIC_MAX ? cap : TOPP_BITONIC_MAX) * 4;
   const size_t walk = pz_sp_walk_lds((cap + PZ_SP_SEG - 1) / PZ_SP_SEG, nc);
   return head + max_sz(max_sz(bins, cum), walk);
 }
@@ -1157,23 +1376,38 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (nc < 1) return -2;
   const size_t lds3 = walk_off + pz_sp_walk_lds(pl.nseg, nc);
   // nucleus: the largest list (and its walk) that fits
+  // (pre-evaluated segments of its walk: as many as fit, 4 to 16)
   int cap = TOPP_CAP_MAX < ws.capg ? TOPP_CAP_MAX : ws.capg;
-  const int nc6 = 16;
-  while (cap > 256 && topp_nucleus_bytes(cap, nc6) + fixed > (size_t)L.max_lds) cap >>= 1;
+  int nc6 = 16;
+  while (topp_nucleus_bytes(cap, nc6) + fixed > (size_t)L.max_lds) {
+    if (nc6 > 4) nc6--;
+    else if (cap > 256) {
+      cap >>= 1;
+      nc6 = 16;
+    } else {
+      break;
+    }
+  }
   const size_t lds4 = topp_nucleus_bytes(cap, nc6);
   if (lds4 + fixed > (size_t)L.max_lds || pen_full + fixed > (size_t)L.max_lds) return -2;
+  const size_t lds5 = topp_fallback_bytes(pen_full, L.sc.slot_n);
+  if (lds5 + fixed > (size_t)L.max_lds || L.sc.slot_n / (TOPP_BIN_MAX + 1) >= FB_BIG) return -2;
+  // passes 1-3 in one launch when a slice fits in LDS beside its tables,
+  // two workgroups per CU
+  const size_t lds_front =
+      ((lds2 + 15) & ~(size_t)15) + (size_t)pl.spw * PZ_SP_SEG * sizeof(float);
+  const bool front = pl.spw <= TOPP_FRONT_SEGS && 2 * (lds_front + fixed) <= (size_t)L.max_lds;
   auto k1 = k_topp_stat<VEC>;
   auto k1e = k_topp_est<VEC>;
   auto k2 = k_topp_rec<VEC>;
   auto k3 = k_topp_walk<VEC>;
   auto k4 = k_topp_nucleus<VEC>;
   auto fb = k_topp_fallback<VEC>;
-  const void* fns[6] = {(const void*)k1, (const void*)k1e, (const void*)k2, (const void*)k3,
-                        (const void*)k4, (const void*)fb};
-  const size_t lds5 = topp_fallback_bytes(pen_full, L.sc.slot_n);
-  if (lds5 + fixed > (size_t)L.max_lds || L.sc.slot_n / (TOPP_BIN_MAX + 1) >= FB_BIG) return -2;
-  const size_t need[6] = {lds1, lds1, lds2, lds3, lds4, lds5};
-  for (int i = 0; i < 6; i++)
+  auto kf = k_topp_front<VEC>;
+  const void* fns[7] = {(const void*)k1, (const void*)k1e, (const void*)k2, (const void*)k3,
+                        (const void*)k4, (const void*)fb, (const void*)kf};
+  const size_t need[7] = {lds1, lds1, lds2, lds3, lds4, lds5, front ? lds_front : 0};
+  for (int i = 0; i < 7; i++)
     if (need[i] > 65536 && hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)need[i]) != hipSuccess)
       return -1;
@@ -1189,9 +1423,13 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   lcap = lcap < ws.capg ? lcap : ws.capg;
 #define TOPP_PASS L.logits, L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, \
                   pl.nseg, pl.spw, pl.S, ws, L.u, L.ids, L.p_out, L.sc
-  hipLaunchKernelGGL(k1, grid, block, lds1, L.stream, TOPP_PASS);
-  hipLaunchKernelGGL(k1e, grid, block, lds1, L.stream, TOPP_PASS);
-  hipLaunchKernelGGL(k2, grid, block, lds2, L.stream, TOPP_PASS, (int)pen_slice);
+  if (front) {
+    hipLaunchKernelGGL(kf, grid, block, lds_front, L.stream, TOPP_PASS, (int)pen_slice);
+  } else {
+    hipLaunchKernelGGL(k1, grid, block, lds1, L.stream, TOPP_PASS);
+    hipLaunchKernelGGL(k1e, grid, block, lds1, L.stream, TOPP_PASS);
+    hipLaunchKernelGGL(k2, grid, block, lds2, L.stream, TOPP_PASS, (int)pen_slice);
+  }
   hipLaunchKernelGGL(k3, dim3(n_rows * (1 + gS)), block, lds3, L.stream, TOPP_PASS,
                      (int)pen_full, nc, n_rows, gS, gspw, (int)goff, lcap);
   hipLaunchKernelGGL(k4, dim3(n_rows), block, lds4, L.stream, TOPP_PASS, cap, nc6);
