@@ -377,9 +377,23 @@ def run_c5(args, torch, cpu):
         call(t % nrot)
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     acc0, out0 = call(0)
+    # the kernels' time: the same verifications enqueued back to back through
+    # the device-resident entry point (inputs already in HBM), bracketed by
+    # events on the sampler's stream
+    d_in = [(torch.from_numpy(np.ascontiguousarray(w["draft_ids"], np.int32)).to(dev),
+             torch.from_numpy(np.ascontiguousarray(w["u_acc"], np.float32)).to(dev),
+             torch.from_numpy(np.ascontiguousarray(w["u_res"], np.float32)).to(dev)) for w in ws]
+    d_acc = torch.empty(B, dtype=torch.int32, device=dev)
+    d_out = torch.empty((B, K + 1), dtype=torch.int32, device=dev)
+    torch.cuda.synchronize()
+
+    def launch(k):
+        w = ws[k]
+        s.spec_verify_async(t_t[k], t_d[k], B, K, V, V, w["has_bonus"], w["tau"], *d_in[k],
+                            d_acc, d_out)
+
     kern = events_ms(torch, s.stream,
-                     [(lambda k=t % nrot: call(k)) for t in range(max(args.steps, 20))],
-                     per_call=True)
+                     [(lambda k=t % nrot: launch(k)) for t in range(max(args.steps, 20))])
     s.close()
     bpl = w0["bytes_per_seq"] * B
     r = {"workload": WORKLOAD_TEXT["c5"], "batch": B, "drafts": K, "vocab": V,

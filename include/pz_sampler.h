@@ -180,6 +180,18 @@ PZ_API int pz_spec_verify(pz_sampler *s, const float *d_target, const float *d_d
                    const float *u_acc, const float *u_res,
                    int32_t *acc_len_out, int32_t *ids_out);
 
+/* pz_spec_verify with device-resident inputs and outputs, enqueued on the
+ * sampler's stream without waiting (a decode loop that keeps everything on
+ * the device; the same kernels and results).  d_draft_ids, d_u_acc: device
+ * [B, K]; d_u_res: device [B]; d_acc_len_out: device [B]; d_ids_out: device
+ * [B, K+1].  The input buffers must stay unchanged until the stream has run
+ * the call; calls on one sampler are ordered on its stream. */
+PZ_API int pz_spec_verify_async(pz_sampler *s, const float *d_target, const float *d_draft,
+                                int B, int K, int V, long ld, int has_bonus,
+                                float temperature, const int32_t *d_draft_ids,
+                                const float *d_u_acc, const float *d_u_res,
+                                int32_t *d_acc_len_out, int32_t *d_ids_out);
+
 /* The models of a speculative decode (docs/architecture/
  * IMPLEMENTATION_PLAN.md:1675-1693), supplied by the caller, who owns their
  * weights and KV caches.  Every call gets the sampler's stream (as void*)

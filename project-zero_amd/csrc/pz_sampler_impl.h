@@ -61,8 +61,10 @@ struct pz_sampler {
   // demand by pz_spec_verify
   void* spec_dev = nullptr;
   size_t spec_dev_bytes = 0;
-  void* spec_host = nullptr;
+  void* spec_host = nullptr;   // mapped, coherent pinned inputs and outputs
+  void* spec_zc = nullptr;     // its device address
   size_t spec_host_bytes = 0;
+  bool spec_busy = false;      // a call's kernels may still read spec_host
 
   char err[512] = {0};
 };

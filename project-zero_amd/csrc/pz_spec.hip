@@ -24,7 +24,10 @@
 //   k_spec_vrec   its exact-term records;
 //   k_spec_vwalk  one workgroup per sequence: Z and the residual draw (or the
 //                 categorical draw from p), the output row.
+#include <limits.h>
 #include <string.h>
+
+#include <chrono>
 
 #include "pz_device.h"
 #include "pz_exact.h"
@@ -455,10 +458,31 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vwalk(SpecArgs A) {
 
 size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Outputs not yet written (no accepted length or id takes this value).
+constexpr int32_t kSpecPending = INT32_MIN;
+
+// Waits until every accepted length and output id has arrived in the mapped
+// buffer (true), or gives up after two seconds (false).  Each value is one
+// 4-byte store, so watching all of them needs no fence on the device side;
+// it returns several microseconds sooner than a stream synchronisation.
+bool wait_spec(volatile const int32_t* acc, int B, volatile const int32_t* out, int n) {
+  const auto t0 = std::chrono::steady_clock::now();
+  unsigned spins = 0;
+  for (int i = 0; i < n; i++) {
+    while (out[i] == kSpecPending || (i < B && acc[i] == kSpecPending))
+      if ((++spins & 0xffffu) == 0 &&
+          std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2))
+        return false;
+  }
+  return true;
+}
+
 template <bool VEC>
 int launch_spec(pz_sampler* s, SpecArgs& A) {
   const size_t fixed = 4096;
-  const PzSplitPlan pl = pz_split_plan(A.V, A.NR, A.ws.smax);
+  // stat and records over the NR rows: about two rounds of workgroups (fewer,
+  // larger slices leave a second round mostly empty; more add overhead)
+  const PzSplitPlan pl = pz_split_plan(A.V, (A.NR + 1) / 2, A.ws.smax);
   const PzSplitPlan pv = pz_split_plan(A.V, A.B, A.ws.smax);
   if (pl.nseg > A.ws.nsc) return -2;
   // two walking workgroups per CU fit when each takes at most half the LDS
@@ -496,64 +520,30 @@ int launch_spec(pz_sampler* s, SpecArgs& A) {
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-}  // namespace
-
-extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float* d_draft, int B,
-                              int K, int V, long ld, int has_bonus, float temperature,
-                              const int32_t* draft_ids, const float* u_acc, const float* u_res,
-                              int32_t* acc_len_out, int32_t* ids_out) {
-  if (!s) return PZ_EINVAL;
-  if (B < 0 || K < 1 || K > 64 || V < 1 || ld < V) return fail(s, PZ_EINVAL, "bad spec shape");
-  if (B == 0) return PZ_OK;
-  if (!d_target || !d_draft || !draft_ids || !u_acc || !u_res || !acc_len_out || !ids_out)
-    return fail(s, PZ_EINVAL, "null spec argument");
-  if (B > s->max_batch) return fail(s, PZ_ERANGE, "B=%d > max_batch=%d", B, s->max_batch);
-  if (V > s->max_vocab) return fail(s, PZ_ERANGE, "V=%d > max_vocab=%d", V, s->max_vocab);
-  PZ_HIP(s, hipSetDevice(s->device));
+// Checks the arguments, sizes the sequences' state and the row-split
+// workspace (device scratch, grown when needed, after a stream
+// synchronisation) and enqueues the launches on the sampler's stream.  The
+// inputs and outputs are device-visible addresses (device memory or mapped
+// pinned memory).
+int spec_enqueue(pz_sampler* s, const float* d_target, const float* d_draft, int B, int K, int V,
+                 long ld, int has_bonus, float temperature, const int32_t* ids_in,
+                 const float* uacc_in, const float* ures_in, int32_t* acc_out,
+                 int32_t* out_ids) {
   const int KT = K + (has_bonus ? 1 : 0);
   const int NR = B * KT + B * K;
-
-  // one input block and one output block, identical layout host and device,
-  // then the sequences' state and the row-split workspace (device only)
-  const size_t o_ids = 0;
-  const size_t o_uacc = up256(o_ids + (size_t)B * K * 4);
-  const size_t o_ures = up256(o_uacc + (size_t)B * K * 4);
-  const size_t in_bytes = up256(o_ures + (size_t)B * 4);
-  const size_t o_acc = in_bytes;
-  const size_t o_out = up256(o_acc + (size_t)B * 4);
-  const size_t io_bytes = up256(o_out + (size_t)B * (K + 1) * 4);
-  const size_t o_seq = io_bytes;
+  const size_t o_seq = 0;
   const size_t o_ws = up256(o_seq + (size_t)B * sizeof(SpecSeq));
   const size_t dev_bytes = o_ws + pz_split_ws_layout(NR + B, V, 0, nullptr, nullptr);
-
-  if (s->spec_dev_bytes < dev_bytes || s->spec_host_bytes < io_bytes) {
+  if (s->spec_dev_bytes < dev_bytes) {
     PZ_HIP(s, hipStreamSynchronize(s->stream));
-    if (s->spec_dev_bytes < dev_bytes) {
-      (void)hipFree(s->spec_dev);
-      s->spec_dev = nullptr;
-      s->spec_dev_bytes = 0;
-      if (hipMalloc(&s->spec_dev, dev_bytes) != hipSuccess)
-        return fail(s, PZ_ENOMEM, "spec scratch of %zu bytes", dev_bytes);
-      s->spec_dev_bytes = dev_bytes;
-    }
-    if (s->spec_host_bytes < io_bytes) {
-      (void)hipHostFree(s->spec_host);
-      s->spec_host = nullptr;
-      s->spec_host_bytes = 0;
-      if (hipHostMalloc(&s->spec_host, io_bytes, 0) != hipSuccess)
-        return fail(s, PZ_ENOMEM, "spec staging of %zu bytes", io_bytes);
-      s->spec_host_bytes = io_bytes;
-    }
+    (void)hipFree(s->spec_dev);
+    s->spec_dev = nullptr;
+    s->spec_dev_bytes = 0;
+    if (hipMalloc(&s->spec_dev, dev_bytes) != hipSuccess)
+      return fail(s, PZ_ENOMEM, "spec scratch of %zu bytes", dev_bytes);
+    s->spec_dev_bytes = dev_bytes;
   }
-  // earlier work on the stream may still read the staging area
-  PZ_HIP(s, hipStreamSynchronize(s->stream));
-  char* h = static_cast<char*>(s->spec_host);
   char* d = static_cast<char*>(s->spec_dev);
-  memcpy(h + o_ids, draft_ids, (size_t)B * K * 4);
-  memcpy(h + o_uacc, u_acc, (size_t)B * K * 4);
-  memcpy(h + o_ures, u_res, (size_t)B * 4);
-  PZ_HIP(s, hipMemcpyAsync(d, h, in_bytes, hipMemcpyHostToDevice, s->stream));
-
   float T = temperature;
   if (T < 1e-6f) T = 1e-6f;  // temperature.c:10 (a NaN temperature stays NaN)
   SpecArgs A;
@@ -571,11 +561,11 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   A.T.t = T;
   A.T.inv = 1.0f / T;
   A.T.div = s->temp_mode == PZ_TEMP_DIV;
-  A.draft_ids = reinterpret_cast<const int32_t*>(d + o_ids);
-  A.u_acc = reinterpret_cast<const float*>(d + o_uacc);
-  A.u_res = reinterpret_cast<const float*>(d + o_ures);
-  A.acc_len = reinterpret_cast<int32_t*>(d + o_acc);
-  A.ids_out = reinterpret_cast<int32_t*>(d + o_out);
+  A.draft_ids = ids_in;
+  A.u_acc = uacc_in;
+  A.u_res = ures_in;
+  A.acc_len = acc_out;
+  A.ids_out = out_ids;
   A.seq = reinterpret_cast<SpecSeq*>(d + o_seq);
   pz_split_ws_layout(NR + B, V, 0, d + o_ws, &A.ws);
   const bool vec = (ld % 4 == 0) && (((uintptr_t)d_target & 15) == 0) &&
@@ -584,9 +574,97 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   if (rc == -2) return fail(s, PZ_ENOTSUP, "V=%d needs more LDS than the device has", V);
   if (rc != 0) return fail(s, PZ_EDEVICE, "spec launch failed: %s",
                            hipGetErrorString(hipGetLastError()));
-  PZ_HIP(s, hipMemcpyAsync(h + o_acc, d + o_acc, io_bytes - in_bytes, hipMemcpyDeviceToHost,
-                           s->stream));
-  PZ_HIP(s, hipStreamSynchronize(s->stream));
+  return PZ_OK;
+}
+
+int spec_check(pz_sampler* s, int B, int K, int V, long ld) {
+  if (B < 0 || K < 1 || K > 64 || V < 1 || ld < V) return fail(s, PZ_EINVAL, "bad spec shape");
+  if (B > s->max_batch) return fail(s, PZ_ERANGE, "B=%d > max_batch=%d", B, s->max_batch);
+  if (V > s->max_vocab) return fail(s, PZ_ERANGE, "V=%d > max_vocab=%d", V, s->max_vocab);
+  return PZ_OK;
+}
+
+}  // namespace
+
+extern "C" int pz_spec_verify_async(pz_sampler* s, const float* d_target, const float* d_draft,
+                                    int B, int K, int V, long ld, int has_bonus,
+                                    float temperature, const int32_t* d_draft_ids,
+                                    const float* d_u_acc, const float* d_u_res,
+                                    int32_t* d_acc_len_out, int32_t* d_ids_out) {
+  if (!s) return PZ_EINVAL;
+  int rc = spec_check(s, B, K, V, ld);
+  if (rc != PZ_OK || B == 0) return rc;
+  if (!d_target || !d_draft || !d_draft_ids || !d_u_acc || !d_u_res || !d_acc_len_out ||
+      !d_ids_out)
+    return fail(s, PZ_EINVAL, "null spec argument");
+  PZ_HIP(s, hipSetDevice(s->device));
+  return spec_enqueue(s, d_target, d_draft, B, K, V, ld, has_bonus, temperature, d_draft_ids,
+                      d_u_acc, d_u_res, d_acc_len_out, d_ids_out);
+}
+
+extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float* d_draft, int B,
+                              int K, int V, long ld, int has_bonus, float temperature,
+                              const int32_t* draft_ids, const float* u_acc, const float* u_res,
+                              int32_t* acc_len_out, int32_t* ids_out) {
+  if (!s) return PZ_EINVAL;
+  int rc = spec_check(s, B, K, V, ld);
+  if (rc != PZ_OK || B == 0) return rc;
+  if (!d_target || !d_draft || !draft_ids || !u_acc || !u_res || !acc_len_out || !ids_out)
+    return fail(s, PZ_EINVAL, "null spec argument");
+  PZ_HIP(s, hipSetDevice(s->device));
+  // the inputs and outputs in mapped, coherent pinned memory: the kernels
+  // read and write them there, no copies
+  const size_t o_ids = 0;
+  const size_t o_uacc = up256(o_ids + (size_t)B * K * 4);
+  const size_t o_ures = up256(o_uacc + (size_t)B * K * 4);
+  const size_t o_acc = up256(o_ures + (size_t)B * 4);
+  const size_t o_out = up256(o_acc + (size_t)B * 4);
+  const size_t io_bytes = up256(o_out + (size_t)B * (K + 1) * 4);
+  if (s->spec_host_bytes < io_bytes) {
+    PZ_HIP(s, hipStreamSynchronize(s->stream));
+    s->spec_busy = false;
+    (void)hipHostFree(s->spec_host);
+    s->spec_host = nullptr;
+    s->spec_zc = nullptr;
+    s->spec_host_bytes = 0;
+    void* z = nullptr;
+    if (hipHostMalloc(&s->spec_host, io_bytes, hipHostMallocMapped | hipHostMallocCoherent) !=
+            hipSuccess ||
+        hipHostGetDevicePointer(&z, s->spec_host, 0) != hipSuccess)
+      return fail(s, PZ_ENOMEM, "spec staging of %zu bytes", io_bytes);
+    s->spec_zc = z;
+    s->spec_host_bytes = io_bytes;
+  }
+  // A call returns once every output is back (wait_spec), and the kernels
+  // write each sequence's outputs after their last read of its inputs: the
+  // staging area is free here unless the previous call failed.
+  if (s->spec_busy) {
+    PZ_HIP(s, hipStreamSynchronize(s->stream));
+    s->spec_busy = false;
+  }
+  char* h = static_cast<char*>(s->spec_host);
+  char* z = static_cast<char*>(s->spec_zc);
+  memcpy(h + o_ids, draft_ids, (size_t)B * K * 4);
+  memcpy(h + o_uacc, u_acc, (size_t)B * K * 4);
+  memcpy(h + o_ures, u_res, (size_t)B * 4);
+  volatile int32_t* h_acc = reinterpret_cast<volatile int32_t*>(h + o_acc);
+  volatile int32_t* h_out = reinterpret_cast<volatile int32_t*>(h + o_out);
+  for (int b = 0; b < B; b++) h_acc[b] = kSpecPending;
+  for (int i = 0; i < B * (K + 1); i++) h_out[i] = kSpecPending;
+  s->spec_busy = true;
+  rc = spec_enqueue(s, d_target, d_draft, B, K, V, ld, has_bonus, temperature,
+                    reinterpret_cast<const int32_t*>(z + o_ids),
+                    reinterpret_cast<const float*>(z + o_uacc),
+                    reinterpret_cast<const float*>(z + o_ures),
+                    reinterpret_cast<int32_t*>(z + o_acc), reinterpret_cast<int32_t*>(z + o_out));
+  if (rc != PZ_OK) return rc;
+  if (!wait_spec(h_acc, B, h_out, B * (K + 1))) {
+    PZ_HIP(s, hipStreamSynchronize(s->stream));
+    for (int i = 0; i < B * (K + 1); i++)
+      if (h_out[i] == kSpecPending || (i < B && h_acc[i] == kSpecPending))
+        return fail(s, PZ_EDEVICE, "speculative verification returned no result");
+  }
+  s->spec_busy = false;
   memcpy(acc_len_out, h + o_acc, (size_t)B * 4);
   memcpy(ids_out, h + o_out, (size_t)B * (K + 1) * 4);
   return PZ_OK;

@@ -22,7 +22,7 @@ PZ_TEMP_MUL_RECIP, PZ_TEMP_DIV = 0, 1
 ABI_SYMBOLS = (
     "pz_sampler_create", "pz_sampler_destroy", "pz_sampler_set_temp_mode",
     "pz_sampler_last_error", "pz_sampler_stream", "pz_sample_batch",
-    "pz_sample_batch_async", "pz_sampler_sync", "pz_spec_verify",
+    "pz_sample_batch_async", "pz_sampler_sync", "pz_spec_verify", "pz_spec_verify_async",
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
     "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
     "pz_sample_step", "pz_sampler_set_eos", "pz_attn_softmax", "pz_lm_head_bf16",
@@ -91,6 +91,8 @@ def load():
     lib.pz_sample_batch_noalloc.argtypes = [_I, _P, _I, _P, _I, _I, _L, _P, _I, _P, _I, _P,
                                             _P, _P]
     lib.pz_spec_verify.argtypes = [_P, _P, _P, _I, _I, _I, _L, _I, _F, _P, _P, _P, _P, _P]
+    lib.pz_spec_verify_async.argtypes = [_P, _P, _P, _I, _I, _I, _L, _I, _F, _P, _P, _P, _P,
+                                         _P]
     lib.pz_device_alloc.argtypes = [ctypes.POINTER(_P), ctypes.c_size_t, _I]
     lib.pz_device_free.argtypes = [_P]
     lib.pz_memcpy_h2d.argtypes = [_P, _P, ctypes.c_size_t]
@@ -306,6 +308,17 @@ class Sampler:
                                      _np_ptr(ua), _np_ptr(ur), _np_ptr(acc), _np_ptr(out))
         self._check(rc)
         return acc, out
+
+    def spec_verify_async(self, d_target, d_draft, B, K, V, ld, has_bonus, temperature,
+                          d_draft_ids, d_u_acc, d_u_res, d_acc_len, d_ids_out):
+        """pz_spec_verify_async: device inputs [B,K] int32 / [B,K] / [B] float32,
+        device outputs [B] and [B,K+1] int32, enqueued on the sampler's stream."""
+        _sync_torch(d_target, d_draft, d_draft_ids, d_u_acc, d_u_res, d_acc_len, d_ids_out)
+        rc = self.lib.pz_spec_verify_async(self.h, _ptr(d_target), _ptr(d_draft), B, K, V, ld,
+                                           int(has_bonus), float(temperature),
+                                           _ptr(d_draft_ids), _ptr(d_u_acc), _ptr(d_u_res),
+                                           _ptr(d_acc_len), _ptr(d_ids_out))
+        self._check(rc)
 
 
 # ---------------------------------------------------------------------------

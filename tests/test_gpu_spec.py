@@ -96,3 +96,33 @@ def test_nan_temperature(torch_cuda):
     w = wl.build_c5(B=4, K=2, V=3000, seed=0xC5 + 21)
     run(torch_cuda, w["target"], w["draft"], w["draft_ids"], w["u_acc"], w["u_res"],
         float("nan"), True, label="nan tau")
+
+
+def test_async_matches_sync_over_repeated_calls(torch_cuda):
+    """pz_spec_verify_async (device inputs and outputs, no wait) gives the
+    synchronous call's results, call after call on one sampler, including a
+    smaller batch after a larger one."""
+    torch = torch_cuda
+    for label, B, K, V, seed in (("c5 shape", 32, 4, 128256, 0xC5 + 21),
+                                 ("smaller", 8, 2, 50000, 0xC5 + 22)):
+        w = wl.build_c5(B=B, K=K, V=V, seed=seed)
+        print(f"case async {label} B={B} K={K} V={V}", flush=True)
+        d_t = to_dev(torch, np.ascontiguousarray(w["target"]))
+        d_d = to_dev(torch, np.ascontiguousarray(w["draft"]))
+        d_ids = to_dev(torch, np.ascontiguousarray(w["draft_ids"], np.int32))
+        d_ua = to_dev(torch, np.ascontiguousarray(w["u_acc"], np.float32))
+        d_ur = to_dev(torch, np.ascontiguousarray(w["u_res"], np.float32))
+        with pz.Sampler(32, 128256) as s:
+            acc, out = s.spec_verify(d_t, d_d, B, K, V, V, True, w["tau"], w["draft_ids"],
+                                     w["u_acc"], w["u_res"])
+            for rep in range(3):
+                d_acc = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+                d_out = torch.full((B, K + 1), -7, dtype=torch.int32, device="cuda")
+                s.spec_verify_async(d_t, d_d, B, K, V, V, True, w["tau"], d_ids, d_ua, d_ur,
+                                    d_acc, d_out)
+                s.sync()
+                assert (d_acc.cpu().numpy() == acc).all(), (label, rep)
+                assert (d_out.cpu().numpy() == out).all(), (label, rep)
+        wacc, wout, _ = po.spec_verify(w["target"], w["draft"], K, True, w["tau"], w["draft_ids"],
+                                       w["u_acc"], w["u_res"])
+        assert (acc == wacc).all() and (out == wout).all(), label
