@@ -9,14 +9,16 @@
 
 // Device scratch owned by a sampler (carved from one allocation).
 constexpr int PZ_FB_SLOTS = 32;        // rows the top-p fallback kernel sorts at once
+constexpr int PZ_COUNTERS = 64;        // words of pz_scratch::counters
 constexpr int PZ_TOPP_MAX_V = 200000;  // top_p.c:27 (larger rows take argmax)
 constexpr int PZ_TOPP_CAPG = 12288;    // top-p candidates a row can gather for the LDS sort
 
 struct pz_scratch {
   float* row_stat;    // [max_batch][4] per-row values handed between kernels
   int32_t* fb_list;   // [max_batch] rows queued for the top-p fallback
-  int32_t* counters;  // [16] queue counters: [0] rows queued, [1] fallback
-                      // workgroups done (both zero between calls)
+  int32_t* counters;  // [PZ_COUNTERS] queue counters: [0] rows queued, [1] fallback
+                      // workgroups done (both zero between calls); [16 + s]: sort
+                      // slot s held by a fused top-p walk (zero when free)
   uint64_t* fb_keys;  // [fb_slots][slot_n] sort buffers of the fallback
   uint64_t* fb_keys2; // [fb_slots][slot_n] its second buffer (keys in bin order)
   int slot_n;         // power of two >= min(max_vocab, PZ_TOPP_MAX_V)

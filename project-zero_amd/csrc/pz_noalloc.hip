@@ -112,7 +112,7 @@ __global__ void k_noalloc_stage(StageChunk c, uint32_t* dst, int32_t* counters,
                                 uint32_t* arrive, uint64_t* meet, uint32_t n_meet) {
   for (uint32_t i = threadIdx.x; i < c.n; i += blockDim.x) dst[c.first + i] = c.w[i];
   if (c.zero_counters) {
-    if (threadIdx.x < 16) counters[threadIdx.x] = 0;
+    if (threadIdx.x < PZ_COUNTERS) counters[threadIdx.x] = 0;
     for (uint32_t i = threadIdx.x; i < PZ_NOALLOC_MAX_BATCH; i += blockDim.x) arrive[i] = 0u;
     for (uint32_t i = threadIdx.x; i < n_meet; i += blockDim.x) meet[i] = 0ull;
   }

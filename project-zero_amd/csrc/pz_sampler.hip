@@ -48,7 +48,7 @@ size_t pz_scratch_layout(int max_batch, int max_vocab, int max_slots, void* base
   size_t off = 0;
   const size_t o_stat = off; off = up(off + B * 4 * sizeof(float));
   const size_t o_list = off; off = up(off + B * sizeof(int32_t));
-  const size_t o_cnt = off;  off = up(off + 16 * sizeof(int32_t));
+  const size_t o_cnt = off;  off = up(off + PZ_COUNTERS * sizeof(int32_t));
   const size_t o_keys = off; off = up(off + slots * slot * sizeof(uint64_t));
   const size_t o_keys2 = off; off = up(off + slots * slot * sizeof(uint64_t));
   if (base && out) {
@@ -120,7 +120,8 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   pz_scratch_layout(max_batch, max_vocab, PZ_FB_SLOTS, s->d_scratch, &s->sc);
   // queue counters start at zero; the fallback kernel re-zeroes them after
   // each launch that read them
-  if (hipMemset(s->sc.counters, 0, 16 * sizeof(int32_t)) != hipSuccess) return bail(PZ_EDEVICE);
+  if (hipMemset(s->sc.counters, 0, PZ_COUNTERS * sizeof(int32_t)) != hipSuccess)
+    return bail(PZ_EDEVICE);
   s->split_bytes = pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, nullptr, nullptr);
   if (hipMalloc(&s->d_split, s->split_bytes) != hipSuccess) return bail(PZ_ENOMEM);
   pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, s->d_split, &s->ws);

@@ -34,6 +34,8 @@
 //                  candidate sorted in a global scratch slot.
 #include <limits.h>
 
+#include <atomic>
+
 #include "pz_device.h"
 #include "pz_exact.h"
 #include "pz_launch.h"
@@ -410,26 +412,117 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_
   for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) gh[i] = ehist[i];
 }
 
-// ---- passes 1-3 in one launch, for slices that fit in LDS ---------------
-// Each workgroup reads its slice once and keeps it, the chain applied, in
-// LDS; the row's S workgroups meet twice (for the row maximum, then for the
-// estimated mass before each slice), and the estimates, the records and the
-// mass histogram all come from LDS.  At a meeting each workgroup posts one
-// 64-bit word (value and a written bit, so no fence orders it: a fence at
-// agent scope writes back or invalidates the whole L2) and wave 0 polls the
-// row's S words.  A row's workgroups are consecutive in the launch order
-// and a CU holds two of them, so every workgroup a wait depends on has been
-// dispatched: the waits end.  (The walk launch, which follows, clears the
-// words.)
-constexpr int TOPP_FRONT_SEGS = 64;  // segments of a slice held in LDS (64 KiB)
+// ---- passes 1-3, the nucleus bins and the gather in one launch ------------
+// For slices that fit in LDS.  Each workgroup reads its slice once and keeps
+// it, the chain applied, in LDS; the row's S workgroups meet twice (for the
+// row maximum, then for the estimated mass before each slice), and the
+// estimates, the records, the e histogram and the gather all come from LDS.
+// At a meeting each workgroup posts one 64-bit word (value and a written
+// bit, so no fence orders it: a fence at agent scope writes back or
+// invalidates the whole L2) and wave 0 polls the row's S words.  The
+// histograms are exchanged the same way, one word per bin (written bit, the
+// call's tag, the count).  A row's workgroups are consecutive in the launch
+// order and a CU holds two of them, so every workgroup a wait depends on has
+// been dispatched: the waits end.  (The walk launch, which follows, clears the
+// words.)  Every workgroup of a row merges the same histograms into the same
+// nucleus bins (a fixed-order reduction), gathers its slice's candidates of
+// those bins as (e, ~id) keys into the row's list (count: ws.arrive[row],
+// plus TOPP_GOVER when a wave's staging overflows), and workgroup 0 records
+// the bins' gate in the row state.
+constexpr int TOPP_FRONT_SEGS = 64;      // segments of a slice held in LDS (64 KiB)
+constexpr uint32_t TOPP_HWRITTEN = 0x80000000u;
+constexpr int TOPP_GOVER = 1 << 30;      // added to a row's count when its gather overflowed
+constexpr int TOPP_STAGE = PZ_SP_SEG / 2;  // keys a 256-term segment of LDS stages (8 B each)
+
+__device__ __forceinline__ uint32_t topp_hword(uint32_t tag, uint32_t count) {
+  return TOPP_HWRITTEN | ((tag & 0xffffu) << 15) | count;
+}
+
+// Nucleus bins of the row from its S published histograms (every thread; a
+// barrier inside): the merged counts in ehist, then wave 0's fixed-order
+// total and selection (every workgroup of the row gets the same bins).
+struct ToppSel {
+  int bsel;
+  uint32_t nsel;
+};
+__device__ __forceinline__ ToppSel topp_front_select(const uint32_t* hrow, int S, uint32_t tag,
+                                                     pz_lds_u32b* ehist, float top_p,
+                                                     ToppSel* sel_sh, float* part_sh) {
+  static_assert(PZ_TOPP_NB <= 2 * PZ_SP_BLOCK, "two bins per thread");
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const uint32_t want = TOPP_HWRITTEN | ((tag & 0xffffu) << 15);
+  const uint32_t mask = TOPP_HWRITTEN | (0xffffu << 15);
+  const int i0 = tid, i1 = tid + PZ_SP_BLOCK;
+  uint32_t c0 = 0, c1 = 0;
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    uint32_t v0[8], v1[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const uint32_t* h = hrow + (size_t)(s0 + q) * PZ_TOPP_NB;
+      const bool in = s0 + q < S;
+      v0[q] = in ? __hip_atomic_load(&h[i0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : want;
+      v1[q] = in && i1 < PZ_TOPP_NB
+                  ? __hip_atomic_load(&h[i1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                  : want;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const uint32_t* h = hrow + (size_t)(s0 + q) * PZ_TOPP_NB;
+      while ((v0[q] & mask) != want) {
+        __builtin_amdgcn_s_sleep(1);
+        v0[q] = __hip_atomic_load(&h[i0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      while ((v1[q] & mask) != want) {
+        __builtin_amdgcn_s_sleep(1);
+        v1[q] = __hip_atomic_load(&h[i1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      c0 += v0[q] & 0x7fffu;
+      c1 += v1[q] & 0x7fffu;
+    }
+  }
+  ehist[i0] = c0;
+  if (i1 < PZ_TOPP_NB) ehist[i1] = c1;
+  // the estimated total mass and count, in a fixed order (every workgroup of
+  // the row gets the same values)
+  float t = (float)c0 * ebin_mid(i0) + (i1 < PZ_TOPP_NB ? (float)c1 * ebin_mid(i1) : 0.0f);
+  uint32_t n = c0 + (i1 < PZ_TOPP_NB ? c1 : 0u);
+  t = pz_wave_sum(t);
+  n = pz_wave_sum_u32(n);
+  if (lane == 0) {
+    part_sh[w] = t;
+    part_sh[PZ_SP_WAVES + w] = __uint_as_float(n);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float tot = 0.0f;
+    uint32_t ncand = 0;
+    for (int j = 0; j < PZ_SP_WAVES; j++) {
+      tot += part_sh[j];
+      ncand += __float_as_uint(part_sh[PZ_SP_WAVES + j]);
+    }
+    int bsel;
+    uint32_t nsel;
+    topp_select_bins(ehist, tot, ncand, top_p, &bsel, &nsel);
+    if (tid == 0) {
+      sel_sh->bsel = bsel;
+      sel_sh->nsel = nsel;
+    }
+  }
+  __syncthreads();
+  return *sel_sh;
+}
 
 template <bool VEC>
 __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOPP_ARGS,
-                                                                             int pen_bytes) {
+                                                                             int pen_bytes,
+                                                                             uint32_t tag) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
   __shared__ float sest[TOPP_FRONT_SEGS];
+  __shared__ ToppSel sel_sh;
+  __shared__ float part_sh[2 * PZ_SP_WAVES];
+  __shared__ int wcnt[PZ_SP_WAVES];
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = pz_row_of(rows, blockIdx.y);
@@ -440,10 +533,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
   pz_lds_f32* ybuf = (pz_lds_f32*)(lds + (((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15));
   uint64_t* meet = ws.meet + (size_t)row * 2 * ws.smax;
-  if (tid == 0) {
-    SS.any = 0u;
-    if (blockIdx.x == 0) ws.rs[row].i[5] = 0;  // the nucleus bins of this call: not yet picked
-  }
+  if (tid == 0) SS.any = 0u;
   for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) ehist[i] = 0u;
   const PzRow<VEC> R =
       topp_row<VEC>(logits, ld, row, V, prm, lds, lo, pz_sp_hi(sl, V), hcap, hist, H);
@@ -478,7 +568,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       q.w = y[uu][3];
       *(pz_lds_f4*)(ybuf + (e0 - lo)) = q;
       m = pz_wave_max(m);
-      if (lane == 0) seg_m[k] = m;  // (NaN-free; the gather skips segments by it)
+      if (lane == 0) seg_m[k] = m;  // (NaN-free; the fallback skips segments by it)
       smx = fmaxf(smx, m);
     }
   }
@@ -521,8 +611,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   __syncthreads();
   const bool degen = topp_degenerate(SS.any);
   const float M = SS.M, thr = M - 20.0f;
-  // 2. the estimated candidate mass of each segment (as k_topp_est), and the
-  // slice's total for the slices after it
+  // 2. the estimated candidate mass of each segment (as k_topp_est) and the
+  // histogram of the estimated e (the nucleus bins), the slice's total for
+  // the slices after it
   if (!degen) {
     for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
       const int e0 = k * PZ_SP_SEG + 4 * lane;
@@ -533,12 +624,23 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       float t = 0.0f;
 #pragma unroll
       for (int c = 0; c < 4; c++)
-        if (c < n && y[c] >= thr) t += pz_fast_exp(y[c] - M);
+        if (c < n && y[c] >= thr) {
+          const float ee = pz_fast_exp(y[c] - M);
+          t += ee;
+          atomicAdd((uint32_t*)&ehist[ebin(ee)], 1u);
+        }
       t = pz_wave_sum(t);
       if (lane == 0) sest[k - sl.k0] = t;
     }
   }
   __syncthreads();
+  uint32_t* hrow = ws.hist + (size_t)blockIdx.y * S * PZ_TOPP_NB;
+  if (!degen) {
+    uint32_t* gh = hrow + (size_t)blockIdx.x * PZ_TOPP_NB;
+    for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK)
+      __hip_atomic_store(&gh[i], topp_hword(tag, ehist[i]), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (tid == 0) {
     float tot = 0.0f;
     if (!degen)
@@ -563,7 +665,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   __syncthreads();
   pz_sp_predict(ToppSliceEst{sest, sl.k0}, SS.carry, row, sl, ws, SS);
   // 3. records from LDS (as k_topp_rec)
-  ToppTermsR<ToppLdsRow> X;
+  PzExpTerms<ToppLdsRow> X;
   X.R.y = ybuf;
   X.R.lo = lo;
   X.R.V = V;
@@ -572,11 +674,111 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   X.inv = 1.0f;
   X.as_p = false;
   X.et = et;
-  X.ehist = ehist;
   pz_sp_records(X, row, sl, ws);
+  // 4. the nucleus bins (the row's histograms were published before meet 2)
   __syncthreads();
-  uint32_t* gh = ws.hist + ((size_t)blockIdx.y * S + blockIdx.x) * PZ_TOPP_NB;
-  for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) gh[i] = ehist[i];
+  const ToppSel sel = topp_front_select(hrow, S, tag, ehist, prm.top_p, &sel_sh, part_sh);
+  const bool all = sel.bsel == 0;
+  const float e_gate = all ? 0.0f : ebin_lo(sel.bsel);
+  const float dgate = all ? -__builtin_inff() : __logf(e_gate) - 0.01f;
+  if (blockIdx.x == 0 && tid == 0) {
+    PzRowState& rs = ws.rs[row];
+    rs.M = M;
+    rs.f[0] = e_gate;
+    rs.f[1] = dgate;
+    rs.i[1] = all ? 1 : 0;
+    rs.i[4] = (int)sel.nsel;
+  }
+  if (sel.nsel > (uint32_t)ws.capg) return;  // too many for the LDS sort: the fallback
+  // 5. the gather: candidates with e >= e_lo = e_gate (1 - 2^-21) (a superset
+  // gate on y - M first; exact e per candidate).  Any e below that bound has
+  // fl(e * inv) < fl(e_gate * inv) (two roundings of 2^-24 cannot close a
+  // 2^-21 gap), so every candidate with p >= fl(e_gate * inv) is gathered.
+  // Each wave stages its keys over its own segments of the LDS slice (read
+  // into registers first), then the workgroup appends them with one atomic.
+  const float e_lo = e_gate * (1.0f - 0x1p-21f);
+  constexpr int WSEG = TOPP_FRONT_SEGS / PZ_SP_WAVES;  // segments a wave owns (k0 + w + 16 j)
+  float yv[WSEG][4];
+  int nv[WSEG];
+  int cap_w = 0;  // keys the wave can stage: TOPP_STAGE per segment it owns
+#pragma unroll
+  for (int j = 0; j < WSEG; j++) {
+    const int k = sl.k0 + w + PZ_SP_WAVES * j;
+    nv[j] = 0;
+    if (k < sl.k1) {
+      cap_w += TOPP_STAGE;
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      int n = V - e0;
+      nv[j] = n < 0 ? 0 : (n > 4 ? 4 : n);
+      const pz_f4 q = *(const pz_lds_f4*)(ybuf + (e0 - lo));
+      yv[j][0] = q.x;
+      yv[j][1] = q.y;
+      yv[j][2] = q.z;
+      yv[j][3] = q.w;
+    }
+  }
+  asm volatile("" ::: "memory");  // the wave's reads of its segments come before its staging
+  int cnt = 0;  // keys this wave staged (wave-uniform)
+  bool over = false;
+#pragma unroll
+  for (int j = 0; j < WSEG; j++) {
+    const int k = sl.k0 + w + PZ_SP_WAVES * j;
+    if (k >= sl.k1) break;
+    const int e0 = k * PZ_SP_SEG + 4 * lane;
+    uint32_t want = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const bool wnt = (c < nv[j]) & (yv[j][c] >= thr) & ((yv[j][c] - M) >= dgate);
+      want |= (wnt ? 1u : 0u) << c;
+    }
+    while (__ballot(want != 0u)) {
+      bool take = false;
+      uint64_t key = 0;
+      if (want) {
+        const uint32_t c = (uint32_t)__builtin_ctz(want);
+        want &= want - 1u;
+        const float yy = pz_sel4f(yv[j][0], yv[j][1], yv[j][2], yv[j][3], (int)c);
+        const float e = pz_expf_l(yy - M, et);
+        take = e >= e_lo;
+        key = topp_key(e, e0 + (int)c);
+      }
+      const uint64_t ball = __ballot(take);
+      if (take) {
+        const int slot = cnt + __popcll(ball & ((1ull << lane) - 1ull));
+        if (slot < cap_w) {
+          // slot q of the wave: segment k0 + w + 16 (q / TOPP_STAGE), key q % TOPP_STAGE
+          const int ks = sl.k0 + w + PZ_SP_WAVES * (slot / TOPP_STAGE);
+          ((pz_lds_u64*)(ybuf + (ks - sl.k0) * PZ_SP_SEG))[slot % TOPP_STAGE] = key;
+        }
+      }
+      cnt += __popcll(ball);
+    }
+  }
+  if (cnt > cap_w) {
+    over = true;
+    cnt = cap_w;
+  }
+  if (lane == 0) wcnt[w] = cnt | (over ? TOPP_GOVER : 0);
+  __syncthreads();
+  if (tid == 0) {
+    int tot = 0;
+    bool ov = false;
+    for (int i = 0; i < PZ_SP_WAVES; i++) {
+      ov |= (wcnt[i] & TOPP_GOVER) != 0;
+      tot += wcnt[i] & (TOPP_GOVER - 1);
+    }
+    SS.cnt = tot > 0 ? (int)atomicAdd(&ws.arrive[row], (uint32_t)tot) : 0;
+    if (ov) atomicOr(&ws.arrive[row], (uint32_t)TOPP_GOVER);
+  }
+  __syncthreads();
+  int base = SS.cnt & (TOPP_GOVER - 1);
+  for (int i = 0; i < w; i++) base += wcnt[i] & (TOPP_GOVER - 1);
+  uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
+  for (int q = lane; q < cnt; q += 64) {
+    if (base + q >= ws.capg) break;  // (the count tells the walk the list overflowed)
+    const int ks = sl.k0 + w + PZ_SP_WAVES * (q / TOPP_STAGE);
+    gkeys[base + q] = ((const pz_lds_u64*)(ybuf + (ks - sl.k0) * PZ_SP_SEG))[q % TOPP_STAGE];
+  }
 }
 
 // Gather of one slice: candidates with e >= e_lo (1 - 2^-21) (a superset
@@ -1098,7 +1300,8 @@ __device__ __forceinline__ bool fb_pass(const float* __restrict__ logits, long l
                                      const int32_t* __restrict__ hist, int H, int hcap, int nseg,
                                      const PzSplitWs& ws, const float* __restrict__ u,
                                      int32_t* __restrict__ ids_out, float* __restrict__ p_out,
-                                     const pz_scratch& sc, int row, float gate) {
+                                     const pz_scratch& sc, int row, float gate, int slot,
+                                     float M, float inv, float rdgate) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   __shared__ ToppShared T;
@@ -1106,8 +1309,8 @@ __device__ __forceinline__ bool fb_pass(const float* __restrict__ logits, long l
   __shared__ int nbig, nchunks;
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  uint64_t* keys = sc.fb_keys + (size_t)blockIdx.x * sc.slot_n;
-  uint64_t* keys2 = sc.fb_keys2 + (size_t)blockIdx.x * sc.slot_n;
+  uint64_t* keys = sc.fb_keys + (size_t)slot * sc.slot_n;
+  uint64_t* keys2 = sc.fb_keys2 + (size_t)slot * sc.slot_n;
   // after the gather: bin counts (then cursors, then ends), bin starts, the
   // big-bin list, then the LDS sort buffer or the walk
   pz_lds_u32b* bcnt = (pz_lds_u32b*)lds;
@@ -1117,8 +1320,7 @@ __device__ __forceinline__ bool fb_pass(const float* __restrict__ logits, long l
   char* region = lds + FB_HEAD;
   pz_lds_u64* sbuf = (pz_lds_u64*)region;
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
-  const PzRowState rs0 = ws.rs[row];
-  const float M = rs0.M, inv = rs0.inv, thr = M - 20.0f;
+  const float thr = M - 20.0f;
   const float* seg_m = ws.seg_m + (size_t)row * ws.nsc;
   __syncthreads();  // the previous pass's LDS is free
   pz_etab_fill((pz_lds_u64*)etab);
@@ -1126,7 +1328,7 @@ __device__ __forceinline__ bool fb_pass(const float* __restrict__ logits, long l
   // gathered: every e >= e_lo, so every p >= p_lo = fl(gate * inv) (p is
   // monotone in e); dgate skips the expf of terms far below the gate
   const float e_lo = gate * (1.0f - 0x1p-21f), p_lo = gate * inv;
-  const float dgate = all ? -__builtin_inff() : rs0.f[1];
+  const float dgate = all ? -__builtin_inff() : rdgate;
   const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
   if (tid == 0) SS.cnt = 0;
   __syncthreads();
@@ -1317,9 +1519,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
     const PzRowState rs0 = ws.rs[row];
     const float gate = rs0.i[1] ? 0.0f : rs0.f[0];
     if (!fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out,
-                      p_out, sc, row, gate))
+                      p_out, sc, row, gate, blockIdx.x, rs0.M, rs0.inv, rs0.f[1]))
       fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out, p_out,
-                   sc, row, 0.0f);  // the cut-off lies past the gated list
+                   sc, row, 0.0f, blockIdx.x, rs0.M, rs0.inv,
+                   rs0.f[1]);  // the cut-off lies past the gated list
   }
   // the last workgroup out re-arms the queue for the next launch (every
   // workgroup has read counters[0] before it counts itself done)
@@ -1330,6 +1533,290 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
       atomicExch(&sc.counters[1], 0);
     }
   }
+}
+
+// ---- walk, nucleus and fallback in one launch (after k_topp_front) --------
+// One workgroup per row.  Wave 0 walks the records (the exact normaliser)
+// while waves 1..7 pre-evaluate its specials and waves 8..15 sort the keys
+// k_topp_front gathered, by e: a counting sort over PBINS bins of e and each
+// key's rank inside its bin (bins above TOPP_BIN_MAX keys: a bitonic sort
+// of p keys after the walk).  With the normaliser, e keys become p keys
+// (p = e * (1/sum) is monotone in e, so the order holds except inside runs
+// of equal p, which are put back in ascending id), and the same workgroup
+// finds the cut-off and the draw; rows whose list overflowed, or whose
+// cut-off lies below the gathered bins, take the fallback pass here, in a
+// sort slot of the scratch held under a lock (a holder never waits, so every
+// wait for a slot ends).
+constexpr int WF_SORT = PZ_SP_BLOCK / 2;  // threads of the sort (waves 8..15)
+constexpr int WF_LOCK0 = 16;             // sc.counters[16 + s]: slot s held
+
+// Barrier of waves 8..15 (a monotonic LDS counter: generation g ends when it
+// reaches 8 g).
+__device__ __forceinline__ void wf_sub_barrier(int* ctr, int& gen) {
+  gen++;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8 * gen)
+    __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// The fallback pass for row in a held sort slot (every thread; out of line).
+template <bool VEC>
+__device__ __noinline__ void wf_fallback(TOPP_ARGS, int row, float gate, float M, float inv,
+                                            float dgate, int* slot_sh) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int slot = -1;
+    for (;;) {
+      for (int i = 0; i < sc.fb_slots && slot < 0; i++)
+        if (atomicCAS(&sc.counters[WF_LOCK0 + i], 0, 1) == 0) slot = i;
+      if (slot >= 0) break;
+      __builtin_amdgcn_s_sleep(8);
+    }
+    // the slot's previous holder released its writes; drop stale lines here
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    *slot_sh = slot;
+  }
+  __syncthreads();
+  const int slot = *slot_sh;
+  if (!fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out, p_out,
+                    sc, row, gate, slot, M, inv, dgate) &&
+      gate != 0.0f)
+    fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out, p_out, sc,
+                 row, 0.0f, slot, M, inv, dgate);  // the cut-off lies past the gated list
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    atomicExch(&sc.counters[WF_LOCK0 + slot], 0);
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_bytes, int nc,
+                                                           int sort_off, int cap, int nc6) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ ToppShared T;
+  __shared__ float sum_sh;
+  __shared__ int m_sh, sb_ctr, path_sh, slot_sh;
+  __shared__ uint64_t etab[32];
+  const pz_lds_u64* et = (const pz_lds_u64*)etab;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = pz_row_of(rows, blockIdx.x);
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // k_topp_front's meetings and histograms are over: clear the row's words
+  // (plain stores: the end of this launch makes them visible to the next)
+  for (int i = tid; i < 2 * ws.smax; i += PZ_SP_BLOCK)
+    ws.meet[(size_t)row * 2 * ws.smax + i] = 0ull;
+  uint32_t* hrow = ws.hist + (size_t)blockIdx.x * S * PZ_TOPP_NB;
+  for (int i = tid; i < S * PZ_TOPP_NB; i += PZ_SP_BLOCK) hrow[i] = 0u;
+  if (tid == 0) {
+    // the gathered count, re-armed for the next call
+    m_sh = (int)ws.arrive[row];
+    ws.arrive[row] = 0u;
+    sb_ctr = 0;
+    path_sh = 0;
+  }
+  pz_sp_row_stat(row, S, ws, SS);
+  const float M = SS.M;
+  const uint32_t flags = SS.any;
+  const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
+  __syncthreads();  // the expf table, the penalty tables, m
+  if (flags & PZ_RS_Y0NAN) {
+    if (tid == 0) {
+      ids_out[row] = 0;
+      if (p_out) p_out[row] = 1.0f;
+    }
+    return;
+  }
+  if (flags & PZ_RS_NONFIN) {
+    if (tid == 0) T.first = INT_MAX;
+    __syncthreads();
+    int mine = INT_MAX;
+    for (int e0 = 4 * tid; e0 < V; e0 += 4 * PZ_SP_BLOCK) {
+      float y[4];
+      const int n = R.get(e0, y);
+      for (int c = 0; c < n; c++)
+        if (y[c] == M && e0 + c < mine) mine = e0 + c;
+    }
+    atomicMin(&T.first, mine);
+    __syncthreads();
+    if (tid == 0) {
+      ids_out[row] = T.first;
+      if (p_out) p_out[row] = __builtin_nanf("");
+    }
+    return;
+  }
+  const PzRowState rs0 = ws.rs[row];  // the nucleus bins (k_topp_front, workgroup 0)
+  const bool all = rs0.i[1] != 0;
+  const float e_gate = rs0.f[0], dgate = rs0.f[1];
+  const int m = m_sh;
+  // the list: sorted here when it fits (else the fallback)
+  const bool listed = (uint32_t)rs0.i[4] <= (uint32_t)ws.capg && m > 0 && m <= cap;
+  PzExpTerms<PzRow<VEC>> X;
+  X.R = R;
+  X.M = M;
+  X.thr = M - 20.0f;
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = et;
+  char* region = lds + pen_bytes;  // the walk's LDS, free again after it
+  pz_lds_u32b* bcnt = (pz_lds_u32b*)(lds + sort_off);
+  pz_lds_u32b* bstart = bcnt + PBINS;
+  pz_lds_u64* bkeys = (pz_lds_u64*)(bstart + PBINS);
+  pz_lds_u16* perm = (pz_lds_u16*)(bkeys + cap);
+  const uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
+  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, region, SS, 7);
+  if (w == 0) {
+    PzAcc st;
+    pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+    if (tid == 0) sum_sh = pz_acc_value(st);
+  } else if (w >= 8 && listed) {
+    // counting sort of the e keys by bin, then the rank inside each bin
+    const int tt = tid - (PZ_SP_BLOCK - WF_SORT);
+    int gen = 0;
+    for (int i = tt; i < PBINS; i += WF_SORT) bcnt[i] = 0u;
+    if (tt == 0) T.bmax = 0u;
+    wf_sub_barrier(&sb_ctr, gen);
+    for (int i = tt; i < m; i += WF_SORT) atomicAdd((uint32_t*)&bcnt[pbin(gkeys[i])], 1u);
+    wf_sub_barrier(&sb_ctr, gen);
+    // exclusive bin starts: thread tt owns bins 8 tt .. 8 tt + 7
+    constexpr int BPT = PBINS / WF_SORT;
+    uint32_t c[BPT], local = 0, mx = 0;
+#pragma unroll
+    for (int j = 0; j < BPT; j++) {
+      c[j] = bcnt[BPT * tt + j];
+      local += c[j];
+      mx = c[j] > mx ? c[j] : mx;
+    }
+    const uint32_t incl = pz_wave_scan_u32(local);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const uint32_t o = __shfl_xor(mx, off, 64);
+      mx = o > mx ? o : mx;
+    }
+    const int sw = w - 8;
+    if (lane == 63) T.wtot[sw] = incl;
+    if (lane == 0) atomicMax(&T.bmax, mx);
+    wf_sub_barrier(&sb_ctr, gen);
+    uint32_t run = incl - local;
+    for (int j = 0; j < sw; j++) run += T.wtot[j];
+#pragma unroll
+    for (int j = 0; j < BPT; j++) {
+      bstart[BPT * tt + j] = run;
+      bcnt[BPT * tt + j] = run;  // cursor
+      run += c[j];
+    }
+    wf_sub_barrier(&sb_ctr, gen);
+    for (int i = tt; i < m; i += WF_SORT) {
+      const uint64_t key = gkeys[i];
+      bkeys[atomicAdd((uint32_t*)&bcnt[pbin(key)], 1u)] = key;
+    }
+    wf_sub_barrier(&sb_ctr, gen);
+    if (T.bmax <= (uint32_t)TOPP_BIN_MAX) {
+      for (int j = tt; j < m; j += WF_SORT) {
+        const uint64_t key = bkeys[j];
+        const int q = pbin(key);
+        const uint32_t b0 = bstart[q], b1 = bcnt[q];
+        uint32_t r = 0, x = b0;
+        for (; x + 4 <= b1; x += 4) {
+          const uint64_t k0 = bkeys[x], k1 = bkeys[x + 1], k2 = bkeys[x + 2], k3 = bkeys[x + 3];
+          r += (k0 > key ? 1u : 0u) + (k1 > key ? 1u : 0u) + (k2 > key ? 1u : 0u) +
+               (k3 > key ? 1u : 0u);
+        }
+        for (; x < b1; x++) r += bkeys[x] > key ? 1u : 0u;
+        perm[b0 + r] = (uint16_t)j;
+      }
+      if (tt == 0) path_sh = 1;  // sorted through perm
+    } else if (tt == 0) {
+      path_sh = 2;  // a bin too large: bitonic sort after the walk
+    }
+  }
+  __syncthreads();
+  const float sum = sum_sh;
+  const float inv = 1.0f / sum;  // top_p.c:72
+  if (tid == 0) {
+    ws.rs[row].sum = sum;
+    ws.rs[row].inv = inv;
+  }
+  const int path = path_sh;
+  const float p_lo = e_gate * inv;
+  bool done = false, whole = false;  // whole: the list was sorted, its cut-off lies past it
+  if (listed && path == 1) {
+    for (int i = tid; i < m; i += PZ_SP_BLOCK) bkeys[i] = topp_pkey(bkeys[i], inv);
+    __syncthreads();
+    // runs of equal p (distinct e can round to one p) back in ascending id
+    for (int j = tid; j < m; j += PZ_SP_BLOCK) {
+      const float pj = key_p(bkeys[perm[j]]);
+      if (j > 0 && key_p(bkeys[perm[j - 1]]) == pj) continue;
+      int e = j + 1;
+      while (e < m && key_p(bkeys[perm[e]]) == pj) e++;
+      for (int a = j + 1; a < e; a++) {  // insertion sort of perm[j, e) by key, descending
+        const uint16_t pa = perm[a];
+        const uint64_t ka = bkeys[pa];
+        int b = a;
+        while (b > j && bkeys[perm[b - 1]] < ka) {
+          perm[b] = perm[b - 1];
+          b--;
+        }
+        perm[b] = pa;
+      }
+    }
+    __syncthreads();
+    if (m < TOPP_BINSORT_MIN) {
+      // a short list: contiguous keys and the lane-ordered walks
+      uint64_t* kk = reinterpret_cast<uint64_t*>(region);
+      float* cum = reinterpret_cast<float*>(region + (size_t)TOPP_BINSORT_MIN * 8);
+      for (int j = tid; j < m; j += PZ_SP_BLOCK) kk[j] = bkeys[perm[j]];
+      __syncthreads();
+      const int cutoff = nucleus_cutoff(kk, cum, m, prm.top_p, all, &T.cutoff);
+      if (cutoff > 0 && (all || key_p(kk[cutoff - 1]) >= p_lo)) {
+        if (tid == 0)
+          nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
+        done = true;
+      }
+    } else {
+      SortedSeg Xs;
+      Xs.bkeys = bkeys;
+      Xs.perm = perm;
+      Xs.m = m;
+      nucleus_pick(Xs, m, row, prm.top_p, u[row], all, p_lo, nc6, region, ws, SS, &T.cutoff);
+      if (T.cutoff >= 0) {
+        if (tid == 0) {
+          const uint64_t k = bkeys[perm[T.cutoff]];
+          ids_out[row] = key_id(k);
+          if (p_out) p_out[row] = key_p(k);
+        }
+        done = true;
+      }
+    }
+    whole = true;
+  } else if (listed && path == 2 && m <= TOPP_BITONIC_MAX) {
+    int N = 1;
+    while (N < m) N <<= 1;
+    for (int i = tid; i < N; i += PZ_SP_BLOCK)
+      bkeys[i] = i < m ? topp_pkey(bkeys[i], inv) : 0ull;  // (N <= cap: a power of two)
+    __syncthreads();
+    pz_bitonic_desc<PZ_SP_BLOCK>(bkeys, N);
+    uint64_t* kk = reinterpret_cast<uint64_t*>(lds + sort_off + (size_t)PBINS * 8);  // bkeys
+    float* cum = reinterpret_cast<float*>(lds + sort_off);  // bins: PBINS * 8 >= 4 * TOPP_BITONIC_MAX
+    const int cutoff = nucleus_cutoff(kk, cum, m, prm.top_p, all, &T.cutoff);
+    if (cutoff > 0 && (all || key_p(kk[cutoff - 1]) >= p_lo)) {
+      if (tid == 0)
+        nucleus_draw(kk, cum, cutoff, u[row], &ids_out[row], p_out ? &p_out[row] : nullptr);
+      done = true;
+    }
+    whole = true;
+  }
+  if (done) return;
+  // the fallback: every candidate at or above the gate (all of them when the
+  // whole gathered list was sorted without reaching the cut-off)
+  const float gate = (all || whole) ? 0.0f : e_gate;
+  wf_fallback<VEC>(logits, ld, V, rows, params, n_params, hist, H, hcap, nseg, spw, S, ws, u,
+                   ids_out, p_out, sc, row, gate, M, inv, dgate, &slot_sh);
 }
 
 // LDS of the fallback: the penalty tables during the gather, then the bins
@@ -1392,22 +1879,62 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (lds4 + fixed > (size_t)L.max_lds || pen_full + fixed > (size_t)L.max_lds) return -2;
   const size_t lds5 = topp_fallback_bytes(pen_full, L.sc.slot_n);
   if (lds5 + fixed > (size_t)L.max_lds || L.sc.slot_n / (TOPP_BIN_MAX + 1) >= FB_BIG) return -2;
-  // passes 1-3 in one launch when a slice fits in LDS beside its tables,
-  // two workgroups per CU
+  // passes 1-3, the bins and the gather in one launch when a slice fits in
+  // LDS beside its tables (two workgroups per CU), then the walk, the
+  // nucleus and the fallback in one more (the keys' sort beside the walk:
+  // the largest list that fits, a power of two for its bitonic path)
   const size_t lds_front =
       ((lds2 + 15) & ~(size_t)15) + (size_t)pl.spw * PZ_SP_SEG * sizeof(float);
-  const bool front = pl.spw <= TOPP_FRONT_SEGS && 2 * (lds_front + fixed) <= (size_t)L.max_lds;
+  const size_t wf_walk_off = (pen_full + 15) & ~(size_t)15;
+  int wf_cap = 0, wf_nc = 0;
+  size_t wf_sort_off = 0;
+  for (int c = TOPP_BITONIC_MAX; c >= 2048 && !wf_cap; c >>= 1) {
+    if (c > ws.capg) continue;
+    for (int n = 16; n >= 4; n--) {
+      const size_t so = (wf_walk_off + pz_sp_walk_lds(pl.nseg, n) + 15) & ~(size_t)15;
+      if (so + (size_t)PBINS * 8 + (size_t)c * 10 + fixed <= (size_t)L.max_lds) {
+        wf_cap = c;
+        wf_nc = n;
+        wf_sort_off = so;
+        break;
+      }
+    }
+  }
+  const size_t lds_wf0 = wf_sort_off + (size_t)PBINS * 8 + (size_t)wf_cap * 10;
+  const size_t lds_wf = lds_wf0 > lds5 ? lds_wf0 : lds5;
+  const bool front = pl.spw <= TOPP_FRONT_SEGS && 2 * (lds_front + fixed) <= (size_t)L.max_lds &&
+                     wf_cap > 0 && pl.S <= 64 && lds_wf + fixed <= (size_t)L.max_lds;
+  if (front) {
+    auto kf = k_topp_front<VEC>;
+    auto kw = k_topp_walkf<VEC>;
+    if ((lds_front > 65536 &&
+         hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)lds_front) != hipSuccess) ||
+        (lds_wf > 65536 &&
+         hipFuncSetAttribute((const void*)kw, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)lds_wf) != hipSuccess))
+      return -1;
+    static std::atomic<uint32_t> g_tag{0};
+    const uint32_t tag = g_tag.fetch_add(1, std::memory_order_relaxed);
+    hipLaunchKernelGGL(kf, dim3(pl.S, n_rows), dim3(PZ_SP_BLOCK), lds_front, L.stream, L.logits,
+                       L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pl.nseg,
+                       pl.spw, pl.S, ws, L.u, L.ids, L.p_out, L.sc, (int)pen_slice, tag);
+    hipLaunchKernelGGL(kw, dim3(n_rows), dim3(PZ_SP_BLOCK), lds_wf, L.stream, L.logits, L.ld,
+                       L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pl.nseg, pl.spw,
+                       pl.S, ws, L.u, L.ids, L.p_out, L.sc, (int)wf_walk_off, wf_nc,
+                       (int)wf_sort_off, wf_cap, wf_nc);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+  }
   auto k1 = k_topp_stat<VEC>;
   auto k1e = k_topp_est<VEC>;
   auto k2 = k_topp_rec<VEC>;
   auto k3 = k_topp_walk<VEC>;
   auto k4 = k_topp_nucleus<VEC>;
   auto fb = k_topp_fallback<VEC>;
-  auto kf = k_topp_front<VEC>;
-  const void* fns[7] = {(const void*)k1, (const void*)k1e, (const void*)k2, (const void*)k3,
-                        (const void*)k4, (const void*)fb, (const void*)kf};
-  const size_t need[7] = {lds1, lds1, lds2, lds3, lds4, lds5, front ? lds_front : 0};
-  for (int i = 0; i < 7; i++)
+  const void* fns[6] = {(const void*)k1, (const void*)k1e, (const void*)k2, (const void*)k3,
+                        (const void*)k4, (const void*)fb};
+  const size_t need[6] = {lds1, lds1, lds2, lds3, lds4, lds5};
+  for (int i = 0; i < 6; i++)
     if (need[i] > 65536 && hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)need[i]) != hipSuccess)
       return -1;
@@ -1423,13 +1950,9 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   lcap = lcap < ws.capg ? lcap : ws.capg;
 #define TOPP_PASS L.logits, L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, \
                   pl.nseg, pl.spw, pl.S, ws, L.u, L.ids, L.p_out, L.sc
-  if (front) {
-    hipLaunchKernelGGL(kf, grid, block, lds_front, L.stream, TOPP_PASS, (int)pen_slice);
-  } else {
-    hipLaunchKernelGGL(k1, grid, block, lds1, L.stream, TOPP_PASS);
-    hipLaunchKernelGGL(k1e, grid, block, lds1, L.stream, TOPP_PASS);
-    hipLaunchKernelGGL(k2, grid, block, lds2, L.stream, TOPP_PASS, (int)pen_slice);
-  }
+  hipLaunchKernelGGL(k1, grid, block, lds1, L.stream, TOPP_PASS);
+  hipLaunchKernelGGL(k1e, grid, block, lds1, L.stream, TOPP_PASS);
+  hipLaunchKernelGGL(k2, grid, block, lds2, L.stream, TOPP_PASS, (int)pen_slice);
   hipLaunchKernelGGL(k3, dim3(n_rows * (1 + gS)), block, lds3, L.stream, TOPP_PASS,
                      (int)pen_full, nc, n_rows, gS, gspw, (int)goff, lcap);
   hipLaunchKernelGGL(k4, dim3(n_rows), block, lds4, L.stream, TOPP_PASS, cap, nc6);
