@@ -477,6 +477,8 @@ struct PzWalk {
   pz_lds_u32* stc;    // [nc] parity corrections of the later ties at g0
   pz_lds_u32* rdy;    // [nc] special + 1 held by the slot (0: none yet)
   pz_lds_u32* consumed;  // specials the walker has read out of the ring
+  pz_lds_u32* s0;     // the sequential fp32 sum of segment 0's terms from 0 (bits), when
+                      // segment 0 is special 0 (else 0xffffffff)
   pz_lds_f32* tmp;    // [256] terms of a segment evaluated during the walk
   int nseg, nc, n_spec;
 };
@@ -702,6 +704,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   W.stc = (pz_lds_u32*)p;      p += (size_t)nc * 4;
   W.rdy = (pz_lds_u32*)p;      p += (size_t)nc * 4;
   W.consumed = (pz_lds_u32*)p; p += 16;
+  W.s0 = W.consumed + 1;
   W.tmp = (pz_lds_f32*)p;      p += PZ_SP_SEG * 4;
   W.d = (pz_lds_u32*)p;        p += (size_t)nseg * 4;
   W.d2 = (pz_lds_u32*)p;       p += (size_t)nseg * 4;
@@ -771,6 +774,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     W.pd[nseg] = base;
     W.chp[nseg] = cbase;
     *W.consumed = 0u;
+    *W.s0 = 0xffffffffu;
   }
   if (tid < nc) W.rdy[tid] = 0u;
   W.n_spec = sbase;
@@ -818,6 +822,21 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
       W.sinfo[sl] = inf.sinfo;
       W.spt1[sl] = inf.pt1;
       W.stc[sl] = inf.tc;
+      if (j == 0 && k == 0) {
+        // the row's first segment from a zero sum, where nearly every term is
+        // an event: its plain sequential fp32 sum, for the walker to take in
+        // one step (one lane, the terms read back in id order)
+        const pz_lds_f4* tq = (const pz_lds_f4*)(W.terms + sl * PZ_SP_SEG);
+        float sum0 = 0.0f;
+        for (int i = 0; i < PZ_SP_SEG / 4; i++) {
+          const pz_f4 t4 = tq[i];
+          sum0 = sum0 + t4.x;
+          sum0 = sum0 + t4.y;
+          sum0 = sum0 + t4.z;
+          sum0 = sum0 + t4.w;
+        }
+        *W.s0 = __float_as_uint(sum0);
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0)
@@ -1353,7 +1372,20 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
     k = b;
     if (j >= np) break;
     // special b
-    if (!pz_sp_has2<MODE>(st, pz_readlane_u32(m.gf, jl), pz_readlane_u32(m.d2, jl), thr)) {
+    bool taken = false;
+    if (j == 0 && b == 0 && st.n == 0u && st.g == 1u) {
+      // the first segment from a zero sum, pre-added (sums only grow: when
+      // its total does not meet the stop, no term of it does)
+      const uint32_t s0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)*W.s0);
+      if (s0 != 0xffffffffu &&
+          !(MODE != PZ_STOP_NONE && pz_stop_hit(__uint_as_float(s0), thr, MODE))) {
+        st = pz_acc_of(__uint_as_float(s0));
+        pz_sp_uni(st);
+        taken = true;
+      }
+    }
+    if (!taken &&
+        !pz_sp_has2<MODE>(st, pz_readlane_u32(m.gf, jl), pz_readlane_u32(m.d2, jl), thr)) {
       const uint32_t g0 = cur.g0, si = cur.sinfo;
       if (!(st.g == g0 && pz_sp_fast_pre<MODE>(st, cur, si, cur.pt1, cur.tc, thr))) {
         uint32_t P[4], Q[4];

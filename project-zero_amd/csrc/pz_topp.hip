@@ -1078,11 +1078,22 @@ struct GSortedSeg {
 // all, :81); otherwise a cut-off term below p_lo, or none inside the list,
 // means the list is too short.  Returns the picked index or -1 (too short).
 template <class X>
-__device__ __forceinline__ int nucleus_pick(const X& xs, int m, int row, float top_p, float uu, bool all,
-                            float p_lo, int nc, char* region, const PzSplitWs& ws,
-                            PzSpShared& SS, int* pick_sh) {
+__device__ __forceinline__ int nucleus_pick(const X& xs, int m, int row0, float top_p, float uu,
+                                            bool all, float p_lo, int nc, char* region,
+                                            const PzSplitWs& ws0, PzSpShared& SS, int* pick_sh,
+                                            char* lrec = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nsl = (m + PZ_SP_SEG - 1) / PZ_SP_SEG;
+  // the list's segment estimates and records: in LDS when the caller has
+  // room for them (lrec, 16 bytes per segment), else the row's global ones
+  PzSplitWs ws = ws0;
+  int row = row0;
+  if (lrec) {
+    ws.seg_s = reinterpret_cast<float*>(lrec);
+    ws.rec = reinterpret_cast<uint32_t*>(lrec + (size_t)nsl * 4);
+    ws.nsc = nsl;
+    row = 0;
+  }
   float* est = ws.seg_s + (size_t)row * ws.nsc;
   for (int k = w; k < nsl; k += PZ_SP_WAVES) {
     float v[4];
@@ -1544,11 +1555,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
 // (p = e * (1/sum) is monotone in e, so the order holds except inside runs
 // of equal p, which are put back in ascending id), and the same workgroup
 // finds the cut-off and the draw; rows whose list overflowed, or whose
-// cut-off lies below the gathered bins, take the fallback pass here, in a
-// sort slot of the scratch held under a lock (a holder never waits, so every
-// wait for a slot ends).
+// cut-off lies below the gathered bins, are queued for k_topp_fallback
+// (which follows; the fallback pass in this launch would spill its
+// registers).
 constexpr int WF_SORT = PZ_SP_BLOCK / 2;  // threads of the sort (waves 8..15)
-constexpr int WF_LOCK0 = 16;             // sc.counters[16 + s]: slot s held
 
 // Barrier of waves 8..15 (a monotonic LDS counter: generation g ends when it
 // reaches 8 g).
@@ -1562,37 +1572,6 @@ __device__ __forceinline__ void wf_sub_barrier(int* ctr, int& gen) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// The fallback pass for row in a held sort slot (every thread; out of line).
-template <bool VEC>
-__device__ __noinline__ void wf_fallback(TOPP_ARGS, int row, float gate, float M, float inv,
-                                            float dgate, int* slot_sh) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int slot = -1;
-    for (;;) {
-      for (int i = 0; i < sc.fb_slots && slot < 0; i++)
-        if (atomicCAS(&sc.counters[WF_LOCK0 + i], 0, 1) == 0) slot = i;
-      if (slot >= 0) break;
-      __builtin_amdgcn_s_sleep(8);
-    }
-    // the slot's previous holder released its writes; drop stale lines here
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    *slot_sh = slot;
-  }
-  __syncthreads();
-  const int slot = *slot_sh;
-  if (!fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out, p_out,
-                    sc, row, gate, slot, M, inv, dgate) &&
-      gate != 0.0f)
-    fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out, p_out, sc,
-                 row, 0.0f, slot, M, inv, dgate);  // the cut-off lies past the gated list
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    atomicExch(&sc.counters[WF_LOCK0 + slot], 0);
-  }
-}
-
 template <bool VEC>
 __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_bytes, int nc,
                                                            int sort_off, int cap, int nc6) {
@@ -1600,19 +1579,22 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   __shared__ PzSpShared SS;
   __shared__ ToppShared T;
   __shared__ float sum_sh;
-  __shared__ int m_sh, sb_ctr, path_sh, slot_sh;
+  __shared__ int m_sh, sb_ctr, path_sh;
   __shared__ uint64_t etab[32];
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = pz_row_of(rows, blockIdx.x);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  // k_topp_front's meetings and histograms are over: clear the row's words
-  // (plain stores: the end of this launch makes them visible to the next)
-  for (int i = tid; i < 2 * ws.smax; i += PZ_SP_BLOCK)
-    ws.meet[(size_t)row * 2 * ws.smax + i] = 0ull;
+  // k_topp_front's meetings and histograms are over: the row's words are
+  // cleared by waves 8..15 during the walk (plain stores: the end of this
+  // launch makes them visible to the next), or here by every thread on the
+  // rows that return early
   uint32_t* hrow = ws.hist + (size_t)blockIdx.x * S * PZ_TOPP_NB;
-  for (int i = tid; i < S * PZ_TOPP_NB; i += PZ_SP_BLOCK) hrow[i] = 0u;
+  auto clear_words = [&](int t0, int nt) {
+    for (int i = t0; i < 2 * ws.smax; i += nt) ws.meet[(size_t)row * 2 * ws.smax + i] = 0ull;
+    for (int i = t0; i < S * PZ_TOPP_NB; i += nt) hrow[i] = 0u;
+  };
   if (tid == 0) {
     // the gathered count, re-armed for the next call
     m_sh = (int)ws.arrive[row];
@@ -1625,6 +1607,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   const uint32_t flags = SS.any;
   const PzRow<VEC> R = topp_row<VEC>(logits, ld, row, V, prm, lds, 0, V, hcap, hist, H);
   __syncthreads();  // the expf table, the penalty tables, m
+  if (flags & (PZ_RS_Y0NAN | PZ_RS_NONFIN)) clear_words(tid, PZ_SP_BLOCK);
   if (flags & PZ_RS_Y0NAN) {
     if (tid == 0) {
       ids_out[row] = 0;
@@ -1674,7 +1657,11 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
     if (tid == 0) sum_sh = pz_acc_value(st);
-  } else if (w >= 8 && listed) {
+  } else if (w >= 8) {
+    const int tt = tid - (PZ_SP_BLOCK - WF_SORT);
+    clear_words(tt, WF_SORT);
+  }
+  if (w >= 8 && listed) {
     // counting sort of the e keys by bin, then the rank inside each bin
     const int tt = tid - (PZ_SP_BLOCK - WF_SORT);
     int gen = 0;
@@ -1783,7 +1770,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
       Xs.bkeys = bkeys;
       Xs.perm = perm;
       Xs.m = m;
-      nucleus_pick(Xs, m, row, prm.top_p, u[row], all, p_lo, nc6, region, ws, SS, &T.cutoff);
+      // (the bins are free: the list's records go there)
+      nucleus_pick(Xs, m, row, prm.top_p, u[row], all, p_lo, nc6, region, ws, SS, &T.cutoff,
+                   lds + sort_off);
       if (T.cutoff >= 0) {
         if (tid == 0) {
           const uint64_t k = bkeys[perm[T.cutoff]];
@@ -1811,12 +1800,15 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     }
     whole = true;
   }
-  if (done) return;
+  if (done || tid != 0) return;
   // the fallback: every candidate at or above the gate (all of them when the
   // whole gathered list was sorted without reaching the cut-off)
-  const float gate = (all || whole) ? 0.0f : e_gate;
-  wf_fallback<VEC>(logits, ld, V, rows, params, n_params, hist, H, hcap, nseg, spw, S, ws, u,
-                   ids_out, p_out, sc, row, gate, M, inv, dgate, &slot_sh);
+  if (whole) {
+    ws.rs[row].f[0] = 0.0f;
+    ws.rs[row].i[1] = 1;
+  }
+  const int q = atomicAdd(&sc.counters[0], 1);
+  sc.fb_list[q] = row;
 }
 
 // LDS of the fallback: the penalty tables during the gather, then the bins
@@ -1900,8 +1892,7 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
       }
     }
   }
-  const size_t lds_wf0 = wf_sort_off + (size_t)PBINS * 8 + (size_t)wf_cap * 10;
-  const size_t lds_wf = lds_wf0 > lds5 ? lds_wf0 : lds5;
+  const size_t lds_wf = wf_sort_off + (size_t)PBINS * 8 + (size_t)wf_cap * 10;
   const bool front = pl.spw <= TOPP_FRONT_SEGS && 2 * (lds_front + fixed) <= (size_t)L.max_lds &&
                      wf_cap > 0 && pl.S <= 64 && lds_wf + fixed <= (size_t)L.max_lds;
   if (front) {
@@ -1923,6 +1914,15 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
                        L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pl.nseg, pl.spw,
                        pl.S, ws, L.u, L.ids, L.p_out, L.sc, (int)wf_walk_off, wf_nc,
                        (int)wf_sort_off, wf_cap, wf_nc);
+    auto fbk = k_topp_fallback<VEC>;
+    if (lds5 > 65536 && hipFuncSetAttribute((const void*)fbk,
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            (int)lds5) != hipSuccess)
+      return -1;
+    const int fb_grid = n_rows < L.sc.fb_slots ? n_rows : L.sc.fb_slots;
+    hipLaunchKernelGGL(fbk, dim3(fb_grid), dim3(PZ_SP_BLOCK), lds5, L.stream, L.logits, L.ld,
+                       L.V, L.params, L.n_params, L.hist, L.H, L.hcap, pl.nseg, ws, L.u, L.ids,
+                       L.p_out, L.sc);
     return hipGetLastError() == hipSuccess ? 0 : -1;
   }
   auto k1 = k_topp_stat<VEC>;
