@@ -555,7 +555,7 @@ def run_attention(args, torch, cpu):
 def run_lm_head(args, torch, cpu):
     """pz_lm_head_bf16 and pz_lm_head_argmax_bf16 at vocab 128256 x hidden
     2560 (656 MB of bf16 weights: every launch streams them from HBM).
-    Bytes per launch: the weights once per batch tile, the activations, and
+    Bytes per launch: the weights once per weight pass, the activations, and
     (unfused) the logits written."""
     import numpy as np
     import pzsample as pz
@@ -577,10 +577,13 @@ def run_lm_head(args, torch, cpu):
             s.h, dw, V, n, dx, B, n, dl, V)] * steps)
         t_fu = events_ms(torch, s.stream, [lambda: s.lib.pz_lm_head_argmax_bf16(
             s.h, dw, V, n, dx, B, n, di)] * steps)
-        passes = -(-B // 8)  # batch tiles of 8 rows re-read the weights
+        # batch 4 and up: the matrix-core kernel, one weight pass per 32 rows;
+        # below, the vector kernel's single tile
+        passes = -(-B // 32) if B >= 4 else 1
         b_un = passes * V * n * 2 + B * n * 4 + B * V * 4
         b_fu = passes * V * n * 2 + B * n * 4 + B * 4
         e = {"batch": B, "weight_passes": passes,
+             "engine": "bf16 MFMA, activations in three bf16 parts" if B >= 4 else "fp32 FMA",
              "unfused_us": t_un * 1e3, "unfused_gbs": b_un / (t_un * 1e-3) / 1e9,
              "fused_us": t_fu * 1e3, "fused_gbs": b_fu / (t_fu * 1e-3) / 1e9}
         e["unfused_frac"] = e["unfused_gbs"] / HBM_PEAK_GBS

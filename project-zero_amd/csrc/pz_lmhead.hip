@@ -8,8 +8,11 @@
 // 16-bit shift), x the fp32 final-norm activations and fp32 accumulation.
 // Here B activation rows are done at once: logits[b, i] = W[i, :] . x[b, :].
 //
-// Layout and schedule (HBM-bound: W is read once per batch tile, 2 bytes per
-// weight):
+// Batch 4 and up run on the matrix cores (k_lmhead_mfma, below).  Batches of
+// 1 to 3 use the vector kernel.
+//
+// Vector kernel layout and schedule (HBM-bound: W is read once per batch
+// tile, 2 bytes per weight):
 //   * a workgroup of 4 waves owns 64 consecutive rows of W; the batch tile of
 //     x (BT rows x n fp32) is staged in LDS once per workgroup;
 //   * a wave takes 4 rows of W at a time; lane l covers elements
@@ -148,6 +151,211 @@ __global__ __launch_bounds__(64 * LM_WAVES) void k_lmhead(
   }
 }
 
+// ---- batch >= 4: bf16 MFMA ---------------------------------------------------
+// logits[b, i] = W[i, :] . x[b, :] as a GEMM on the matrix cores.  Each fp32
+// activation is split into three bf16 parts, x = x0 + x1 + x2 (its 24
+// significant bits in three 8-bit pieces, by truncation: exact for finite x;
+// an infinite or NaN x keeps x0 = x and zero parts), so every bf16 x bf16
+// product is exact in fp32 and the sum of the three part-products per weight
+// is the fp32-accumulated product the reference forms -- the order of the
+// fp32 additions differs (as it does in the VALU kernel), inside the same
+// summation bound.  A weight of +-inf would meet a zero part (inf * 0 = NaN
+// where the reference has +-inf): rows holding one are flagged while they
+// stream and recomputed with fp32 fused multiply-adds in the epilogue.
+//   * v_mfma_f32_16x16x32_bf16: A = 16 rows of W x 32 k (lane l: row l % 16,
+//     its 8 k of group l / 16, one 16-byte load), B = 32 k x 16 batch rows of
+//     one part (the same k per lane from LDS), D = 16 rows x 16 batch rows
+//     (lane l: batch row l % 16, rows 4 (l / 16) .. +3);
+//   * a workgroup of 8 waves owns LMM_ROWS = 256 rows of W (2 tiles of 16 per
+//     wave; two workgroups per CU, one loading while the other computes),
+//     walks k in chunks of LMM_KC: the chunk's activation parts of the
+//     batch tile (16 NT rows) in LDS, each wave's W loads for the chunk all in
+//     flight (8 per tile), three parts x NT MFMAs per 32 k and tile;
+//   * W is read once per batch tile of 16 NT rows; the activations once per
+//     workgroup.
+// MODE 1 (argmax keys) as in k_lmhead.
+typedef __bf16 lm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float lm_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t lm_u32x4 __attribute__((ext_vector_type(4)));
+constexpr int LMM_WAVES = 8;
+constexpr int LMM_TILES = 2;                       // 16-row tiles per wave
+constexpr int LMM_ROWS = LMM_WAVES * LMM_TILES * 16;  // 256 (two workgroups per CU)
+constexpr int LMM_KC = 128;                        // k per LDS chunk
+constexpr int LMM_KS = LMM_KC / 32;                // MFMA k-steps per chunk
+constexpr int LMM_PAD = 8;                         // bf16 of padding per LDS row (banks)
+constexpr int LMM_RS = LMM_KC + LMM_PAD;           // LDS row stride in bf16
+
+__device__ __forceinline__ float lm_bf16_f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// A 16-byte load of 8 weights holds an infinite or NaN one.
+__device__ __forceinline__ bool lm_nonfinite8(const lm_u32x4 q) {
+  bool r = false;
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+    r |= ((q[c] & 0x7f800000u) == 0x7f800000u) | ((q[c] & 0x7f80u) == 0x7f80u);
+  return r;
+}
+
+template <int NT, int MODE>
+__global__ __launch_bounds__(64 * LMM_WAVES) __attribute__((amdgpu_waves_per_eu(4))) void k_lmhead_mfma(
+    const uint16_t* __restrict__ W, int V, int n, const float* __restrict__ X, long ldx, int nb,
+    float* __restrict__ logits, long ld, unsigned long long* __restrict__ keys,
+    uint8_t* __restrict__ nan0) {
+  // the chunk's activation parts: [3][16 NT][LMM_RS] bf16
+  __shared__ __align__(16) uint16_t xs[3 * 16 * NT * LMM_RS];
+  __shared__ unsigned long long best_sh[LMM_WAVES][16 * NT];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int m = lane & 15, g = lane >> 4;
+  const int wrow0 = blockIdx.x * LMM_ROWS + w * LMM_TILES * 16;  // the wave's first row
+  lm_f32x4 acc[LMM_TILES][NT];
+#pragma unroll
+  for (int t = 0; t < LMM_TILES; t++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[t][j] = lm_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // this lane's W rows (clamped into range: rows past V compute unused values)
+  const uint16_t* wr[LMM_TILES];
+#pragma unroll
+  for (int t = 0; t < LMM_TILES; t++) {
+    const int r = wrow0 + t * 16 + m;
+    wr[t] = W + (size_t)(r < V ? r : V - 1) * n;
+  }
+  uint32_t bad = 0;  // bit t: this lane's row of tile t holds a non-finite weight
+  for (int k0 = 0; k0 < n; k0 += LMM_KC) {
+    // this chunk's W, every load in flight before the MFMAs (the previous
+    // chunk's MFMAs are done with the LDS once the barrier passes)
+    lm_u32x4 a[LMM_TILES][LMM_KS];
+#pragma unroll
+    for (int t = 0; t < LMM_TILES; t++)
+#pragma unroll
+      for (int s = 0; s < LMM_KS; s++) {
+        const int k = k0 + 32 * s + 8 * g;
+        a[t][s] = k < n ? *reinterpret_cast<const lm_u32x4*>(wr[t] + k) : lm_u32x4{0u, 0u, 0u, 0u};
+      }
+    __syncthreads();
+    for (int i = tid; i < 16 * NT * LMM_KC; i += 64 * LMM_WAVES) {
+      const int b = i / LMM_KC, kk = i - b * LMM_KC;
+      const float x = b < nb && k0 + kk < n ? X[(size_t)b * ldx + k0 + kk] : 0.0f;
+      const uint32_t ux = __float_as_uint(x);
+      const bool fin = (ux & 0x7f800000u) != 0x7f800000u;
+      // (a NaN whose payload sits in the low bits stays a NaN)
+      const uint16_t h0 = fin || !(ux & 0x7fffffu) ? (uint16_t)(ux >> 16) : (uint16_t)0x7fc0u;
+      const float r0 = fin ? x - lm_bf16_f(h0) : 0.0f;  // exact: x's low 16 significand bits
+      const uint16_t h1 = (uint16_t)(__float_as_uint(r0) >> 16);
+      const float r1 = r0 - lm_bf16_f(h1);  // exact: at most 8 significant bits left
+      const uint16_t h2 = (uint16_t)(__float_as_uint(r1) >> 16);
+      xs[(0 * 16 * NT + b) * LMM_RS + kk] = h0;
+      xs[(1 * 16 * NT + b) * LMM_RS + kk] = h1;
+      xs[(2 * 16 * NT + b) * LMM_RS + kk] = h2;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < LMM_KS; s++) {
+      lm_bf16x8 bx[3][NT];
+#pragma unroll
+      for (int p = 0; p < 3; p++)
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+          bx[p][j] = *reinterpret_cast<const lm_bf16x8*>(
+              &xs[(p * 16 * NT + j * 16 + m) * LMM_RS + 32 * s + 8 * g]);
+#pragma unroll
+      for (int t = 0; t < LMM_TILES; t++) {
+        bad |= lm_nonfinite8(a[t][s]) ? 1u << t : 0u;
+        const lm_bf16x8 av = __builtin_bit_cast(lm_bf16x8, a[t][s]);
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+          // the largest part first: the small ones add to an accumulator of
+          // the product's own size
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[2][j], acc[t][j], 0, 0, 0);
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[1][j], acc[t][j], 0, 0, 0);
+          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[0][j], acc[t][j], 0, 0, 0);
+        }
+      }
+    }
+  }
+  // rows with a non-finite weight: fp32 fused multiply-adds over k (lanes),
+  // in every batch row, into the lanes that hold them (rare: a loop per row)
+#pragma unroll
+  for (int t = 0; t < LMM_TILES; t++) {
+    uint64_t rows_bad = __ballot((bad >> t) & 1u) ;
+    // lanes l, l + 16, l + 32, l + 48 share a row: fold the groups
+    const uint32_t rb = (uint32_t)(rows_bad | (rows_bad >> 16) | (rows_bad >> 32) | (rows_bad >> 48)) &
+                        0xffffu;
+    for (uint32_t mm = rb; mm; mm &= mm - 1u) {
+      const int r16 = (int)__builtin_ctz(mm);
+      const int row = wrow0 + t * 16 + r16;
+      if (row >= V) break;
+      const uint16_t* wrow = W + (size_t)row * n;
+      for (int b = 0; b < nb && b < 16 * NT; b++) {
+        float d = 0.0f;
+        for (int k = lane; k < n; k += 64)
+          d = __builtin_fmaf(lm_bf16_f(wrow[k]), X[(size_t)b * ldx + k], d);
+        d = pz_wave_sum(d);
+        if (g == (r16 >> 2) && m == (b & 15))
+#pragma unroll
+          for (int j = 0; j < NT; j++)
+            if (j == (b >> 4))
+#pragma unroll
+              for (int i = 0; i < 4; i++)
+                if (i == (r16 & 3)) acc[t][j][i] = d;
+      }
+    }
+  }
+  // epilogue: lane l holds batch row 16 j + l % 16, rows 4 (l / 16) + i of each tile
+  unsigned long long best[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) best[j] = 0ull;
+#pragma unroll
+  for (int t = 0; t < LMM_TILES; t++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      const int b = 16 * j + m;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = wrow0 + t * 16 + 4 * g + i;
+        const float v = acc[t][j][i];
+        if (row < V && b < nb) {
+          if (MODE == 0) {
+            logits[(size_t)b * ld + row] = v;
+          } else {
+            if (row == 0) nan0[b] = v != v ? 1 : 0;
+            if (!(v != v)) {
+              const unsigned long long kk = argmax_key(v, row);
+              best[j] = kk > best[j] ? kk : best[j];
+            }
+          }
+        }
+      }
+    }
+  if (MODE == 1) {
+    // the maximum key per batch row: over the four lane groups, then the waves
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+#pragma unroll
+      for (int off = 16; off < 64; off <<= 1) {
+        const unsigned long long o = __shfl_xor(best[j], off, 64);
+        best[j] = o > best[j] ? o : best[j];
+      }
+      if (g == 0) best_sh[w][16 * j + m] = best[j];
+    }
+    __syncthreads();
+    if (tid < 16 * NT && tid < nb) {
+      unsigned long long mx = best_sh[0][tid];
+      for (int i = 1; i < LMM_WAVES; i++) mx = best_sh[i][tid] > mx ? best_sh[i][tid] : mx;
+      if (mx) atomicMax(&keys[tid], mx);
+    }
+  }
+}
+
+template <int NT, int MODE>
+int launch_mfma(pz_sampler* s, const uint16_t* d_w, int V, int n, const float* x, long ldx,
+                int nb, float* out, long ld, unsigned long long* keys, uint8_t* nan0) {
+  const int grid = (V + LMM_ROWS - 1) / LMM_ROWS;
+  hipLaunchKernelGGL((k_lmhead_mfma<NT, MODE>), dim3(grid), dim3(64 * LMM_WAVES), 0, s->stream,
+                     d_w, V, n, x, ldx, nb, out, ld, keys, nan0);
+  PZ_HIP(s, hipGetLastError());
+  return PZ_OK;
+}
+
 // Keys to ids (argmax.c:3-13); clears the keys for the next call.
 __global__ void k_lmhead_finish(int B, unsigned long long* keys, const uint8_t* nan0,
                                 int32_t* ids) {
@@ -187,6 +395,21 @@ int tile_for(int B, int n) {
 template <int MODE>
 int run(pz_sampler* s, const uint16_t* d_w, int V, int n, const float* d_x, int B, long ldx,
         float* d_logits, long ld) {
+  // batch 4 and up: the matrix cores, batch tiles of 32 (or 16), W 16-byte
+  // aligned with rows of a multiple of 8 weights
+  if (B >= 4 && n % 8 == 0 && ((uintptr_t)d_w & 15) == 0) {
+    for (int b0 = 0; b0 < B; b0 += 32) {
+      const int nb = B - b0 < 32 ? B - b0 : 32;
+      const float* x = d_x + (size_t)b0 * ldx;
+      float* out = MODE == 0 ? d_logits + (size_t)b0 * ld : nullptr;
+      unsigned long long* keys = s->d_lmh_keys + b0;
+      uint8_t* nan0 = s->d_lmh_nan + b0;
+      const int rc = nb > 16 ? launch_mfma<2, MODE>(s, d_w, V, n, x, ldx, nb, out, ld, keys, nan0)
+                             : launch_mfma<1, MODE>(s, d_w, V, n, x, ldx, nb, out, ld, keys, nan0);
+      if (rc != PZ_OK) return rc;
+    }
+    return PZ_OK;
+  }
   const int bt = tile_for(B, n);
   if (!bt) return fail(s, PZ_ENOTSUP, "n=%d: the activation row does not fit in LDS", n);
   for (int b0 = 0; b0 < B; b0 += bt) {
