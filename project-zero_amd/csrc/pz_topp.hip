@@ -1560,6 +1560,19 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
 // registers).
 constexpr int WF_SORT = PZ_SP_BLOCK / 2;  // threads of the sort (waves 8..15)
 
+__host__ __device__ inline int pz_pow2_ceil(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+// Offset of the keys in the fused walk's sort LDS (packed bins, then the
+// order): at least 4 * TOPP_BITONIC_MAX bytes before them, for the bitonic
+// path's running sums.
+__host__ __device__ inline size_t wf_keys_off(int cap) {
+  const size_t o = ((size_t)PBINS * 4 + (size_t)cap * 2 + 15) & ~(size_t)15;
+  return o > (size_t)TOPP_BITONIC_MAX * 4 ? o : (size_t)TOPP_BITONIC_MAX * 4;
+}
+
 // Barrier of waves 8..15 (a monotonic LDS counter: generation g ends when it
 // reaches 8 g).
 __device__ __forceinline__ void wf_sub_barrier(int* ctr, int& gen) {
@@ -1647,10 +1660,12 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   X.as_p = false;
   X.et = et;
   char* region = lds + pen_bytes;  // the walk's LDS, free again after it
+  // the sort's LDS: bin counts and starts packed two per word (every count
+  // fits 16 bits: cap < 65536), the order, the keys
   pz_lds_u32b* bcnt = (pz_lds_u32b*)(lds + sort_off);
-  pz_lds_u32b* bstart = bcnt + PBINS;
-  pz_lds_u64* bkeys = (pz_lds_u64*)(bstart + PBINS);
-  pz_lds_u16* perm = (pz_lds_u16*)(bkeys + cap);
+  pz_lds_u32b* bstart = bcnt + PBINS / 2;
+  pz_lds_u16* perm = (pz_lds_u16*)(bstart + PBINS / 2);
+  pz_lds_u64* bkeys = (pz_lds_u64*)(lds + sort_off + wf_keys_off(cap));
   const uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
   const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, region, SS, 7);
   if (w == 0) {
@@ -1665,17 +1680,20 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     // counting sort of the e keys by bin, then the rank inside each bin
     const int tt = tid - (PZ_SP_BLOCK - WF_SORT);
     int gen = 0;
-    for (int i = tt; i < PBINS; i += WF_SORT) bcnt[i] = 0u;
+    for (int i = tt; i < PBINS / 2; i += WF_SORT) bcnt[i] = 0u;
     if (tt == 0) T.bmax = 0u;
     wf_sub_barrier(&sb_ctr, gen);
-    for (int i = tt; i < m; i += WF_SORT) atomicAdd((uint32_t*)&bcnt[pbin(gkeys[i])], 1u);
+    for (int i = tt; i < m; i += WF_SORT) {
+      const int q = pbin(gkeys[i]);
+      atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
+    }
     wf_sub_barrier(&sb_ctr, gen);
-    // exclusive bin starts: thread tt owns bins 8 tt .. 8 tt + 7
+    // exclusive bin starts: thread tt owns bins 8 tt .. 8 tt + 7 (words 4 tt ..)
     constexpr int BPT = PBINS / WF_SORT;
     uint32_t c[BPT], local = 0, mx = 0;
 #pragma unroll
     for (int j = 0; j < BPT; j++) {
-      c[j] = bcnt[BPT * tt + j];
+      c[j] = (bcnt[(BPT * tt + j) >> 1] >> (16 * (j & 1))) & 0xffffu;
       local += c[j];
       mx = c[j] > mx ? c[j] : mx;
     }
@@ -1692,22 +1710,26 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     uint32_t run = incl - local;
     for (int j = 0; j < sw; j++) run += T.wtot[j];
 #pragma unroll
-    for (int j = 0; j < BPT; j++) {
-      bstart[BPT * tt + j] = run;
-      bcnt[BPT * tt + j] = run;  // cursor
-      run += c[j];
+    for (int j = 0; j < BPT; j += 2) {
+      const uint32_t s0 = run, s1 = run + c[j];
+      bstart[(BPT * tt + j) >> 1] = s0 | (s1 << 16);
+      bcnt[(BPT * tt + j) >> 1] = s0 | (s1 << 16);  // cursors
+      run = s1 + c[j + 1];
     }
     wf_sub_barrier(&sb_ctr, gen);
     for (int i = tt; i < m; i += WF_SORT) {
       const uint64_t key = gkeys[i];
-      bkeys[atomicAdd((uint32_t*)&bcnt[pbin(key)], 1u)] = key;
+      const int q = pbin(key);
+      const uint32_t old = atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
+      bkeys[(old >> (16 * (q & 1))) & 0xffffu] = key;
     }
     wf_sub_barrier(&sb_ctr, gen);
     if (T.bmax <= (uint32_t)TOPP_BIN_MAX) {
       for (int j = tt; j < m; j += WF_SORT) {
         const uint64_t key = bkeys[j];
         const int q = pbin(key);
-        const uint32_t b0 = bstart[q], b1 = bcnt[q];
+        const uint32_t b0 = (bstart[q >> 1] >> (16 * (q & 1))) & 0xffffu;
+        const uint32_t b1 = (bcnt[q >> 1] >> (16 * (q & 1))) & 0xffffu;
         uint32_t r = 0, x = b0;
         for (; x + 4 <= b1; x += 4) {
           const uint64_t k0 = bkeys[x], k1 = bkeys[x + 1], k2 = bkeys[x + 2], k3 = bkeys[x + 3];
@@ -1783,15 +1805,15 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
       }
     }
     whole = true;
-  } else if (listed && path == 2 && m <= TOPP_BITONIC_MAX) {
-    int N = 1;
-    while (N < m) N <<= 1;
+  } else if (listed && path == 2 && m <= TOPP_BITONIC_MAX && pz_pow2_ceil(m) <= cap) {
+    const int N = pz_pow2_ceil(m);
     for (int i = tid; i < N; i += PZ_SP_BLOCK)
-      bkeys[i] = i < m ? topp_pkey(bkeys[i], inv) : 0ull;  // (N <= cap: a power of two)
+      bkeys[i] = i < m ? topp_pkey(bkeys[i], inv) : 0ull;
     __syncthreads();
     pz_bitonic_desc<PZ_SP_BLOCK>(bkeys, N);
-    uint64_t* kk = reinterpret_cast<uint64_t*>(lds + sort_off + (size_t)PBINS * 8);  // bkeys
-    float* cum = reinterpret_cast<float*>(lds + sort_off);  // bins: PBINS * 8 >= 4 * TOPP_BITONIC_MAX
+    uint64_t* kk = reinterpret_cast<uint64_t*>(lds + sort_off + wf_keys_off(cap));  // bkeys
+    // the running sums over the bins and the order (free here): m <= 8192 floats
+    float* cum = reinterpret_cast<float*>(lds + sort_off);
     const int cutoff = nucleus_cutoff(kk, cum, m, prm.top_p, all, &T.cutoff);
     if (cutoff > 0 && (all || key_p(kk[cutoff - 1]) >= p_lo)) {
       if (tid == 0)
@@ -1880,11 +1902,11 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   const size_t wf_walk_off = (pen_full + 15) & ~(size_t)15;
   int wf_cap = 0, wf_nc = 0;
   size_t wf_sort_off = 0;
-  for (int c = TOPP_BITONIC_MAX; c >= 2048 && !wf_cap; c >>= 1) {
+  for (int c = TOPP_CAP_MAX; c >= 2048 && !wf_cap; c -= 1024) {
     if (c > ws.capg) continue;
     for (int n = 16; n >= 4; n--) {
       const size_t so = (wf_walk_off + pz_sp_walk_lds(pl.nseg, n) + 15) & ~(size_t)15;
-      if (so + (size_t)PBINS * 8 + (size_t)c * 10 + fixed <= (size_t)L.max_lds) {
+      if (so + wf_keys_off(c) + (size_t)c * 8 + fixed <= (size_t)L.max_lds) {
         wf_cap = c;
         wf_nc = n;
         wf_sort_off = so;
@@ -1892,7 +1914,7 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
       }
     }
   }
-  const size_t lds_wf = wf_sort_off + (size_t)PBINS * 8 + (size_t)wf_cap * 10;
+  const size_t lds_wf = wf_sort_off + wf_keys_off(wf_cap) + (size_t)wf_cap * 8;
   const bool front = pl.spw <= TOPP_FRONT_SEGS && 2 * (lds_front + fixed) <= (size_t)L.max_lds &&
                      wf_cap > 0 && pl.S <= 64 && lds_wf + fixed <= (size_t)L.max_lds;
   if (front) {
