@@ -63,8 +63,7 @@ WORKLOAD_TEXT = {
 }
 KERNELS = {
     "c4": "k_greedy",
-    "c2": "k_topp_max + k_topp_est + k_topp_rec + k_topp_walk + k_topp_gather + "
-          "k_topp_nucleus + k_topp_fallback",
+    "c2": "k_topp_front + k_topp_walkf + k_topp_fallback",
     "c3": "k_topk",
     "c1": "k_topk",
     "c5": "k_spec_stat + k_spec_rec + k_spec_walk + k_spec_accept + k_spec_vest + "
