@@ -1162,10 +1162,12 @@ __device__ __forceinline__ bool pz_sp_slot_ready(const PzWalk& W, int j) {
 }
 
 // The pre-evaluated data of special j (one round of LDS reads), once in the
-// ring.
-__device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int j, PzSpSeg& d) {
+// ring (ready: the caller has seen it there).
+__device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int j, PzSpSeg& d,
+                                                bool ready = false) {
   const int lane = threadIdx.x & 63;
-  while (!pz_sp_slot_ready(W, j)) __builtin_amdgcn_s_sleep(1);
+  if (!ready)
+    while (!pz_sp_slot_ready(W, j)) __builtin_amdgcn_s_sleep(1);
   const int s = j % W.nc;
   d.g0 = (uint32_t)W.g0[s];
   d.sinfo = W.sinfo[s];
@@ -1345,19 +1347,20 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
     const int b = __builtin_amdgcn_readlane(m.k, jl);
     PzSpSeg cur = nxt;
     if (j < np && !have) pz_sp_load_slot(W, j, cur);
-    // the next special's loads overlap this step when it is already in the
-    // ring; the slots of the specials before j are released to the
-    // producers once their reads are done (special j's slot stays: the
-    // serial path reads its terms there).  The producer of special j + 1
-    // needs consumed > j + 1 - nc, which holds with nc >= 2.
-    have = j + 1 < np && pz_sp_slot_ready(W, j + 1);
-    if (have) pz_sp_load_slot(W, j + 1, nxt);
+    // the slots of the specials before j are released to the producers (their
+    // reads are done: special j's data came in with the last step's loads;
+    // special j's slot stays, the serial path reads its terms there), then
+    // the next special's loads, when it is already in the ring, overlap this
+    // step (no fence waits for them).  The producer of special j + 1 needs
+    // consumed > j + 1 - nc, which holds with nc >= 2.
     if (j < np) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
       if (lane == 0)
         __hip_atomic_store((uint32_t*)W.consumed, (uint32_t)j, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+    have = j + 1 < np && pz_sp_slot_ready(W, j + 1);
+    if (have) pz_sp_load_slot(W, j + 1, nxt, true);
     if (k < b) {
       const uint32_t D = pz_readlane_u32(m.D, jl), G = pz_readlane_u32(m.G, jl);
       if (G == st.g && D < (1u << 24) - st.n &&
