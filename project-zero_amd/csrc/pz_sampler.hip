@@ -122,9 +122,10 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   // each launch that read them
   if (hipMemset(s->sc.counters, 0, PZ_COUNTERS * sizeof(int32_t)) != hipSuccess)
     return bail(PZ_EDEVICE);
-  s->split_bytes = pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, nullptr, nullptr);
+  s->split_bytes =
+      pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, nullptr, nullptr, true);
   if (hipMalloc(&s->d_split, s->split_bytes) != hipSuccess) return bail(PZ_ENOMEM);
-  pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, s->d_split, &s->ws);
+  pz_split_ws_layout(max_batch, max_vocab, PZ_TOPP_CAPG, s->d_split, &s->ws, true);
   // arrival counters start at zero; every pass's last workgroup re-zeroes
   // its row's
   if (hipMemset(s->d_split, 0, s->split_bytes) != hipSuccess) return bail(PZ_EDEVICE);

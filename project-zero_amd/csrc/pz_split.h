@@ -116,13 +116,21 @@ inline PzSplitPlan pz_split_plan(int V, int nrows, int smax) {
   return p;
 }
 
+// Segments of a row slice the top-p front launch keeps in LDS (64 KiB).
+constexpr int PZ_SP_FRONT_SEGS = 64;
+
 // Bytes of a workspace for `rows` rows of up to V ids (top-p buffers when
-// capg > 0); with base != nullptr also carves it.
-inline size_t pz_split_ws_layout(int rows, int V, int capg, void* base, PzSplitWs* out) {
+// capg > 0); with base != nullptr also carves it.  front_hist: histogram
+// slots for the top-p front launch at any batch (every row's slices at
+// once), else for one round of workgroups.
+inline size_t pz_split_ws_layout(int rows, int V, int capg, void* base, PzSplitWs* out,
+                                 bool front_hist = false) {
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const int nsc = pz_sp_nseg(V);
   const int smax = (nsc + PZ_SP_WAVES - 1) / PZ_SP_WAVES;
-  const int hslots = capg > 0 ? PZ_SP_TARGET_WG + rows : 0;
+  const int sfront = (nsc + PZ_SP_FRONT_SEGS - 1) / PZ_SP_FRONT_SEGS;
+  const int hslots =
+      capg > 0 ? PZ_SP_TARGET_WG + rows * (front_hist && sfront > 1 ? sfront : 1) : 0;
   const size_t R = (size_t)rows;
   size_t off = 0;
   const size_t o_rs = off;   off = up(off + R * sizeof(PzRowState));

@@ -429,7 +429,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_
 // those bins as (e, ~id) keys into the row's list (count: ws.arrive[row],
 // plus TOPP_GOVER when a wave's staging overflows), and workgroup 0 records
 // the bins' gate in the row state.
-constexpr int TOPP_FRONT_SEGS = 64;      // segments of a slice held in LDS (64 KiB)
+constexpr int TOPP_FRONT_SEGS = PZ_SP_FRONT_SEGS;  // segments of a slice held in LDS
 constexpr uint32_t TOPP_HWRITTEN = 0x80000000u;
 constexpr int TOPP_GOVER = 1 << 30;      // added to a row's count when its gather overflowed
 constexpr int TOPP_STAGE = PZ_SP_SEG / 2;  // keys a 256-term segment of LDS stages (8 B each)
@@ -1897,8 +1897,18 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   // LDS beside its tables (two workgroups per CU), then the walk, the
   // nucleus and the fallback in one more (the keys' sort beside the walk:
   // the largest list that fits, a power of two for its bitonic path)
-  const size_t lds_front =
-      ((lds2 + 15) & ~(size_t)15) + (size_t)pl.spw * PZ_SP_SEG * sizeof(float);
+  // the front launch's slices: the plan's, or -- when a batch is large
+  // enough that the plan's slices exceed LDS -- TOPP_FRONT_SEGS segments,
+  // the rows then running in several rounds of workgroups (every row's
+  // histogram slots at once)
+  PzSplitPlan pf = pl;
+  if (pf.spw > TOPP_FRONT_SEGS) {
+    pf.spw = TOPP_FRONT_SEGS;
+    pf.S = (pl.nseg + pf.spw - 1) / pf.spw;
+  }
+  const size_t pen_slice_f = pen_region(L, pf.spw * PZ_SP_SEG);
+  const size_t lds_front = ((pen_slice_f + PZ_TOPP_NB * 4 + 15) & ~(size_t)15) +
+                           (size_t)pf.spw * PZ_SP_SEG * sizeof(float);
   const size_t wf_walk_off = (pen_full + 15) & ~(size_t)15;
   int wf_cap = 0, wf_nc = 0;
   size_t wf_sort_off = 0;
@@ -1915,8 +1925,9 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
     }
   }
   const size_t lds_wf = wf_sort_off + wf_keys_off(wf_cap) + (size_t)wf_cap * 8;
-  const bool front = pl.spw <= TOPP_FRONT_SEGS && 2 * (lds_front + fixed) <= (size_t)L.max_lds &&
-                     wf_cap > 0 && pl.S <= 64 && lds_wf + fixed <= (size_t)L.max_lds;
+  const bool front = (size_t)n_rows * pf.S <= (size_t)ws.hslots && pf.S <= 64 &&
+                     2 * (lds_front + fixed) <= (size_t)L.max_lds && wf_cap > 0 &&
+                     lds_wf + fixed <= (size_t)L.max_lds;
   if (front) {
     auto kf = k_topp_front<VEC>;
     auto kw = k_topp_walkf<VEC>;
@@ -1929,12 +1940,12 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
       return -1;
     static std::atomic<uint32_t> g_tag{0};
     const uint32_t tag = g_tag.fetch_add(1, std::memory_order_relaxed);
-    hipLaunchKernelGGL(kf, dim3(pl.S, n_rows), dim3(PZ_SP_BLOCK), lds_front, L.stream, L.logits,
-                       L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pl.nseg,
-                       pl.spw, pl.S, ws, L.u, L.ids, L.p_out, L.sc, (int)pen_slice, tag);
+    hipLaunchKernelGGL(kf, dim3(pf.S, n_rows), dim3(PZ_SP_BLOCK), lds_front, L.stream, L.logits,
+                       L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pf.nseg,
+                       pf.spw, pf.S, ws, L.u, L.ids, L.p_out, L.sc, (int)pen_slice_f, tag);
     hipLaunchKernelGGL(kw, dim3(n_rows), dim3(PZ_SP_BLOCK), lds_wf, L.stream, L.logits, L.ld,
-                       L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pl.nseg, pl.spw,
-                       pl.S, ws, L.u, L.ids, L.p_out, L.sc, (int)wf_walk_off, wf_nc,
+                       L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pf.nseg, pf.spw,
+                       pf.S, ws, L.u, L.ids, L.p_out, L.sc, (int)wf_walk_off, wf_nc,
                        (int)wf_sort_off, wf_cap, wf_nc);
     auto fbk = k_topp_fallback<VEC>;
     if (lds5 > 65536 && hipFuncSetAttribute((const void*)fbk,
