@@ -98,6 +98,30 @@ __device__ __noinline__ float pz_expf_l(float x, const pz_lds_u64* tab) {
   return pz_expf_tab(x, tab);
 }
 
+// x_c for a per-lane c in 0..3.  The values pass through an empty asm
+// first: a select between elements of one array would otherwise become a
+// load at a per-lane index, which puts the array in scratch memory.
+__device__ __forceinline__ uint32_t pz_sel4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                            int c) {
+  asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
+  const uint32_t lo = (c & 1) ? x1 : x0, hi = (c & 1) ? x3 : x2;
+  return (c & 2) ? hi : lo;
+}
+__device__ __forceinline__ float pz_sel4f(float x0, float x1, float x2, float x3, int c) {
+  return __uint_as_float(pz_sel4(__float_as_uint(x0), __float_as_uint(x1), __float_as_uint(x2),
+                                 __float_as_uint(x3), c));
+}
+
+// Workgroup barrier that orders LDS only: the waves' global stores still
+// in flight stay in flight (__syncthreads waits for every one of them to
+// complete first).  Only where no thread reads global memory another wave
+// of the workgroup wrote before the barrier.
+__device__ __forceinline__ void pz_lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Out of line: the exact exponential sits on paths that are rare next to the
 // streaming passes, and inlining it into every one of them multiplies the
 // kernels' code size beyond the instruction cache.

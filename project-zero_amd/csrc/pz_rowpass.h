@@ -223,19 +223,9 @@ __device__ __forceinline__ void pz_rec_segment(const X& x, const typename X::Raw
   const bool has2 = (gf & PZ_GF_HAS2) != 0;
   uint32_t s1 = 0, s2 = 0;
   bool d1 = false, d2 = false;
-#pragma unroll
-  for (int c = 0; c < 4; c++) {
-    uint32_t cls;
-    s1 += x.inc(raw, a, c, g, &cls);
-    d1 |= cls != PZ_INC_PLAIN;
-  }
+  x.inc4(raw, a, g, s1, d1);
   if (has2) {
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      uint32_t cls;
-      s2 += x.inc(raw, a, c, g - 1u, &cls);
-      d2 |= cls != PZ_INC_PLAIN;
-    }
+    x.inc4(raw, a, g - 1u, s2, d2);
     s2 = pz_wave_sum_u32(s2);
   }
   s1 = pz_wave_sum_u32(s1);
@@ -265,7 +255,9 @@ __device__ __forceinline__ void pz_rec_segment(const X& x, const typename X::Raw
 //   void prep(e0, n, Raw&, a[4])   finishes the element data, estimates the
 //                                  terms (relative error < 2^-16)
 //   void observe(e0, Raw&, a[4])   per-kernel side work (histograms, ...)
-//   uint32_t inc(Raw&, a[4], c, g, cls*)  exact increment of term c at grid g
+//   void inc4(Raw&, a[4], g, s&, dirty&)  adds the exact increments of the
+//                                  four terms at grid g to s; sets dirty on a
+//                                  tie or a big term
 //   void cache_put(lds, Raw&, a[4]) / cache_terms(lds, v[4])
 //                                  keep / rebuild a segment's exact terms
 //   void seg(k, v[4])              exact terms of segment k from memory
@@ -409,27 +401,17 @@ __device__ __forceinline__ float pz_fast_exp(float d) {
 // row) always take the exact path, so estimates that underflow cannot
 // matter; so do terms of 2^20 grid steps or more, whose fraction fp32 no
 // longer resolves against the bound.
+// Branch-free (selects only): the value returned is meaningful only where
+// *exact is false.  a == 0 gives t = 0, fr = 0, no exact evaluation and 0.
 __device__ __forceinline__ uint32_t pz_inc_from_estimate(float a, float d, uint32_t g,
                                                          bool* exact) {
-  *exact = false;
-  if (g < 50u) {
-    *exact = true;
-    return 0u;
-  }
-  if (a == 0.0f) return 0u;
-  const float t = a * __uint_as_float((277u - g) << 23);  // a / 2^(g - 150), exact
-  if (t >= 1048576.0f) {
-    *exact = true;
-    return 0u;
-  }
+  const uint32_t gc = g < 50u ? 50u : g;
+  const float t = a * __uint_as_float((277u - gc) << 23);  // a / 2^(g - 150), exact
   const float fl = floorf(t);
   const float fr = t - fl;
   const float eps = (fabsf(d) + 3.0f) * 0x1p-22f;
-  if (fabsf(fr - 0.5f) <= t * eps + 0x1p-20f) {
-    *exact = true;
-    return 0u;
-  }
-  return (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+  *exact = (g < 50u) | (t >= 1048576.0f) | (fabsf(fr - 0.5f) <= t * eps + 0x1p-20f);
+  return (uint32_t)fminf(fl, 1048576.0f) + (fr > 0.5f ? 1u : 0u);
 }
 
 // Terms of one row: e = expf(y - M) for y >= thr (0 otherwise), times inv
@@ -456,12 +438,29 @@ struct PzExpTerms {
     }
   }
   __device__ __forceinline__ void observe(int, const Raw&, const float (&)[4]) {}
-  __device__ __forceinline__ uint32_t inc(const Raw& y, const float (&a)[4], int c, uint32_t g,
-                                          uint32_t* cls) const {
-    bool ex;
-    *cls = PZ_INC_PLAIN;
-    const uint32_t i = pz_inc_from_estimate(a[c], y[c] - M, g, &ex);
-    return ex ? pz_inc(exact_term(y[c]), g, cls) : i;
+  // The estimates settle most terms; the rest are evaluated exactly, one per
+  // lane per round, so a wave calls the exact exponential once per round
+  // rather than once per term position that any lane needed.  (A term the
+  // estimate settles is neither a tie nor big: both fail its test.)
+  __device__ __forceinline__ void inc4(const Raw& y, const float (&a)[4], uint32_t g,
+                                       uint32_t& s, bool& dirty) const {
+    uint32_t need = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      bool ex;
+      const uint32_t i = pz_inc_from_estimate(a[c], y[c] - M, g, &ex);
+      if (ex) need |= 1u << c;
+      else s += i;
+    }
+    while (__ballot(need != 0u)) {
+      if (need) {
+        const int c = __builtin_ctz(need);
+        need &= need - 1u;
+        uint32_t cls;
+        s += pz_inc(exact_term(pz_sel4f(y[0], y[1], y[2], y[3], c)), g, &cls);
+        dirty |= cls != PZ_INC_PLAIN;
+      }
+    }
   }
   // The cache keeps the exact terms, evaluated here by the segment's whole
   // wave in the parallel pass, so the serial walk only reads them.

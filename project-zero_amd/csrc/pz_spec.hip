@@ -113,9 +113,14 @@ struct ResidualTerms {
     for (int c = 0; c < 4; c++)
       if (a[c] > 0.0f) lastpos = e0 + c;
   }
-  __device__ __forceinline__ uint32_t inc(const Raw&, const float (&a)[4], int c, uint32_t g,
-                                          uint32_t* cls) const {
-    return pz_inc(a[c], g, cls);
+  __device__ __forceinline__ void inc4(const Raw&, const float (&a)[4], uint32_t g, uint32_t& s,
+                                       bool& dirty) const {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      uint32_t cls;
+      s += pz_inc(a[c], g, &cls);
+      dirty |= cls != PZ_INC_PLAIN;
+    }
   }
   __device__ __forceinline__ void seg(int k, float (&v)[4]) const {
     Raw r;

@@ -365,29 +365,39 @@ __device__ __forceinline__ float pz_sp_prefix(const Est& est, int k0, PzSpShared
 // Predicted grid and flags of the slice's segments, from the running-sum
 // estimate at the slice start (carry) and the segments' estimates: each
 // wave predicts the segments it will record (k = k0 + w + 16 j) after a scan
-// over the slice.  Writes rec_gf.  Every thread calls it; barriers inside.
+// over the slice.  Writes rec_gf, and with lgf also lgf[k - k0] (a slice of
+// at most PZ_SP_BLOCK segments), which pz_sp_records then reads instead:
+// the barriers inside order LDS only.  Every thread calls it.
 template <class Est>
 __device__ __forceinline__ void pz_sp_predict(const Est& est, float carry, int row,
                                               const PzSlice& sl, const PzSplitWs& ws,
-                                              PzSpShared& S) {
+                                              PzSpShared& S, pz_lds_u32* lgf = nullptr) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   uint32_t* gf = pz_sp_rec_gf(ws, row);
+  auto barrier = [&] {
+    if (lgf) pz_lds_barrier();
+    else __syncthreads();
+  };
   if (tid == 0) S.carry = carry;
-  __syncthreads();
+  barrier();
   for (int c0 = sl.k0; c0 < sl.k1; c0 += PZ_SP_BLOCK) {
     const int k = c0 + tid;
     const float e = k < sl.k1 ? est(k) : 0.0f;
     const float incl = pz_wave_scan_f32(e);
     if (lane == 63) S.red[w] = incl;
-    __syncthreads();
-    float off = S.carry;
-    for (int i = 0; i < w; i++) off += S.red[i];
+    barrier();
+    // (the waves before this one: a wave reduction, one LDS load per lane)
+    const float off = S.carry + pz_wave_sum(lane < w ? S.red[lane] : 0.0f);
     const float start = off + (incl - e), end = off + incl;
-    if (k < sl.k1)
-      gf[k] = pz_predict_gf(start) | (pz_grid_of(end) != pz_grid_of(start) ? PZ_GF_XING : 0u);
-    __syncthreads();
+    if (k < sl.k1) {
+      const uint32_t v =
+          pz_predict_gf(start) | (pz_grid_of(end) != pz_grid_of(start) ? PZ_GF_XING : 0u);
+      gf[k] = v;
+      if (lgf) lgf[k - sl.k0] = v;
+    }
+    barrier();
     if (tid == PZ_SP_BLOCK - 1) S.carry = end;
-    __syncthreads();
+    barrier();
   }
 }
 
@@ -395,12 +405,13 @@ __device__ __forceinline__ void pz_sp_predict(const Est& est, float carry, int r
 // Records pass over the slice's segments.  X provides (as for
 // pz_record_pass): typename Raw; load(e0, Raw&) -> count < V;
 // prep(e0, n, Raw&, a[4]); observe(e0, Raw&, a[4]);
-// inc(Raw&, a[4], c, g, cls*).  The predicted grid and flags of segment k
-// are in rec_gf (pz_sp_predict); PZ_NO_RECORD skips a segment.
+// inc4(Raw&, a[4], g, s&, dirty&).  The predicted grid and flags of segment k
+// are in rec_gf, or lgf[k - k0] (pz_sp_predict); PZ_NO_RECORD skips a segment.
 // ---------------------------------------------------------------------------
 template <class X>
 __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
-                                              const PzSplitWs& ws) {
+                                              const PzSplitWs& ws,
+                                              const pz_lds_u32* lgf = nullptr) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint32_t* rd = pz_sp_rec_d(ws, row);
   uint32_t* rd2 = pz_sp_rec_d2(ws, row);
@@ -408,14 +419,18 @@ __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
   for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
   typename X::Raw raws[PZ_SP_U];
   int ns[PZ_SP_U];
+  uint32_t gfs[PZ_SP_U];  // every grid word in flight before the first is used
 #pragma unroll
-  for (int u = 0; u < PZ_SP_U; u++)
-    ns[u] = x.load((kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, raws[u]);
+  for (int u = 0; u < PZ_SP_U; u++) {
+    const int k = kb + u * PZ_SP_WAVES;
+    ns[u] = x.load(k * PZ_SP_SEG + 4 * lane, raws[u]);
+    gfs[u] = k < sl.k1 ? (lgf ? lgf[k - sl.k0] : rgf[k]) : PZ_NO_RECORD;
+  }
 #pragma unroll
   for (int u = 0; u < PZ_SP_U; u++) {
     const int k = kb + u * PZ_SP_WAVES;
     if (k >= sl.k1) break;
-    const uint32_t gf = rgf[k];
+    const uint32_t gf = gfs[u];
     if (gf == PZ_NO_RECORD) continue;
     const int e0 = k * PZ_SP_SEG + 4 * lane;
     typename X::Raw& raw = raws[u];
@@ -427,19 +442,9 @@ __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
     const bool has2 = (gf & PZ_GF_HAS2) != 0;
     uint32_t s1 = 0, s2 = 0;
     bool d1 = false, d2 = false;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      uint32_t cls;
-      s1 += x.inc(raw, a, c, g, &cls);
-      d1 |= cls != PZ_INC_PLAIN;
-    }
+    x.inc4(raw, a, g, s1, d1);
     if (has2) {
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        uint32_t cls;
-        s2 += x.inc(raw, a, c, g - 1u, &cls);
-        d2 |= cls != PZ_INC_PLAIN;
-      }
+      x.inc4(raw, a, g - 1u, s2, d2);
       s2 = pz_wave_sum_u32(s2);
     }
     s1 = pz_wave_sum_u32(s1);
@@ -554,20 +559,6 @@ __device__ __forceinline__ float pz_sp_elemf(const float (&a)[4], int i) {
   const uint32_t u[4] = {__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]),
                          __float_as_uint(a[3])};
   return __uint_as_float(pz_sp_elem(u, i));
-}
-
-// x_c for a per-lane c in 0..3.  The values pass through an empty asm
-// first: a select between elements of one array would otherwise become a
-// load at a per-lane index, which puts the array in scratch memory.
-__device__ __forceinline__ uint32_t pz_sel4(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
-                                            int c) {
-  asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
-  const uint32_t lo = (c & 1) ? x1 : x0, hi = (c & 1) ? x3 : x2;
-  return (c & 2) ? hi : lo;
-}
-__device__ __forceinline__ float pz_sel4f(float x0, float x1, float x2, float x3, int c) {
-  return __uint_as_float(pz_sel4(__float_as_uint(x0), __float_as_uint(x1), __float_as_uint(x2),
-                                 __float_as_uint(x3), c));
 }
 
 // Index of the first element (lane-major, 4 per lane) whose predicate holds,

@@ -482,34 +482,51 @@ __device__ __forceinline__ ToppSel topp_front_select(const uint32_t* hrow, int S
   }
   ehist[i0] = c0;
   if (i1 < PZ_TOPP_NB) ehist[i1] = c1;
-  // the estimated total mass and count, in a fixed order (every workgroup of
-  // the row gets the same values)
-  float t = (float)c0 * ebin_mid(i0) + (i1 < PZ_TOPP_NB ? (float)c1 * ebin_mid(i1) : 0.0f);
-  uint32_t n = c0 + (i1 < PZ_TOPP_NB ? c1 : 0u);
-  t = pz_wave_sum(t);
-  n = pz_wave_sum_u32(n);
-  if (lane == 0) {
-    part_sh[w] = t;
-    part_sh[PZ_SP_WAVES + w] = __uint_as_float(n);
+  if (tid == 0) sel_sh->bsel = INT_MAX;  // (the first crossing, as a position from the top)
+  pz_lds_barrier();
+  // The bins from the top down, two per thread (positions 2 tid, 2 tid + 1
+  // are bins NB-1-2 tid, NB-2-2 tid): the estimated mass and count above
+  // each one by a workgroup scan in a fixed order, so every workgroup of
+  // the row finds the same bins.  The first position whose running mass
+  // reaches the goal (as topp_select_bins): the lowest bin kept.
+  const int bh = PZ_TOPP_NB - 1 - 2 * tid, bl = bh - 1;
+  const uint32_t nh = bh >= 0 ? ehist[bh] : 0u, nl = bl >= 0 ? ehist[bl] : 0u;
+  const float mh = bh >= 0 ? (float)nh * ebin_mid(bh) : 0.0f;
+  const float ml = bl >= 0 ? (float)nl * ebin_mid(bl) : 0.0f;
+  const float pm = mh + ml;
+  const uint32_t pn = nh + nl;
+  const float incl = pz_wave_scan_f32(pm);
+  const uint32_t cincl = pz_wave_scan_u32(pn);
+  if (lane == 63) {
+    part_sh[w] = incl;
+    part_sh[PZ_SP_WAVES + w] = __uint_as_float(cincl);
   }
-  __syncthreads();
-  if (tid < 64) {
-    float tot = 0.0f;
-    uint32_t ncand = 0;
-    for (int j = 0; j < PZ_SP_WAVES; j++) {
-      tot += part_sh[j];
-      ncand += __float_as_uint(part_sh[PZ_SP_WAVES + j]);
-    }
-    int bsel;
-    uint32_t nsel;
-    topp_select_bins(ehist, tot, ncand, top_p, &bsel, &nsel);
-    if (tid == 0) {
-      sel_sh->bsel = bsel;
-      sel_sh->nsel = nsel;
-    }
+  pz_lds_barrier();
+  const float pw = lane < PZ_SP_WAVES ? part_sh[lane] : 0.0f;
+  const uint32_t cw = lane < PZ_SP_WAVES ? __float_as_uint(part_sh[PZ_SP_WAVES + lane]) : 0u;
+  const float tot = pz_wave_sum(pw);
+  const uint32_t ncand = pz_wave_sum_u32(cw);
+  const float wpre = pz_wave_sum(lane < w ? pw : 0.0f);
+  const uint32_t cpre = pz_wave_sum_u32(lane < w ? cw : 0u);
+  const float goal = (top_p * 1.012f + 3e-4f) * tot;
+  const float cum_h = wpre + (incl - pm) + mh, cum_l = cum_h + ml;
+  const int pos = bh >= 0 && cum_h >= goal ? 2 * tid : (bl >= 0 && cum_l >= goal ? 2 * tid + 1 : INT_MAX);
+  // (positions grow with the lane: the wave's first crossing is its lowest)
+  const uint64_t crossed = __ballot(pos != INT_MAX);
+  if (crossed && lane == (int)__builtin_ctzll(crossed)) atomicMin(&sel_sh->bsel, pos);
+  pz_lds_barrier();
+  const int fp = sel_sh->bsel;
+  ToppSel r;
+  if (fp == INT_MAX) {  // never reached: every bin
+    r.bsel = 0;
+    r.nsel = ncand;
+  } else {
+    r.bsel = PZ_TOPP_NB - 1 - fp;
+    if ((fp >> 1) == tid) sel_sh->nsel = cpre + (cincl - pn) + nh + ((fp & 1) ? nl : 0u);
+    pz_lds_barrier();
+    r.nsel = sel_sh->nsel;
   }
-  __syncthreads();
-  return *sel_sh;
+  return r;
 }
 
 template <bool VEC>
@@ -523,6 +540,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   __shared__ ToppSel sel_sh;
   __shared__ float part_sh[2 * PZ_SP_WAVES];
   __shared__ int wcnt[PZ_SP_WAVES];
+  __shared__ uint32_t sgf[TOPP_FRONT_SEGS];  // the slice's predicted grids
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = pz_row_of(rows, blockIdx.y);
@@ -574,10 +592,12 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   }
   if (__ballot(nan) && lane == 0) atomicOr(&SS.any, 1u);
   if (lane == 0) SS.red[w] = smx;
-  __syncthreads();
+  pz_lds_barrier();
+  // (reductions over LDS words by a wave, not one thread's loop: every load
+  // of a serial loop waits out the LDS latency)
+  const float mm = w == 0 ? pz_wave_max(lane < PZ_SP_WAVES ? SS.red[lane] : -__builtin_inff())
+                          : 0.0f;
   if (tid == 0) {
-    float mm = SS.red[0];
-    for (int i = 1; i < PZ_SP_WAVES; i++) mm = fmaxf(mm, SS.red[i]);
     uint32_t f = SS.any;
     ws.slice_m[(size_t)row * ws.smax + blockIdx.x] = mm;
     ws.slice_f[(size_t)row * ws.smax + blockIdx.x] = f;
@@ -608,7 +628,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       SS.any = flags;
     }
   }
-  __syncthreads();
+  pz_lds_barrier();
   const bool degen = topp_degenerate(SS.any);
   const float M = SS.M, thr = M - 20.0f;
   // 2. the estimated candidate mass of each segment (as k_topp_est) and the
@@ -633,7 +653,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       if (lane == 0) sest[k - sl.k0] = t;
     }
   }
-  __syncthreads();
+  pz_lds_barrier();
   uint32_t* hrow = ws.hist + (size_t)blockIdx.y * S * PZ_TOPP_NB;
   if (!degen) {
     uint32_t* gh = hrow + (size_t)blockIdx.x * PZ_TOPP_NB;
@@ -641,10 +661,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       __hip_atomic_store(&gh[i], topp_hword(tag, ehist[i]), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
+  static_assert(TOPP_FRONT_SEGS <= 64, "one estimate per lane");
+  const float tot =
+      w == 0 && !degen ? pz_wave_sum(lane < sl.k1 - sl.k0 ? sest[lane] : 0.0f) : 0.0f;
   if (tid == 0) {
-    float tot = 0.0f;
-    if (!degen)
-      for (int k = sl.k0; k < sl.k1; k++) tot += sest[k - sl.k0];
     // meet 2: every slice's estimated mass
     __hip_atomic_store(&meet[ws.smax + blockIdx.x], (1ull << 63) | (uint64_t)__float_as_uint(tot),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -662,8 +682,8 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
     const float carry = pz_wave_sum(lane < (int)blockIdx.x ? __uint_as_float((uint32_t)v) : 0.0f);
     if (lane == 0) SS.carry = carry;
   }
-  __syncthreads();
-  pz_sp_predict(ToppSliceEst{sest, sl.k0}, SS.carry, row, sl, ws, SS);
+  pz_lds_barrier();
+  pz_sp_predict(ToppSliceEst{sest, sl.k0}, SS.carry, row, sl, ws, SS, (pz_lds_u32*)sgf);
   // 3. records from LDS (as k_topp_rec)
   PzExpTerms<ToppLdsRow> X;
   X.R.y = ybuf;
@@ -674,9 +694,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   X.inv = 1.0f;
   X.as_p = false;
   X.et = et;
-  pz_sp_records(X, row, sl, ws);
+  pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)sgf);
   // 4. the nucleus bins (the row's histograms were published before meet 2)
-  __syncthreads();
+  pz_lds_barrier();
   const ToppSel sel = topp_front_select(hrow, S, tag, ehist, prm.top_p, &sel_sh, part_sh);
   const bool all = sel.bsel == 0;
   const float e_gate = all ? 0.0f : ebin_lo(sel.bsel);
@@ -759,20 +779,21 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
     cnt = cap_w;
   }
   if (lane == 0) wcnt[w] = cnt | (over ? TOPP_GOVER : 0);
-  __syncthreads();
-  if (tid == 0) {
-    int tot = 0;
-    bool ov = false;
-    for (int i = 0; i < PZ_SP_WAVES; i++) {
-      ov |= (wcnt[i] & TOPP_GOVER) != 0;
-      tot += wcnt[i] & (TOPP_GOVER - 1);
+  pz_lds_barrier();
+  // every wave reads the 16 counts once (one lane each): its offset among
+  // the workgroup's keys, and (wave 0) the total and the overflow flag
+  const int wc = lane < PZ_SP_WAVES ? wcnt[lane] : 0;
+  const uint32_t before = pz_wave_sum_u32(lane < w ? (uint32_t)(wc & (TOPP_GOVER - 1)) : 0u);
+  if (w == 0) {
+    const uint32_t gtot = pz_wave_sum_u32((uint32_t)(wc & (TOPP_GOVER - 1)));
+    const bool ov = __ballot((wc & TOPP_GOVER) != 0) != 0;
+    if (lane == 0) {
+      SS.cnt = gtot > 0 ? (int)atomicAdd(&ws.arrive[row], gtot) : 0;
+      if (ov) atomicOr(&ws.arrive[row], (uint32_t)TOPP_GOVER);
     }
-    SS.cnt = tot > 0 ? (int)atomicAdd(&ws.arrive[row], (uint32_t)tot) : 0;
-    if (ov) atomicOr(&ws.arrive[row], (uint32_t)TOPP_GOVER);
   }
-  __syncthreads();
-  int base = SS.cnt & (TOPP_GOVER - 1);
-  for (int i = 0; i < w; i++) base += wcnt[i] & (TOPP_GOVER - 1);
+  pz_lds_barrier();
+  const int base = (SS.cnt & (TOPP_GOVER - 1)) + (int)before;
   uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
   for (int q = lane; q < cnt; q += 64) {
     if (base + q >= ws.capg) break;  // (the count tells the walk the list overflowed)
@@ -1648,7 +1669,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   }
   const PzRowState rs0 = ws.rs[row];  // the nucleus bins (k_topp_front, workgroup 0)
   const bool all = rs0.i[1] != 0;
-  const float e_gate = rs0.f[0], dgate = rs0.f[1];
+  const float e_gate = rs0.f[0];
   const int m = m_sh;
   // the list: sorted here when it fits (else the fallback)
   const bool listed = (uint32_t)rs0.i[4] <= (uint32_t)ws.capg && m > 0 && m <= cap;
