@@ -744,20 +744,16 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
       S.red2[w] = (uint32_t)__popcll(cb);
     }
     __syncthreads();
-    uint32_t off = base, coff = cbase;
-    int soff = sbase;
-    for (int i = 0; i < w; i++) {
-      off += (uint32_t)S.list[i];
-      soff += __float_as_int(S.red[i]);
-      coff += S.red2[i];
-    }
-    uint32_t tot = 0, ctot = 0;
-    int stot = 0;
-    for (int i = 0; i < nw; i++) {
-      tot += (uint32_t)S.list[i];
-      stot += __float_as_int(S.red[i]);
-      ctot += S.red2[i];
-    }
+    // the waves' totals, one per lane, summed by wave reductions (mod 2^32)
+    const bool in_w = lane < nw;
+    const uint32_t lt = in_w ? (uint32_t)S.list[lane] : 0u;
+    const uint32_t ls = in_w ? (uint32_t)__float_as_int(S.red[lane]) : 0u;
+    const uint32_t lc = in_w ? S.red2[lane] : 0u;
+    const uint32_t off = base + pz_wave_sum_u32(lane < w ? lt : 0u);
+    const int soff = sbase + (int)pz_wave_sum_u32(lane < w ? ls : 0u);
+    const uint32_t coff = cbase + pz_wave_sum_u32(lane < w ? lc : 0u);
+    const uint32_t tot = pz_wave_sum_u32(lt), ctot = pz_wave_sum_u32(lc);
+    const int stot = (int)pz_wave_sum_u32(ls);
     const uint64_t below = (1ull << lane) - 1ull;
     if (k < nseg) {
       W.pd[k] = off + incl - d;

@@ -1629,6 +1629,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     for (int i = t0; i < 2 * ws.smax; i += nt) ws.meet[(size_t)row * 2 * ws.smax + i] = 0ull;
     for (int i = t0; i < S * PZ_TOPP_NB; i += nt) hrow[i] = 0u;
   };
+  // the nucleus bins (k_topp_front, workgroup 0): loaded at once, beside the
+  // row's maxima below
+  const PzRowState rs0 = ws.rs[row];
   if (tid == 0) {
     // the gathered count, re-armed for the next call
     m_sh = (int)ws.arrive[row];
@@ -1667,7 +1670,6 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     }
     return;
   }
-  const PzRowState rs0 = ws.rs[row];  // the nucleus bins (k_topp_front, workgroup 0)
   const bool all = rs0.i[1] != 0;
   const float e_gate = rs0.f[0];
   const int m = m_sh;
@@ -1796,7 +1798,46 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
       }
     }
     __syncthreads();
-    if (m < TOPP_BINSORT_MIN) {
+    if (m <= 64) {
+      // a list of one wave: each lane holds one p, and the reference's loops
+      // run as written over them (top_p.c:80-93 the cumulative to the first
+      // sum >= top_p, :96-105 the first cumulative > u * trunc_sum), every
+      // add a plain fp32 add in list order
+      if (w == 0) {
+        const float pl = lane < m ? key_p(bkeys[perm[lane]]) : 0.0f;
+        auto p_at = [&](int j) {
+          return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pl), j));
+        };
+        float cum = 0.0f;
+        int cutoff = -1;
+        for (int j = 0; j < m; j++) {
+          cum = cum + p_at(j);
+          if (cum >= prm.top_p) {
+            cutoff = j + 1;
+            break;
+          }
+        }
+        if (cutoff < 0 && all) cutoff = m;  // cum: the whole sum
+        if (cutoff > 0 && (all || p_at(cutoff - 1) >= p_lo)) {
+          const float r = u[row] * cum;  // cum: the cumulative at the cut-off
+          float c2 = 0.0f;
+          int pick = 0;
+          for (int j = 0; j < cutoff; j++) {
+            c2 = c2 + p_at(j);
+            if (c2 > r) {
+              pick = j;
+              break;
+            }
+          }
+          if (lane == 0) {
+            const uint64_t k = bkeys[perm[pick]];
+            ids_out[row] = key_id(k);
+            if (p_out) p_out[row] = key_p(k);
+          }
+          done = true;
+        }
+      }
+    } else if (m < TOPP_BINSORT_MIN) {
       // a short list: contiguous keys and the lane-ordered walks
       uint64_t* kk = reinterpret_cast<uint64_t*>(region);
       float* cum = reinterpret_cast<float*>(region + (size_t)TOPP_BINSORT_MIN * 8);

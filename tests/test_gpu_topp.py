@@ -171,3 +171,22 @@ def test_strided_rows_and_mixed_modes(torch_cuda):
                      pz.row_params(temperature=0.9, top_p=0.85),
                      pz.row_params(temperature=1.0, top_k=30, top_p=0.9)][b % 3])
     check(torch_cuda, x, prms, u, label="mixed strided", ld=12347)
+
+
+@pytest.mark.parametrize("top_p", [0.3, 0.9, 1.0])
+def test_short_lists(torch_cuda, top_p):
+    """Rows with 1 to 72 candidates (every other logit 30 below the maximum,
+    outside the reference's max - 20 window): lists of one wave and just
+    past it, the cumulative cut inside the list or (top_p 1.0) never
+    reached, draws at u = 0 and u = 1 among them."""
+    B, V = 72, 5000
+    rng = np.random.default_rng(0x5107 + int(top_p * 10))
+    x = np.full((B, V), -30.0, np.float32)
+    for b in range(B):
+        k = b + 1
+        pos = rng.choice(V, size=k, replace=False)
+        x[b, pos] = rng.normal(0.0, 1.5, size=k).astype(np.float32)
+    u = pz.synth_draws(B, 0x5108)
+    u[0], u[1], u[70] = 0.0, 1.0, 1.0
+    check(torch_cuda, x, [pz.row_params(temperature=1.0, top_p=top_p)], u,
+          label=f"short lists p={top_p}")
