@@ -16,8 +16,8 @@ constexpr int PZ_TOPP_CAPG = 12288;    // top-p candidates a row can gather for 
 struct pz_scratch {
   float* row_stat;    // [max_batch][4] per-row values handed between kernels
   int32_t* fb_list;   // [max_batch] rows queued for the top-p fallback
-  int32_t* counters;  // [PZ_COUNTERS] queue counters: [0] rows queued, [1] fallback
-                      // workgroups done (both zero between calls)
+  int32_t* counters;  // [PZ_COUNTERS] queue counters: [0] rows queued for the top-p
+                      // fallback (emptied by a top-p launch's first kernel)
   uint64_t* fb_keys;  // [fb_slots][slot_n] sort buffers of the fallback
   uint64_t* fb_keys2; // [fb_slots][slot_n] its second buffer (keys in bin order)
   int slot_n;         // power of two >= min(max_vocab, PZ_TOPP_MAX_V)

@@ -287,6 +287,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_stat(TOPP
   if (threadIdx.x == 0) {
     SS.any = 0u;
     if (blockIdx.x == 0) ws.rs[row].i[5] = 0;  // the nucleus bins of this launch: not yet picked
+    // the fallback queue, empty for this launch's later kernels (the one
+    // before, k_topp_fallback, has read it: launches on a stream run in order)
+    if (blockIdx.x == 0 && blockIdx.y == 0) sc.counters[0] = 0;
   }
   const PzRow<VEC> R =
       topp_row<VEC>(logits, ld, row, V, prm, lds, pz_sp_lo(sl), pz_sp_hi(sl, V), hcap, hist, H);
@@ -552,6 +555,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   pz_lds_f32* ybuf = (pz_lds_f32*)(lds + (((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15));
   uint64_t* meet = ws.meet + (size_t)row * 2 * ws.smax;
   if (tid == 0) SS.any = 0u;
+  // the fallback queue, empty for k_topp_walkf (the k_topp_fallback before
+  // has read it: launches on a stream run in order)
+  if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) sc.counters[0] = 0;
   for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) ehist[i] = 0u;
   const PzRow<VEC> R =
       topp_row<VEC>(logits, ld, row, V, prm, lds, lo, pz_sp_hi(sl, V), hcap, hist, H);
@@ -1545,6 +1551,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
     const int32_t* __restrict__ hist, int H, int hcap, int nseg, PzSplitWs ws,
     const float* __restrict__ u, int32_t* __restrict__ ids_out, float* __restrict__ p_out,
     pz_scratch sc) {
+  // (the queue is emptied by the first kernel of the next launch)
   const int n_fb = sc.counters[0];
   for (int q = blockIdx.x; q < n_fb; q += gridDim.x) {
     const int row = sc.fb_list[q];
@@ -1555,15 +1562,6 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
       fb_pass<VEC>(logits, ld, V, params, n_params, hist, H, hcap, nseg, ws, u, ids_out, p_out,
                    sc, row, 0.0f, blockIdx.x, rs0.M, rs0.inv,
                    rs0.f[1]);  // the cut-off lies past the gated list
-  }
-  // the last workgroup out re-arms the queue for the next launch (every
-  // workgroup has read counters[0] before it counts itself done)
-  if (threadIdx.x == 0) {
-    __threadfence();
-    if (atomicAdd(&sc.counters[1], 1) == (int)gridDim.x - 1) {
-      atomicExch(&sc.counters[0], 0);
-      atomicExch(&sc.counters[1], 0);
-    }
   }
 }
 
