@@ -1593,15 +1593,33 @@ __host__ __device__ inline size_t wf_keys_off(int cap) {
 }
 
 // Barrier of waves 8..15 (a monotonic LDS counter: generation g ends when it
-// reaches 8 g).
+// reaches 8 g).  It orders LDS only (the sort's data): the waves' stores
+// that clear the row's words stay in flight.
 __device__ __forceinline__ void wf_sub_barrier(int* ctr, int& gen) {
   gen++;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   if ((threadIdx.x & 63) == 0)
     __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 8 * gen)
     __builtin_amdgcn_s_sleep(1);
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Bin of an e key for the fused walk's counting sort: PBINS bins spread
+// over the row's e range [e_min, 1] (e = expf(y - max) <= 1), the finest
+// power-of-two width that keeps them within PBINS, so a short range gets
+// narrow bins and the ranks inside them take few comparisons.  Bins grow as
+// e falls (keys below e_min, none expected, share the last).
+__device__ __forceinline__ int wf_shift(float e_min) {
+  const uint32_t span = 0x3f800000u - (__float_as_uint(e_min) < 0x3f800000u ? __float_as_uint(e_min) : 0x3f800000u);
+  int s = 0;
+  while ((span >> s) >= (uint32_t)PBINS) s++;
+  return s;
+}
+__device__ __forceinline__ int wf_bin(uint64_t key, int shift) {
+  const uint32_t b = (uint32_t)(key >> 32);  // bits(e)
+  const uint32_t q = (0x3f800000u - (b < 0x3f800000u ? b : 0x3f800000u)) >> shift;
+  return q < (uint32_t)PBINS - 1u ? (int)q : PBINS - 1;
 }
 
 template <bool VEC>
@@ -1699,14 +1717,24 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   }
   if (w >= 8 && listed) {
     // counting sort of the e keys by bin, then the rank inside each bin
+    // (every gathered e is >= e_gate (1 - 2^-21), or >= expf(-20) > 2^-29)
     const int tt = tid - (PZ_SP_BLOCK - WF_SORT);
+    const int shw = wf_shift(all ? 0x1p-29f : e_gate * (1.0f - 0x1p-21f));
     int gen = 0;
     for (int i = tt; i < PBINS / 2; i += WF_SORT) bcnt[i] = 0u;
     if (tt == 0) T.bmax = 0u;
     wf_sub_barrier(&sb_ctr, gen);
-    for (int i = tt; i < m; i += WF_SORT) {
-      const int q = pbin(gkeys[i]);
-      atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
+    // (four keys' loads in flight per thread and trip in both passes)
+    for (int i0 = tt; i0 < m; i0 += 4 * WF_SORT) {
+      uint64_t kq[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) kq[r] = i0 + r * WF_SORT < m ? gkeys[i0 + r * WF_SORT] : 0ull;
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if (i0 + r * WF_SORT < m) {
+          const int q = wf_bin(kq[r], shw);
+          atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
+        }
     }
     wf_sub_barrier(&sb_ctr, gen);
     // exclusive bin starts: thread tt owns bins 8 tt .. 8 tt + 7 (words 4 tt ..)
@@ -1738,17 +1766,23 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
       run = s1 + c[j + 1];
     }
     wf_sub_barrier(&sb_ctr, gen);
-    for (int i = tt; i < m; i += WF_SORT) {
-      const uint64_t key = gkeys[i];
-      const int q = pbin(key);
-      const uint32_t old = atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
-      bkeys[(old >> (16 * (q & 1))) & 0xffffu] = key;
+    for (int i0 = tt; i0 < m; i0 += 4 * WF_SORT) {
+      uint64_t kq[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) kq[r] = i0 + r * WF_SORT < m ? gkeys[i0 + r * WF_SORT] : 0ull;
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if (i0 + r * WF_SORT < m) {
+          const int q = wf_bin(kq[r], shw);
+          const uint32_t old = atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
+          bkeys[(old >> (16 * (q & 1))) & 0xffffu] = kq[r];
+        }
     }
     wf_sub_barrier(&sb_ctr, gen);
     if (T.bmax <= (uint32_t)TOPP_BIN_MAX) {
       for (int j = tt; j < m; j += WF_SORT) {
         const uint64_t key = bkeys[j];
-        const int q = pbin(key);
+        const int q = wf_bin(key, shw);
         const uint32_t b0 = (bstart[q >> 1] >> (16 * (q & 1))) & 0xffffu;
         const uint32_t b1 = (bcnt[q >> 1] >> (16 * (q & 1))) & 0xffffu;
         uint32_t r = 0, x = b0;
