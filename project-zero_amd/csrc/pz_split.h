@@ -288,10 +288,12 @@ __device__ __forceinline__ void pz_sp_stat_slice(const Row& R, int row, const Pz
   }
   if (__ballot(nan) && lane == 0) atomicOr(&S.any, 1u);
   if (lane == 0) S.red[w] = smax;
-  __syncthreads();
+  // (LDS only: the segments' stores stay in flight; one wave reduces the
+  // waves' maxima, one LDS load per lane)
+  pz_lds_barrier();
+  const float mm = w == 0 ? pz_wave_max(lane < PZ_SP_WAVES ? S.red[lane] : -__builtin_inff())
+                          : 0.0f;
   if (tid == 0) {
-    float mm = S.red[0];
-    for (int i = 1; i < PZ_SP_WAVES; i++) mm = fmaxf(mm, S.red[i]);
     ws.slice_m[(size_t)row * ws.smax + blockIdx.x] = mm;
     ws.slice_f[(size_t)row * ws.smax + blockIdx.x] = S.any;
     if (blockIdx.x == 0) {
@@ -355,9 +357,7 @@ __device__ __forceinline__ float pz_sp_prefix(const Est& est, int k0, PzSpShared
   __syncthreads();
   if (lane == 0) S.red[w] = t;
   __syncthreads();
-  float tot = 0.0f;
-#pragma unroll
-  for (int i = 0; i < PZ_SP_WAVES; i++) tot += S.red[i];
+  const float tot = pz_wave_sum(lane < PZ_SP_WAVES ? S.red[lane] : 0.0f);
   __syncthreads();
   return tot;
 }
