@@ -1812,21 +1812,41 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   if (listed && path == 1) {
     for (int i = tid; i < m; i += PZ_SP_BLOCK) bkeys[i] = topp_pkey(bkeys[i], inv);
     __syncthreads();
-    // runs of equal p (distinct e can round to one p) back in ascending id
-    for (int j = tid; j < m; j += PZ_SP_BLOCK) {
-      const float pj = key_p(bkeys[perm[j]]);
-      if (j > 0 && key_p(bkeys[perm[j - 1]]) == pj) continue;
-      int e = j + 1;
-      while (e < m && key_p(bkeys[perm[e]]) == pj) e++;
-      for (int a = j + 1; a < e; a++) {  // insertion sort of perm[j, e) by key, descending
-        const uint16_t pa = perm[a];
-        const uint64_t ka = bkeys[pa];
-        int b = a;
-        while (b > j && bkeys[perm[b - 1]] < ka) {
-          perm[b] = perm[b - 1];
-          b--;
+    // runs of equal p (distinct e can round to one p) back in ascending id:
+    // each thread checks 8 consecutive positions, the p of those and of
+    // their two neighbours loaded at once (-1 outside the list: no p equals
+    // it); only a run longer than one goes on key by key
+    constexpr int CH = 8;
+    for (int j0 = tid * CH; j0 < m; j0 += PZ_SP_BLOCK * CH) {
+      float pv[CH + 2];  // p at positions j0 - 1 .. j0 + CH
+      uint32_t ix[CH + 2];
+#pragma unroll
+      for (int c = 0; c < CH + 2; c++) {
+        const int jj = j0 - 1 + c;
+        ix[c] = jj >= 0 && jj < m ? (uint32_t)perm[jj] : 0u;
+      }
+#pragma unroll
+      for (int c = 0; c < CH + 2; c++) {
+        const int jj = j0 - 1 + c;
+        pv[c] = jj >= 0 && jj < m ? key_p(bkeys[ix[c]]) : -1.0f;
+      }
+#pragma unroll
+      for (int c = 1; c <= CH; c++) {
+        const int j = j0 - 1 + c;
+        if (j >= m || pv[c - 1] == pv[c] || pv[c + 1] != pv[c]) continue;
+        const float pj = pv[c];
+        int e = j + 1;
+        while (e < m && key_p(bkeys[perm[e]]) == pj) e++;
+        for (int a = j + 1; a < e; a++) {  // insertion sort of perm[j, e) by key, descending
+          const uint16_t pa = perm[a];
+          const uint64_t ka = bkeys[pa];
+          int b = a;
+          while (b > j && bkeys[perm[b - 1]] < ka) {
+            perm[b] = perm[b - 1];
+            b--;
+          }
+          perm[b] = pa;
         }
-        perm[b] = pa;
       }
     }
     __syncthreads();
