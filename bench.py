@@ -12,8 +12,9 @@ The same line carries
                c2 64 x 128256, temperature 0.7 + top-p 0.9, 5 spikes per row
                c3 256 x 151936, presence/frequency + top-k 20 + top-p 0.8
                c5 speculative verification, 32 sequences x 4 drafts x 128256
-  batch_sweep  greedy (as the headline) and top-p (as c2) at vocab 128256,
-               batch 1, 8, 64, 256, 1024
+  batch_sweep  greedy (as the headline), top-p (as c2) and the plain
+               categorical draw (c2's logits at T 1.0, top-p 1.0: the HTTP
+               default) at vocab 128256, batch 1, 8, 64, 256, 1024
   attention    the reference softmax over attention scores (the tn_softmax of
                attention.c:210), 32 heads x valid context 128, 4096, 32768
   lm_head      the bf16 LM head producing the logits (parallel_matmul_bf16,
@@ -84,6 +85,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the CPU baseline and the parity checks")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--sweep", default="all",
+                    help="comma-separated sweep kinds (greedy, top_p, categorical) or all")
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
                     help="CPU time of each baseline sample (per thread count)")
     return ap.parse_args()
@@ -440,16 +443,19 @@ def run_c5(args, torch, cpu):
 
 
 def run_sweep(args, torch, cpu):
-    """Greedy (headline chain) and top-p (c2 chain) at vocab 128256 over a
-    1024-row pool (525 MB, beyond the Infinity Cache): step t of batch B
-    reads rows [tB mod 1024, +B)."""
+    """Greedy (headline chain), top-p (c2 chain) and the categorical draw at
+    vocab 128256 over a 1024-row pool (525 MB, beyond the Infinity Cache):
+    step t of batch B reads rows [tB mod 1024, +B)."""
     import numpy as np
     import pzsample as pz
     import workloads as wl
     V, P = 128256, 1024
-    out = {"vocab": V, "pool_rows": P, "greedy": [], "top_p": []}
+    out = {"vocab": V, "pool_rows": P, "greedy": [], "top_p": [], "categorical": []}
     dev = torch.device("cuda:0")
-    for kind, build in (("greedy", wl.build_c4), ("top_p", wl.build_c2)):
+    kinds = (("greedy", wl.build_c4), ("top_p", wl.build_c2), ("categorical", wl.build_cat))
+    for kind, build in kinds:
+        if args.sweep != "all" and kind not in args.sweep.split(","):
+            continue
         w = build(B=P, V=V)
         x, hist, u = w["logits"], w["hist"], w["u"]
         H = hist.shape[1] if hist is not None else 0

@@ -39,6 +39,11 @@ extern "C" {
 #define PZ_ERANGE  (-4) /* size above what the sampler was created for        */
 #define PZ_ENOTSUP (-5) /* request the build does not support                 */
 
+/* Id written for a row whose kernels gave up a bounded wait between the
+ * workgroups that share the row (a device that did not run them together);
+ * ids are otherwise -1 .. V-1.  The synchronous calls return PZ_EDEVICE. */
+#define PZ_ID_FAILED (-2)
+
 /* Temperature forms of src/sampling/temperature.c: the AVX-512 build
  * multiplies by 1.0f/T (:11-20), the scalar build divides by T (:22-23).
  * The default is PZ_TEMP_MUL_RECIP (reference built with -march=native on an

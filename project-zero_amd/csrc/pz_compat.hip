@@ -109,6 +109,7 @@ int run_row(const float* logits, int V, int mode, float temperature, int top_k, 
                                   c.z_id, nullptr);
   // drained on every path: the next call rewrites h_u
   if (hipStreamSynchronize(s->stream) != hipSuccess && c.status == PZ_OK) c.status = PZ_EDEVICE;
+  if (c.status == PZ_OK && *c.h_id == PZ_ID_FAILED) c.status = PZ_EDEVICE;
   return c.status == PZ_OK ? *c.h_id : -1;
 }
 

@@ -48,15 +48,17 @@ struct GrBest {
   pz_f4 bx;     // that float4's values, as compared
 };
 
+// lo: the id of x4[0] (0 for a whole row, a multiple of 32 for a range).
 template <int BLOCK, int U, bool TEMPER, bool PEN>
 __device__ __forceinline__ void gr_group(const PzPenalty& P, const pz_row_params_dev& prm,
-                                         int n4, int base, const pz_f4 (&v)[U], GrBest& B) {
+                                         int lo, int n4, int base, const pz_f4 (&v)[U],
+                                         GrBest& B) {
   const int tid = threadIdx.x;
   uint32_t nib[U];
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int i4 = base + u * BLOCK + tid;
-    nib[u] = PEN ? pz_pen_nibble(P, (i4 < n4 ? i4 : n4 - 1) << 2) : 0u;
+    nib[u] = PEN ? pz_pen_nibble(P, lo + ((i4 < n4 ? i4 : n4 - 1) << 2)) : 0u;
   }
 #pragma unroll
   for (int u = 0; u < U; u++) {
@@ -93,20 +95,20 @@ __device__ __forceinline__ void gr_group(const PzPenalty& P, const pz_row_params
 // in flight, and it then drains every load at the loop head.
 template <int BLOCK, int U, bool TEMPER, bool PEN>
 __device__ __forceinline__ void gr_stream(const PzPenalty& P, const pz_row_params_dev& prm,
-                                          const pz_f4* x4, int n4, pz_f4 (&a)[U],
+                                          int lo, const pz_f4* x4, int n4, pz_f4 (&a)[U],
                                           pz_f4 (&b)[U], GrBest& B) {
   constexpr int STEP = BLOCK * U;
   const int ng = (n4 + STEP - 1) / STEP;
   int g = 0;
   for (; g + 1 < ng; g += 2) {
     gr_load<BLOCK, U>(x4, n4, (g + 1) * STEP, b);
-    gr_group<BLOCK, U, TEMPER, PEN>(P, prm, n4, g * STEP, a, B);
+    gr_group<BLOCK, U, TEMPER, PEN>(P, prm, lo, n4, g * STEP, a, B);
     __builtin_amdgcn_sched_barrier(0);
     gr_load<BLOCK, U>(x4, n4, (g + 2) * STEP, a);
-    gr_group<BLOCK, U, TEMPER, PEN>(P, prm, n4, (g + 1) * STEP, b, B);
+    gr_group<BLOCK, U, TEMPER, PEN>(P, prm, lo, n4, (g + 1) * STEP, b, B);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (g < ng) gr_group<BLOCK, U, TEMPER, PEN>(P, prm, n4, g * STEP, a, B);
+  if (g < ng) gr_group<BLOCK, U, TEMPER, PEN>(P, prm, lo, n4, g * STEP, a, B);
   gr_drain(a);
   gr_drain(b);
 }
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
     B.bv = -__builtin_inff();
     B.b4 = 0x7fffffff;
     B.bx = pz_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    gr_stream<BLOCK, U, TEMPER, PEN>(P, prm, x4, n4, a, b, B);
+    gr_stream<BLOCK, U, TEMPER, PEN>(P, prm, 0, x4, n4, a, b, B);
     if (B.b4 != 0x7fffffff) {  // the first of the float4's values equal to the best
       bv = B.bv;
       bi = (B.b4 << 2) + (B.bx.x == bv ? 0 : B.bx.y == bv ? 1 : B.bx.z == bv ? 2 : 3);
@@ -194,7 +196,9 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
       float e = pz_penalize_inline(j == tid ? hx0 : x[id], id, P.rep, P.pres, P.freq, P.hcap,
                                    P.hkey, P.hcnt);
       if (temper) e = pz_temper(e, prm);
-      pz_argmax_combine(bv, bi, e, id);
+      // -inf never enters (as in the stream): a row whose maximum is -inf
+      // returns id 0, where the reference's scan starts
+      if (e > -__builtin_inff()) pz_argmax_combine(bv, bi, e, id);
     }
   }
 
@@ -211,19 +215,199 @@ __global__ __launch_bounds__(BLOCK) void k_greedy(
   }
 }
 
+
+// Small batches: each row split over gridDim.x workgroups of `chunk` ids
+// (a multiple of 1024, so a range starts 16-byte aligned and on a bitmap
+// word).  Workgroup (s, b) streams the ids [s*chunk, min(V, (s+1)*chunk)) of
+// its row with the loop above, its penalty tables covering that range only,
+// and posts its best as the key (pz_key(v) << 32) | ~id -- the larger key is
+// the larger value, then the lower id, exactly the order of argmax.c's
+// strict '>' scan.  Every posted word is nonzero: 1 means no candidate (below
+// every value's key), and the range holding id 0 posts all ones (above every
+// value's key) when y[0] is NaN, which returns id 0.  The workgroup that
+// arrives last takes the largest word (pz_sp_post_last).  words: the row's
+// meeting words (zero between launches); arrive: zero between launches.
+template <int BLOCK, int U, bool TEMPER, bool PEN>
+__global__ __launch_bounds__(BLOCK) void k_greedy_split(
+    const float* __restrict__ logits, long ld, int V, int chunk,
+    const int32_t* __restrict__ rows, const pz_row_params_dev* __restrict__ params,
+    int n_params, const int32_t* __restrict__ hist, int H, int hcap,
+    int32_t* __restrict__ ids_out, float* __restrict__ p_out, uint64_t* __restrict__ words,
+    int wstride, uint32_t* __restrict__ arrive) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ float red_v[BLOCK / PZ_WAVE];
+  __shared__ int red_i[BLOCK / PZ_WAVE];
+
+  const int sl = blockIdx.x, S = gridDim.x;
+  const int row = pz_row_of(rows, blockIdx.y);
+  const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
+  const int lo = sl * chunk;
+  const int hi = lo + chunk < V ? lo + chunk : V;
+  const float* x = logits + (long)row * ld;
+  const int32_t* hrow = hist ? hist + (long)row * H : nullptr;
+  const int tid = threadIdx.x;
+  const pz_f4* x4 = reinterpret_cast<const pz_f4*>(x + lo);
+  const int n4 = (hi - lo) >> 2;  // 0 only for a last range of 1-3 ids
+
+  int hid0 = -1;
+  if (hrow && tid < H) hid0 = hrow[tid];
+  pz_f4 a[U], b[U];
+  if (n4 > 0) gr_load<BLOCK, U>(x4, n4, 0, a);
+  const float x0 = (sl == 0 && tid == 0) ? x[0] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+
+  PzPenalty P;
+  pz_penalty_setup_range<BLOCK>(P, lds, lo, hi, hcap, PEN && hrow != nullptr && H > 0, prm);
+  float hx0 = 0.0f;
+  const bool hin0 = hid0 >= lo && hid0 < hi;
+  if (PEN) {
+    if (!P.active) {
+      pz_lds_u32* bm = (pz_lds_u32*)lds;
+      for (int w = tid; w < ((hi - lo + 31) >> 5); w += BLOCK) bm[w] = 0u;
+    }
+    __syncthreads();
+    if (P.active) {
+      if (tid < H && hin0) {
+        pz_penalty_insert(P, lds, V, hid0, nullptr, nullptr);
+        hx0 = x[hid0];
+      }
+      for (int j = tid + BLOCK; j < H; j += BLOCK)
+        pz_penalty_insert(P, lds, V, hrow[j], nullptr, nullptr);  // skips ids out of range
+    }
+    __syncthreads();
+  }
+
+  float bv = -__builtin_inff();
+  int bi = 0x7fffffff;
+  if (n4 > 0) {
+    GrBest B;
+    B.bv = -__builtin_inff();
+    B.b4 = 0x7fffffff;
+    B.bx = pz_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    gr_stream<BLOCK, U, TEMPER, PEN>(P, prm, lo, x4, n4, a, b, B);
+    if (B.b4 != 0x7fffffff) {
+      bv = B.bv;
+      bi = lo + (B.b4 << 2) + (B.bx.x == bv ? 0 : B.bx.y == bv ? 1 : B.bx.z == bv ? 2 : 3);
+    }
+  }
+  for (int i = lo + (n4 << 2) + tid; i < hi; i += BLOCK) {
+    if (P.active && pz_pen_member(P, i)) continue;
+    float e = x[i];
+    if (TEMPER) e = pz_temper(e, prm);
+    if (e > bv) { bv = e; bi = i; }
+  }
+  if (P.active) {
+    for (int j = tid; j < H; j += BLOCK) {
+      const int id = j == tid ? hid0 : hrow[j];
+      if (id < lo || id >= hi) continue;
+      float e = pz_penalize_inline(j == tid ? hx0 : x[id], id, P.rep, P.pres, P.freq, P.hcap,
+                                   P.hkey, P.hcnt);
+      if (TEMPER) e = pz_temper(e, prm);
+      if (e > -__builtin_inff()) pz_argmax_combine(bv, bi, e, id);
+    }
+  }
+
+  pz_block_argmax<BLOCK>(bv, bi, red_v, red_i);
+  if (tid >= PZ_WAVE) return;  // wave 0 posts and, in the last workgroup, merges
+  uint64_t* w = words + (size_t)row * wstride;
+  int last = 0;
+  if (tid == 0) {
+    uint64_t key = bi == 0x7fffffff ? 1ull
+                                    : ((uint64_t)pz_key(bv) << 32) | (uint32_t)~(uint32_t)bi;
+    if (sl == 0) {
+      float y0 = x0;
+      if (P.active && pz_pen_member(P, 0)) y0 = pz_penalize(P, y0, 0);
+      if (TEMPER) y0 = pz_temper(y0, prm);
+      if (y0 != y0) key = ~0ull;  // argmax.c:4-5: a NaN x[0] is never replaced
+    }
+    last = pz_sp_post_last(w, sl, key, arrive, row, S);
+  }
+  if (!__builtin_amdgcn_readfirstlane(last)) return;
+  uint64_t k = 1ull;
+  bool seen = true;
+  for (int j = tid; j < S; j += PZ_WAVE) {
+    const uint64_t o = pz_poll_u64(&w[j]);
+    seen = seen && o != 0ull;
+    k = o > k ? o : k;
+    __hip_atomic_store(&w[j], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t lo32 = (uint32_t)__shfl_xor((int)(uint32_t)k, off, PZ_WAVE);
+    const uint32_t hi32 = (uint32_t)__shfl_xor((int)(uint32_t)(k >> 32), off, PZ_WAVE);
+    const uint64_t o = ((uint64_t)hi32 << 32) | lo32;
+    k = o > k ? o : k;
+  }
+  const bool all_seen = __builtin_amdgcn_ballot_w64(!seen) == 0ull;
+  if (tid == 0) {
+    // no candidate (every value NaN or -inf): the scan ends on index 0
+    ids_out[row] = !all_seen ? PZ_ID_FAILED : (k == 1ull || k == ~0ull) ? 0
+                                                                      : (int32_t)~(uint32_t)k;
+    if (p_out) p_out[row] = 1.0f;
+    __hip_atomic_store(&arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 }  // namespace
 
 constexpr int GREEDY_BLOCK = 256;
 constexpr int GREEDY_U = 4;
 
+// Rows split over workgroups while a launch has fewer than GREEDY_SPLIT_WG
+// workgroups' worth of rows: ranges of at least GREEDY_MIN_CHUNK ids.
+#ifndef GREEDY_SPLIT_WG
+#define GREEDY_SPLIT_WG 512
+#endif
+#ifndef GREEDY_MIN_CHUNK
+#define GREEDY_MIN_CHUNK 4096
+#endif
+constexpr int GREEDY_MAX_SPLIT = 128;
+#ifndef GREEDY_SPLIT_BLOCK
+#define GREEDY_SPLIT_BLOCK 256
+#endif
+#ifndef GREEDY_SPLIT_U
+#define GREEDY_SPLIT_U 4
+#endif
+
+// Workgroups per row (1: one workgroup owns the row) and the ids of each.
+static int greedy_split(int V, int n_rows, int* chunk) {
+  int S = (GREEDY_SPLIT_WG + n_rows - 1) / n_rows;
+  const int smax = V / GREEDY_MIN_CHUNK;
+  if (S > smax) S = smax;
+  if (S > GREEDY_MAX_SPLIT) S = GREEDY_MAX_SPLIT;
+  if (S < 2) return 1;
+  int c = (V + S - 1) / S;
+  c = (c + 1023) & ~1023;
+  *chunk = c;
+  return (V + c - 1) / c;
+}
+
 template <bool TEMPER>
 static int launch_argmax(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   if (n_rows <= 0) return 0;
+  constexpr size_t kStatic = 2 * (GREEDY_BLOCK / PZ_WAVE) * 4;
+  const bool vec = (L.ld % 4 == 0) && (((uintptr_t)L.logits & 15) == 0) && L.V >= 4;
+  int chunk = 0;
+  const int S = vec && L.ws.meet && L.ws.arrive ? greedy_split(L.V, n_rows, &chunk) : 1;
+  if (S > 1 && S <= 2 * L.ws.smax) {
+    const size_t lds = L.pen_any ? pz_penalty_lds_bytes(chunk, L.hcap) : 0;
+    constexpr size_t kStaticS = 2 * (GREEDY_SPLIT_BLOCK / PZ_WAVE) * 4;
+    if (lds + kStaticS > (size_t)L.max_lds) return -2;
+    auto k = L.pen_any ? k_greedy_split<GREEDY_SPLIT_BLOCK, GREEDY_SPLIT_U, TEMPER, true>
+                       : k_greedy_split<GREEDY_SPLIT_BLOCK, GREEDY_SPLIT_U, TEMPER, false>;
+    if (lds > 65536 && hipFuncSetAttribute((const void*)k,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds) != hipSuccess)
+      return -1;
+    hipLaunchKernelGGL(k, dim3(S, n_rows), dim3(GREEDY_SPLIT_BLOCK), lds, L.stream, L.logits,
+                       L.ld,
+                       L.V, chunk, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, L.ids,
+                       L.p_out, L.ws.meet, 2 * L.ws.smax, L.ws.arrive);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+  }
   const size_t lds = L.pen_any ? pz_penalty_lds_bytes(L.V, L.hcap) : 0;
   // static LDS: the block argmax scratch (2 words per wave)
-  constexpr size_t kStatic = 2 * (GREEDY_BLOCK / PZ_WAVE) * 4;
   if (lds + kStatic > (size_t)L.max_lds) return -2;
-  const bool vec = (L.ld % 4 == 0) && (((uintptr_t)L.logits & 15) == 0) && L.V >= 4;
   dim3 grid(n_rows), block(GREEDY_BLOCK);
   auto k = vec ? (L.pen_any ? k_greedy<GREEDY_BLOCK, GREEDY_U, true, TEMPER, true>
                             : k_greedy<GREEDY_BLOCK, GREEDY_U, true, TEMPER, false>)

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "pz_params.h"
+#include "pz_sampler.h"
 #include "pz_split.h"
 
 // Device scratch owned by a sampler (carved from one allocation).

@@ -430,6 +430,9 @@ extern "C" int pz_sample_batch(pz_sampler* s, const float* d_logits, int B, int 
   }
   memcpy(ids_out, s->h_ids, (size_t)B * sizeof(int32_t));
   if (p_out) memcpy(p_out, s->h_p, (size_t)B * sizeof(float));
+  for (int b = 0; b < B; b++)
+    if (ids_out[b] == PZ_ID_FAILED)
+      return fail(s, PZ_EDEVICE, "row %d: a wait between the row's workgroups gave up", b);
   return PZ_OK;
 }
 

@@ -217,6 +217,41 @@ __device__ __forceinline__ bool pz_sp_arrive(uint32_t* arrive, int row, int S, i
   return *flag_sh != 0;
 }
 
+// Polls a word published by another workgroup of the launch with an
+// agent-scope relaxed atomic load (coherent across the XCDs' L2s) until it
+// is nonzero, at most PZ_POLL_CAP times; returns 0 if it never was.
+#ifndef PZ_POLL_CAP
+#define PZ_POLL_CAP (1u << 22)
+#endif
+__device__ __forceinline__ uint64_t pz_poll_u64(const uint64_t* w, uint32_t cap = PZ_POLL_CAP) {
+  uint64_t v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (uint32_t n = 1; v == 0ull && n < cap; n++) {
+    __builtin_amdgcn_s_sleep(1);
+    v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return v;
+}
+
+// "Last workgroup merges" for one nonzero 64-bit word per workgroup, with no
+// L2 write-back or invalidation (an agent-scope release/acquire pair costs
+// one of each per workgroup, which stalls every other workgroup's stream on
+// that XCD's L2).  Thread 0 of each of the row's S workgroups stores its
+// word w[sl] with an agent-scope relaxed atomic store, then counts itself in
+// at arrive[row]; the call returns true in thread 0 of the workgroup whose
+// increment brings the counter to S (false everywhere else).  That
+// workgroup then reads the words with pz_poll_u64: every other workgroup
+// issued its store before its increment, so each poll ends as soon as that
+// store lands -- the waiting workgroup is the last one, so no wait depends
+// on a workgroup that has not run.  The merging wave clears the words and
+// the counter (zero between launches).
+__device__ __forceinline__ bool pz_sp_post_last(uint64_t* w, int sl, uint64_t word,
+                                                uint32_t* arrive, int row, int S) {
+  __hip_atomic_store(&w[sl], word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t prev =
+      __hip_atomic_fetch_add(&arrive[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return prev == (uint32_t)(S - 1);
+}
+
 __device__ __forceinline__ void pz_sp_rearm(uint32_t* arrive, int row) {
   if (threadIdx.x == 0)
     __hip_atomic_store(&arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

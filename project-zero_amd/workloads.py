@@ -13,12 +13,14 @@ Each builder returns a dict with the host inputs of one configuration:
   c4  1024 x 128256, N(0,3^2); repetition 1.15 over 256 uniform ids; greedy
   c5  speculative verify: 32 seqs x 4 drafts x 128256, target N(0,2.5^2),
       draft = target + N(0,0.5^2), tau 0.8 (see build_c5)
+  cat the plain path's full-vocabulary draw (the HTTP default T 1.0, top-p
+      1.0: softmax + ascending-id CDF, generate.c:157-169) over c2's logits
 """
 import numpy as np
 
 import pzsample as pz
 
-SEEDS = {"c1": 0xC1, "c2": 0xC2, "c3": 0xC3, "c4": 0xC4, "c5": 0xC5}
+SEEDS = {"c1": 0xC1, "c2": 0xC2, "c3": 0xC3, "c4": 0xC4, "c5": 0xC5, "cat": 0xCA}
 
 
 def _draw_seed(base):
@@ -42,6 +44,16 @@ def build_c2(B=64, V=128256, seed=None):
     prm = pz.row_params(temperature=0.7, top_p=0.9)
     u = pz.synth_draws(B, _draw_seed(seed))
     return dict(name="c2", logits=x, params=[prm], u=u, hist=None,
+                bytes_per_row=V * 4 + 4 + 4)
+
+
+def build_cat(B=64, V=128256, seed=None):
+    seed = SEEDS["cat"] if seed is None else seed
+    x = pz.synth_normal(B, V, 2.0, seed)
+    pz.synth_spikes(x, 5, 8.0, 12.0, seed + 1)
+    prm = pz.row_params(temperature=1.0)
+    u = pz.synth_draws(B, _draw_seed(seed))
+    return dict(name="cat", logits=x, params=[prm], u=u, hist=None,
                 bytes_per_row=V * 4 + 4 + 4)
 
 
@@ -83,4 +95,5 @@ def build_c5(B=32, K=4, V=128256, has_bonus=True, seed=None):
                 bytes_per_seq=(2 * K + (1 if has_bonus else 0)) * V * 4 + K * 8 + 4 + (K + 2) * 4)
 
 
-BUILDERS = {"c1": build_c1, "c2": build_c2, "c3": build_c3, "c4": build_c4, "c5": build_c5}
+BUILDERS = {"c1": build_c1, "c2": build_c2, "c3": build_c3, "c4": build_c4, "c5": build_c5,
+            "cat": build_cat}

@@ -70,8 +70,10 @@ def test_ties_lowest_id(torch_cuda):
     assert ids[3] == 0 and ids[4] == 10 and ids[5] == 0
 
 
-def test_nan_and_inf_rows(torch_cuda):
-    V = 4096
+@pytest.mark.parametrize("V", [4000, 8192, 128256])
+def test_nan_and_inf_rows(torch_cuda, V):
+    """V=4000 takes one workgroup per row, the others split rows; with and
+    without a penalty history (a history id's -inf stays -inf)."""
     x = pz.synth_normal(6, V, 1.0, 9)
     x[0, 0] = np.nan                 # NaN at 0 -> 0
     x[1, 5] = np.nan                 # NaN elsewhere is skipped
@@ -79,9 +81,13 @@ def test_nan_and_inf_rows(torch_cuda):
     x[3, :] = np.nan
     x[4, 100] = np.inf
     x[5, 1:] = -np.inf
-    ids, _ = run_gpu(torch_cuda, x, [pz.row_params(temperature=0.0)])
-    want, _, _, _ = po.sample_batch(x, [po.params(temperature=0.0)])
-    assert (ids == want).all(), (ids, want)
+    hist = pz.synth_uniform_ids(6, 32, V, 10)
+    hist[:, 0] = 5
+    for prm in (pz.row_params(temperature=0.0), pz.row_params(temperature=0.0, rep_penalty=1.2),
+                pz.row_params(temperature=0.0, presence_penalty=0.5, frequency_penalty=0.3)):
+        ids, _ = run_gpu(torch_cuda, x, [prm], hist)
+        want, _, _, _ = po.sample_batch(x, [orc_params(prm)], hist=hist)
+        assert (ids == want).all(), (V, prm.rep_penalty, ids, want)
 
 
 def test_penalty_edge_ids(torch_cuda):
@@ -124,3 +130,72 @@ def test_per_row_params_and_errors(torch_cuda):
         with pytest.raises(pz.PzError) as e:
             s.sample(d_x, B, V, V, [pz.row_params(temperature=0.0)])
         assert e.value.code == pz.PZ_ERANGE
+
+
+def split_plan(V, n_rows, target_wg=512, min_chunk=4096, max_split=128):
+    """The launcher's rule (pz_greedy.hip, greedy_split): workgroups per row
+    and ids per range, a multiple of 1024."""
+    S = min(-(-target_wg // n_rows), V // min_chunk, max_split)
+    if S < 2:
+        return 1, V
+    c = -(-V // S)
+    c = (c + 1023) & ~1023
+    return -(-V // c), c
+
+
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_split_rows_small_batches(torch_cuda, B):
+    """Small batches split each row over workgroups (ranges of a multiple of
+    1024 ids) and merge the ranges' bests: ids stay bit-exact, with ties and
+    history ids placed on both sides of the range boundaries."""
+    V = 128256
+    x = pz.synth_normal(B, V, 3.0, 4000 + B)
+    hist = pz.synth_uniform_ids(B, 256, V, 4100 + B)
+    S, chunk = split_plan(V, B)
+    assert S > 1
+    b24 = chunk * (S // 2)  # a boundary between two ranges in the middle of the row
+    x[0, b24 - 1] = x[0, b24] = 50.0                    # tie across the boundary -> b24 - 1
+    if B > 1:
+        x[1, :] = -1.0
+        x[1, b24 - 1], x[1, b24] = -0.0, 0.0            # -0.0 == +0.0 -> b24 - 1
+    if B > 2:
+        x[2, 5000::7000] = 60.0                         # one tie in many ranges -> 5000
+        x[2, V - 1] = 60.0
+    if B > 3:
+        x[3, 0] = np.nan                                # NaN at x[0] -> 0
+    if B > 4:
+        x[4, :] = -np.inf                               # nothing beats -inf -> 0
+        x[4, V - 1] = np.nan
+    if B > 5:
+        x[5, b24 - 1] = 40.0                            # penalised away (history below)
+        x[5, b24] = 39.0
+        hist[5, :4] = [b24 - 1, b24 - 1, V, -3]
+    if B > 6:
+        x[6, V - 1] = 70.0                              # the last id, in the last range
+    for prm in (pz.row_params(temperature=0.0),
+                pz.row_params(temperature=0.0, rep_penalty=1.15),
+                pz.row_params(temperature=0.0, presence_penalty=0.5, frequency_penalty=0.3)):
+        print(f"case split greedy B={B} rep={prm.rep_penalty} pres={prm.presence_penalty}",
+              flush=True)
+        ids, p = run_gpu(torch_cuda, x, [prm], hist)
+        want, _, _, _ = po.sample_batch(x, [orc_params(prm)], hist=hist)
+        assert (ids == want).all(), (np.nonzero(ids != want)[0][:10], ids[:8], want[:8])
+        assert (p == 1.0).all()
+    assert want[0] == b24 - 1
+
+
+@pytest.mark.parametrize("V", [8192, 8193, 12291, 20481, 20482, 20483, 49152, 151936])
+def test_split_rows_range_tails(torch_cuda, V):
+    """Vocabularies whose last range holds 1-3 ids (or a partial float4)."""
+    B = 3
+    S, chunk = split_plan(V, B)
+    assert S > 1
+    x = pz.synth_normal(B, V, 2.0, 4200 + V)
+    x[1, V - 1] = 30.0
+    x[2, V - 3:] = 30.0
+    hist = pz.synth_uniform_ids(B, 64, V, 4300 + V)
+    hist[2, 0] = V - 3
+    for prm in (pz.row_params(temperature=0.0), pz.row_params(temperature=0.0, rep_penalty=1.3)):
+        ids, _ = run_gpu(torch_cuda, x, [prm], hist)
+        want, _, _, _ = po.sample_batch(x, [orc_params(prm)], hist=hist)
+        assert (ids == want).all(), (V, ids, want)
