@@ -83,6 +83,15 @@ PZ_API void pz_sampler_destroy(pz_sampler *s);
 /* PZ_TEMP_MUL_RECIP or PZ_TEMP_DIV. */
 PZ_API int pz_sampler_set_temp_mode(pz_sampler *s, int mode);
 
+/* Bound of every wait between the workgroups that share a row inside one
+ * launch, in polls of the awaited word (0 restores the default, 2^22 polls:
+ * tenths of a second).  The waits end by themselves on a device that runs a
+ * row's workgroups together; one that reaches the bound gives up, every
+ * kernel still exits, and the row's id is PZ_ID_FAILED (the synchronous
+ * calls return PZ_EDEVICE).  A bound of a few polls makes rows fail on
+ * purpose, which tests that path. */
+PZ_API int pz_sampler_set_wait_bound(pz_sampler *s, uint32_t polls);
+
 /* Last error message of this sampler ("" when none). */
 PZ_API const char *pz_sampler_last_error(const pz_sampler *s);
 
@@ -154,7 +163,10 @@ PZ_API int pz_sampler_set_eos(pz_sampler *s, const int32_t *eos_ids, int n_eos);
  * Every call on one GPU shares that GPU's array, which keeps the last call's
  * contents: calls that overlap on one GPU (other streams, other host threads)
  * race, so order them on one stream.  Errors are reported by return code
- * only.  Asynchronous on `stream`. */
+ * only.  Asynchronous on `stream`; the caller's current device is left as it
+ * was.  A call can be captured into a HIP graph (it enqueues kernels only,
+ * no copies or memsets) once a first call on the device has run outside the
+ * capture; replays keep the captured arguments. */
 #define PZ_NOALLOC_MAX_BATCH 64
 #define PZ_NOALLOC_MAX_VOCAB 262144
 #define PZ_NOALLOC_MAX_HIST 2048

@@ -233,7 +233,7 @@ __global__ __launch_bounds__(BLOCK) void k_greedy_split(
     const int32_t* __restrict__ rows, const pz_row_params_dev* __restrict__ params,
     int n_params, const int32_t* __restrict__ hist, int H, int hcap,
     int32_t* __restrict__ ids_out, float* __restrict__ p_out, uint64_t* __restrict__ words,
-    int wstride, uint32_t* __restrict__ arrive) {
+    int wstride, uint32_t* __restrict__ arrive, uint32_t cap) {
   extern __shared__ __align__(16) char lds[];
   __shared__ float red_v[BLOCK / PZ_WAVE];
   __shared__ int red_i[BLOCK / PZ_WAVE];
@@ -326,7 +326,7 @@ __global__ __launch_bounds__(BLOCK) void k_greedy_split(
   uint64_t k = 1ull;
   bool seen = true;
   for (int j = tid; j < S; j += PZ_WAVE) {
-    const uint64_t o = pz_poll_u64(&w[j]);
+    const uint64_t o = pz_poll_u64(&w[j], cap);
     seen = seen && o != 0ull;
     k = o > k ? o : k;
     __hip_atomic_store(&w[j], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -402,7 +402,7 @@ static int launch_argmax(const pz_launch& L, int n_rows, const int32_t* d_rows) 
     hipLaunchKernelGGL(k, dim3(S, n_rows), dim3(GREEDY_SPLIT_BLOCK), lds, L.stream, L.logits,
                        L.ld,
                        L.V, chunk, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, L.ids,
-                       L.p_out, L.ws.meet, 2 * L.ws.smax, L.ws.arrive);
+                       L.p_out, L.ws.meet, 2 * L.ws.smax, L.ws.arrive, L.wait_polls);
     return hipGetLastError() == hipSuccess ? 0 : -1;
   }
   const size_t lds = L.pen_any ? pz_penalty_lds_bytes(L.V, L.hcap) : 0;

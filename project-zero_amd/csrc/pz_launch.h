@@ -51,6 +51,8 @@ struct pz_launch {
   PzSplitWs ws;          // workspace of the row-split passes
   int kmax = 0;         // largest top_k among the launch's top-k rows (0: unknown)
   int max_lds;          // max dynamic LDS per workgroup on this device
+  uint32_t wait_polls = PZ_POLL_CAP;  // bound of a wait between workgroups, in polls
+  int n_cu = 0;                       // compute units of the device
   hipStream_t stream;
 };
 

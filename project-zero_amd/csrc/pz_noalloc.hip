@@ -68,6 +68,7 @@ size_t carve(char* base, NoallocLayout* out) {
 struct DeviceState {
   bool ready = false;
   int max_lds = 0;
+  int n_cu = 0;
   NoallocLayout lay{};
 };
 
@@ -84,7 +85,9 @@ int device_setup(int device, const DeviceState** out) {
     if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return PZ_EDEVICE;
     if (carve(nullptr, nullptr) > kScratchBytes) return PZ_ENOTSUP;
     if (hipDeviceGetAttribute(&d.max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device) !=
-        hipSuccess)
+            hipSuccess ||
+        hipDeviceGetAttribute(&d.n_cu, hipDeviceAttributeMultiprocessorCount, device) !=
+            hipSuccess)
       return PZ_EDEVICE;
     carve(static_cast<char*>(ptr), &d.lay);
     d.ready = true;
@@ -155,6 +158,14 @@ extern "C" int pz_sample_batch_noalloc(int device, void* stream, int temp_mode,
   if (B > PZ_NOALLOC_MAX_BATCH || V > PZ_NOALLOC_MAX_VOCAB || H > PZ_NOALLOC_MAX_HIST)
     return PZ_ERANGE;
   if (B == 0) return PZ_OK;
+  // the caller's current device is restored on every return
+  struct DeviceGuard {
+    int prev = -1;
+    ~DeviceGuard() {
+      if (prev >= 0) (void)hipSetDevice(prev);
+    }
+  } guard;
+  if (hipGetDevice(&guard.prev) != hipSuccess) guard.prev = -1;
   if (hipSetDevice(device) != hipSuccess) return PZ_EDEVICE;
   const DeviceState* ds = nullptr;
   const int rc0 = device_setup(device, &ds);
@@ -210,6 +221,7 @@ extern "C" int pz_sample_batch_noalloc(int device, void* stream, int temp_mode,
   L.ws = lay.ws;
   L.kmax = pz_max_top_k(img.res, B, n_params);
   L.max_lds = ds->max_lds;
+  L.n_cu = ds->n_cu;
   L.stream = st;
   int m = -1;
   rc = pz_launch_modes(L, count, offset, modes_present, lay.rows, &m);

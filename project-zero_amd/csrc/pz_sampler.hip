@@ -82,7 +82,9 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
   };
   if (hipSetDevice(device) != hipSuccess) return bail(PZ_EDEVICE);
   if (hipDeviceGetAttribute(&s->max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock,
-                            device) != hipSuccess)
+                            device) != hipSuccess ||
+      hipDeviceGetAttribute(&s->n_cu, hipDeviceAttributeMultiprocessorCount, device) !=
+          hipSuccess)
     return bail(PZ_EDEVICE);
   if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess)
     return bail(PZ_EDEVICE);
@@ -161,6 +163,12 @@ extern "C" void pz_sampler_destroy(pz_sampler* s) {
 extern "C" int pz_sampler_set_temp_mode(pz_sampler* s, int mode) {
   if (!s || (mode != PZ_TEMP_MUL_RECIP && mode != PZ_TEMP_DIV)) return PZ_EINVAL;
   s->temp_mode = mode;
+  return PZ_OK;
+}
+
+extern "C" int pz_sampler_set_wait_bound(pz_sampler* s, uint32_t polls) {
+  if (!s) return PZ_EINVAL;
+  s->wait_polls = polls ? polls : PZ_POLL_CAP;
   return PZ_OK;
 }
 
@@ -351,6 +359,8 @@ int pz_dispatch_resolved(pz_sampler* s, const float* d_logits, int B, int V, lon
   L.ws = s->ws;
   L.kmax = pz_max_top_k(res, B, n_params);
   L.max_lds = s->max_lds;
+  L.wait_polls = s->wait_polls;
+  L.n_cu = s->n_cu;
   L.stream = s->stream;
 
   if (hooks && pz_launch_step_draw(L, B, hooks->state, s->d_u_step) != 0)

@@ -14,6 +14,8 @@ struct pz_sampler {
   int max_batch = 0, max_vocab = 0, max_hist = 0;
   int temp_mode = PZ_TEMP_MUL_RECIP;
   int max_lds = 0;
+  int n_cu = 0;                       // compute units of the device
+  uint32_t wait_polls = PZ_POLL_CAP;  // bound of the waits between workgroups
   hipStream_t stream = nullptr;
   hipEvent_t staged = nullptr;  // guards reuse of the pinned staging area
 

@@ -423,11 +423,15 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_
 // At a meeting each workgroup posts one 64-bit word (value and a written
 // bit, so no fence orders it: a fence at agent scope writes back or
 // invalidates the whole L2) and wave 0 polls the row's S words.  The
-// histograms are exchanged the same way, one word per bin (written bit, the
-// call's tag, the count).  A row's workgroups are consecutive in the launch
-// order and a CU holds two of them, so every workgroup a wait depends on has
-// been dispatched: the waits end.  (The walk launch, which follows, clears the
-// words.)  Every workgroup of a row merges the same histograms into the same
+// histograms are exchanged the same way, one word per bin (written bit and
+// the count).  A row's workgroups are consecutive in the launch order, each
+// posts everything it owes before its first wait, and the S <= 64 of them
+// fit on the device together, so every workgroup a wait depends on gets
+// dispatched: the waits end.  Each wait is bounded all the same (`cap`
+// polls): one that gives up posts what its workgroup still owes, marks the
+// row failed (rs.i[7]) and leaves; the walk launch then returns
+// PZ_ID_FAILED for the row.  (The walk launch, which follows, clears the
+// words and the mark on every path.)  Every workgroup of a row merges the same histograms into the same
 // nucleus bins (a fixed-order reduction), gathers its slice's candidates of
 // those bins as (e, ~id) keys into the row's list (count: ws.arrive[row],
 // plus TOPP_GOVER when a wave's staging overflows), and workgroup 0 records
@@ -437,26 +441,33 @@ constexpr uint32_t TOPP_HWRITTEN = 0x80000000u;
 constexpr int TOPP_GOVER = 1 << 30;      // added to a row's count when its gather overflowed
 constexpr int TOPP_STAGE = PZ_SP_SEG / 2;  // keys a 256-term segment of LDS stages (8 B each)
 
-__device__ __forceinline__ uint32_t topp_hword(uint32_t tag, uint32_t count) {
-  return TOPP_HWRITTEN | ((tag & 0xffffu) << 15) | count;
+__device__ __forceinline__ uint32_t topp_hword(uint32_t count) { return TOPP_HWRITTEN | count; }
+
+// Marks the row failed: a wait between its workgroups gave up (read and
+// cleared by the walk launch).
+__device__ __forceinline__ void topp_mark_failed(const PzSplitWs& ws, int row) {
+  __hip_atomic_store(&ws.rs[row].i[7], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Nucleus bins of the row from its S published histograms (every thread; a
 // barrier inside): the merged counts in ehist, then wave 0's fixed-order
 // total and selection (every workgroup of the row gets the same bins).
+// bsel < 0: a bin's wait gave up (the row is failed).
 struct ToppSel {
   int bsel;
   uint32_t nsel;
 };
-__device__ __forceinline__ ToppSel topp_front_select(const uint32_t* hrow, int S, uint32_t tag,
+__device__ __forceinline__ ToppSel topp_front_select(const uint32_t* hrow, int S, uint32_t cap,
                                                      pz_lds_u32b* ehist, float top_p,
-                                                     ToppSel* sel_sh, float* part_sh) {
+                                                     ToppSel* sel_sh, float* part_sh,
+                                                     int* fail_sh) {
   static_assert(PZ_TOPP_NB <= 2 * PZ_SP_BLOCK, "two bins per thread");
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const uint32_t want = TOPP_HWRITTEN | ((tag & 0xffffu) << 15);
-  const uint32_t mask = TOPP_HWRITTEN | (0xffffu << 15);
+  const uint32_t want = TOPP_HWRITTEN;
+  const uint32_t mask = TOPP_HWRITTEN;
   const int i0 = tid, i1 = tid + PZ_SP_BLOCK;
   uint32_t c0 = 0, c1 = 0;
+  bool gave_up = false;
   for (int s0 = 0; s0 < S; s0 += 8) {
     uint32_t v0[8], v1[8];
 #pragma unroll
@@ -471,22 +482,30 @@ __device__ __forceinline__ ToppSel topp_front_select(const uint32_t* hrow, int S
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       const uint32_t* h = hrow + (size_t)(s0 + q) * PZ_TOPP_NB;
-      while ((v0[q] & mask) != want) {
+      for (uint32_t n = 1; (v0[q] & mask) != want && n < cap; n++) {
         __builtin_amdgcn_s_sleep(1);
         v0[q] = __hip_atomic_load(&h[i0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      while ((v1[q] & mask) != want) {
+      for (uint32_t n = 1; (v1[q] & mask) != want && n < cap; n++) {
         __builtin_amdgcn_s_sleep(1);
         v1[q] = __hip_atomic_load(&h[i1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      c0 += v0[q] & 0x7fffu;
-      c1 += v1[q] & 0x7fffu;
+      gave_up |= (v0[q] & mask) != want || (v1[q] & mask) != want;
+      c0 += v0[q] & 0x7fffffffu;
+      c1 += v1[q] & 0x7fffffffu;
     }
   }
   ehist[i0] = c0;
   if (i1 < PZ_TOPP_NB) ehist[i1] = c1;
   if (tid == 0) sel_sh->bsel = INT_MAX;  // (the first crossing, as a position from the top)
+  if (gave_up) *fail_sh = 1;
   pz_lds_barrier();
+  if (*fail_sh) {
+    ToppSel r;
+    r.bsel = -1;
+    r.nsel = 0;
+    return r;
+  }
   // The bins from the top down, two per thread (positions 2 tid, 2 tid + 1
   // are bins NB-1-2 tid, NB-2-2 tid): the estimated mass and count above
   // each one by a workgroup scan in a fixed order, so every workgroup of
@@ -535,7 +554,7 @@ __device__ __forceinline__ ToppSel topp_front_select(const uint32_t* hrow, int S
 template <bool VEC>
 __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOPP_ARGS,
                                                                              int pen_bytes,
-                                                                             uint32_t tag) {
+                                                                             uint32_t cap) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
@@ -544,6 +563,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   __shared__ float part_sh[2 * PZ_SP_WAVES];
   __shared__ int wcnt[PZ_SP_WAVES];
   __shared__ uint32_t sgf[TOPP_FRONT_SEGS];  // the slice's predicted grids
+  __shared__ int fail_sh;                     // a wait of this workgroup gave up
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = pz_row_of(rows, blockIdx.y);
@@ -554,7 +574,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
   pz_lds_f32* ybuf = (pz_lds_f32*)(lds + (((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15));
   uint64_t* meet = ws.meet + (size_t)row * 2 * ws.smax;
-  if (tid == 0) SS.any = 0u;
+  if (tid == 0) {
+    SS.any = 0u;
+    fail_sh = 0;
+  }
   // the fallback queue, empty for k_topp_walkf (the k_topp_fallback before
   // has read it: launches on a stream run in order)
   if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) sc.counters[0] = 0;
@@ -618,9 +641,13 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   }
   if (w == 0) {
     uint64_t v = 1ull << 63;
-    for (;;) {
+    for (uint32_t n = 1;; n++) {
       if (lane < S) v = __hip_atomic_load(&meet[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__ballot((v >> 63) == 0) == 0) break;
+      if (n >= cap) {
+        if (lane == 0) fail_sh = 1;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
     const float M = pz_wave_max(lane < S ? __uint_as_float((uint32_t)v) : -__builtin_inff());
@@ -635,6 +662,19 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
     }
   }
   pz_lds_barrier();
+  if (fail_sh) {
+    // meet 1 gave up: post what the others wait for (an empty histogram, no
+    // mass), mark the row and leave
+    uint32_t* gh = ws.hist + ((size_t)blockIdx.y * S + blockIdx.x) * PZ_TOPP_NB;
+    for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK)
+      __hip_atomic_store(&gh[i], topp_hword(0u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+      __hip_atomic_store(&meet[ws.smax + blockIdx.x], 1ull << 63, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      topp_mark_failed(ws, row);
+    }
+    return;
+  }
   const bool degen = topp_degenerate(SS.any);
   const float M = SS.M, thr = M - 20.0f;
   // 2. the estimated candidate mass of each segment (as k_topp_est) and the
@@ -664,7 +704,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   if (!degen) {
     uint32_t* gh = hrow + (size_t)blockIdx.x * PZ_TOPP_NB;
     for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK)
-      __hip_atomic_store(&gh[i], topp_hword(tag, ehist[i]), __ATOMIC_RELAXED,
+      __hip_atomic_store(&gh[i], topp_hword(ehist[i]), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
   static_assert(TOPP_FRONT_SEGS <= 64, "one estimate per lane");
@@ -678,10 +718,14 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   if (degen) return;  // (every workgroup of the row; the words are cleared all the same)
   if (w == 0) {
     uint64_t v = 1ull << 63;
-    for (;;) {
+    for (uint32_t n = 1;; n++) {
       if (lane < (int)blockIdx.x)
         v = __hip_atomic_load(&meet[ws.smax + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__ballot((v >> 63) == 0) == 0) break;
+      if (n >= cap) {
+        if (lane == 0) fail_sh = 1;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
     }
     // the estimated mass before this slice
@@ -689,6 +733,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
     if (lane == 0) SS.carry = carry;
   }
   pz_lds_barrier();
+  if (fail_sh) {  // (this workgroup's histogram and meet-2 word are posted)
+    if (tid == 0) topp_mark_failed(ws, row);
+    return;
+  }
   pz_sp_predict(ToppSliceEst{sest, sl.k0}, SS.carry, row, sl, ws, SS, (pz_lds_u32*)sgf);
   // 3. records from LDS (as k_topp_rec)
   PzExpTerms<ToppLdsRow> X;
@@ -703,7 +751,12 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)sgf);
   // 4. the nucleus bins (the row's histograms were published before meet 2)
   pz_lds_barrier();
-  const ToppSel sel = topp_front_select(hrow, S, tag, ehist, prm.top_p, &sel_sh, part_sh);
+  const ToppSel sel =
+      topp_front_select(hrow, S, cap, ehist, prm.top_p, &sel_sh, part_sh, &fail_sh);
+  if (sel.bsel < 0) {
+    if (tid == 0) topp_mark_failed(ws, row);
+    return;
+  }
   const bool all = sel.bsel == 0;
   const float e_gate = all ? 0.0f : ebin_lo(sel.bsel);
   const float dgate = all ? -__builtin_inff() : __logf(e_gate) - 0.01f;
@@ -818,20 +871,30 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
 template <bool VEC>
 __device__ __forceinline__ void topp_gather_slice(TOPP_ARGS, int row, int slice, int gspw,
                                                   char* lds, pz_lds_u64* lkeys, int lcap,
-                                                  const pz_lds_u64* et, PzSpShared& SS) {
+                                                  const pz_lds_u64* et, PzSpShared& SS,
+                                                  uint32_t cap) {
+  __shared__ int ready_sh;
   pz_sp_row_stat(row, S, ws, SS);
   if (topp_degenerate(SS.any)) return;
   // the row's nucleus bins, picked by the walking workgroup of this launch
   // (it has a lower block index, so it was dispatched first, and it waits on
-  // nothing here: the wait ends)
+  // nothing here: the wait ends; bounded all the same -- a gather that gives
+  // up marks the row failed, which the nucleus launch reports)
   // (relaxed polls -- an acquire per poll would invalidate the L2 the walks
   // read from -- then one acquire)
   if (threadIdx.x == 0) {
-    while (__hip_atomic_load(&ws.rs[row].i[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+    int ready = 0;
+    for (uint32_t n = 1;; n++) {
+      ready = __hip_atomic_load(&ws.rs[row].i[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (ready != 0 || n >= cap) break;
       __builtin_amdgcn_s_sleep(8);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    if (ready) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    else topp_mark_failed(ws, row);
+    ready_sh = ready;
   }
   __syncthreads();
+  if (!ready_sh) return;
   const PzRowState rs0 = ws.rs[row];
   if (rs0.i[0] == TP_DONE) return;
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
@@ -925,7 +988,7 @@ __device__ __forceinline__ void topp_gather_slice(TOPP_ARGS, int row, int slice,
 template <bool VEC>
 __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walk(TOPP_ARGS, int pen_bytes, int nc,
                                                           int n_rows, int gS, int gspw,
-                                                          int goff, int lcap) {
+                                                          int goff, int lcap, uint32_t cap) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   __shared__ int first_sh, merged_sh;
@@ -938,7 +1001,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walk(TOPP_ARGS, int pen_by
     const int g = (int)blockIdx.x - n_rows;
     topp_gather_slice<VEC>(logits, ld, V, rows, params, n_params, hist, H, hcap, nseg, spw, S,
                            ws, u, ids_out, p_out, sc, pz_row_of(rows, g / gS), g % gS, gspw,
-                           lds, (pz_lds_u64*)(lds + goff), lcap, et, SS);
+                           lds, (pz_lds_u64*)(lds + goff), lcap, et, SS, cap);
     return;
   }
   const int row = pz_row_of(rows, blockIdx.x);
@@ -1202,6 +1265,18 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_nucleus(TOPP_ARGS, int cap
   __shared__ ToppShared T;
   const int row = pz_row_of(rows, blockIdx.x);
   const PzRowState rs0 = ws.rs[row];
+  if (rs0.i[7]) {
+    // a gather's wait gave up: the list is incomplete (a row the walk
+    // settled, or queued for the fallback, keeps that result)
+    if (threadIdx.x == 0) {
+      ws.rs[row].i[7] = 0;
+      if (rs0.i[0] != TP_DONE) {
+        ids_out[row] = PZ_ID_FAILED;
+        if (p_out) p_out[row] = __builtin_nanf("");
+      }
+    }
+    return;
+  }
   if (rs0.i[0] == TP_DONE) return;
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const int tid = threadIdx.x;
@@ -1655,6 +1730,15 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     sb_ctr = 0;
     path_sh = 0;
   }
+  if (rs0.i[7]) {  // a wait of k_topp_front gave up on this row
+    clear_words(tid, PZ_SP_BLOCK);
+    if (tid == 0) {
+      ws.rs[row].i[7] = 0;
+      ids_out[row] = PZ_ID_FAILED;
+      if (p_out) p_out[row] = __builtin_nanf("");
+    }
+    return;
+  }
   pz_sp_row_stat(row, S, ws, SS);
   const float M = SS.M;
   const uint32_t flags = SS.any;
@@ -2039,7 +2123,11 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
     }
   }
   const size_t lds_wf = wf_sort_off + wf_keys_off(wf_cap) + (size_t)wf_cap * 8;
+  // (the front launch's waits end because a row's S workgroups can all be
+  // resident at once: S <= 64 and, on a device or partition with few CUs,
+  // at most one per CU)
   const bool front = (size_t)n_rows * pf.S <= (size_t)ws.hslots && pf.S <= 64 &&
+                     (L.n_cu <= 0 || pf.S <= L.n_cu) &&
                      2 * (lds_front + fixed) <= (size_t)L.max_lds && wf_cap > 0 &&
                      lds_wf + fixed <= (size_t)L.max_lds;
   if (front) {
@@ -2052,11 +2140,10 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
          hipFuncSetAttribute((const void*)kw, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)lds_wf) != hipSuccess))
       return -1;
-    static std::atomic<uint32_t> g_tag{0};
-    const uint32_t tag = g_tag.fetch_add(1, std::memory_order_relaxed);
     hipLaunchKernelGGL(kf, dim3(pf.S, n_rows), dim3(PZ_SP_BLOCK), lds_front, L.stream, L.logits,
                        L.ld, L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pf.nseg,
-                       pf.spw, pf.S, ws, L.u, L.ids, L.p_out, L.sc, (int)pen_slice_f, tag);
+                       pf.spw, pf.S, ws, L.u, L.ids, L.p_out, L.sc, (int)pen_slice_f,
+                       L.wait_polls);
     hipLaunchKernelGGL(kw, dim3(n_rows), dim3(PZ_SP_BLOCK), lds_wf, L.stream, L.logits, L.ld,
                        L.V, d_rows, L.params, L.n_params, L.hist, L.H, L.hcap, pf.nseg, pf.spw,
                        pf.S, ws, L.u, L.ids, L.p_out, L.sc, (int)wf_walk_off, wf_nc,
@@ -2101,7 +2188,7 @@ int launch_topp_t(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   hipLaunchKernelGGL(k1e, grid, block, lds1, L.stream, TOPP_PASS);
   hipLaunchKernelGGL(k2, grid, block, lds2, L.stream, TOPP_PASS, (int)pen_slice);
   hipLaunchKernelGGL(k3, dim3(n_rows * (1 + gS)), block, lds3, L.stream, TOPP_PASS,
-                     (int)pen_full, nc, n_rows, gS, gspw, (int)goff, lcap);
+                     (int)pen_full, nc, n_rows, gS, gspw, (int)goff, lcap, L.wait_polls);
   hipLaunchKernelGGL(k4, dim3(n_rows), block, lds4, L.stream, TOPP_PASS, cap, nc6);
 #undef TOPP_PASS
   const int fb_grid = n_rows < L.sc.fb_slots ? n_rows : L.sc.fb_slots;

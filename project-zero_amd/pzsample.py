@@ -26,7 +26,7 @@ ABI_SYMBOLS = (
     "pz_device_alloc", "pz_device_free", "pz_memcpy_h2d", "pz_memcpy_d2h",
     "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
     "pz_sample_step", "pz_sampler_set_eos", "pz_attn_softmax", "pz_lm_head_bf16",
-    "pz_lm_head_argmax_bf16", "pz_spec_decode",
+    "pz_lm_head_argmax_bf16", "pz_spec_decode", "pz_sampler_set_wait_bound",
     # include/pz_sampling_compat.h: the reference sampler's own symbols
     "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
     "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
@@ -79,6 +79,7 @@ def load():
     lib.pz_sampler_destroy.argtypes = [_P]
     lib.pz_sampler_destroy.restype = None
     lib.pz_sampler_set_temp_mode.argtypes = [_P, _I]
+    lib.pz_sampler_set_wait_bound.argtypes = [_P, ctypes.c_uint32]
     lib.pz_sampler_last_error.argtypes = [_P]
     lib.pz_sampler_last_error.restype = ctypes.c_char_p
     lib.pz_sampler_stream.argtypes = [_P]
@@ -192,6 +193,10 @@ class Sampler:
 
     def set_temp_mode(self, mode):
         self._check(self.lib.pz_sampler_set_temp_mode(self.h, mode))
+
+    def set_wait_bound(self, polls):
+        """Bound of the waits between a row's workgroups (0: the default)."""
+        self._check(self.lib.pz_sampler_set_wait_bound(self.h, polls))
 
     @property
     def stream(self):
@@ -400,6 +405,7 @@ def synth_draft_ids(draft, tau, seed):
 
 
 PZ_NOALLOC_MAX_BATCH, PZ_NOALLOC_MAX_VOCAB, PZ_NOALLOC_MAX_HIST = 64, 262144, 2048
+PZ_ID_FAILED = -2  # a row whose wait between workgroups gave up
 
 
 def sample_noalloc(d_logits, B, V, ld, params, d_u, d_ids, d_p=None, d_hist=None, H=0,

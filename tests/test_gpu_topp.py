@@ -27,6 +27,25 @@ def same_p(a, b):
     return (a == b) | (np.isnan(a) & np.isnan(b))
 
 
+def oracle_rows(x, params, u, hist=None, temp_mode=pz.PZ_TEMP_MUL_RECIP, threads=16):
+    """The oracle over row blocks on several threads (its buffers are per
+    thread), for batches whose rows take seconds on one core."""
+    from concurrent.futures import ThreadPoolExecutor
+    B = x.shape[0]
+    n = max(1, min(threads, B))
+    cuts = [B * i // n for i in range(n + 1)]
+    op = [orc(q) for q in params]
+
+    def part(i):
+        lo, hi = cuts[i], cuts[i + 1]
+        return po.sample_batch(x[lo:hi], op if len(op) == 1 else op[lo:hi],
+                               u=None if u is None else u[lo:hi],
+                               hist=None if hist is None else hist[lo:hi], temp_mode=temp_mode)
+    with ThreadPoolExecutor(n) as ex:
+        parts = list(ex.map(part, range(n)))
+    return tuple(np.concatenate([q[i] for q in parts]) for i in range(4))
+
+
 def check(torch, x, params, u, hist=None, temp_mode=pz.PZ_TEMP_MUL_RECIP, label="", ld=None):
     B, V = x.shape
     print(f"case {label} B={B} V={V}", flush=True)
@@ -41,8 +60,7 @@ def check(torch, x, params, u, hist=None, temp_mode=pz.PZ_TEMP_MUL_RECIP, label=
     d_h = to_dev(torch, np.ascontiguousarray(hist)) if hist is not None else None
     with pz.Sampler(B, V, max_hist=max(H, 1), temp_mode=temp_mode) as s:
         ids, p = s.sample(d_x, B, V, ld, params, u=u, d_hist=d_h, H=H, want_p=True)
-    want, pw, dd, dc = po.sample_batch(x, [orc(q) for q in params], u=u, hist=hist,
-                                       temp_mode=temp_mode)
+    want, pw, dd, dc = oracle_rows(x, params, u, hist=hist, temp_mode=temp_mode)
     boundary = (dd < 1e-5) | (dc < 1e-5)
     bad = ids != want
     print(f"  rows={B} boundary={int(boundary.sum())} mismatches={int(bad.sum())}", flush=True)
@@ -63,6 +81,14 @@ def test_c2_full_size(torch_cuda):
 def test_c2_more_rows(torch_cuda):
     w = wl.build_c2(B=256, seed=0xC2 + 7)
     check(torch_cuda, w["logits"], w["params"], w["u"], label="c2 x256")
+
+
+def test_c2_batch_1024(torch_cuda):
+    """The top of the metric's batch range: 1024 x 128256 in one call (the
+    front launch runs 8192 workgroups in several rounds, each row's slices
+    meeting through the workspace); every row against the oracle."""
+    w = wl.build_c2(B=1024, seed=0xC2 + 11)
+    check(torch_cuda, w["logits"], w["params"], w["u"], label="c2 x1024")
 
 
 @pytest.mark.parametrize("V", [1, 3, 5, 1000, 4099, 49152, 151936, 200000])

@@ -3,7 +3,10 @@ object, scratch in one static device array per GPU) against the existing
 pz_sample_batch_async on the same device inputs: ids and p(chosen) must be
 bit-identical.  Two calls in a row, the second with a smaller input, then the
 first again, so contents the array keeps from one call cannot leak into the
-next; sizes beyond the stated maximum are rejected before anything runs."""
+next; sizes beyond the stated maximum are rejected before anything runs.
+The call also runs captured in a HIP graph (torch.cuda.CUDAGraph on a side
+stream), replayed on new logits and uniforms in the same buffers: each
+replay equals an eager call on the same inputs."""
 import numpy as np
 import pytest
 
@@ -106,3 +109,53 @@ def test_noalloc_rejects_oversize(torch_cuda):
                              prm, u, ids) == pz.PZ_ERANGE
     assert pz.sample_noalloc(d, 1, 16, 16, prm, u, ids, d_hist=ids,
                              H=pz.PZ_NOALLOC_MAX_HIST + 1) == pz.PZ_ERANGE
+
+
+def test_noalloc_graph_capture_replays(torch_cuda):
+    torch = torch_cuda
+    B, V, H = 16, 128256, 64
+    x0 = pz.synth_normal(B, V, 2.0, 0x7C0)
+    pz.synth_spikes(x0, 5, 8.0, 12.0, 0x7C1)
+    params = [pz.row_params(temperature=0.7, top_p=0.9) for _ in range(B)]
+    params[1] = pz.row_params(temperature=0.0, rep_penalty=1.2)
+    params[2] = pz.row_params(temperature=0.8, top_k=40, top_p=0.95, rep_penalty=1.1)
+    params[5] = pz.row_params(temperature=0.9)
+    hist = pz.synth_uniform_ids(B, H, V, 0x7C2)
+    d_x = to_dev(torch, x0)
+    d_u = to_dev(torch, pz.synth_draws(B, 0x7C3).astype(np.float32))
+    d_h = to_dev(torch, hist)
+    ids = torch.full((B,), -9, dtype=torch.int32, device="cuda")
+    p = torch.full((B,), -9.0, dtype=torch.float32, device="cuda")
+    side = torch.cuda.Stream()
+    # first call eagerly on the side stream (the per-device set-up runs here)
+    with torch.cuda.stream(side):
+        assert pz.sample_noalloc(d_x, B, V, V, params, d_u, ids, p, d_hist=d_h, H=H,
+                                 stream=side.cuda_stream) == pz.PZ_OK
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    print("case noalloc capture B=16 V=128256", flush=True)
+    with torch.cuda.graph(g, stream=side):
+        rc = pz.sample_noalloc(d_x, B, V, V, params, d_u, ids, p, d_hist=d_h, H=H,
+                               stream=side.cuda_stream)
+    assert rc == pz.PZ_OK
+    with pz.Sampler(B, V, max_hist=H) as s:
+        want_ids = torch.full((B,), -7, dtype=torch.int32, device="cuda")
+        want_p = torch.full((B,), -7.0, dtype=torch.float32, device="cuda")
+        for k in range(3):
+            print(f"case noalloc replay {k}", flush=True)
+            xk = pz.synth_normal(B, V, 2.0, 0x7D0 + k)
+            pz.synth_spikes(xk, 5, 8.0, 12.0, 0x7E0 + k)
+            d_x.copy_(torch.from_numpy(xk))
+            d_u.copy_(torch.from_numpy(pz.synth_draws(B, 0x7F0 + k).astype(np.float32)))
+            ids.fill_(-9)
+            p.fill_(-9.0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            # eager reference on the same inputs (between the replays)
+            s.sample_async(d_x, B, V, V, params, d_u, want_ids, want_p, d_hist=d_h, H=H)
+            s.sync()
+            gi, gp = ids.cpu().numpy(), p.cpu().numpy()
+            wi, wp = want_ids.cpu().numpy(), want_p.cpu().numpy()
+            assert (gi == wi).all(), (k, np.nonzero(gi != wi)[0][:8], gi[:8], wi[:8])
+            assert (gp.view(np.uint32) == wp.view(np.uint32)).all(), (k, np.nonzero(gp != wp)[0])
