@@ -176,7 +176,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_rec(SpecA
   X.inv = 1.0f;
   X.as_p = false;
   X.et = (const pz_lds_u64*)etab;
-  pz_sp_records(X, q, sl, A.ws);
+  pz_sp_records(X, q, sl, A.ws, nullptr, true);
 }
 
 // ---- one workgroup per row: the exact normaliser -----------------------------
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vrec(SpecArgs A) {
     if (threadIdx.x == 0 && last_sh >= 0) atomicMax(&A.seq[b].last, last_sh);
   } else {
     PzExpTerms<PzTempRow<VEC>> X = p_terms<VEC>(A, s.qt, et);
-    pz_sp_records(X, r, sl, A.ws);
+    pz_sp_records(X, r, sl, A.ws, nullptr, true);
   }
 }
 

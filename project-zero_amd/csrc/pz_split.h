@@ -442,11 +442,16 @@ __device__ __forceinline__ void pz_sp_predict(const Est& est, float carry, int r
 // prep(e0, n, Raw&, a[4]); observe(e0, Raw&, a[4]);
 // inc4(Raw&, a[4], g, s&, dirty&).  The predicted grid and flags of segment k
 // are in rec_gf, or lgf[k - k0] (pz_sp_predict); PZ_NO_RECORD skips a segment.
+// skip_xing: segments predicted to cross a binade are skipped too (their
+// grid word, written by the prediction, already makes them specials, whose
+// increments the walk never reads) -- only for terms whose observer does
+// nothing.
 // ---------------------------------------------------------------------------
 template <class X>
 __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
                                               const PzSplitWs& ws,
-                                              const pz_lds_u32* lgf = nullptr) {
+                                              const pz_lds_u32* lgf = nullptr,
+                                              bool skip_xing = false) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint32_t* rd = pz_sp_rec_d(ws, row);
   uint32_t* rd2 = pz_sp_rec_d2(ws, row);
@@ -466,7 +471,7 @@ __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
     const int k = kb + u * PZ_SP_WAVES;
     if (k >= sl.k1) break;
     const uint32_t gf = gfs[u];
-    if (gf == PZ_NO_RECORD) continue;
+    if (gf == PZ_NO_RECORD || (skip_xing && (gf & PZ_GF_XING))) continue;
     const int e0 = k * PZ_SP_SEG + 4 * lane;
     typename X::Raw& raw = raws[u];
     const int n = ns[u];
@@ -852,21 +857,20 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
       W.sinfo[sl] = inf.sinfo;
       W.spt1[sl] = inf.pt1;
       W.stc[sl] = inf.tc;
-      if (j == 0 && k == 0) {
-        // the row's first segment from a zero sum, where nearly every term is
-        // an event: its plain sequential fp32 sum, for the walker to take in
-        // one step (one lane, the terms read back in id order)
-        const pz_lds_f4* tq = (const pz_lds_f4*)(W.terms + sl * PZ_SP_SEG);
-        float sum0 = 0.0f;
-        for (int i = 0; i < PZ_SP_SEG / 4; i++) {
-          const pz_f4 t4 = tq[i];
-          sum0 = sum0 + t4.x;
-          sum0 = sum0 + t4.y;
-          sum0 = sum0 + t4.z;
-          sum0 = sum0 + t4.w;
-        }
-        *W.s0 = __float_as_uint(sum0);
+    }
+    if (j == 0 && k == 0) {
+      // the row's first segment from a zero sum, where nearly every term is
+      // an event: its plain sequential fp32 sum, for the walker to take in
+      // one step -- the whole wave in lockstep, each term read out of its
+      // lane's registers in id order (no LDS round trip per term)
+      float sum0 = 0.0f;
+      for (int l = 0; l < 64; l++) {
+        sum0 = sum0 + pz_readlane_f32(v[0], l);
+        sum0 = sum0 + pz_readlane_f32(v[1], l);
+        sum0 = sum0 + pz_readlane_f32(v[2], l);
+        sum0 = sum0 + pz_readlane_f32(v[3], l);
       }
+      if (lane == 0) *W.s0 = __float_as_uint(sum0);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0)

@@ -409,7 +409,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_rec(TOPP_
   X.et = et;
   X.ehist = ehist;
   __syncthreads();
-  pz_sp_records(X, row, sl, ws);
+  pz_sp_records(X, row, sl, ws);  // (every segment: the observer fills the histogram)
   __syncthreads();
   uint32_t* gh = ws.hist + ((size_t)blockIdx.y * S + blockIdx.x) * PZ_TOPP_NB;
   for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK) gh[i] = ehist[i];
@@ -748,7 +748,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   X.inv = 1.0f;
   X.as_p = false;
   X.et = et;
-  pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)sgf);
+  pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)sgf, true);
   // 4. the nucleus bins (the row's histograms were published before meet 2)
   pz_lds_barrier();
   const ToppSel sel =
