@@ -91,3 +91,28 @@ def test_penalties_and_temperature_forms(torch_cuda):
         check(torch_cuda, x, [pz.row_params(temperature=0.7, rep_penalty=1.2,
                                              presence_penalty=0.3, frequency_penalty=0.2)],
               u, hist=hist, temp_mode=mode, label=f"pen temp {mode}")
+
+
+@pytest.mark.parametrize("B", [1, 64, 1024])
+def test_default_chain_batches(torch_cuda, B):
+    """The HTTP default (T 1.0, top-p 1.0: softmax + CDF draw) over spiked
+    N(0, 2^2) rows at vocab 128256, from batch 1 to 1024 (the bench's sweep):
+    every row against the oracle (on several threads: its buffers are per
+    thread)."""
+    from concurrent.futures import ThreadPoolExecutor
+    import workloads as wl
+    w = wl.build_cat(B=B, seed=0xCA + B)
+    x, params, u = w["logits"], w["params"], w["u"]
+    print(f"case categorical default chain B={B}", flush=True)
+    d_x = to_dev(torch_cuda, x)
+    with pz.Sampler(B, x.shape[1]) as s:
+        ids, p = s.sample(d_x, B, x.shape[1], x.shape[1], params, u=u, want_p=True)
+    n = min(16, B)
+    cuts = [B * i // n for i in range(n + 1)]
+    with ThreadPoolExecutor(n) as ex:
+        parts = list(ex.map(lambda i: po.sample_batch(x[cuts[i]:cuts[i + 1]], [orc(params[0])],
+                                                      u=u[cuts[i]:cuts[i + 1]]), range(n)))
+    want = np.concatenate([q[0] for q in parts])
+    pw = np.concatenate([q[1] for q in parts])
+    assert (ids == want).all(), (np.nonzero(ids != want)[0][:8], ids[:4], want[:4])
+    assert (p == pw).all()
