@@ -10,11 +10,15 @@
 // comparison succeeds and the draw is V-1.
 //
 // Row-split design (the default, any batch): each row is cut into slices of
-// segments over several workgroups (pz_split.h), five launches:
-//   k_cat_stat   (HBM)  per slice its maximum and NaN flag, per segment its
-//                       maximum and mass estimate;
-//   k_cat_rec    (L2)   the exact e = expf(y - M) terms' records at the grids
-//                       the estimates predict;
+// segments over several workgroups (pz_split.h):
+//   k_cat_front  (HBM)  each slice read once into LDS: its maximum and NaN
+//                       flag, the row's workgroups meet for the row maximum,
+//                       then the segments' mass estimates, a second meeting
+//                       for the mass before the slice, and the exact
+//                       e = expf(y - M) terms' records at the predicted
+//                       grids (pz_sp_front);
+//     (or, for slices that do not fit: k_cat_stat (HBM) maxima and
+//     estimates, k_cat_rec (L2) the records)
 //   k_cat_walk          one workgroup per row walks them: the exact
 //                       sequential normaliser, inv = 1 / sum;
 //   k_cat_prec   (L2)   the records of p = e * inv at the CDF's predicted
@@ -133,6 +137,7 @@ struct CatArgs {
   float* p_out;
   PzSplitWs ws;
   int nseg, spw, S, nc;
+  int est_abs;  // seg_s holds the front pass's absolute estimates
 };
 
 template <bool VEC>
@@ -151,7 +156,30 @@ __device__ __forceinline__ PzRow<VEC> cat_row(const CatArgs& A, int row, char* l
 // softmax.c:4-23 gives NaN everywhere when any y is NaN or the maximum is not
 // finite: the draw then falls back to V-1 (generate.c:161)
 __device__ __forceinline__ bool cat_bad(uint32_t flags) {
-  return (flags & (PZ_RS_NAN | PZ_RS_NONFIN)) != 0;
+  return (flags & (PZ_RS_NAN | PZ_RS_NONFIN | PZ_RS_FAILED)) != 0;
+}
+
+// Stat and records in one read of each slice (pen_bytes: the slice's penalty
+// tables, then the slice).
+template <bool VEC>
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_cat_front(CatArgs A,
+                                                                            int pen_bytes,
+                                                                            uint32_t cap) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ PzFrontShared F;
+  __shared__ uint64_t etab[32];
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = pz_row_of(A.rows, blockIdx.y);
+  const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
+  if (threadIdx.x == 0) {
+    SS.any = 0u;
+    F.fail = 0;
+  }
+  const PzRow<VEC> R = cat_row<VEC>(A, row, lds, pz_sp_lo(sl), pz_sp_hi(sl, A.V));
+  __syncthreads();
+  pz_sp_front(R, row, sl, A.S, -__builtin_inff(), A.ws, SS, F, (pz_lds_f32*)(lds + pen_bytes),
+              (const pz_lds_u64*)etab, cap);
 }
 
 template <bool VEC>
@@ -191,11 +219,16 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_cat_rec(CatArg
   pz_sp_records(X, row, sl, A.ws, nullptr, true);
 }
 
-// Estimated p mass of segment k: the stat pass's e estimate times inv.
+// Estimated p mass of segment k: the e estimate times inv (abs: the front
+// pass's estimates in units of exp(y - M), else the stat pass's relative
+// ones).
 struct CatEstP {
   PzEstRel e;
   float inv;
-  __device__ __forceinline__ float operator()(int k) const { return e(k) * inv; }
+  int abs;
+  __device__ __forceinline__ float operator()(int k) const {
+    return (abs ? e.s[k] : e(k)) * inv;
+  }
 };
 
 // One workgroup per row (512 threads: two per CU with room for the walk's
@@ -210,13 +243,16 @@ __global__ __launch_bounds__(CAT_WALK_BLOCK) void k_cat_walk(CatArgs A, int pen_
   __shared__ float sum_sh;
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = pz_row_of(A.rows, blockIdx.x);
-  pz_sp_row_stat(row, A.S, A.ws, SS);
   PzRowState& rs = A.ws.rs[row];
-  if (cat_bad(SS.any)) {
+  const int failed = rs.i[7];
+  pz_sp_clear_meet(A.ws, row);  // the front launch's meetings are over
+  pz_sp_row_stat(row, A.S, A.ws, SS);
+  if (failed || cat_bad(SS.any)) {
     if (threadIdx.x == 0) {
       rs.M = SS.M;
-      rs.flags = SS.any;
+      rs.flags = SS.any | (failed ? PZ_RS_FAILED : 0u);
       rs.inv = __builtin_nanf("");
+      rs.i[7] = 0;
     }
     return;
   }
@@ -260,7 +296,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_cat_prec(CatAr
   const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
   const CatEstP est{{A.ws.seg_m + (size_t)row * A.ws.nsc, A.ws.seg_s + (size_t)row * A.ws.nsc,
                      rs.M},
-                    rs.inv};
+                    rs.inv, A.est_abs};
   const float carry = pz_sp_prefix(est, sl.k0, SS);
   pz_sp_predict(est, carry, row, sl, A.ws, SS);
   PzExpTerms<PzRow<VEC>> X;
@@ -274,10 +310,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_cat_prec(CatAr
   pz_sp_records(X, row, sl, A.ws, nullptr, true);
 }
 
-// One workgroup per row: the CDF of p in ascending id to the first cdf > r
-// (generate.c:162-168), V-1 when none (:161).
+// One workgroup per row (as the normaliser walk): the CDF of p in ascending
+// id to the first cdf > r (generate.c:162-168), V-1 when none (:161).
 template <bool VEC>
-__global__ __launch_bounds__(PZ_SP_BLOCK) void k_cat_draw(CatArgs A, int pen_bytes) {
+__global__ __launch_bounds__(CAT_WALK_BLOCK) void k_cat_draw(CatArgs A, int pen_bytes) {
   extern __shared__ __align__(16) char lds[];
   __shared__ PzSpShared SS;
   __shared__ uint64_t etab[32];
@@ -287,7 +323,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_cat_draw(CatArgs A, int pen_byt
   const PzRowState rs = A.ws.rs[row];
   if (cat_bad(rs.flags)) {
     if (threadIdx.x == 0) {
-      A.ids_out[row] = A.V - 1;
+      A.ids_out[row] = (rs.flags & PZ_RS_FAILED) ? PZ_ID_FAILED : A.V - 1;
       if (A.p_out) A.p_out[row] = __builtin_nanf("");
     }
     return;
@@ -297,7 +333,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_cat_draw(CatArgs A, int pen_byt
   X.R.x = A.logits + (long)row * A.ld;
   X.R.V = A.V;
   X.R.T = PzTemp::of(prm);
-  pz_penalty_build_range<PZ_SP_BLOCK>(X.R.P, lds, A.V, 0, A.V, A.hcap,
+  pz_penalty_build_range<CAT_WALK_BLOCK>(X.R.P, lds, A.V, 0, A.V, A.hcap,
                                       A.hist ? A.hist + (long)row * A.H : nullptr, A.H, prm);
   X.M = rs.M;
   X.thr = -__builtin_inff();
@@ -334,7 +370,19 @@ template <bool VEC>
 int launch_cat_split(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   const PzSplitWs& ws = L.ws;
   if (!ws.rs || !ws.rec) return -2;
-  const PzSplitPlan pl = pz_split_plan(L.V, n_rows, ws.smax);
+  // the front pass when its workgroups run in one round (at larger batches
+  // the rounds wait on each other's meetings: the separate stat and records
+  // passes are quicker), a slice fits in LDS beside its tables (two
+  // workgroups per CU) and a row's slices fit the device together
+  const PzSplitPlan pf = pz_front_plan(L.V, n_rows, ws.smax);
+  const size_t pen_f = L.pen_any
+                           ? (pz_penalty_lds_bytes(pf.spw * PZ_SP_SEG, L.hcap) + 15) & ~(size_t)15
+                           : 0;
+  const size_t lds_front = pen_f + (size_t)pf.spw * PZ_SP_SEG * 4;
+  const bool front = (long)n_rows * pf.S <= PZ_SP_TARGET_WG && pf.S <= 64 &&
+                     (L.n_cu <= 0 || pf.S <= L.n_cu) && ws.meet &&
+                     2 * (lds_front + 4096) <= (size_t)L.max_lds;
+  const PzSplitPlan pl = front ? pf : pz_split_plan(L.V, n_rows, ws.smax);
   if (pl.nseg > ws.nsc || pl.S > ws.smax) return -2;
   const size_t fixed = 4096;
   auto pen = [&](int n) {
@@ -365,6 +413,7 @@ int launch_cat_split(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   A.spw = pl.spw;
   A.S = pl.S;
   A.nc = nc;
+  A.est_abs = front ? 1 : 0;
   const void* big[2] = {(const void*)k_cat_walk<VEC>, (const void*)k_cat_draw<VEC>};
   for (int i = 0; i < 2; i++)
     if (lds_walk > 65536 &&
@@ -372,12 +421,21 @@ int launch_cat_split(const pz_launch& L, int n_rows, const int32_t* d_rows) {
             hipSuccess)
       return -1;
   const dim3 grid(pl.S, n_rows), block(PZ_SP_BLOCK);
-  hipLaunchKernelGGL(k_cat_stat<VEC>, grid, block, pen_slice, L.stream, A);
-  hipLaunchKernelGGL(k_cat_rec<VEC>, grid, block, pen_slice, L.stream, A);
+  if (front) {
+    auto kf = k_cat_front<VEC>;
+    if (lds_front > 65536 &&
+        hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds_front) != hipSuccess)
+      return -1;
+    hipLaunchKernelGGL(kf, grid, block, lds_front, L.stream, A, (int)pen_f, L.wait_polls);
+  } else {
+    hipLaunchKernelGGL(k_cat_stat<VEC>, grid, block, pen_slice, L.stream, A);
+    hipLaunchKernelGGL(k_cat_rec<VEC>, grid, block, pen_slice, L.stream, A);
+  }
   hipLaunchKernelGGL(k_cat_walk<VEC>, dim3(n_rows), dim3(CAT_WALK_BLOCK), lds_walk, L.stream, A,
                      (int)pen_full);
   hipLaunchKernelGGL(k_cat_prec<VEC>, grid, block, pen_slice, L.stream, A);
-  hipLaunchKernelGGL(k_cat_draw<VEC>, dim3(n_rows), block, lds_walk, L.stream, A,
+  hipLaunchKernelGGL(k_cat_draw<VEC>, dim3(n_rows), dim3(CAT_WALK_BLOCK), lds_walk, L.stream, A,
                      (int)pen_full);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -54,6 +54,7 @@ enum {
   PZ_RS_NAN = 1,      // some y is NaN
   PZ_RS_Y0NAN = 2,    // y[0] is NaN
   PZ_RS_NONFIN = 4,   // the NaN-free maximum is +-inf (or there is no value at all)
+  PZ_RS_FAILED = 8,   // a wait between the row's workgroups gave up
 };
 
 // Per-row values handed from pass to pass (device scratch, 64 bytes).
@@ -498,6 +499,225 @@ __device__ __forceinline__ void pz_sp_records(X& x, int row, const PzSlice& sl,
     }
   }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Front pass: stat and records of a slice in one launch, the slice read once
+// (HBM) into LDS with the row's chain applied.  The row's S workgroups meet
+// twice through the row's meeting words (ws.meet, zero between launches):
+// for the row maximum (meet 1: slice maximum, NaN and y[0] flags) and for
+// the estimated mass of the slices before each one (meet 2).  Each workgroup
+// posts a word (value and a written bit; no fence) and wave 0 polls the S
+// words with agent-scope atomic loads, at most `cap` times.  A row's
+// workgroups are consecutive in the launch order and each posts everything
+// it owes before it waits, so with the row's S <= 64 workgroups resident
+// together the waits end; one that gives up posts what it still owes and
+// marks the row failed (rs.i[7], cleared by the walk launch).  Writes what
+// the stat pass writes (slice maxima and flags, y[0]; the segments' maxima,
+// and their masses as absolute estimates in units of exp(y - M)) and the
+// records of the terms exp(y - M), y >= M + thr_rel, at the predicted grids.
+// Returns whether the row is settled here (degenerate or failed).
+// ---------------------------------------------------------------------------
+struct PzLdsRow {
+  const pz_lds_f32* y;
+  int lo, V;
+  __device__ __forceinline__ int load(int e0, float (&r)[4]) const {
+    int n = V - e0;
+    n = n < 0 ? 0 : (n > 4 ? 4 : n);
+    const pz_f4 q = *(const pz_lds_f4*)(y + (e0 - lo));
+    r[0] = q.x;
+    r[1] = q.y;
+    r[2] = q.z;
+    r[3] = q.w;
+    return n;
+  }
+  __device__ __forceinline__ void apply(int, int, float (&)[4]) const {}
+  __device__ __forceinline__ int get(int e0, float (&r)[4]) const { return load(e0, r); }
+};
+
+struct PzSliceEst {
+  const float* s;
+  int k0;
+  __device__ __forceinline__ float operator()(int k) const { return s[k - k0]; }
+};
+
+constexpr int PZ_FRONT_SEGS = 64;  // segments of a slice held in LDS
+
+struct PzFrontShared {
+  float sest[PZ_FRONT_SEGS];
+  uint32_t sgf[PZ_FRONT_SEGS];
+  int fail;
+};
+
+__device__ __forceinline__ void pz_sp_mark_failed(const PzSplitWs& ws, int row) {
+  __hip_atomic_store(&ws.rs[row].i[7], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls the first n words of w (lane i: w[i]) until every one has its
+// written bit, at most cap times (wave 0).  Returns false if it gave up.
+__device__ __forceinline__ bool pz_sp_meet(const uint64_t* w, int n, uint32_t cap, uint64_t& v) {
+  const int lane = threadIdx.x & 63;
+  v = 1ull << 63;
+  for (uint32_t t = 1;; t++) {
+    if (lane < n) v = __hip_atomic_load(&w[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__ballot((v >> 63) == 0) == 0) return true;
+    if (t >= cap) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+template <class Row>
+__device__ __forceinline__ bool pz_sp_front(const Row& R, int row, const PzSlice& sl, int S,
+                                            float thr_rel, const PzSplitWs& ws,
+                                            PzSpShared& SS, PzFrontShared& F, pz_lds_f32* ybuf,
+                                            const pz_lds_u64* et, uint32_t cap) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lo = pz_sp_lo(sl);
+  const int V = R.V;
+  uint64_t* meet = ws.meet + (size_t)row * 2 * ws.smax;
+  float* seg_m = ws.seg_m + (size_t)row * ws.nsc;
+  float* seg_s = ws.seg_s + (size_t)row * ws.nsc;
+  // 1. the slice, once: chain applied, into LDS; segment and slice maxima
+  float smx = -__builtin_inff();
+  bool nan = false;
+  for (int kb = sl.k0 + w; kb < sl.k1; kb += PZ_SP_U * PZ_SP_WAVES) {
+    float y[PZ_SP_U][4];
+    int n[PZ_SP_U];
+#pragma unroll
+    for (int uu = 0; uu < PZ_SP_U; uu++)
+      n[uu] = R.load((kb + uu * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane, y[uu]);
+#pragma unroll
+    for (int uu = 0; uu < PZ_SP_U; uu++) {
+      const int k = kb + uu * PZ_SP_WAVES;
+      if (k >= sl.k1) break;
+      const int e0 = k * PZ_SP_SEG + 4 * lane;
+      R.apply(e0, n[uu], y[uu]);
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        if (c >= n[uu]) continue;
+        if (y[uu][c] != y[uu][c]) nan = true;
+        else m = fmaxf(m, y[uu][c]);
+      }
+      pz_f4 q;
+      q.x = y[uu][0];
+      q.y = y[uu][1];
+      q.z = y[uu][2];
+      q.w = y[uu][3];
+      *(pz_lds_f4*)(ybuf + (e0 - lo)) = q;
+      m = pz_wave_max(m);
+      if (lane == 0) seg_m[k] = m;
+      smx = fmaxf(smx, m);
+    }
+  }
+  if (__ballot(nan) && lane == 0) atomicOr(&SS.any, 1u);
+  if (lane == 0) SS.red[w] = smx;
+  pz_lds_barrier();
+  const float mm = w == 0 ? pz_wave_max(lane < PZ_SP_WAVES ? SS.red[lane] : -__builtin_inff())
+                          : 0.0f;
+  if (tid == 0) {
+    uint32_t f = SS.any;
+    ws.slice_m[(size_t)row * ws.smax + blockIdx.x] = mm;
+    ws.slice_f[(size_t)row * ws.smax + blockIdx.x] = f;
+    if (blockIdx.x == 0) {
+      ws.rs[row].y0 = ybuf[0];
+      if (ybuf[0] != ybuf[0]) f |= PZ_RS_Y0NAN;
+    }
+    // meet 1: every slice's maximum and flags
+    __hip_atomic_store(&meet[blockIdx.x],
+                       (1ull << 63) | ((uint64_t)f << 32) | (uint64_t)__float_as_uint(mm),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (w == 0) {
+    uint64_t v;
+    if (!pz_sp_meet(meet, S, cap, v) && lane == 0) F.fail = 1;
+    const float M = pz_wave_max(lane < S ? __uint_as_float((uint32_t)v) : -__builtin_inff());
+    const bool anyf = __ballot(lane < S && (((uint32_t)(v >> 32) & PZ_RS_NAN) != 0)) != 0;
+    const bool y0nan = __ballot(lane < S && (((uint32_t)(v >> 32) & PZ_RS_Y0NAN) != 0)) != 0;
+    if (lane == 0) {
+      uint32_t flags = anyf ? PZ_RS_NAN : 0u;
+      if (y0nan) flags |= PZ_RS_Y0NAN;
+      if (!(M > -__builtin_inff() && M < __builtin_inff())) flags |= PZ_RS_NONFIN;
+      SS.M = M;
+      SS.any = flags;
+    }
+  }
+  pz_lds_barrier();
+  const bool degen = (SS.any & (PZ_RS_NAN | PZ_RS_Y0NAN | PZ_RS_NONFIN)) != 0;
+  if (F.fail || degen) {
+    // what the others may wait for: no mass; the failure mark
+    if (tid == 0) {
+      __hip_atomic_store(&meet[ws.smax + blockIdx.x], 1ull << 63, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      if (F.fail) pz_sp_mark_failed(ws, row);
+    }
+    return true;
+  }
+  const float M = SS.M, thr = M + thr_rel;
+  // 2. the estimated mass of each segment's terms
+  for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
+    const int e0 = k * PZ_SP_SEG + 4 * lane;
+    int n = V - e0;
+    n = n < 0 ? 0 : (n > 4 ? 4 : n);
+    const pz_f4 q = *(const pz_lds_f4*)(ybuf + (e0 - lo));
+    const float y[4] = {q.x, q.y, q.z, q.w};
+    float t = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (c < n && y[c] >= thr) t += pz_fast_exp(y[c] - M);
+    t = pz_wave_sum(t);
+    if (lane == 0) {
+      F.sest[k - sl.k0] = t;
+      seg_s[k] = t;
+    }
+  }
+  pz_lds_barrier();
+  static_assert(PZ_FRONT_SEGS <= 64, "one estimate per lane");
+  const float tot = w == 0 ? pz_wave_sum(lane < sl.k1 - sl.k0 ? F.sest[lane] : 0.0f) : 0.0f;
+  if (tid == 0)  // meet 2: every slice's estimated mass
+    __hip_atomic_store(&meet[ws.smax + blockIdx.x], (1ull << 63) | (uint64_t)__float_as_uint(tot),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (w == 0) {
+    uint64_t v;
+    if (!pz_sp_meet(meet + ws.smax, (int)blockIdx.x, cap, v) && lane == 0) F.fail = 1;
+    const float carry = pz_wave_sum(lane < (int)blockIdx.x ? __uint_as_float((uint32_t)v) : 0.0f);
+    if (lane == 0) SS.carry = carry;
+  }
+  pz_lds_barrier();
+  if (F.fail) {
+    if (tid == 0) pz_sp_mark_failed(ws, row);
+    return true;
+  }
+  pz_sp_predict(PzSliceEst{F.sest, sl.k0}, SS.carry, row, sl, ws, SS, (pz_lds_u32*)F.sgf);
+  // 3. records from LDS
+  PzExpTerms<PzLdsRow> X;
+  X.R.y = ybuf;
+  X.R.lo = lo;
+  X.R.V = V;
+  X.M = M;
+  X.thr = thr;
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = et;
+  pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)F.sgf, true);
+  return false;
+}
+
+// Clears the row's meeting words (every thread of the walk's workgroup;
+// plain stores, which the launch boundary makes visible to the next launch).
+__device__ __forceinline__ void pz_sp_clear_meet(const PzSplitWs& ws, int row) {
+  for (int i = threadIdx.x; i < 2 * ws.smax; i += blockDim.x)
+    ws.meet[(size_t)row * 2 * ws.smax + i] = 0ull;
+}
+
+// Front-pass plan: the split plan's slices capped at PZ_FRONT_SEGS segments.
+inline PzSplitPlan pz_front_plan(int V, int nrows, int smax) {
+  PzSplitPlan p = pz_split_plan(V, nrows, smax);
+  if (p.spw > PZ_FRONT_SEGS) {
+    p.spw = PZ_FRONT_SEGS;
+    p.S = (p.nseg + p.spw - 1) / p.spw;
+  }
+  return p;
 }
 
 // ---------------------------------------------------------------------------

@@ -70,3 +70,10 @@ def test_greedy_split_merge_bound(torch_cuda):
     """Greedy rows split over workgroups (8 x 128256): the last workgroup's
     reads of the others' posted words."""
     forced(torch_cuda, wl.build_c4(B=8))
+
+
+def test_categorical_front_waits_give_up_cleanly(torch_cuda):
+    """The categorical draw's front launch (64 x 128256): its two meetings."""
+    failed = forced(torch_cuda, wl.build_cat())
+    print(f"  rows that gave up: {failed}", flush=True)
+    assert failed > 0
