@@ -209,6 +209,21 @@ PZ_API int pz_spec_verify_async(pz_sampler *s, const float *d_target, const floa
                                 const float *d_u_acc, const float *d_u_res,
                                 int32_t *d_acc_len_out, int32_t *d_ids_out);
 
+/* Verification of greedy drafts (IMPLEMENTATION_PLAN.md:1680: the draft
+ * model's argmax, q one-hot at each draft; no draft logits): draft j is
+ * accepted iff u_acc < p(d_j), and on the first rejection the residual is p
+ * with p(d_j) replaced by 0 (max(0, p - q), fp32); otherwise as
+ * pz_spec_verify / pz_spec_verify_async. */
+PZ_API int pz_spec_verify_greedy(pz_sampler *s, const float *d_target, int B, int K, int V,
+                                 long ld, int has_bonus, float temperature,
+                                 const int32_t *draft_ids, const float *u_acc,
+                                 const float *u_res, int32_t *acc_len_out, int32_t *ids_out);
+PZ_API int pz_spec_verify_greedy_async(pz_sampler *s, const float *d_target, int B, int K,
+                                       int V, long ld, int has_bonus, float temperature,
+                                       const int32_t *d_draft_ids, const float *d_u_acc,
+                                       const float *d_u_res, int32_t *d_acc_len_out,
+                                       int32_t *d_ids_out);
+
 /* The models of a speculative decode (docs/architecture/
  * IMPLEMENTATION_PLAN.md:1675-1693), supplied by the caller, who owns their
  * weights and KV caches.  Every call gets the sampler's stream (as void*)
@@ -251,6 +266,29 @@ PZ_API int pz_spec_decode(pz_sampler *s, const pz_spec_models *m, int B, int K, 
                           float tau, int32_t *tokens, int32_t *len, int max_len, int rounds,
                           uint64_t *d_draft_state, uint64_t *verify_state,
                           int32_t *accepted_out);
+
+/* pz_spec_decode with options (a NULL opts is pz_spec_decode):
+ *   greedy_draft: each draft is the draft model's argmax (argmax.c:3-13, no
+ *     draw, the draft RNG states stay as they are) and the verification
+ *     takes q one-hot at the draft (pz_spec_verify_greedy), as the plan's
+ *     greedy drafting (IMPLEMENTATION_PLAN.md:1680).
+ *   stop_at_eos: the committed tokens of a round are scanned in order and
+ *     the first id of the sampler's EOS list (pz_sampler_set_eos) ends the
+ *     sequence as generate.c:198-211 ends generation: the EOS itself is not
+ *     committed, both caches keep only what precedes it, and in later rounds
+ *     the sequence's tokens, length, RNG states and caches stay as they are
+ *     (its accepted count reads -1).
+ * done: host [B] flags or NULL; sequences flagged on entry take no part,
+ * and a sequence that stops is flagged on return. */
+typedef struct {
+  int greedy_draft;
+  int stop_at_eos;
+} pz_spec_opts;
+PZ_API int pz_spec_decode_opts(pz_sampler *s, const pz_spec_models *m,
+                               const pz_spec_opts *opts, int B, int K, int V, float tau,
+                               int32_t *tokens, int32_t *len, int max_len, int rounds,
+                               uint64_t *d_draft_state, uint64_t *verify_state,
+                               int32_t *accepted_out, uint8_t *done);
 
 /* The reference's temperature (src/sampling/temperature.c:8-25) over device
  * rows [B, ld], in place, on the sampler's stream (asynchronous). */

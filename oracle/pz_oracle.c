@@ -447,7 +447,10 @@ void orc_sample_step(const float *x, int rows, int n, long ld,
  * first x with u_res * Z < cdf_r(x), falling back to the last x with
  * r(x) > 0; if Z == 0 the token is drawn from p with the a5 rule.  When every
  * draft is accepted and a bonus target row is present, the bonus token is
- * drawn from p_K with the a5 rule and u_res. */
+ * drawn from p_K with the a5 rule and u_res.
+ * draft == NULL: greedy drafting (IMPLEMENTATION_PLAN.md:1680), q is one-hot
+ * at the draft (q(d_j) = 1, 0 elsewhere; an id outside [0, n) has q = 0): so
+ * d_j is accepted iff u_acc < p(d_j), and r = p with r(d_j) = 0. */
 static float spec_softmax(const float *logits, int n, float tau, int mode,
                           float *out) {
   memcpy(out, logits, (size_t)n * sizeof(float));
@@ -471,10 +474,15 @@ void orc_spec_verify(const float *target, const float *draft, int B, int K,
     int j = 0;
     for (; j < K; j++) {
       const float *T = target + ((long)b * KT + j) * n;
-      const float *D = draft + ((long)b * K + j) * n;
-      spec_softmax(T, n, temperature, temp_mode, p);
-      spec_softmax(D, n, temperature, temp_mode, q);
+      const float *D = draft ? draft + ((long)b * K + j) * n : NULL;
       int d = draft_ids[(long)b * K + j];
+      spec_softmax(T, n, temperature, temp_mode, p);
+      if (draft) {
+        spec_softmax(D, n, temperature, temp_mode, q);
+      } else {
+        memset(q, 0, (size_t)n * sizeof(float));
+        if (d >= 0 && d < n) q[d] = 1.0f;
+      }
       float ua = u_acc[(long)b * K + j];
       int accept = 0;
       if (d >= 0 && d < n && q[d] > 0.0f) {

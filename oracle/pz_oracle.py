@@ -177,10 +177,14 @@ def sample_row(x, prm, u=0.0, hist=None, temp_mode=TEMP_MUL_RECIP):
 
 def spec_verify(target, draft, K, has_bonus, tau, draft_ids, u_acc, u_res,
                 temp_mode=TEMP_MUL_RECIP):
+    """draft None: greedy drafting, q one-hot at each draft id."""
     target = np.ascontiguousarray(target, np.float32)
-    draft = np.ascontiguousarray(draft, np.float32)
-    B = draft.shape[0] // K if draft.ndim == 2 else draft.shape[0]
-    V = draft.shape[-1]
+    V = target.shape[-1]
+    if draft is None:
+        B = np.asarray(draft_ids).reshape(-1, K).shape[0]
+    else:
+        draft = np.ascontiguousarray(draft, np.float32)
+        B = draft.shape[0] // K if draft.ndim == 2 else draft.shape[0]
     acc = np.empty(B, np.int32)
     out = np.empty((B, K + 1), np.int32)
     dist = np.empty(B, np.float32)
@@ -241,21 +245,32 @@ def ref(avx512=None):
 # pz_spec_decode runs, restated over the oracle's own step and verification.
 # ---------------------------------------------------------------------------
 def spec_decode(models, B, K, V, tau, tokens, lens, rounds, draft_state, verify_state,
-                temp_mode=TEMP_MUL_RECIP):
+                temp_mode=TEMP_MUL_RECIP, greedy_draft=False, eos=None, done=None):
     """models: object with draft(tokens[B], pos[B]) -> [B, V] logits,
     target(tokens[B, n], pos[B]) -> [B, n, V] logits and rollback(model,
     pos[B]).  tokens [B, max_len] and lens [B] are advanced in place,
     draft_state (uint64 [B]) and verify_state (uint64 [B]) too.  Returns the
-    accepted counts [rounds, B]."""
+    accepted counts [rounds, B] (-1 for a sequence that had stopped).
+
+    greedy_draft: each draft is the draft model's argmax (no draw; q is
+    one-hot in the verification).  eos (ids) with done (uint8 [B], in/out):
+    a sequence stops at the first committed id in eos, which is not
+    committed (generate.c:198-211); from then on the sequence's tokens,
+    length and RNG states stay as they are and both caches are rolled back
+    to where they were."""
     o = oracle()
     acc_all = np.zeros((rounds, B), np.int32)
     q = np.empty((B, K, V), np.float32)
-    prm = params(temperature=tau, top_k=0, top_p=1.0)
+    prm = params(temperature=0.0 if greedy_draft else tau, top_k=0, top_p=1.0)
+    eos = set(int(e) for e in (eos if eos is not None else ()))
+    if done is None:
+        done = np.zeros(B, np.uint8)
     for r in range(rounds):
         p0 = lens - 1
         x = tokens[np.arange(B), p0].copy()
         drafts = np.empty((B, K), np.int32)
         cur = x
+        ds0 = draft_state.copy()
         for j in range(K + 1):
             lg = models.draft(cur, p0 + j)
             if j < K:
@@ -263,22 +278,37 @@ def spec_decode(models, B, K, V, tau, tokens, lens, rounds, draft_state, verify_
                 ids, _, _ = sample_step(lg, [prm], draft_state, temp_mode=temp_mode)
                 drafts[:, j] = ids
                 cur = ids
+        draft_state[done != 0] = ds0[done != 0]  # a stopped sequence draws nothing
         tt = np.concatenate([x[:, None], drafts], axis=1)
         p = models.target(tt, p0)
-        u_acc = np.empty((B, K), np.float32)
-        u_res = np.empty(B, np.float32)
+        u_acc = np.zeros((B, K), np.float32)
+        u_res = np.zeros(B, np.float32)
         for b in range(B):
+            if done[b]:
+                continue
             s = ctypes.c_ulonglong(int(verify_state[b]))
             for j in range(K):
                 u_acc[b, j] = o.orc_rng_float(ctypes.byref(s))
             u_res[b] = o.orc_rng_float(ctypes.byref(s))
             verify_state[b] = s.value
-        acc, out, _ = spec_verify(p, q, K, True, tau, drafts, u_acc, u_res, temp_mode=temp_mode)
+        acc, out, _ = spec_verify(p, None if greedy_draft else q, K, True, tau, drafts, u_acc,
+                                  u_res, temp_mode=temp_mode)
+        pos_new = p0.copy()
         for b in range(B):
+            if done[b]:
+                acc_all[r, b] = -1
+                continue
             a = int(acc[b])
-            tokens[b, lens[b]:lens[b] + a + 1] = out[b, :a + 1]
-            lens[b] += a + 1
-        acc_all[r] = acc
-        models.rollback(0, p0 + acc + 1)
-        models.rollback(1, p0 + acc + 1)
+            n = a + 1
+            for i in range(a + 1):
+                if int(out[b, i]) in eos:
+                    n = i
+                    done[b] = 1
+                    break
+            tokens[b, lens[b]:lens[b] + n] = out[b, :n]
+            lens[b] += n
+            pos_new[b] = p0[b] + n
+            acc_all[r, b] = a
+        models.rollback(0, pos_new)
+        models.rollback(1, pos_new)
     return acc_all

@@ -48,6 +48,7 @@ struct pz_sampler {
   float* d_u_step = nullptr;
   int32_t* d_eos = nullptr;
   int n_eos = 0;
+  int32_t h_eos[PZ_MAX_EOS] = {0};  // host copy of the list (the speculative loop's stops)
 
   // fused LM head + argmax: per-row argmax keys (zero between calls) and
   // the NaN flag of logit 0 (max_batch each)

@@ -7,6 +7,8 @@
 //   p = softmax(target_j / T), q = softmax(draft_j / T) with
 //   apply_temperature (temperature.c:8-25) and softmax.c:4-23;
 //   draft d_j is accepted iff u_acc < p(d_j) / q(d_j) (q(d_j) == 0 rejects);
+//   with greedy drafting (IMPLEMENTATION_PLAN.md:1680) q is one-hot at the
+//   draft instead (no draft rows: accept iff u_acc < p(d_j));
 //   at the first rejection r(x) = max(0, p(x) - q(x)) (fp32 difference),
 //   Z = sequential fp32 sum of r in ascending id, and the token is the first
 //   x with u_res * Z < cdf_r(x) (the last x with r(x) > 0 if none); when
@@ -44,9 +46,10 @@ enum { SQ_DONE = 0, SQ_RES = 1, SQ_CAT = 2 };
 struct SpecSeq {
   int mode;   // SQ_*
   int js;     // accepted drafts
-  int qt, qd; // target / draft row of the draw (logits row indices)
+  int qt, qd; // target / draft row of the draw (logits row indices; qd < 0: one-hot q)
   int last;   // residual: the last x with r(x) > 0
-  int pad[3];
+  int dr;     // the rejected draft (one-hot q)
+  int pad[2];
 };
 
 struct SpecArgs {
@@ -54,6 +57,7 @@ struct SpecArgs {
   const float* draft;   // [B, K, ld]
   long ld;
   int V, B, K, KT, NT, NR, has_bonus;
+  int onehot;  // greedy drafts: q one-hot at the draft, no draft rows (NR == NT)
   PzTemp T;
   const int32_t* draft_ids;  // [B, K]
   const float* u_acc;        // [B, K]
@@ -74,8 +78,9 @@ __device__ __forceinline__ float prob_at(const PzTempRow<VEC>& R, int x, float M
   return pz_expf(R.T.apply(R.x[x]) - M) * inv;
 }
 
-// Residual terms r(x) = max(0, p(x) - q(x)) of a target/draft row pair,
-// evaluated exactly in prep; the observer tracks the last x with r(x) > 0.
+// Residual terms r(x) = max(0, p(x) - q(x)) of a target/draft row pair (or,
+// with oh, of the target row and q one-hot at the draft ohd), evaluated
+// exactly in prep; the observer tracks the last x with r(x) > 0.
 template <bool VEC>
 struct ResidualTerms {
   struct Raw {
@@ -84,21 +89,25 @@ struct ResidualTerms {
   };
   PzTempRow<VEC> T, D;
   float MT, invT, MD, invD;
+  bool oh;     // q one-hot at ohd (greedy drafts) rather than the draft row's softmax
+  int ohd;     // (an id outside [0, V): q == 0 everywhere)
   int lastpos;
   const pz_lds_u64* et;  // the workgroup's LDS copy of the expf table
   __device__ __forceinline__ int load(int e0, Raw& r) const {
-    T.load(e0, r.t);
-    return D.load(e0, r.d);
+    const int n = T.load(e0, r.t);
+    if (!oh) D.load(e0, r.d);
+    return n;
   }
   __device__ __forceinline__ void residual(int e0, int n, Raw& r, float (&v)[4]) const {
     T.apply(e0, n, r.t);
-    D.apply(e0, n, r.d);
+    if (!oh) D.apply(e0, n, r.d);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       float res = 0.0f;
       if (c < n) {
         const float p = pz_expf_tab(r.t[c] - MT, et) * invT;
-        const float qq = pz_expf_tab(r.d[c] - MD, et) * invD;
+        const float qq = !oh ? pz_expf_tab(r.d[c] - MD, et) * invD
+                             : (e0 + c == ohd ? 1.0f : 0.0f);
         const float t = p - qq;
         res = t > 0.0f ? t : 0.0f;
       }
@@ -234,9 +243,26 @@ __global__ __launch_bounds__(64) void k_spec_accept(SpecArgs A) {
     const int d = A.draft_ids[b * A.K + lane];
     if (d >= 0 && d < A.V) {
       const float pd = prob_at(temp_row<VEC>(A, qt), d, rs[qt].M, rs[qt].inv);
-      const float qv = prob_at(temp_row<VEC>(A, qd), d, rs[qd].M, rs[qd].inv);
+      const float qv = A.onehot ? 1.0f : prob_at(temp_row<VEC>(A, qd), d, rs[qd].M, rs[qd].inv);
       accept = qv > 0.0f && A.u_acc[b * A.K + lane] < pd / qv;
     }
+  }
+  // a row whose front wait gave up fails the whole sequence
+  bool failed = false;
+  for (int j = lane; j < A.KT; j += 64) failed |= (rs[b * A.KT + j].flags & PZ_RS_FAILED) != 0;
+  if (!A.onehot)
+    for (int j = lane; j < A.K; j += 64)
+      failed |= (rs[A.NT + b * A.K + j].flags & PZ_RS_FAILED) != 0;
+  if (__ballot(failed)) {
+    if (lane == 0) {
+      SpecSeq s;
+      memset(&s, 0, sizeof(s));
+      s.mode = SQ_DONE;
+      A.seq[b] = s;
+      A.acc_len[b] = PZ_ID_FAILED;
+      for (int j = 0; j <= A.K; j++) A.ids_out[(long)b * (A.K + 1) + j] = PZ_ID_FAILED;
+    }
+    return;
   }
   const uint64_t rej = __ballot(lane < A.K && !accept);
   const int js = rej ? (int)__builtin_ctzll(rej) : A.K;
@@ -245,19 +271,21 @@ __global__ __launch_bounds__(64) void k_spec_accept(SpecArgs A) {
   s.js = js;
   s.last = -1;
   s.qt = s.qd = -1;
+  s.dr = -1;
   int tok = -1;
   s.mode = SQ_DONE;
   if (js < A.K) {
     const int qt = b * A.KT + js, qd = A.NT + b * A.K + js;
     if (spec_bad(rs[qt].flags)) {
       tok = A.V - 1;  // p is NaN everywhere: r == 0, and the p-draw falls back
-    } else if (spec_bad(rs[qd].flags)) {
+    } else if (!A.onehot && spec_bad(rs[qd].flags)) {
       s.mode = SQ_CAT;  // q is NaN: every p - q fails t > 0, Z == 0
       s.qt = qt;
     } else {
       s.mode = SQ_RES;
       s.qt = qt;
-      s.qd = qd;
+      s.qd = A.onehot ? -1 : qd;
+      s.dr = A.draft_ids[b * A.K + js];
     }
   } else if (A.has_bonus) {
     const int qt = b * A.KT + A.K;
@@ -280,11 +308,13 @@ __device__ __forceinline__ ResidualTerms<VEC> residual_terms(const SpecArgs& A, 
                                                              const pz_lds_u64* et) {
   ResidualTerms<VEC> X;
   X.T = temp_row<VEC>(A, s.qt);
-  X.D = temp_row<VEC>(A, s.qd);
+  X.oh = s.qd < 0;
+  X.ohd = s.dr;
+  X.D = s.qd < 0 ? X.T : temp_row<VEC>(A, s.qd);
   X.MT = A.ws.rs[s.qt].M;
   X.invT = A.ws.rs[s.qt].inv;
-  X.MD = A.ws.rs[s.qd].M;
-  X.invD = A.ws.rs[s.qd].inv;
+  X.MD = s.qd < 0 ? 0.0f : A.ws.rs[s.qd].M;
+  X.invD = s.qd < 0 ? 0.0f : A.ws.rs[s.qd].inv;
   X.lastpos = -1;
   X.et = et;
   return X;
@@ -314,7 +344,8 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vest(Spec
   const float MT = A.ws.rs[s.qt].M, invT = A.ws.rs[s.qt].inv;
   float MD = 0.0f, invD = 0.0f;
   PzTempRow<VEC> D = T;
-  if (s.mode == SQ_RES) {
+  const bool two = s.mode == SQ_RES && s.qd >= 0;  // q from a draft row (else one-hot)
+  if (two) {
     D = temp_row<VEC>(A, s.qd);
     MD = A.ws.rs[s.qd].M;
     invD = A.ws.rs[s.qd].inv;
@@ -327,7 +358,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vest(Spec
     for (int u = 0; u < PZ_SP_U; u++) {
       const int e0 = (kb + u * PZ_SP_WAVES) * PZ_SP_SEG + 4 * lane;
       ns[u] = T.load(e0, yts[u]);
-      if (s.mode == SQ_RES) D.load(e0, yds[u]);
+      if (two) D.load(e0, yds[u]);
     }
 #pragma unroll
     for (int u = 0; u < PZ_SP_U; u++) {
@@ -339,12 +370,19 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vest(Spec
       float (&yd)[4] = yds[u];
       T.apply(e0, n, yt);
       float t = 0.0f;
-      if (s.mode == SQ_RES) {
+      if (two) {
         D.apply(e0, n, yd);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           if (c >= n) continue;
           const float r = pz_fast_exp(yt[c] - MT) * invT - pz_fast_exp(yd[c] - MD) * invD;
+          t += r > 0.0f ? r : 0.0f;
+        }
+      } else if (s.mode == SQ_RES) {  // one-hot q: p, less 1 at the draft
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          if (c >= n) continue;
+          const float r = pz_fast_exp(yt[c] - MT) * invT - (e0 + c == s.dr ? 1.0f : 0.0f);
           t += r > 0.0f ? r : 0.0f;
         }
       } else {
@@ -535,7 +573,8 @@ int spec_enqueue(pz_sampler* s, const float* d_target, const float* d_draft, int
                  const float* uacc_in, const float* ures_in, int32_t* acc_out,
                  int32_t* out_ids) {
   const int KT = K + (has_bonus ? 1 : 0);
-  const int NR = B * KT + B * K;
+  const bool onehot = d_draft == nullptr;  // greedy drafts: no draft rows
+  const int NR = B * KT + (onehot ? 0 : B * K);
   const size_t o_seq = 0;
   const size_t o_ws = up256(o_seq + (size_t)B * sizeof(SpecSeq));
   const size_t dev_bytes = o_ws + pz_split_ws_layout(NR + B, V, 0, nullptr, nullptr);
@@ -563,6 +602,7 @@ int spec_enqueue(pz_sampler* s, const float* d_target, const float* d_draft, int
   A.NT = B * KT;
   A.NR = NR;
   A.has_bonus = has_bonus ? 1 : 0;
+  A.onehot = onehot ? 1 : 0;
   A.T.t = T;
   A.T.inv = 1.0f / T;
   A.T.div = s->temp_mode == PZ_TEMP_DIV;
@@ -591,31 +631,36 @@ int spec_check(pz_sampler* s, int B, int K, int V, long ld) {
 
 }  // namespace
 
-extern "C" int pz_spec_verify_async(pz_sampler* s, const float* d_target, const float* d_draft,
-                                    int B, int K, int V, long ld, int has_bonus,
-                                    float temperature, const int32_t* d_draft_ids,
-                                    const float* d_u_acc, const float* d_u_res,
-                                    int32_t* d_acc_len_out, int32_t* d_ids_out) {
+namespace {
+
+// greedy: drafts are the draft model's argmax (q one-hot; no draft logits)
+int verify_async(pz_sampler* s, bool greedy, const float* d_target, const float* d_draft, int B,
+                 int K, int V, long ld, int has_bonus, float temperature,
+                 const int32_t* d_draft_ids, const float* d_u_acc, const float* d_u_res,
+                 int32_t* d_acc_len_out, int32_t* d_ids_out) {
   if (!s) return PZ_EINVAL;
   int rc = spec_check(s, B, K, V, ld);
   if (rc != PZ_OK || B == 0) return rc;
-  if (!d_target || !d_draft || !d_draft_ids || !d_u_acc || !d_u_res || !d_acc_len_out ||
-      !d_ids_out)
+  if (!d_target || (!greedy && !d_draft) || !d_draft_ids || !d_u_acc || !d_u_res ||
+      !d_acc_len_out || !d_ids_out)
     return fail(s, PZ_EINVAL, "null spec argument");
+  if (greedy) d_draft = nullptr;
   PZ_HIP(s, hipSetDevice(s->device));
   return spec_enqueue(s, d_target, d_draft, B, K, V, ld, has_bonus, temperature, d_draft_ids,
                       d_u_acc, d_u_res, d_acc_len_out, d_ids_out);
 }
 
-extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float* d_draft, int B,
-                              int K, int V, long ld, int has_bonus, float temperature,
-                              const int32_t* draft_ids, const float* u_acc, const float* u_res,
-                              int32_t* acc_len_out, int32_t* ids_out) {
+int verify_sync(pz_sampler* s, bool greedy, const float* d_target, const float* d_draft, int B,
+                int K, int V, long ld, int has_bonus, float temperature,
+                const int32_t* draft_ids, const float* u_acc, const float* u_res,
+                int32_t* acc_len_out, int32_t* ids_out) {
   if (!s) return PZ_EINVAL;
   int rc = spec_check(s, B, K, V, ld);
   if (rc != PZ_OK || B == 0) return rc;
-  if (!d_target || !d_draft || !draft_ids || !u_acc || !u_res || !acc_len_out || !ids_out)
+  if (!d_target || (!greedy && !d_draft) || !draft_ids || !u_acc || !u_res || !acc_len_out ||
+      !ids_out)
     return fail(s, PZ_EINVAL, "null spec argument");
+  if (greedy) d_draft = nullptr;
   PZ_HIP(s, hipSetDevice(s->device));
   // the inputs and outputs in mapped, coherent pinned memory: the kernels
   // read and write them there, no copies
@@ -672,5 +717,45 @@ extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float*
   s->spec_busy = false;
   memcpy(acc_len_out, h + o_acc, (size_t)B * 4);
   memcpy(ids_out, h + o_out, (size_t)B * (K + 1) * 4);
+  for (int b = 0; b < B; b++)
+    if (acc_len_out[b] == PZ_ID_FAILED)
+      return fail(s, PZ_EDEVICE, "sequence %d: a wait between workgroups gave up", b);
   return PZ_OK;
+}
+
+}  // namespace
+
+extern "C" int pz_spec_verify_async(pz_sampler* s, const float* d_target, const float* d_draft,
+                                    int B, int K, int V, long ld, int has_bonus,
+                                    float temperature, const int32_t* d_draft_ids,
+                                    const float* d_u_acc, const float* d_u_res,
+                                    int32_t* d_acc_len_out, int32_t* d_ids_out) {
+  return verify_async(s, false, d_target, d_draft, B, K, V, ld, has_bonus, temperature, d_draft_ids,
+                      d_u_acc, d_u_res, d_acc_len_out, d_ids_out);
+}
+
+extern "C" int pz_spec_verify(pz_sampler* s, const float* d_target, const float* d_draft, int B,
+                              int K, int V, long ld, int has_bonus, float temperature,
+                              const int32_t* draft_ids, const float* u_acc, const float* u_res,
+                              int32_t* acc_len_out, int32_t* ids_out) {
+  return verify_sync(s, false, d_target, d_draft, B, K, V, ld, has_bonus, temperature, draft_ids, u_acc,
+                     u_res, acc_len_out, ids_out);
+}
+
+extern "C" int pz_spec_verify_greedy_async(pz_sampler* s, const float* d_target, int B, int K,
+                                           int V, long ld, int has_bonus, float temperature,
+                                           const int32_t* d_draft_ids, const float* d_u_acc,
+                                           const float* d_u_res, int32_t* d_acc_len_out,
+                                           int32_t* d_ids_out) {
+  return verify_async(s, true, d_target, nullptr, B, K, V, ld, has_bonus, temperature, d_draft_ids,
+                      d_u_acc, d_u_res, d_acc_len_out, d_ids_out);
+}
+
+extern "C" int pz_spec_verify_greedy(pz_sampler* s, const float* d_target, int B, int K, int V,
+                                     long ld, int has_bonus, float temperature,
+                                     const int32_t* draft_ids, const float* u_acc,
+                                     const float* u_res, int32_t* acc_len_out,
+                                     int32_t* ids_out) {
+  return verify_sync(s, true, d_target, nullptr, B, K, V, ld, has_bonus, temperature, draft_ids, u_acc,
+                     u_res, acc_len_out, ids_out);
 }

@@ -19,6 +19,14 @@
 //   4. commit: the a accepted drafts and the resampled (or bonus) token are
 //      appended; both caches are rolled back to p + a + 1 (they keep x and
 //      the accepted drafts; the next round forwards the new token there).
+// Options (pz_spec_decode_opts):
+//   greedy drafts (IMPLEMENTATION_PLAN.md:1680): d_j is the draft model's
+//      argmax (argmax.c:3-13, no draw), q is one-hot at d_j in the
+//      verification (pz_spec_verify_greedy: accept iff u < p(d_j));
+//   EOS stops (generate.c:198-211): the committed tokens are scanned in
+//      order and the first id of the sampler's EOS list ends the sequence
+//      -- it is not committed, the caches keep what precedes it, and later
+//      rounds leave the sequence, its RNG states and its caches as they are.
 #include <hip/hip_runtime.h>
 
 #include <string.h>
@@ -38,11 +46,14 @@ struct DevBuf {
 
 }  // namespace
 
-extern "C" int pz_spec_decode(pz_sampler* s, const pz_spec_models* m, int B, int K, int V,
-                              float tau, int32_t* tokens, int32_t* len, int max_len, int rounds,
-                              uint64_t* d_draft_state, uint64_t* verify_state,
-                              int32_t* accepted_out) {
+extern "C" int pz_spec_decode_opts(pz_sampler* s, const pz_spec_models* m,
+                                   const pz_spec_opts* opts, int B, int K, int V, float tau,
+                                   int32_t* tokens, int32_t* len, int max_len, int rounds,
+                                   uint64_t* d_draft_state, uint64_t* verify_state,
+                                   int32_t* accepted_out, uint8_t* done) {
   if (!s) return PZ_EINVAL;
+  const bool greedy = opts && opts->greedy_draft;
+  const bool stop_eos = opts && opts->stop_at_eos && s->n_eos > 0;
   if (!m || !m->draft_step || !m->target_forward || !m->kv_rollback || !tokens || !len ||
       !d_draft_state || !verify_state || B < 0 || V <= 0 || rounds < 0)
     return fail(s, PZ_EINVAL, "bad speculative decode arguments");
@@ -57,8 +68,9 @@ extern "C" int pz_spec_decode(pz_sampler* s, const pz_spec_models* m, int B, int
   if (B == 0 || rounds == 0) return PZ_OK;
   PZ_HIP(s, hipSetDevice(s->device));
   const size_t BV = (size_t)B * V;
-  DevBuf q, p, junk, tok, ids, tt;
+  DevBuf q, p, junk, tok, ids, tt, ds0;
   if (hipMalloc(&q.p, BV * K * sizeof(float)) != hipSuccess ||
+      hipMalloc(&ds0.p, (size_t)B * sizeof(uint64_t)) != hipSuccess ||
       hipMalloc(&p.p, BV * (K + 1) * sizeof(float)) != hipSuccess ||
       hipMalloc(&junk.p, BV * sizeof(float)) != hipSuccess ||
       hipMalloc(&tok.p, (size_t)B * sizeof(int32_t)) != hipSuccess ||
@@ -73,9 +85,13 @@ extern "C" int pz_spec_decode(pz_sampler* s, const pz_spec_models* m, int B, int
   std::vector<int32_t> h_tok(B), pos0(B), posj(B), h_ids((size_t)K * B), draft_ids((size_t)B * K),
       h_tt((size_t)B * (K + 1)), acc(B), out((size_t)B * (K + 1)), pos_new(B);
   std::vector<float> u_acc((size_t)B * K), u_res(B);
+  std::vector<uint8_t> fin(B, 0);  // stopped sequences
+  if (done)
+    for (int b = 0; b < B; b++) fin[b] = done[b] ? 1 : 0;
+  uint64_t* d_ds0 = static_cast<uint64_t*>(ds0.p);
   pz_row_params prm;
   memset(&prm, 0, sizeof(prm));
-  prm.temperature = tau;
+  prm.temperature = greedy ? 0.0f : tau;  // greedy drafts: argmax, no draw
   prm.top_k = 0;
   prm.top_p = 1.0f;
   prm.rep_penalty = 1.0f;
@@ -87,6 +103,11 @@ extern "C" int pz_spec_decode(pz_sampler* s, const pz_spec_models* m, int B, int
     }
     PZ_HIP(s, hipMemcpyAsync(d_tok, h_tok.data(), (size_t)B * sizeof(int32_t),
                              hipMemcpyHostToDevice, s->stream));
+    bool any_fin = false;
+    for (int b = 0; b < B; b++) any_fin |= fin[b] != 0;
+    if (any_fin && !greedy)  // the stopped sequences' draft states, restored after the draws
+      PZ_HIP(s, hipMemcpyAsync(d_ds0, d_draft_state, (size_t)B * sizeof(uint64_t),
+                               hipMemcpyDeviceToDevice, s->stream));
     // 1. draft steps and their draws
     for (int j = 0; j <= K; j++) {
       for (int b = 0; b < B; b++) posj[b] = pos0[b] + j;
@@ -101,6 +122,11 @@ extern "C" int pz_spec_decode(pz_sampler* s, const pz_spec_models* m, int B, int
         if (rc != PZ_OK) return rc;
       }
     }
+    if (any_fin && !greedy)
+      for (int b = 0; b < B; b++)
+        if (fin[b])
+          PZ_HIP(s, hipMemcpyAsync(d_draft_state + b, d_ds0 + b, sizeof(uint64_t),
+                                   hipMemcpyDeviceToDevice, s->stream));
     PZ_HIP(s, hipMemcpyAsync(h_ids.data(), d_ids, (size_t)K * B * sizeof(int32_t),
                              hipMemcpyDeviceToHost, s->stream));
     PZ_HIP(s, hipStreamSynchronize(s->stream));
@@ -119,26 +145,59 @@ extern "C" int pz_spec_decode(pz_sampler* s, const pz_spec_models* m, int B, int
       return fail(s, PZ_EDEVICE, "target model forward of round %d failed", r);
     // 3. verification
     for (int b = 0; b < B; b++) {
+      if (fin[b]) {  // a stopped sequence draws nothing
+        for (int j = 0; j < K; j++) u_acc[(size_t)b * K + j] = 0.0f;
+        u_res[b] = 0.0f;
+        continue;
+      }
       unsigned long long vs = verify_state[b];
       for (int j = 0; j < K; j++) u_acc[(size_t)b * K + j] = rng_float(&vs);
       u_res[b] = rng_float(&vs);
       verify_state[b] = vs;
     }
-    const int rc = pz_spec_verify(s, d_p, d_q, B, K, V, (long)V, 1, tau, draft_ids.data(),
-                                  u_acc.data(), u_res.data(), acc.data(), out.data());
+    const int rc =
+        greedy ? pz_spec_verify_greedy(s, d_p, B, K, V, (long)V, 1, tau, draft_ids.data(),
+                                       u_acc.data(), u_res.data(), acc.data(), out.data())
+               : pz_spec_verify(s, d_p, d_q, B, K, V, (long)V, 1, tau, draft_ids.data(),
+                                u_acc.data(), u_res.data(), acc.data(), out.data());
     if (rc != PZ_OK) return rc;
     // 4. commit and roll the caches back
     for (int b = 0; b < B; b++) {
+      if (fin[b]) {
+        pos_new[b] = pos0[b];
+        if (accepted_out) accepted_out[(size_t)r * B + b] = -1;
+        continue;
+      }
       const int a = acc[b];
-      for (int i = 0; i <= a; i++)
+      int n = a + 1;  // tokens committed: up to the first EOS, which is not
+      for (int i = 0; stop_eos && i <= a && n == a + 1; i++) {
+        const int32_t t = out[(size_t)b * (K + 1) + i];
+        for (int e = 0; e < s->n_eos; e++)
+          if (t == s->h_eos[e]) {
+            n = i;
+            fin[b] = 1;
+            break;
+          }
+      }
+      for (int i = 0; i < n; i++)
         tokens[(size_t)b * max_len + len[b] + i] = out[(size_t)b * (K + 1) + i];
-      len[b] += a + 1;
-      pos_new[b] = pos0[b] + a + 1;
+      len[b] += n;
+      pos_new[b] = pos0[b] + n;
       if (accepted_out) accepted_out[(size_t)r * B + b] = a;
     }
     if (m->kv_rollback(m->ctx, 0, pos_new.data(), B) != 0 ||
         m->kv_rollback(m->ctx, 1, pos_new.data(), B) != 0)
       return fail(s, PZ_EDEVICE, "KV cache rollback of round %d failed", r);
   }
+  if (done)
+    for (int b = 0; b < B; b++) done[b] = fin[b];
   return PZ_OK;
+}
+
+extern "C" int pz_spec_decode(pz_sampler* s, const pz_spec_models* m, int B, int K, int V,
+                              float tau, int32_t* tokens, int32_t* len, int max_len, int rounds,
+                              uint64_t* d_draft_state, uint64_t* verify_state,
+                              int32_t* accepted_out) {
+  return pz_spec_decode_opts(s, m, nullptr, B, K, V, tau, tokens, len, max_len, rounds,
+                             d_draft_state, verify_state, accepted_out, nullptr);
 }

@@ -125,6 +125,7 @@ extern "C" int pz_sampler_set_eos(pz_sampler* s, const int32_t* eos_ids, int n_e
   if (n_eos > 0)
     PZ_HIP(s, hipMemcpy(s->d_eos, eos_ids, (size_t)n_eos * sizeof(int32_t),
                         hipMemcpyHostToDevice));
+  if (n_eos > 0) memcpy(s->h_eos, eos_ids, (size_t)n_eos * sizeof(int32_t));
   s->n_eos = n_eos;
   return PZ_OK;
 }

@@ -27,6 +27,7 @@ ABI_SYMBOLS = (
     "pz_temperature_batch", "pz_softmax_batch", "pz_sample_batch_noalloc",
     "pz_sample_step", "pz_sampler_set_eos", "pz_attn_softmax", "pz_lm_head_bf16",
     "pz_lm_head_argmax_bf16", "pz_spec_decode", "pz_sampler_set_wait_bound",
+    "pz_spec_verify_greedy", "pz_spec_verify_greedy_async", "pz_spec_decode_opts",
     # include/pz_sampling_compat.h: the reference sampler's own symbols
     "sample_argmax", "apply_temperature", "sample_top_p", "sample_top_k", "rng_seed",
     "rng_float", "pz_tn_softmax", "pz_compat_set_temp_mode", "pz_compat_last_status",
@@ -104,6 +105,11 @@ def load():
     lib.pz_lm_head_bf16.argtypes = [_P, _P, _I, _I, _P, _I, _L, _P, _L]
     lib.pz_lm_head_argmax_bf16.argtypes = [_P, _P, _I, _I, _P, _I, _L, _P]
     lib.pz_spec_decode.argtypes = [_P, _P, _I, _I, _I, _F, _P, _P, _I, _I, _P, _P, _P]
+    lib.pz_spec_decode_opts.argtypes = [_P, _P, _P, _I, _I, _I, _F, _P, _P, _I, _I, _P, _P, _P,
+                                        _P]
+    lib.pz_spec_verify_greedy.argtypes = [_P, _P, _I, _I, _I, _L, _I, _F, _P, _P, _P, _P, _P]
+    lib.pz_spec_verify_greedy_async.argtypes = [_P, _P, _I, _I, _I, _L, _I, _F, _P, _P, _P,
+                                                _P, _P]
     pull = ctypes.POINTER(ctypes.c_ulonglong)
     lib.sample_argmax.argtypes = [_P, _I]
     lib.apply_temperature.argtypes = [_P, _I, _F]
@@ -299,6 +305,7 @@ class Sampler:
 
     def spec_verify(self, d_target, d_draft, B, K, V, ld, has_bonus, temperature,
                     draft_ids, u_acc, u_res):
+        """d_draft None: greedy drafts (pz_spec_verify_greedy, q one-hot)."""
         _sync_torch(d_target, d_draft)
         acc = np.empty(B, np.int32)
         out = np.empty((B, K + 1), np.int32)
@@ -308,9 +315,15 @@ class Sampler:
         for name, a, need in (("draft_ids", di, B * K), ("u_acc", ua, B * K), ("u_res", ur, B)):
             if a.size < need:
                 raise ValueError(f"{name} holds {a.size} entries, B={B}, K={K} need {need}")
-        rc = self.lib.pz_spec_verify(self.h, _ptr(d_target), _ptr(d_draft), B, K, V, ld,
-                                     int(has_bonus), float(temperature), _np_ptr(di),
-                                     _np_ptr(ua), _np_ptr(ur), _np_ptr(acc), _np_ptr(out))
+        if d_draft is None:
+            rc = self.lib.pz_spec_verify_greedy(self.h, _ptr(d_target), B, K, V, ld,
+                                                int(has_bonus), float(temperature), _np_ptr(di),
+                                                _np_ptr(ua), _np_ptr(ur), _np_ptr(acc),
+                                                _np_ptr(out))
+        else:
+            rc = self.lib.pz_spec_verify(self.h, _ptr(d_target), _ptr(d_draft), B, K, V, ld,
+                                         int(has_bonus), float(temperature), _np_ptr(di),
+                                         _np_ptr(ua), _np_ptr(ur), _np_ptr(acc), _np_ptr(out))
         self._check(rc)
         return acc, out
 

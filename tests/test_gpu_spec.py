@@ -126,3 +126,29 @@ def test_async_matches_sync_over_repeated_calls(torch_cuda):
         wacc, wout, _ = po.spec_verify(w["target"], w["draft"], K, True, w["tau"], w["draft_ids"],
                                        w["u_acc"], w["u_res"])
         assert (acc == wacc).all() and (out == wout).all(), label
+
+
+@pytest.mark.parametrize("has_bonus", [True, False])
+def test_greedy_drafts(torch_cuda, has_bonus):
+    """Greedy drafting (q one-hot at each draft, no draft rows): the draft
+    ids are the draft rows' argmax, with invalid ids, a draft the target
+    gives p = 1 (u = 1.0 then rejects with Z == 0) and u = 0 mixed in."""
+    w = wl.build_c5(B=32, K=4, seed=0xC5 + 21, has_bonus=has_bonus)
+    B, K, V, tau = w["B"], w["K"], w["V"], w["tau"]
+    target = w["target"].copy()
+    ids = np.argmax(w["draft"], axis=2).astype(np.int32)
+    ids[2, 0] = -1
+    ids[5, 2] = V
+    target[7, 0, :] = -1e30
+    target[7, 0, ids[7, 0]] = 0.0  # p(d) == 1
+    u_acc = w["u_acc"].copy()
+    u_acc[7, 0] = 1.0
+    u_acc[9, :] = 0.0
+    print(f"case greedy drafts B={B} K={K} V={V} bonus={has_bonus}", flush=True)
+    d_t = to_dev(torch_cuda, np.ascontiguousarray(target))
+    with pz.Sampler(B, V) as s:
+        acc, out = s.spec_verify(d_t, None, B, K, V, V, has_bonus, tau, ids, u_acc, w["u_res"])
+    wacc, wout, _ = po.spec_verify(target, None, K, has_bonus, tau, ids, u_acc, w["u_res"])
+    assert (acc == wacc).all(), (acc, wacc)
+    assert (out == wout).all(), np.nonzero((out != wout).any(axis=1))[0]
+    assert acc[7] == 0 and acc[9] == K and acc[2] == 0

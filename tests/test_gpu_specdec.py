@@ -89,12 +89,16 @@ class ToyNumpy:
         self.len[m][:] = pos
 
 
+class SpecOpts(ctypes.Structure):
+    _fields_ = [("greedy_draft", ctypes.c_int), ("stop_at_eos", ctypes.c_int)]
+
+
 class SpecModels(ctypes.Structure):
     _fields_ = [("ctx", ctypes.c_void_p), ("draft_step", ctypes.c_void_p),
                 ("target_forward", ctypes.c_void_p), ("kv_rollback", ctypes.c_void_p)]
 
 
-def run_case(torch, B, K, V, tau, rounds, seed):
+def run_case(torch, B, K, V, tau, rounds, seed, greedy=False, eos=None):
     max_len = 8 + rounds * (K + 1)
     rng = np.random.default_rng(seed)
     lens = rng.integers(1, 8, B).astype(np.int32)
@@ -108,7 +112,9 @@ def run_case(torch, B, K, V, tau, rounds, seed):
     o_tokens, o_lens = tokens.copy(), lens.copy().astype(np.int64)
     o_ds, o_vs = draft_seed.copy(), verify_seed.copy()
     model = ToyNumpy(B, V, max_len, toy_seed, tokens, lens)
-    want_acc = po.spec_decode(model, B, K, V, tau, o_tokens, o_lens, rounds, o_ds, o_vs)
+    o_done = np.zeros(B, np.uint8)
+    want_acc = po.spec_decode(model, B, K, V, tau, o_tokens, o_lens, rounds, o_ds, o_vs,
+                              greedy_draft=greedy, eos=eos, done=o_done)
     # device
     lib = ctypes.CDLL(TOY)
     lib.toy_create.restype = ctypes.c_void_p
@@ -125,12 +131,22 @@ def run_case(torch, B, K, V, tau, rounds, seed):
     d_ds = to_dev(torch, draft_seed.view(np.int64))
     g_vs = verify_seed.copy()
     acc = np.zeros((rounds, B), np.int32)
+    done = np.zeros(B, np.uint8)
     with pz.Sampler(B, V) as s:
         assert s.lib.pz_spec_decode.argtypes is not None
         torch.cuda.synchronize()
-        rc = s.lib.pz_spec_decode(s.h, ctypes.addressof(m), B, K, V, tau, g_tokens.ctypes.data,
-                                  g_lens.ctypes.data, max_len, rounds, d_ds.data_ptr(),
-                                  g_vs.ctypes.data, acc.ctypes.data)
+        if greedy or eos is not None:
+            if eos is not None:
+                s.set_eos(eos)
+            opts = SpecOpts(int(greedy), int(eos is not None))
+            rc = s.lib.pz_spec_decode_opts(s.h, ctypes.addressof(m), ctypes.addressof(opts), B,
+                                           K, V, tau, g_tokens.ctypes.data, g_lens.ctypes.data,
+                                           max_len, rounds, d_ds.data_ptr(), g_vs.ctypes.data,
+                                           acc.ctypes.data, done.ctypes.data)
+        else:
+            rc = s.lib.pz_spec_decode(s.h, ctypes.addressof(m), B, K, V, tau,
+                                      g_tokens.ctypes.data, g_lens.ctypes.data, max_len, rounds,
+                                      d_ds.data_ptr(), g_vs.ctypes.data, acc.ctypes.data)
         assert rc == pz.PZ_OK, s.lib.pz_sampler_last_error(s.h)
     errors = lib.toy_errors(ctx)
     lib.toy_destroy(ctx)
@@ -144,12 +160,38 @@ def run_case(torch, B, K, V, tau, rounds, seed):
     assert (g_tokens == o_tokens).all()
     assert (g_vs == o_vs).all()
     assert (d_ds.cpu().numpy().view(np.uint64) == o_ds).all()
-    return acc
+    assert (done == o_done).all()
+    return acc, done
 
 
 @pytest.mark.parametrize("B,K,V,tau", [(4, 4, 4096, 0.8), (3, 7, 1000, 1.3), (1, 1, 257, 0.5)])
 def test_spec_decode_loop_matches_oracle(torch_cuda, B, K, V, tau):
     print(f"case specdec B={B} K={K} V={V} tau={tau}", flush=True)
-    acc = run_case(torch_cuda, B, K, V, tau, rounds=24, seed=B * 100 + K)
+    acc, _ = run_case(torch_cuda, B, K, V, tau, rounds=24, seed=B * 100 + K)
     # the trace exercises acceptances and rejections
     assert acc.max() >= 1 and acc.min() < K
+
+
+@pytest.mark.parametrize("B,K,V,tau", [(4, 4, 64, 0.3), (3, 5, 257, 0.5)])
+def test_spec_decode_greedy_drafts(torch_cuda, B, K, V, tau):
+    """Greedy drafting: argmax drafts (no draws: the draft RNG states stay)
+    verified with q one-hot."""
+    print(f"case specdec greedy B={B} K={K} V={V} tau={tau}", flush=True)
+    acc, _ = run_case(torch_cuda, B, K, V, tau, rounds=24, seed=B * 100 + K + 7, greedy=True)
+    assert acc.max() >= 1
+
+
+@pytest.mark.parametrize("greedy", [False, True])
+def test_spec_decode_stops_at_eos(torch_cuda, greedy):
+    """EOS ids end sequences (not committed); stopped sequences keep their
+    tokens, states and caches through the remaining rounds."""
+    B, K, V, tau = 6, 3, 1000, 0.9
+    eos = list(range(7, V, 41))  # 24 ids
+    print(f"case specdec eos greedy={greedy} B={B} K={K} V={V}", flush=True)
+    acc, done = run_case(torch_cuda, B, K, V, tau, rounds=24, seed=4242 + int(greedy),
+                         greedy=greedy, eos=eos)
+    assert done.any(), "no sequence reached an EOS id"
+    for b in np.nonzero(done)[0]:  # once stopped, a sequence takes no part
+        stopped = np.nonzero(acc[:, b] < 0)[0]
+        if stopped.size:
+            assert (acc[stopped[0]:, b] < 0).all()

@@ -13,7 +13,12 @@ inline categorical draw it never tests (CPU only).
   a11 speculative verification: draft == target accepts everything, a
       rejected draft is never resampled, and the first emitted token is
       distributed as the target softmax (Leviathan et al. 2023, Thm. 1),
-      checked by simulation on a 5-token vocabulary.
+      checked by simulation on a 5-token vocabulary; greedy (one-hot)
+      drafts against a float64 model of the rule and by the same theorem;
+  f3  the speculative decode loop: the first token each round commits is
+      distributed as the target softmax (chi-square over 20000 seeded
+      sequences, drawn and greedy drafts), and EOS stops (the EOS is not
+      committed; a stopped sequence's state stays as it is).
 """
 import ctypes
 
@@ -208,3 +213,142 @@ def test_spec_first_token_is_distributed_as_target():
     assert np.all(np.abs(freq - p) < 5 * sigma + 1e-4), (freq, p)
     # and the acceptance rate is sum(min(p, q))
     assert abs(acc.mean() - np.minimum(p, q).sum()) < 5 * np.sqrt(0.25 / N)
+
+
+# ------------------------------------------------- a11: greedy (one-hot) drafts
+def test_spec_greedy_drafts_closed_form():
+    """q one-hot at the draft: accepted iff u < p(d); on rejection the token
+    comes from p with p(d) removed (float64 model, away from boundaries)."""
+    rng = np.random.default_rng(11)
+    B, K, V, tau = 200, 3, 30, 0.9
+    target = (rng.standard_normal((B, K + 1, V)) * 1.5).astype(np.float32)
+    ids = rng.integers(-1, V, size=(B, K)).astype(np.int32)  # -1: never accepted
+    ua = rng.uniform(size=(B, K)).astype(np.float32)
+    ur = rng.uniform(size=B).astype(np.float32)
+    acc, out, _ = po.spec_verify(target, None, K, True, tau, ids, ua, ur)
+    checked = 0
+    for b in range(B):
+        j = 0
+        while j < K:
+            d = ids[b, j]
+            p = softmax64(target[b, j], tau)
+            if d < 0 or not ua[b, j] < p[d]:
+                break
+            j += 1
+        if any(abs(float(ua[b, i]) - softmax64(target[b, i], tau)[ids[b, i]]) < 1e-5
+               for i in range(min(j + 1, K)) if ids[b, i] >= 0):
+            continue  # too close to the acceptance boundary for a float64 model
+        assert acc[b] == j, (b, acc[b], j)
+        assert (out[b, :j] == ids[b, :j]).all()
+        if j < K:
+            r = softmax64(target[b, j], tau)
+            if ids[b, j] >= 0:
+                r[ids[b, j]] = 0.0
+            cdf = np.cumsum(r)
+            x = ur[b] * cdf[-1]
+            if np.min(np.abs(cdf - x)) < 1e-5:
+                continue
+            assert out[b, j] == int(np.searchsorted(cdf, x, side="right")), b
+            assert out[b, j] != ids[b, j]
+        checked += 1
+    assert checked > B // 2
+
+
+def test_spec_greedy_draft_first_token_is_distributed_as_target():
+    """With a fixed (greedy) draft the emitted token is still distributed as
+    the target softmax: accepted with probability p(d), else drawn from p
+    without d."""
+    rng = np.random.default_rng(12)
+    V, tau, N = 5, 0.8, 40000
+    t_row = np.array([1.0, 0.2, -0.5, 2.0, 0.0], np.float32)
+    p = softmax64(t_row, tau)
+    target = np.broadcast_to(t_row, (N, 1, V)).copy()
+    ids = np.full((N, 1), 3, np.int32)  # the draft model's argmax
+    ua = rng.uniform(size=(N, 1)).astype(np.float32)
+    ur = rng.uniform(size=N).astype(np.float32)
+    acc, out, _ = po.spec_verify(target, None, 1, False, tau, ids, ua, ur)
+    freq = np.bincount(out[:, 0], minlength=V) / N
+    sigma = np.sqrt(p * (1 - p) / N)
+    assert np.all(np.abs(freq - p) < 5 * sigma + 1e-4), (freq, p)
+    assert abs(acc.mean() - p[3]) < 5 * np.sqrt(0.25 / N)
+
+
+class FixedModels:
+    """Draft and target models whose logits ignore the context (fixed rows),
+    with the cache bookkeeping of a real pair (positions checked)."""
+
+    def __init__(self, B, lens, d_row, t_row):
+        self.d, self.t = d_row, t_row
+        self.len = [np.asarray(lens, np.int64) - 1, np.asarray(lens, np.int64) - 1]
+
+    def draft(self, tok, pos):
+        assert (np.asarray(pos) == self.len[0]).all()
+        self.len[0] = np.asarray(pos) + 1
+        return np.broadcast_to(self.d, (len(tok), self.d.size)).copy()
+
+    def target(self, tok, pos):
+        assert (np.asarray(pos) == self.len[1]).all()
+        B, n = np.asarray(tok).shape
+        self.len[1] = np.asarray(pos) + n
+        return np.broadcast_to(self.t, (B, n, self.t.size)).copy()
+
+    def rollback(self, m, pos):
+        assert (np.asarray(pos) <= self.len[m]).all()
+        self.len[m] = np.asarray(pos).copy()
+
+
+@pytest.mark.parametrize("greedy", [False, True])
+def test_spec_decode_first_committed_token_is_distributed_as_target(greedy):
+    """The loop (draft draws or greedy drafts, the uniforms' order, the
+    verification, the commit): over many sequences with their own RNG
+    seeds, the first token each round commits follows softmax(target/tau)."""
+    V, K, tau, N = 6, 2, 0.9, 20000
+    t_row = np.array([0.5, 1.8, -0.3, 1.0, 0.0, -1.2], np.float32)
+    d_row = np.array([1.2, 0.4, 0.2, 1.5, -0.5, 0.0], np.float32)
+    p = softmax64(t_row, tau)
+    lens = np.ones(N, np.int64)
+    tokens = np.zeros((N, 1 + K + 1), np.int32)
+    ds = (np.arange(1, N + 1, dtype=np.uint64) * np.uint64(7919)) | np.uint64(1)
+    vs = (np.arange(1, N + 1, dtype=np.uint64) * np.uint64(104729)) ^ np.uint64(5)
+    m = FixedModels(N, lens, d_row, t_row)
+    acc = po.spec_decode(m, N, K, V, tau, tokens, lens, 1, ds, vs, greedy_draft=greedy)
+    first = tokens[:, 1]
+    freq = np.bincount(first, minlength=V) / N
+    # chi-square against p (5 degrees of freedom; 0.1 % critical value 20.5)
+    chi2 = float(((freq - p) ** 2 / p).sum() * N)
+    assert chi2 < 20.5, (chi2, freq, p)
+    assert (lens == 1 + acc[0] + 1).all()
+    if greedy:
+        assert (acc[0] >= 0).all()
+        assert (ds == (np.arange(1, N + 1, dtype=np.uint64) * np.uint64(7919)) | np.uint64(1)).all()
+
+
+def test_spec_decode_stops_at_eos():
+    """A sequence stops at the first committed EOS id (not committed); later
+    rounds leave its tokens, length and RNG states alone."""
+    V, K, tau, B = 8, 3, 0.7, 64
+    t_row = np.array([0.0, 3.0, 0.0, 1.0, 0.0, 0.0, 0.0, 0.0], np.float32)
+    d_row = np.array([0.0, 3.0, 0.0, 0.8, 0.0, 0.0, 0.0, 0.0], np.float32)
+    rounds = 6
+    max_len = 1 + (rounds + 1) * (K + 1)
+    lens = np.ones(B, np.int64)
+    tokens = np.zeros((B, max_len), np.int32)
+    ds = (np.arange(1, B + 1, dtype=np.uint64) * np.uint64(7919)) | np.uint64(1)
+    vs = (np.arange(1, B + 1, dtype=np.uint64) * np.uint64(104729)) ^ np.uint64(5)
+    done = np.zeros(B, np.uint8)
+    m = FixedModels(B, lens, d_row, t_row)
+    acc = po.spec_decode(m, B, K, V, tau, tokens, lens, rounds, ds, vs, eos=[3], done=done)
+    assert done.any() and not done.all()
+    for b in range(B):
+        seq = tokens[b, 1:lens[b]]
+        assert 3 not in seq  # the EOS is never committed
+        if not done[b]:
+            assert (acc[:, b] >= 0).all()
+            assert lens[b] == 1 + sum(int(a) + 1 for a in acc[:, b])
+    # sequences that stopped before the last round keep their state there
+    later = np.nonzero(acc[-1] < 0)[0]
+    assert later.size > 0
+    ds2, vs2, tok2, len2 = ds.copy(), vs.copy(), tokens.copy(), lens.copy()
+    po.spec_decode(m, B, K, V, tau, tokens, lens, 1, ds, vs, eos=[3], done=done)
+    assert (ds[later] == ds2[later]).all() and (vs[later] == vs2[later]).all()
+    assert (lens[later] == len2[later]).all() and (tokens[later] == tok2[later]).all()
