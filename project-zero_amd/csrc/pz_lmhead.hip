@@ -196,13 +196,121 @@ __device__ __forceinline__ bool lm_nonfinite8(const lm_u32x4 q) {
   return r;
 }
 
+// Keys of the fused argmax spread over LMM_SLOTS slots per batch row (one
+// per workgroup index modulo LMM_SLOTS, each on its own cache line), so the
+// workgroups' atomics do not all meet on the batch's few words.
+constexpr int LMM_SLOTS = 16;
+
+// One chunk's activations: 16 NT batch rows x LMM_KC, loaded into registers
+// (XPT per thread), then split into the three bf16 parts in LDS.
+template <int NT>
+struct LmX {
+  static constexpr int XPT = 16 * NT * LMM_KC / (64 * LMM_WAVES);
+  float v[XPT];
+};
+
+template <int NT>
+__device__ __forceinline__ void lm_x_load(LmX<NT>& xr, const float* __restrict__ X, long ldx,
+                                          int nb, int n, int k0) {
+#pragma unroll
+  for (int q = 0; q < LmX<NT>::XPT; q++) {
+    const int i = (int)threadIdx.x + q * 64 * LMM_WAVES;
+    const int b = i / LMM_KC, kk = i - b * LMM_KC;
+    xr.v[q] = b < nb && k0 + kk < n ? X[(size_t)b * ldx + k0 + kk] : 0.0f;
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void lm_x_store(const LmX<NT>& xr, uint16_t* xs) {
+#pragma unroll
+  for (int q = 0; q < LmX<NT>::XPT; q++) {
+    const int i = (int)threadIdx.x + q * 64 * LMM_WAVES;
+    const int b = i / LMM_KC, kk = i - b * LMM_KC;
+    const float x = xr.v[q];
+    const uint32_t ux = __float_as_uint(x);
+    const bool fin = (ux & 0x7f800000u) != 0x7f800000u;
+    // (a NaN whose payload sits in the low bits stays a NaN)
+    const uint16_t h0 = fin || !(ux & 0x7fffffu) ? (uint16_t)(ux >> 16) : (uint16_t)0x7fc0u;
+    const float r0 = fin ? x - lm_bf16_f(h0) : 0.0f;  // exact: x's low 16 significand bits
+    const uint16_t h1 = (uint16_t)(__float_as_uint(r0) >> 16);
+    const float r1 = r0 - lm_bf16_f(h1);  // exact: at most 8 significant bits left
+    const uint16_t h2 = (uint16_t)(__float_as_uint(r1) >> 16);
+    xs[(0 * 16 * NT + b) * LMM_RS + kk] = h0;
+    xs[(1 * 16 * NT + b) * LMM_RS + kk] = h1;
+    xs[(2 * 16 * NT + b) * LMM_RS + kk] = h2;
+  }
+}
+
+__device__ __forceinline__ void lm_w_load(lm_u32x4 (&a)[LMM_TILES][LMM_KS],
+                                          const uint16_t* const (&wr)[LMM_TILES], int n, int k0,
+                                          int g) {
+#pragma unroll
+  for (int t = 0; t < LMM_TILES; t++)
+#pragma unroll
+    for (int s = 0; s < LMM_KS; s++) {
+      const int k = k0 + 32 * s + 8 * g;
+      a[t][s] = k < n ? *reinterpret_cast<const lm_u32x4*>(wr[t] + k) : lm_u32x4{0u, 0u, 0u, 0u};
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void lm_mfma(const lm_u32x4 (&a)[LMM_TILES][LMM_KS],
+                                        const uint16_t* xs, lm_f32x4 (&acc)[LMM_TILES][NT],
+                                        uint32_t& bad, int m, int g) {
+#pragma unroll
+  for (int s = 0; s < LMM_KS; s++) {
+    lm_bf16x8 bx[3][NT];
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+#pragma unroll
+      for (int j = 0; j < NT; j++)
+        bx[p][j] = *reinterpret_cast<const lm_bf16x8*>(
+            &xs[(p * 16 * NT + j * 16 + m) * LMM_RS + 32 * s + 8 * g]);
+#pragma unroll
+    for (int t = 0; t < LMM_TILES; t++) {
+      bad |= lm_nonfinite8(a[t][s]) ? 1u << t : 0u;
+      const lm_bf16x8 av = __builtin_bit_cast(lm_bf16x8, a[t][s]);
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        // the largest part first: the small ones add to an accumulator of
+        // the product's own size
+        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[2][j], acc[t][j], 0, 0, 0);
+        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[1][j], acc[t][j], 0, 0, 0);
+        acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[0][j], acc[t][j], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// One chunk step of the pipeline: the next chunk's activations and weights
+// are loaded (activations first: converting them waits only for them) and
+// its activation parts stored in the other LDS buffer while this chunk's
+// MFMAs run; one barrier per chunk.
+template <int NT>
+__device__ __forceinline__ void lm_step(int k0, int n, const float* __restrict__ X, long ldx,
+                                        int nb, const uint16_t* const (&wr)[LMM_TILES],
+                                        const lm_u32x4 (&cur)[LMM_TILES][LMM_KS],
+                                        lm_u32x4 (&nxt)[LMM_TILES][LMM_KS], const uint16_t* xs_cur,
+                                        uint16_t* xs_nxt, lm_f32x4 (&acc)[LMM_TILES][NT],
+                                        uint32_t& bad, int m, int g) {
+  const bool more = k0 + LMM_KC < n;
+  LmX<NT> xr;
+  if (more) {
+    lm_x_load<NT>(xr, X, ldx, nb, n, k0 + LMM_KC);
+    lm_w_load(nxt, wr, n, k0 + LMM_KC, g);
+    lm_x_store<NT>(xr, xs_nxt);
+  }
+  lm_mfma<NT>(cur, xs_cur, acc, bad, m, g);
+  __syncthreads();
+}
+
 template <int NT, int MODE>
 __global__ __launch_bounds__(64 * LMM_WAVES) __attribute__((amdgpu_waves_per_eu(4))) void k_lmhead_mfma(
     const uint16_t* __restrict__ W, int V, int n, const float* __restrict__ X, long ldx, int nb,
-    float* __restrict__ logits, long ld, unsigned long long* __restrict__ keys,
+    float* __restrict__ logits, long ld, unsigned long long* __restrict__ keys, int kstride,
     uint8_t* __restrict__ nan0) {
-  // the chunk's activation parts: [3][16 NT][LMM_RS] bf16
-  __shared__ __align__(16) uint16_t xs[3 * 16 * NT * LMM_RS];
+  // the activation parts of two chunks (this one and the next): [2][3][16 NT][LMM_RS] bf16
+  __shared__ __align__(16) uint16_t xs[2][3 * 16 * NT * LMM_RS];
   __shared__ unsigned long long best_sh[LMM_WAVES][16 * NT];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int m = lane & 15, g = lane >> 4;
@@ -220,56 +328,35 @@ __global__ __launch_bounds__(64 * LMM_WAVES) __attribute__((amdgpu_waves_per_eu(
     wr[t] = W + (size_t)(r < V ? r : V - 1) * n;
   }
   uint32_t bad = 0;  // bit t: this lane's row of tile t holds a non-finite weight
-  for (int k0 = 0; k0 < n; k0 += LMM_KC) {
-    // this chunk's W, every load in flight before the MFMAs (the previous
-    // chunk's MFMAs are done with the LDS once the barrier passes)
-    lm_u32x4 a[LMM_TILES][LMM_KS];
-#pragma unroll
-    for (int t = 0; t < LMM_TILES; t++)
-#pragma unroll
-      for (int s = 0; s < LMM_KS; s++) {
-        const int k = k0 + 32 * s + 8 * g;
-        a[t][s] = k < n ? *reinterpret_cast<const lm_u32x4*>(wr[t] + k) : lm_u32x4{0u, 0u, 0u, 0u};
-      }
-    __syncthreads();
-    for (int i = tid; i < 16 * NT * LMM_KC; i += 64 * LMM_WAVES) {
-      const int b = i / LMM_KC, kk = i - b * LMM_KC;
-      const float x = b < nb && k0 + kk < n ? X[(size_t)b * ldx + k0 + kk] : 0.0f;
-      const uint32_t ux = __float_as_uint(x);
-      const bool fin = (ux & 0x7f800000u) != 0x7f800000u;
-      // (a NaN whose payload sits in the low bits stays a NaN)
-      const uint16_t h0 = fin || !(ux & 0x7fffffu) ? (uint16_t)(ux >> 16) : (uint16_t)0x7fc0u;
-      const float r0 = fin ? x - lm_bf16_f(h0) : 0.0f;  // exact: x's low 16 significand bits
-      const uint16_t h1 = (uint16_t)(__float_as_uint(r0) >> 16);
-      const float r1 = r0 - lm_bf16_f(h1);  // exact: at most 8 significant bits left
-      const uint16_t h2 = (uint16_t)(__float_as_uint(r1) >> 16);
-      xs[(0 * 16 * NT + b) * LMM_RS + kk] = h0;
-      xs[(1 * 16 * NT + b) * LMM_RS + kk] = h1;
-      xs[(2 * 16 * NT + b) * LMM_RS + kk] = h2;
+  if (NT == 1) {
+    // two chunks' weights in registers: the next chunk's loads overlap this
+    // chunk's MFMAs
+    lm_u32x4 a0[LMM_TILES][LMM_KS], a1[LMM_TILES][LMM_KS];
+    {
+      LmX<NT> xr;
+      lm_x_load<NT>(xr, X, ldx, nb, n, 0);
+      lm_w_load(a0, wr, n, 0, g);
+      lm_x_store<NT>(xr, xs[0]);
     }
     __syncthreads();
-#pragma unroll
-    for (int s = 0; s < LMM_KS; s++) {
-      lm_bf16x8 bx[3][NT];
-#pragma unroll
-      for (int p = 0; p < 3; p++)
-#pragma unroll
-        for (int j = 0; j < NT; j++)
-          bx[p][j] = *reinterpret_cast<const lm_bf16x8*>(
-              &xs[(p * 16 * NT + j * 16 + m) * LMM_RS + 32 * s + 8 * g]);
-#pragma unroll
-      for (int t = 0; t < LMM_TILES; t++) {
-        bad |= lm_nonfinite8(a[t][s]) ? 1u << t : 0u;
-        const lm_bf16x8 av = __builtin_bit_cast(lm_bf16x8, a[t][s]);
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-          // the largest part first: the small ones add to an accumulator of
-          // the product's own size
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[2][j], acc[t][j], 0, 0, 0);
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[1][j], acc[t][j], 0, 0, 0);
-          acc[t][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bx[0][j], acc[t][j], 0, 0, 0);
-        }
-      }
+    for (int k0 = 0; k0 < n; k0 += 2 * LMM_KC) {
+      lm_step<NT>(k0, n, X, ldx, nb, wr, a0, a1, xs[0], xs[1], acc, bad, m, g);
+      if (k0 + LMM_KC >= n) break;
+      lm_step<NT>(k0 + LMM_KC, n, X, ldx, nb, wr, a1, a0, xs[1], xs[0], acc, bad, m, g);
+    }
+  } else {
+    // 32 batch rows: one chunk's weights in registers (two would spill at
+    // two workgroups per CU), every load of a chunk in flight before its
+    // MFMAs
+    for (int k0 = 0; k0 < n; k0 += LMM_KC) {
+      lm_u32x4 a[LMM_TILES][LMM_KS];
+      LmX<NT> xr;
+      lm_x_load<NT>(xr, X, ldx, nb, n, k0);
+      lm_w_load(a, wr, n, k0, g);
+      __syncthreads();  // the previous chunk's MFMAs are done with the LDS
+      lm_x_store<NT>(xr, xs[0]);
+      __syncthreads();
+      lm_mfma<NT>(a, xs[0], acc, bad, m, g);
     }
   }
   // rows with a non-finite weight: fp32 fused multiply-adds over k (lanes),
@@ -341,7 +428,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) __attribute__((amdgpu_waves_per_eu(
     if (tid < 16 * NT && tid < nb) {
       unsigned long long mx = best_sh[0][tid];
       for (int i = 1; i < LMM_WAVES; i++) mx = best_sh[i][tid] > mx ? best_sh[i][tid] : mx;
-      if (mx) atomicMax(&keys[tid], mx);
+      if (mx) atomicMax(&keys[(size_t)(blockIdx.x % LMM_SLOTS) * kstride + tid], mx);
     }
   }
 }
@@ -351,17 +438,24 @@ int launch_mfma(pz_sampler* s, const uint16_t* d_w, int V, int n, const float* x
                 int nb, float* out, long ld, unsigned long long* keys, uint8_t* nan0) {
   const int grid = (V + LMM_ROWS - 1) / LMM_ROWS;
   hipLaunchKernelGGL((k_lmhead_mfma<NT, MODE>), dim3(grid), dim3(64 * LMM_WAVES), 0, s->stream,
-                     d_w, V, n, x, ldx, nb, out, ld, keys, nan0);
+                     d_w, V, n, x, ldx, nb, out, ld, keys, s->max_batch, nan0);
   PZ_HIP(s, hipGetLastError());
   return PZ_OK;
 }
 
-// Keys to ids (argmax.c:3-13); clears the keys for the next call.
-__global__ void k_lmhead_finish(int B, unsigned long long* keys, const uint8_t* nan0,
+// Keys to ids (argmax.c:3-13); clears the keys for the next call.  The
+// matrix-core kernel spreads each row's key over LMM_SLOTS slots (stride
+// kstride); the others use slot 0 only (the rest stay zero).
+__global__ void k_lmhead_finish(int B, unsigned long long* keys, int kstride, const uint8_t* nan0,
                                 int32_t* ids) {
   const int b = blockIdx.x * blockDim.x + threadIdx.x;
   if (b >= B) return;
-  const unsigned long long k = keys[b];
+  unsigned long long k = 0ull;
+  for (int sl = 0; sl < LMM_SLOTS; sl++) {
+    const unsigned long long o = keys[(size_t)sl * kstride + b];
+    k = o > k ? o : k;
+    if (sl) keys[(size_t)sl * kstride + b] = 0ull;
+  }
   // logit 0 NaN: argmax.c returns 0; no key at all means every logit was NaN,
   // logit 0 among them
   ids[b] = nan0[b] || !k ? 0 : (int32_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
@@ -461,7 +555,7 @@ extern "C" int pz_lm_head_argmax_bf16(pz_sampler* s, const uint16_t* d_w, int V,
   const int r = run<1>(s, d_w, V, n, d_x, B, ldx, nullptr, 0);
   if (r != PZ_OK) return r;
   hipLaunchKernelGGL(k_lmhead_finish, dim3((B + 255) / 256), dim3(256), 0, s->stream, B,
-                     s->d_lmh_keys, s->d_lmh_nan, d_ids);
+                     s->d_lmh_keys, s->max_batch, s->d_lmh_nan, d_ids);
   PZ_HIP(s, hipGetLastError());
   return PZ_OK;
 }

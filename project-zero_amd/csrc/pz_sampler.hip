@@ -110,10 +110,11 @@ extern "C" int pz_sampler_create(pz_sampler** out, int max_batch, int max_vocab,
       hipMalloc((void**)&s->d_rows, B * sizeof(int32_t)) != hipSuccess ||
       hipMalloc((void**)&s->d_u_step, B * sizeof(float)) != hipSuccess ||
       hipMalloc((void**)&s->d_eos, PZ_MAX_EOS * sizeof(int32_t)) != hipSuccess ||
-      hipMalloc((void**)&s->d_lmh_keys, B * sizeof(unsigned long long)) != hipSuccess ||
+      hipMalloc((void**)&s->d_lmh_keys, 16 * B * sizeof(unsigned long long)) != hipSuccess ||
       hipMalloc((void**)&s->d_lmh_nan, B) != hipSuccess)
     return bail(PZ_ENOMEM);
-  if (hipMemset(s->d_lmh_keys, 0, B * sizeof(unsigned long long)) != hipSuccess)
+  // the fused LM head's argmax keys: 16 slots per row (zero between calls)
+  if (hipMemset(s->d_lmh_keys, 0, 16 * B * sizeof(unsigned long long)) != hipSuccess)
     return bail(PZ_EDEVICE);
   s->res_params = new (std::nothrow) pz_row_params_dev[B];
   if (!s->res_params) return bail(PZ_ENOMEM);
