@@ -13,8 +13,14 @@
 // segment by serial fp32 adds, every later one through the integer state --
 // a segment with at most one binade exit and no tie in one step
 // (pz_sp_fast), else one ballot per event over the segment's increment
-// prefix, each taken with one exact add (pz_sp_events).  Longer rows use
-// the one-workgroup-per-row softmax (pz_softmax.hip).
+// prefix, each taken with one exact add (pz_sp_events).  Rows of more than
+// ATTN_WAVE_SHORT scores (and up to ATTN_ROW_MAX) take one 1024-thread
+// workgroup each instead (k_attn_row): its 16 waves estimate every 256-score
+// segment's mass, predict the binade the running sum sits in at each
+// segment, record the segments' integer increment sums there in LDS, and
+// pre-evaluate the segments the records cannot serve while wave 0 walks the
+// row (pz_split.h) -- the serial work left is one step per segment.  Longer
+// rows use the one-workgroup-per-row softmax (pz_softmax.hip).
 #include <hip/hip_runtime.h>
 
 #include "../../include/pz_sampler.h"
@@ -27,6 +33,9 @@ namespace {
 
 constexpr int ATTN_WAVES = 4;               // rows per workgroup
 constexpr int ATTN_WAVE_MAX = 16 * 256;     // longest row of the wave kernel
+#ifndef ATTN_WAVE_SHORT
+#define ATTN_WAVE_SHORT 1024                // longer rows: one workgroup each
+#endif
 
 // One 256-term segment added to the running sum st (the whole wave, lane l
 // holding terms 4l .. 4l+3): serial fp32 adds from a zero sum, else the
@@ -146,6 +155,203 @@ int launch_wave(pz_sampler* s, const float* d_in, long ld_in, float* d_out, long
   return PZ_OK;
 }
 
+
+// ---- one workgroup per row ----------------------------------------------------
+constexpr int AR_BLOCK = 1024;
+constexpr int AR_WAVES = AR_BLOCK / 64;
+constexpr int ATTN_ROW_MAX = 128 * 256;  // longest row of k_attn_row (128 segments)
+
+// Row r's scores as the walk reads them: V = the row's valid length.
+struct AttnRow {
+  const float* x;
+  int V;
+  bool vec;
+  __device__ __forceinline__ int load(int e0, float (&y)[4]) const {
+    return vec ? pz_load4<true, false>(x, V, e0, y) : pz_load4<false, false>(x, V, e0, y);
+  }
+  __device__ __forceinline__ void apply(int, int, float (&)[4]) const {}
+  __device__ __forceinline__ int get(int e0, float (&y)[4]) const { return load(e0, y); }
+};
+
+struct AttnShared {
+  float est[128];
+  float red[AR_WAVES];
+  uint32_t bad[AR_WAVES];
+  float carry;
+  float sum;
+};
+
+template <bool VEC_IN, bool VEC_OUT>
+__global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_in, float* out,
+                                                      long ld_out, int n_rows, int n,
+                                                      const int32_t* lens, int nc) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ AttnShared A;
+  __shared__ uint64_t etab[32];
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int row = blockIdx.x;
+  int len = lens ? lens[row] : n;
+  len = len < n ? len : n;
+  if (len <= 0) return;  // softmax.c with size 0 writes nothing (every thread)
+  const int nseg = (len + 255) >> 8;
+  AttnRow R;
+  R.x = in + (size_t)row * ld_in;
+  R.V = len;
+  R.vec = VEC_IN;
+  float* o = out + (size_t)row * ld_out;
+  // 1. the maximum and the NaN check (segments w, w + 16, ...)
+  float m = -__builtin_inff();
+  bool nan = false;
+  for (int k = w; k < nseg; k += AR_WAVES) {
+    float y[4];
+    const int c0 = R.load(k * PZ_SP_SEG + 4 * lane, y);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      if (c >= c0) continue;
+      nan |= y[c] != y[c];
+      m = fmaxf(m, y[c]);
+    }
+  }
+  m = pz_wave_max(m);
+  const bool wnan = __ballot(nan) != 0ull;
+  if (lane == 0) {
+    A.red[w] = m;
+    A.bad[w] = wnan ? 1u : 0u;
+  }
+  __syncthreads();
+  float M = -__builtin_inff();
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < AR_WAVES; i++) {
+    M = fmaxf(M, A.red[i]);
+    bad |= A.bad[i] != 0u;
+  }
+  // softmax.c:6-9: a NaN anywhere, or an infinite maximum, makes every
+  // output NaN (as k_attn_wave)
+  if (bad || !(M > -__builtin_inff() && M < __builtin_inff())) {
+    for (int i = tid; i < len; i += AR_BLOCK) o[i] = __builtin_nanf("");
+    return;
+  }
+  // 2. each segment's estimated mass (hardware exp)
+  for (int k = w; k < nseg; k += AR_WAVES) {
+    float y[4];
+    const int c0 = R.load(k * PZ_SP_SEG + 4 * lane, y);
+    float t = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      if (c < c0) t += pz_fast_exp(y[c] - M);
+    t = pz_wave_sum(t);
+    if (lane == 0) A.est[k] = t;
+  }
+  __syncthreads();
+  // 3. the predicted grid of each segment: the binade of the estimated
+  // running sum at its start (and whether the segment leaves it)
+  PzWalk W = pz_sp_walk_layout(lds, nseg, nc);
+  if (w == 0) {
+    float carry = 0.0f;
+    for (int c0 = 0; c0 < nseg; c0 += 64) {
+      const int k = c0 + lane;
+      const float e = k < nseg ? A.est[k] : 0.0f;
+      const float incl = pz_wave_scan_f32(e);
+      const float start = carry + (incl - e), end = carry + incl;
+      if (k < nseg)
+        W.gf[k] = pz_predict_gf(start) | (pz_grid_of(end) != pz_grid_of(start) ? PZ_GF_XING : 0u);
+      carry += pz_readlane_f32(incl, 63);
+    }
+  }
+  __syncthreads();
+  // 4. records at the predicted grids, in LDS (segments predicted to cross
+  // a binade are specials: no record)
+  PzExpTerms<AttnRow> X;
+  X.R = R;
+  X.M = M;
+  X.thr = -__builtin_inff();
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = (const pz_lds_u64*)etab;
+  for (int k = w; k < nseg; k += AR_WAVES) {
+    const uint32_t gf = W.gf[k];
+    if (gf & PZ_GF_XING) {
+      if (lane == 0) {
+        W.d[k] = 0u;
+        W.d2[k] = 0u;
+      }
+      continue;
+    }
+    float raw[4], a[4];
+    const int e0 = k * PZ_SP_SEG + 4 * lane;
+    const int c0 = X.load(e0, raw);
+    X.prep(e0, c0, raw, a);
+    const uint32_t g = gf & 0xffu;
+    const bool has2 = (gf & PZ_GF_HAS2) != 0;
+    uint32_t s1 = 0, s2 = 0;
+    bool d1 = false, d2 = false;
+    X.inc4(raw, a, g, s1, d1);
+    if (has2) {
+      X.inc4(raw, a, g - 1u, s2, d2);
+      s2 = pz_wave_sum_u32(s2);
+    }
+    s1 = pz_wave_sum_u32(s1);
+    const bool D1 = __ballot(d1) != 0;
+    const bool D2 = has2 && __ballot(d2) != 0;
+    if (lane == 0) {
+      W.d[k] = s1;
+      W.d2[k] = s2;
+      W.gf[k] = (gf & (0xffu | PZ_GF_HAS2 | PZ_GF_XING)) | (D1 ? PZ_GF_DIRTY : 0u) |
+                (D2 ? PZ_GF_DIRTY2 : 0u);
+    }
+  }
+  __syncthreads();
+  // 5. the walk: wave 0, waves 1..15 pre-evaluating its specials
+  W = pz_sp_walk_start(X, W, SS);
+  if (w == 0) {
+    PzAcc st;
+    pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+    if (lane == 0) A.sum = pz_acc_value(st);
+  }
+  __syncthreads();
+  // 6. p = e * (1 / sum) (softmax.c:19-22), every exact term again
+  const float inv = 1.0f / A.sum;
+  for (int k = w; k < nseg; k += AR_WAVES) {
+    float v[4];
+    X.seg(k, v);
+    const int i0 = k * PZ_SP_SEG + 4 * lane;
+    if (VEC_OUT && i0 + 3 < len) {
+      pz_f4 q;
+      q.x = v[0] * inv;
+      q.y = v[1] * inv;
+      q.z = v[2] * inv;
+      q.w = v[3] * inv;
+      *reinterpret_cast<pz_f4*>(o + i0) = q;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        if (i0 + c < len) o[i0 + c] = v[c] * inv;
+    }
+  }
+}
+
+int launch_row(pz_sampler* s, const float* d_in, long ld_in, float* d_out, long ld_out,
+               int n_rows, int n, const int32_t* d_len) {
+  const int nseg = (n + 255) / 256;
+  const size_t fixed = sizeof(PzSpShared) + sizeof(AttnShared) + 512;
+  const int nc = pz_sp_walk_nc(nseg, (size_t)s->max_lds - fixed);
+  if (nc < 2) return -2;
+  const size_t lds = pz_sp_walk_lds(nseg, nc);
+  const bool vi = (ld_in % 4 == 0) && (((uintptr_t)d_in & 15) == 0);
+  const bool vo = (ld_out % 4 == 0) && (((uintptr_t)d_out & 15) == 0);
+  auto k = vi ? (vo ? k_attn_row<true, true> : k_attn_row<true, false>)
+              : (vo ? k_attn_row<false, true> : k_attn_row<false, false>);
+  if (lds > 65536 && hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(k, dim3(n_rows), dim3(AR_BLOCK), lds, s->stream, d_in, ld_in, d_out, ld_out,
+                     n_rows, n, d_len, nc);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 }  // namespace
 
 extern "C" int pz_attn_softmax(pz_sampler* s, const float* d_in, long ld_in, float* d_out,
@@ -155,6 +361,11 @@ extern "C" int pz_attn_softmax(pz_sampler* s, const float* d_in, long ld_in, flo
     return fail(s, PZ_EINVAL, "bad attention softmax shape");
   if (n_rows == 0 || n == 0) return PZ_OK;
   PZ_HIP(s, hipSetDevice(s->device));
+  if (n > ATTN_WAVE_SHORT && n <= ATTN_ROW_MAX) {
+    const int rc = launch_row(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len);
+    if (rc == 0) return PZ_OK;
+    if (rc != -2) return fail(s, PZ_EDEVICE, "attention softmax launch failed");
+  }
   if (n > ATTN_WAVE_MAX) {
     PzTemp one;  // scores are softmaxed as they are: x * 1.0f == x
     one.t = 1.0f;

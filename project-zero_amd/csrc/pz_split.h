@@ -933,21 +933,8 @@ __device__ __forceinline__ void pz_sp_prep(const float (&v)[4], uint32_t g0, uin
   inf.tc = pz_wave_sum_u32(corr);
 }
 
-// Stages the row's records in LDS, lists every special segment (dirty,
-// crossing, or without a record) in id order, and starts the pre-evaluation
-// of the specials into the ring: exact terms (X::seg) and increment
-// prefixes and flags at the record's grid and the grid the segment is
-// expected to end in.  Every thread calls it; it returns without a final
-// barrier: waves 1 .. n_producers keep filling the ring while the walker
-// (wave 0) consumes it (pz_sp_load_slot), the other waves may go on to other
-// work.  Any block size that is a multiple of 64, up to 1024.
-template <class X>
-__device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg, int nc,
-                                                   const PzSplitWs& ws, char* lds,
-                                                   PzSpShared& S, int n_producers = -1) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int nt = (int)blockDim.x, nw = nt >> 6;
-  if (n_producers < 0) n_producers = nw - 1;
+// The walk's LDS layout for nseg segments and nc ring slots at lds.
+__device__ __forceinline__ PzWalk pz_sp_walk_layout(char* lds, int nseg, int nc) {
   PzWalk W;
   W.nseg = nseg;
   W.nc = nc;
@@ -971,9 +958,20 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   W.pd = (pz_lds_u32*)p;       p += (size_t)(nseg + 1) * 4;
   W.chp = (pz_lds_u32*)p;      p += (size_t)(nseg + 1) * 4;
   W.spk = (pz_lds_i32*)p;
-  const uint32_t* rd = pz_sp_rec_d(ws, row);
-  const uint32_t* rd2 = pz_sp_rec_d2(ws, row);
-  const uint32_t* rgf = pz_sp_rec_gf(ws, row);
+  W.n_spec = 0;
+  return W;
+}
+
+// The second half of the set-up for records already in LDS (W.d, W.d2,
+// W.gf of a layout from pz_sp_walk_layout, written before a barrier):
+// prefixes, the special list, the ring and its producers.
+template <class X>
+__device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpShared& S,
+                                                   int n_producers = -1) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int nt = (int)blockDim.x, nw = nt >> 6;
+  if (n_producers < 0) n_producers = nw - 1;
+  const int nseg = W.nseg, nc = W.nc;
   // records, their prefix, the grid changes between clean neighbours, and
   // the special segments in id order
   uint32_t base = 0;  // prefix carried over the chunks (thread-uniform)
@@ -983,12 +981,9 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     const int k = c0 + tid;
     uint32_t d = 0, gf = PZ_NO_RECORD, gfp = PZ_NO_RECORD;
     if (k < nseg) {
-      d = rd[k];
-      gf = rgf[k];
-      if (k > 0) gfp = rgf[k - 1];
-      W.d[k] = d;
-      W.d2[k] = rd2[k];
-      W.gf[k] = gf;
+      d = W.d[k];
+      gf = W.gf[k];
+      if (k > 0) gfp = W.gf[k - 1];
     }
     const bool special = k < nseg && !pz_sp_clean(gf);
     const bool chg = k < nseg && pz_sp_clean(gf) && pz_sp_clean(gfp) && ((gf ^ gfp) & 0xffu) != 0u;
@@ -1098,6 +1093,31 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
                          __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   return W;
+}
+
+// Stages the row's records in LDS, lists every special segment (dirty,
+// crossing, or without a record) in id order, and starts the pre-evaluation
+// of the specials into the ring: exact terms (X::seg) and increment
+// prefixes and flags at the record's grid and the grid the segment is
+// expected to end in.  Every thread calls it; it returns without a final
+// barrier: waves 1 .. n_producers keep filling the ring while the walker
+// (wave 0) consumes it (pz_sp_load_slot), the other waves may go on to other
+// work.  Any block size that is a multiple of 64, up to 1024.
+template <class X>
+__device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg, int nc,
+                                                   const PzSplitWs& ws, char* lds,
+                                                   PzSpShared& S, int n_producers = -1) {
+  PzWalk W = pz_sp_walk_layout(lds, nseg, nc);
+  const uint32_t* rd = pz_sp_rec_d(ws, row);
+  const uint32_t* rd2 = pz_sp_rec_d2(ws, row);
+  const uint32_t* rgf = pz_sp_rec_gf(ws, row);
+  for (int k = threadIdx.x; k < nseg; k += blockDim.x) {
+    W.d[k] = rd[k];
+    W.d2[k] = rd2[k];
+    W.gf[k] = rgf[k];
+  }
+  __syncthreads();
+  return pz_sp_walk_start(x, W, S, n_producers);
 }
 
 // Sequential fp32 accumulation of the segment's terms from position start,
