@@ -87,6 +87,8 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--sweep", default="all",
                     help="comma-separated sweep kinds (greedy, top_p, categorical) or all")
+    ap.add_argument("--batches", default=None,
+                    help="comma-separated sweep batch sizes (default 1,8,64,256,1024)")
     ap.add_argument("--cpu-seconds", type=float, default=3.0,
                     help="CPU time of each baseline sample (per thread count)")
     return ap.parse_args()
@@ -159,6 +161,44 @@ class Cpu:
         return {"rows": int(B), "boundary_rows": int(bnd.sum()),
                 "mismatches_nonboundary": int((bad & ~bnd).sum()),
                 "mismatches_boundary": int((bad & bnd).sum())}
+
+    def ref_baseline(self, x, params, draw_seed, gpu_ids, budget):
+        """The reference's own sampler (oracle/_ref: src/sampling/*.c
+        compiled from their sources) on rows that are exactly one reference
+        call -- apply_temperature + sample_top_p, each row's RNG state seeded
+        as the workload's uniforms were (so it draws the same u) -- timed on
+        one thread over a bounded sample; its ids are compared with the
+        GPU's.  None when the reference build is absent."""
+        import ctypes
+        import numpy as np
+        po = self.po
+        ref = po.ref(self.avx512) if po is not None else None
+        if ref is None or len(params) != 1 or params[0].top_k > 0:
+            return None
+        p = params[0]
+        if not (0.0 < p.top_p < 1.0) or p.temperature < 1e-6 or p.rep_penalty != 1.0 or \
+                p.presence_penalty != 0.0 or p.frequency_penalty != 0.0:
+            return None
+        B, V = x.shape
+        work = np.empty(V, np.float32)
+        st = ctypes.c_ulonglong(0)
+        ids = []
+        t0 = time.perf_counter()
+        rows = 0
+        while rows < B and (rows < 4 or time.perf_counter() - t0 < budget):
+            work[:] = x[rows]
+            ref.rng_seed(ctypes.byref(st), (int(draw_seed) ^ (rows + 1)) & ((1 << 64) - 1))
+            ref.apply_temperature(work.ctypes.data, V, float(p.temperature))
+            ids.append(ref.sample_top_p(work.ctypes.data, V, float(p.top_p), ctypes.byref(st)))
+            rows += 1
+        dt = time.perf_counter() - t0
+        match = int((np.array(ids) == np.asarray(gpu_ids[:rows])).sum())
+        return {"value": rows / dt, "unit": "rows/s", "cores": 1, "kind": "reference",
+                "sample": f"the first {rows} of {B} rows ({dt:.1f} s): apply_temperature + "
+                          "sample_top_p per row, row copied first (temperature works in place)",
+                "build": "gcc -std=c99 -O3 -march=x86-64-v4 (or -v3 without AVX-512) of the "
+                         "reference's src/sampling/*.c and src/math/softmax.c (oracle/Makefile ref)",
+                "ids_equal_to_gpu": f"{match} of {rows}"}
 
     def baseline(self, x, params, u, hist, budget, unit="rows/s"):
         """Rows/s of the oracle on a bounded sample of the batch: one
@@ -294,6 +334,12 @@ def run_batched(args, torch, cpu, name):
         r["parity"] = cpu.parity(w0["logits"], params, w0["u"], w0["hist"], ids0)
         r["cpu_baseline"], r["cpu_baseline_ncore"] = cpu.baseline(
             w0["logits"], params, w0["u"], w0["hist"], args.cpu_seconds)
+        if "draw_seed" in w0:
+            rb = cpu.ref_baseline(w0["logits"], params, w0["draw_seed"], ids0, args.cpu_seconds)
+            if rb is not None:
+                # the reference's own code is the baseline where one call is the chain
+                r["cpu_baseline_port"] = r["cpu_baseline"]
+                r["cpu_baseline"] = rb
     del t_x, t_h, t_u
     torch.cuda.empty_cache()
     return r
@@ -465,7 +511,7 @@ def run_sweep(args, torch, cpu):
         t_ids = torch.empty(P, dtype=torch.int32, device=dev)
         torch.cuda.synchronize()
         params = w["params"]
-        for B in SWEEP_B:
+        for B in (SWEEP_B if not args.batches else [int(b) for b in args.batches.split(",")]):
             s = pz.Sampler(B, V, max_hist=max(H, 1), temp_mode=cpu.temp_mode())
             steps = 100 if B <= 64 else (40 if B <= 256 else 20)
             dx = t_x.data_ptr()

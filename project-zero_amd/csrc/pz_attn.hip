@@ -181,7 +181,10 @@ struct AttnShared {
   float sum;
 };
 
-template <bool VEC_IN, bool VEC_OUT>
+// NSW: segments per wave (rows of up to 16 NSW segments); each wave holds
+// its segments' scores (segments w, w + 16, ...) in registers through the
+// records, and reads them once more for the probabilities.
+template <int NSW, bool VEC_IN, bool VEC_OUT>
 __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_in, float* out,
                                                       long ld_out, int n_rows, int n,
                                                       const int32_t* lens, int nc) {
@@ -201,19 +204,25 @@ __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_
   R.V = len;
   R.vec = VEC_IN;
   float* o = out + (size_t)row * ld_out;
-  // 1. the maximum and the NaN check (segments w, w + 16, ...)
+  // 1. the wave's segments into registers (every load in flight at once),
+  // the maximum and the NaN check
+  float y[NSW][4];
+  int cnt[NSW];
+#pragma unroll
+  for (int j = 0; j < NSW; j++) {
+    const int k = w + AR_WAVES * j;
+    cnt[j] = k < nseg ? R.load(k * PZ_SP_SEG + 4 * lane, y[j]) : 0;
+  }
   float m = -__builtin_inff();
   bool nan = false;
-  for (int k = w; k < nseg; k += AR_WAVES) {
-    float y[4];
-    const int c0 = R.load(k * PZ_SP_SEG + 4 * lane, y);
+#pragma unroll
+  for (int j = 0; j < NSW; j++)
 #pragma unroll
     for (int c = 0; c < 4; c++) {
-      if (c >= c0) continue;
-      nan |= y[c] != y[c];
-      m = fmaxf(m, y[c]);
+      if (c >= cnt[j]) continue;
+      nan |= y[j][c] != y[j][c];
+      m = fmaxf(m, y[j][c]);
     }
-  }
   m = pz_wave_max(m);
   const bool wnan = __ballot(nan) != 0ull;
   if (lane == 0) {
@@ -235,13 +244,14 @@ __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_
     return;
   }
   // 2. each segment's estimated mass (hardware exp)
-  for (int k = w; k < nseg; k += AR_WAVES) {
-    float y[4];
-    const int c0 = R.load(k * PZ_SP_SEG + 4 * lane, y);
+#pragma unroll
+  for (int j = 0; j < NSW; j++) {
+    const int k = w + AR_WAVES * j;
+    if (k >= nseg) break;
     float t = 0.0f;
 #pragma unroll
     for (int c = 0; c < 4; c++)
-      if (c < c0) t += pz_fast_exp(y[c] - M);
+      if (c < cnt[j]) t += pz_fast_exp(y[j][c] - M);
     t = pz_wave_sum(t);
     if (lane == 0) A.est[k] = t;
   }
@@ -271,7 +281,10 @@ __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_
   X.inv = 1.0f;
   X.as_p = false;
   X.et = (const pz_lds_u64*)etab;
-  for (int k = w; k < nseg; k += AR_WAVES) {
+#pragma unroll
+  for (int j = 0; j < NSW; j++) {
+    const int k = w + AR_WAVES * j;
+    if (k >= nseg) break;
     const uint32_t gf = W.gf[k];
     if (gf & PZ_GF_XING) {
       if (lane == 0) {
@@ -280,10 +293,9 @@ __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_
       }
       continue;
     }
-    float raw[4], a[4];
-    const int e0 = k * PZ_SP_SEG + 4 * lane;
-    const int c0 = X.load(e0, raw);
-    X.prep(e0, c0, raw, a);
+    float raw[4] = {y[j][0], y[j][1], y[j][2], y[j][3]};
+    float a[4];
+    X.prep(k * PZ_SP_SEG + 4 * lane, cnt[j], raw, a);
     const uint32_t g = gf & 0xffu;
     const bool has2 = (gf & PZ_GF_HAS2) != 0;
     uint32_t s1 = 0, s2 = 0;
@@ -312,25 +324,51 @@ __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_
     if (lane == 0) A.sum = pz_acc_value(st);
   }
   __syncthreads();
-  // 6. p = e * (1 / sum) (softmax.c:19-22), every exact term again
+  // 6. p = e * (1 / sum) (softmax.c:19-22), every exact term again: the
+  // scores reloaded (all loads in flight at once; holding them across the
+  // walk would spill)
   const float inv = 1.0f / A.sum;
-  for (int k = w; k < nseg; k += AR_WAVES) {
+#pragma unroll
+  for (int j = 0; j < NSW; j++) {
+    const int k = w + AR_WAVES * j;
+    cnt[j] = k < nseg ? R.load(k * PZ_SP_SEG + 4 * lane, y[j]) : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < NSW; j++) {
+    const int k = w + AR_WAVES * j;
+    if (k >= nseg) break;
     float v[4];
-    X.seg(k, v);
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = c < cnt[j] ? X.exact_term(y[j][c]) * inv : 0.0f;
     const int i0 = k * PZ_SP_SEG + 4 * lane;
     if (VEC_OUT && i0 + 3 < len) {
       pz_f4 q;
-      q.x = v[0] * inv;
-      q.y = v[1] * inv;
-      q.z = v[2] * inv;
-      q.w = v[3] * inv;
+      q.x = v[0];
+      q.y = v[1];
+      q.z = v[2];
+      q.w = v[3];
       *reinterpret_cast<pz_f4*>(o + i0) = q;
     } else {
 #pragma unroll
       for (int c = 0; c < 4; c++)
-        if (i0 + c < len) o[i0 + c] = v[c] * inv;
+        if (i0 + c < len) o[i0 + c] = v[c];
     }
   }
+}
+
+template <int NSW>
+int launch_row_t(pz_sampler* s, const float* d_in, long ld_in, float* d_out, long ld_out,
+                 int n_rows, int n, const int32_t* d_len, int nc, size_t lds) {
+  const bool vi = (ld_in % 4 == 0) && (((uintptr_t)d_in & 15) == 0);
+  const bool vo = (ld_out % 4 == 0) && (((uintptr_t)d_out & 15) == 0);
+  auto k = vi ? (vo ? k_attn_row<NSW, true, true> : k_attn_row<NSW, true, false>)
+              : (vo ? k_attn_row<NSW, false, true> : k_attn_row<NSW, false, false>);
+  if (lds > 65536 && hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         (int)lds) != hipSuccess)
+    return -1;
+  hipLaunchKernelGGL(k, dim3(n_rows), dim3(AR_BLOCK), lds, s->stream, d_in, ld_in, d_out, ld_out,
+                     n_rows, n, d_len, nc);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_row(pz_sampler* s, const float* d_in, long ld_in, float* d_out, long ld_out,
@@ -340,16 +378,11 @@ int launch_row(pz_sampler* s, const float* d_in, long ld_in, float* d_out, long 
   const int nc = pz_sp_walk_nc(nseg, (size_t)s->max_lds - fixed);
   if (nc < 2) return -2;
   const size_t lds = pz_sp_walk_lds(nseg, nc);
-  const bool vi = (ld_in % 4 == 0) && (((uintptr_t)d_in & 15) == 0);
-  const bool vo = (ld_out % 4 == 0) && (((uintptr_t)d_out & 15) == 0);
-  auto k = vi ? (vo ? k_attn_row<true, true> : k_attn_row<true, false>)
-              : (vo ? k_attn_row<false, true> : k_attn_row<false, false>);
-  if (lds > 65536 && hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         (int)lds) != hipSuccess)
-    return -1;
-  hipLaunchKernelGGL(k, dim3(n_rows), dim3(AR_BLOCK), lds, s->stream, d_in, ld_in, d_out, ld_out,
-                     n_rows, n, d_len, nc);
-  return hipGetLastError() == hipSuccess ? 0 : -1;
+  const int nsw = (nseg + AR_WAVES - 1) / AR_WAVES;
+  if (nsw <= 1) return launch_row_t<1>(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len, nc, lds);
+  if (nsw <= 2) return launch_row_t<2>(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len, nc, lds);
+  if (nsw <= 4) return launch_row_t<4>(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len, nc, lds);
+  return launch_row_t<8>(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len, nc, lds);
 }
 
 }  // namespace

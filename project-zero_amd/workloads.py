@@ -43,7 +43,8 @@ def build_c2(B=64, V=128256, seed=None):
     pz.synth_spikes(x, 5, 8.0, 12.0, seed + 1)
     prm = pz.row_params(temperature=0.7, top_p=0.9)
     u = pz.synth_draws(B, _draw_seed(seed))
-    return dict(name="c2", logits=x, params=[prm], u=u, hist=None,
+    # draw_seed: u[b] is rng_float of a state rng_seed(draw_seed ^ (b + 1))
+    return dict(name="c2", logits=x, params=[prm], u=u, hist=None, draw_seed=_draw_seed(seed),
                 bytes_per_row=V * 4 + 4 + 4)
 
 
