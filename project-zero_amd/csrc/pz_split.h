@@ -1073,19 +1073,22 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
       W.spt1[sl] = inf.pt1;
       W.stc[sl] = inf.tc;
     }
-    if (j == 0 && k == 0) {
+    if (j == 0 && k == 0 && lane == 0) {
       // the row's first segment from a zero sum, where nearly every term is
       // an event: its plain sequential fp32 sum, for the walker to take in
-      // one step -- the whole wave in lockstep, each term read out of its
-      // lane's registers in id order (no LDS round trip per term)
+      // one step (one lane, the terms read back in id order; reading them
+      // out of the wave's registers with v_readlane is slower: each add
+      // waits for the scalar register the readlane writes)
+      const pz_lds_f4* tq = (const pz_lds_f4*)(W.terms + sl * PZ_SP_SEG);
       float sum0 = 0.0f;
-      for (int l = 0; l < 64; l++) {
-        sum0 = sum0 + pz_readlane_f32(v[0], l);
-        sum0 = sum0 + pz_readlane_f32(v[1], l);
-        sum0 = sum0 + pz_readlane_f32(v[2], l);
-        sum0 = sum0 + pz_readlane_f32(v[3], l);
+      for (int i = 0; i < PZ_SP_SEG / 4; i++) {
+        const pz_f4 t4 = tq[i];
+        sum0 = sum0 + t4.x;
+        sum0 = sum0 + t4.y;
+        sum0 = sum0 + t4.z;
+        sum0 = sum0 + t4.w;
       }
-      if (lane == 0) *W.s0 = __float_as_uint(sum0);
+      *W.s0 = __float_as_uint(sum0);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0)
