@@ -443,6 +443,15 @@ constexpr int TOPP_STAGE = PZ_SP_SEG / 2;  // keys a 256-term segment of LDS sta
 
 __device__ __forceinline__ uint32_t topp_hword(uint32_t count) { return TOPP_HWRITTEN | count; }
 
+// The row's nucleus-bin selection as one word (rs.i[6], zero between
+// launches): written bit, the lowest bin kept (11 bits; TOPP_SEL_FAILED: a
+// wait gave up) and the candidates in the kept bins (20 bits, saturated:
+// only its comparison with the list capacity matters).
+constexpr uint32_t TOPP_SEL_FAILED = 0x7ffu;
+__device__ __forceinline__ uint32_t topp_sel_word(uint32_t bsel, uint32_t nsel) {
+  return TOPP_HWRITTEN | (bsel << 20) | (nsel < 0xfffffu ? nsel : 0xfffffu);
+}
+
 // Marks the row failed: a wait between its workgroups gave up (read and
 // cleared by the walk launch).
 __device__ __forceinline__ void topp_mark_failed(const PzSplitWs& ws, int row) {
@@ -671,6 +680,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
     if (tid == 0) {
       __hip_atomic_store(&meet[ws.smax + blockIdx.x], 1ull << 63, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+      if (blockIdx.x == S - 1)  // the others wait for its selection
+        __hip_atomic_store(&ws.rs[row].i[6], (int)topp_sel_word(TOPP_SEL_FAILED, 0u),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       topp_mark_failed(ws, row);
     }
     return;
@@ -735,7 +747,23 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   pz_lds_barrier();
   if (fail_sh) {  // (this workgroup's histogram and meet-2 word are posted)
     if (tid == 0) topp_mark_failed(ws, row);
+    if (blockIdx.x == S - 1 && tid == 0)  // the others wait for its selection
+      __hip_atomic_store(&ws.rs[row].i[6], (int)topp_sel_word(TOPP_SEL_FAILED, 0u),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
+  }
+  // 4. the nucleus bins: the last slice merges the row's histograms (every
+  // one is posted, bin by bin, before its workgroup's meet-2 word, so the
+  // polls end at once) and posts the selection for the others, which take
+  // it after their records -- one workgroup per row reads the S histograms
+  ToppSel sel;
+  if (blockIdx.x == S - 1) {
+    sel = topp_front_select(hrow, S, cap, ehist, prm.top_p, &sel_sh, part_sh, &fail_sh);
+    if (tid == 0)
+      __hip_atomic_store(&ws.rs[row].i[6],
+                         (int)topp_sel_word(sel.bsel < 0 ? TOPP_SEL_FAILED : (uint32_t)sel.bsel,
+                                            sel.nsel),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   pz_sp_predict(ToppSliceEst{sest, sl.k0}, SS.carry, row, sl, ws, SS, (pz_lds_u32*)sgf);
   // 3. records from LDS (as k_topp_rec)
@@ -749,10 +777,22 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   X.as_p = false;
   X.et = et;
   pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)sgf, true);
-  // 4. the nucleus bins (the row's histograms were published before meet 2)
-  pz_lds_barrier();
-  const ToppSel sel =
-      topp_front_select(hrow, S, cap, ehist, prm.top_p, &sel_sh, part_sh, &fail_sh);
+  if (blockIdx.x != S - 1) {
+    if (tid == 0) {
+      uint32_t v = 0;
+      for (uint32_t t = 1;; t++) {
+        v = (uint32_t)__hip_atomic_load(&ws.rs[row].i[6], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+        if ((v & TOPP_HWRITTEN) || t >= cap) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      const uint32_t b = (v >> 20) & 0x7ffu;
+      sel_sh.bsel = !(v & TOPP_HWRITTEN) || b == TOPP_SEL_FAILED ? -1 : (int)b;
+      sel_sh.nsel = v & 0xfffffu;
+    }
+    pz_lds_barrier();
+    sel = sel_sh;
+  }
   if (sel.bsel < 0) {
     if (tid == 0) topp_mark_failed(ws, row);
     return;
@@ -1724,9 +1764,10 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   // row's maxima below
   const PzRowState rs0 = ws.rs[row];
   if (tid == 0) {
-    // the gathered count, re-armed for the next call
+    // the gathered count, re-armed for the next call, and the selection word
     m_sh = (int)ws.arrive[row];
     ws.arrive[row] = 0u;
+    ws.rs[row].i[6] = 0;
     sb_ctr = 0;
     path_sh = 0;
   }
