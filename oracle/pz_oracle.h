@@ -134,7 +134,9 @@ void orc_sample_step(const float *x, int rows, int n, long ld,
 
 /* ---- a11: speculative verification (build-defined) ---------------------
  * target [B, K+has_bonus, n], draft [B, K, n] logits; draft_ids [B, K];
- * u_acc [B, K]; u_res [B].  Outputs acc_len[B] and out_ids[B, K+1]
+ * u_acc [B, K]; u_res [B].  draft == NULL: greedy drafts, q one-hot at each
+ * draft id (accept iff u < p(d); residual max(0, p - [i == d])).
+ * Outputs acc_len[B] and out_ids[B, K+1]
  * (accepted drafts, then the resampled or bonus token; -1 pads).
  * dist[B] receives the minimum boundary distance over the tests taken. */
 void orc_spec_verify(const float *target, const float *draft, int B, int K,

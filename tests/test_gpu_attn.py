@@ -75,7 +75,8 @@ def run(torch, x, lens=None, ld_out=None, in_place=False, label=""):
         assert (d_o.cpu().numpy()[:, n:] == SENTINEL).all()
 
 
-@pytest.mark.parametrize("ctx", [1, 7, 128, 255, 256, 257, 1000, 2048, 4096, 4097, 32768])
+@pytest.mark.parametrize("ctx", [1, 7, 128, 255, 256, 257, 1000, 1024, 1025, 2048, 4096, 4097,
+                                 32768, 32769])
 def test_heads_by_context(torch_cuda, ctx):
     print(f"case attn heads={HEADS} ctx={ctx}", flush=True)
     run(torch_cuda, scores(HEADS, ctx, 0xA0 + ctx), label=f"ctx{ctx}")
@@ -101,11 +102,12 @@ def test_in_place_and_padded_output(torch_cuda, n):
     run(torch_cuda, x, ld_out=n + 3, label=f"padded{n}")  # misaligned output rows
 
 
-def test_special_values(torch_cuda):
+@pytest.mark.parametrize("n", [700, 5000])
+def test_special_values(torch_cuda, n):
     """NaN first / later, +inf, all -inf, -inf entries, ties, tiny and huge
-    spreads (sums that leave and re-enter binades)."""
-    n = 700
-    x = scores(16, n, 0xD0)
+    spreads (sums that leave and re-enter binades); rows of one wave (700)
+    and of one workgroup (5000)."""
+    x = scores(16, n, 0xD0 + n)
     x[0, 0] = np.nan
     x[1, 99] = np.nan
     x[2, 5] = np.inf
@@ -119,5 +121,5 @@ def test_special_values(torch_cuda):
     x[10, :] = -80.0 + x[10, :] * 1e-3
     x[11, 10] = -0.0
     x[11, 11] = 0.0
-    print("case attn special", flush=True)
-    run(torch_cuda, x, label="special")
+    print(f"case attn special n={n}", flush=True)
+    run(torch_cuda, x, label=f"special{n}")
