@@ -727,6 +727,8 @@ typedef uint32_t pz_u4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pz_u4 pz_lds_u4;
 typedef __attribute__((address_space(3))) uint8_t pz_lds_u8;
 
+constexpr uint32_t PZ_WALK_DONE = 0xffffffffu;  // consumed: the walk is over
+
 struct PzWalk {
   pz_lds_u32* d;      // [nseg] increments at the record's grid
   pz_lds_u32* d2;     // [nseg] increments at the grid below (HAS2)
@@ -749,7 +751,8 @@ struct PzWalk {
   pz_lds_u32* spt1;   // [nc] pa at the first tie
   pz_lds_u32* stc;    // [nc] parity corrections of the later ties at g0
   pz_lds_u32* rdy;    // [nc] special + 1 held by the slot (0: none yet)
-  pz_lds_u32* consumed;  // specials the walker has read out of the ring
+  pz_lds_u32* consumed;  // specials the walker has read out of the ring (PZ_WALK_DONE:
+                         // the walk is over, the producers stop)
   pz_lds_u32* s0;     // the sequential fp32 sum of segment 0's terms from 0 (bits), when
                       // segment 0 is special 0 (else 0xffffffff)
   pz_lds_f32* tmp;    // [256] terms of a segment evaluated during the walk
@@ -1034,11 +1037,18 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
   // for the special it needs next; the producer of that special handles its
   // specials in increasing order and waits only until special j - nc is
   // consumed, which it is by then -- so every wait ends.
+  // A walk that stops early (a stop hit) marks itself over
+  // (PZ_WALK_DONE), which ends every producer's wait and loop.
   for (int j = w - 1; w > 0 && w <= n_producers && j < sbase; j += n_producers) {
+    uint32_t c = __hip_atomic_load((uint32_t*)W.consumed, __ATOMIC_ACQUIRE,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
     if (j >= nc)
-      while (__hip_atomic_load((uint32_t*)W.consumed, __ATOMIC_ACQUIRE,
-                               __HIP_MEMORY_SCOPE_WORKGROUP) <= (uint32_t)(j - nc))
+      while (c <= (uint32_t)(j - nc)) {
         __builtin_amdgcn_s_sleep(1);
+        c = __hip_atomic_load((uint32_t*)W.consumed, __ATOMIC_ACQUIRE,
+                              __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+    if (c == PZ_WALK_DONE) break;
     const int k = W.spk[j];
     const int sl = j % nc;
     float v[4];
@@ -1438,14 +1448,28 @@ __device__ __forceinline__ bool pz_sp_slot_ready(const PzWalk& W, int j) {
                            __HIP_MEMORY_SCOPE_WORKGROUP) == (uint32_t)(j + 1);
 }
 
-// The pre-evaluated data of special j (one round of LDS reads), once in the
-// ring (ready: the caller has seen it there).
-__device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int j, PzSpSeg& d,
-                                                bool ready = false) {
+// How many specials from j1 on (slot s1, the next ones in the following
+// slots) are in the ring: lane i reads the ready word of special j1 + i,
+// one LDS round trip for up to nc specials (acquire: their data is read
+// after).  A special seen there stays until the walker has consumed it.
+__device__ __forceinline__ int pz_sp_ready_count(const PzWalk& W, int j1, int s1) {
   const int lane = threadIdx.x & 63;
-  if (!ready)
-    while (!pz_sp_slot_ready(W, j)) __builtin_amdgcn_s_sleep(1);
-  const int s = j % W.nc;
+  bool rdy = false;
+  if (lane < W.nc) {
+    int s = s1 + lane;
+    s = s >= W.nc ? s - W.nc : s;
+    rdy = __hip_atomic_load((uint32_t*)&W.rdy[s], __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_WORKGROUP) == (uint32_t)(j1 + lane + 1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  const uint64_t nb = ~__ballot(rdy);
+  return nb ? (int)__builtin_ctzll(nb) : 64;
+}
+
+// The pre-evaluated data of the special in slot s (one round of LDS reads),
+// once in the ring.
+__device__ __forceinline__ void pz_sp_load_slot_at(const PzWalk& W, int s, PzSpSeg& d) {
+  const int lane = threadIdx.x & 63;
   d.g0 = (uint32_t)W.g0[s];
   d.sinfo = W.sinfo[s];
   d.pt1 = W.spt1[s];
@@ -1458,6 +1482,12 @@ __device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int j, PzSpSeg&
   d.v[0] = q.x; d.v[1] = q.y; d.v[2] = q.z; d.v[3] = q.w;
   d.P[0] = a4.x; d.P[1] = a4.y; d.P[2] = a4.z; d.P[3] = a4.w;
   d.Q[0] = b4.x; d.Q[1] = b4.y; d.Q[2] = b4.z; d.Q[3] = b4.w;
+}
+
+// The same for special j, waiting until it is in the ring.
+__device__ __forceinline__ void pz_sp_load_slot(const PzWalk& W, int j, PzSpSeg& d) {
+  while (!pz_sp_slot_ready(W, j)) __builtin_amdgcn_s_sleep(1);
+  pz_sp_load_slot_at(W, j % W.nc, d);
 }
 
 // Lane i of the walker: the clean run before special j0 + i (its end, the
@@ -1588,12 +1618,14 @@ struct PzWalkCk {
 // from (a record of an earlier walk over the same terms whose sums never
 // met this walk's stop before the point it resumes from), the walk starts at
 // the last recorded state that does not meet the stop -- the sums only grow,
-// so no hit lies before it.
+// so no hit lies before it.  A resumed walk does not read the ring (the
+// earlier walk has released its slots to the producers): it evaluates its
+// specials itself (pz_sp_special).
 template <int MODE, class X>
-__device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr, const X& x,
-                                          PzWalkCk* rec = nullptr,
-                                          const PzWalkCk* from = nullptr) {
+__device__ __forceinline__ int pz_sp_walk_run(PzAcc& st, const PzWalk& W, float thr, const X& x,
+                                              PzWalkCk* rec, const PzWalkCk* from) {
   const int lane = threadIdx.x & 63;
+  const bool ring = from == nullptr;
   st.n = 0;
   st.g = 1;
   const int np = W.n_spec;
@@ -1613,31 +1645,44 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
   }
   int base = j0 & ~63;  // specials of the lanes
   PzRunLanes m = pz_sp_run_lanes(W, base);
+  // (the run lanes settle before the loop's ring loads are issued, so no use
+  // of them waits for those)
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
   PzSpSeg nxt;
-  bool have = false;  // nxt holds special j
+  bool have = false;     // nxt holds special j
+  int ready_to = j0;     // the specials below it are known to be in the ring
+  int slot = j0 % W.nc;  // special j's slot
   for (int j = j0;; j++) {
     if (j - base == 64) {
       base = j;
       m = pz_sp_run_lanes(W, base);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
     }
     const int jl = j - base;
     const int b = __builtin_amdgcn_readlane(m.k, jl);
+    const int slot1 = slot + 1 == W.nc ? 0 : slot + 1;  // special j + 1's slot
     PzSpSeg cur = nxt;
-    if (j < np && !have) pz_sp_load_slot(W, j, cur);
-    // the slots of the specials before j are released to the producers (their
-    // reads are done: special j's data came in with the last step's loads;
-    // special j's slot stays, the serial path reads its terms there), then
-    // the next special's loads, when it is already in the ring, overlap this
-    // step (no fence waits for them).  The producer of special j + 1 needs
-    // consumed > j + 1 - nc, which holds with nc >= 2.
-    if (j < np) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (lane == 0)
-        __hip_atomic_store((uint32_t*)W.consumed, (uint32_t)j, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (ring) {
+      if (j < np && !have) pz_sp_load_slot(W, j, cur);
+      // the slots of the specials before j are released to the producers
+      // (their reads are done: special j's data came in with the last step's
+      // loads; special j's slot stays, the serial path reads its terms
+      // there), then the next special's loads, when it is already in the
+      // ring, overlap this step (no fence waits for them).  The producer of
+      // special j + 1 needs consumed > j + 1 - nc, which holds with nc >= 2.
+      // Which specials are in the ring is read for several at once, again
+      // when the walk gets past them.
+      if (j < np) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0)
+          __hip_atomic_store((uint32_t*)W.consumed, (uint32_t)j, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      if (j + 1 < np && j + 1 >= ready_to)
+        ready_to = j + 1 + pz_sp_ready_count(W, j + 1, slot1);
+      have = j + 1 < np && j + 1 < ready_to;
+      if (have) pz_sp_load_slot_at(W, slot1, nxt);
     }
-    have = j + 1 < np && pz_sp_slot_ready(W, j + 1);
-    if (have) pz_sp_load_slot(W, j + 1, nxt, true);
     if (k < b) {
       const uint32_t D = pz_readlane_u32(m.D, jl), G = pz_readlane_u32(m.G, jl);
       if (G == st.g && D < (1u << 24) - st.n &&
@@ -1664,8 +1709,11 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
         taken = true;
       }
     }
-    if (!taken &&
-        !pz_sp_has2<MODE>(st, pz_readlane_u32(m.gf, jl), pz_readlane_u32(m.d2, jl), thr)) {
+    if (!taken && !ring) {
+      const int r = pz_sp_special<MODE>(st, W, thr, x, b);
+      if (r >= 0) return b * PZ_SP_SEG + r;
+    } else if (!taken &&
+               !pz_sp_has2<MODE>(st, pz_readlane_u32(m.gf, jl), pz_readlane_u32(m.d2, jl), thr)) {
       const uint32_t g0 = cur.g0, si = cur.sinfo;
       if (!(st.g == g0 && pz_sp_fast_pre<MODE>(st, cur, si, cur.pt1, cur.tc, thr))) {
         uint32_t P[4], Q[4];
@@ -1675,11 +1723,12 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
           Q[c] = cur.Q[c];
         }
         const int r = pz_sp_events<MODE>(st, cur.v, g0, P, cur.fa & 15u, si & 0xffu, Q,
-                                         cur.fb & 15u, thr, W.terms + (j % W.nc) * PZ_SP_SEG);
+                                         cur.fb & 15u, thr, W.terms + slot * PZ_SP_SEG);
         if (r >= 0) return b * PZ_SP_SEG + r;
       }
     }
     k = b + 1;
+    slot = slot1;
     if (rec && j < 64) {
       rec->n = lane == j ? st.n : rec->n;
       rec->g = lane == j ? st.g : rec->g;
@@ -1687,6 +1736,24 @@ __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr,
     }
   }
   return -1;
+}
+
+// The walk, then (a walk that reads the ring) the mark that it is over: a
+// walk that stopped early leaves specials its producers would otherwise
+// wait to write, so every producer's wait ends and its loop stops, and the
+// workgroup's next barrier is reached whatever the stop.
+template <int MODE, class X>
+__device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr, const X& x,
+                                          PzWalkCk* rec = nullptr,
+                                          const PzWalkCk* from = nullptr) {
+  const int r = pz_sp_walk_run<MODE>(st, W, thr, x, rec, from);
+  if (from == nullptr) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0)
+      __hip_atomic_store((uint32_t*)W.consumed, PZ_WALK_DONE, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  return r;
 }
 
 #endif

@@ -58,6 +58,24 @@ def test_top_p_one_and_zero_take_the_plain_path(torch_cuda):
         check(torch_cuda, x, [pz.row_params(temperature=0.9, top_p=tp)], u, label=f"top_p={tp}")
 
 
+def test_early_stop_with_many_specials_after(torch_cuda):
+    """Rows whose mass grows geometrically with the id (x_i = i ln2 / 1024:
+    the CDF doubles every 1024 ids) drawn with tiny uniforms: the draw stops
+    about 30 binade crossings before the row's end, more special segments
+    after the stop than the walk's ring holds.  The walk's producers must
+    stop with it (every kernel ends) and the ids match the oracle."""
+    B, V = 4, 128256
+    i = np.arange(V, dtype=np.float64)
+    x = np.empty((B, V), np.float32)
+    x[0] = (i * np.log(2.0) / 1024).astype(np.float32)
+    x[1] = x[0]
+    x[2] = (i * np.log(2.0) / 256).astype(np.float32)
+    x[3] = x[0]
+    u = np.array([2.0 ** -30, 2.0 ** -20, 1e-9, 0.5], np.float32)
+    ids, _ = check(torch_cuda, x, [pz.row_params(temperature=1.0)], u, label="ramps")
+    assert ids[0] < V - 25 * 1024 and ids[2] < V - 25 * 256, ids
+
+
 def test_degenerate_rows(torch_cuda):
     B, V = 7, 3000
     x = pz.synth_normal(B, V, 2.0, 88)

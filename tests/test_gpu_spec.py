@@ -65,6 +65,27 @@ def test_forced_paths(torch_cuda):
     assert acc[0] == K and acc[1] == 0 and acc[2] == 0
 
 
+def test_residual_draw_stops_early_after_many_specials(torch_cuda):
+    """The residual draw resumes from the first walk's recorded states: with
+    p growing geometrically with the id (target x_i = i ln2 / 1024), q
+    concentrated on the low ids (draft = the reversed ramp) and u_res tiny,
+    it stops about 30 binade crossings before the row's end, past the
+    specials the walk's ring still holds.  Both drafts are rejected (low
+    p(d) / q(d)); accepted lengths and tokens match the oracle."""
+    B, K, V = 2, 1, 128256
+    i = np.arange(V, dtype=np.float64)
+    ramp = (i * np.log(2.0) / 1024).astype(np.float32)
+    target = np.stack([ramp, ramp]).reshape(B, K, V).astype(np.float32)
+    target = np.concatenate([target, target], axis=1)  # + the bonus row
+    draft = np.stack([ramp[::-1], ramp[::-1]]).reshape(B, K, V).copy()
+    draft_ids = np.array([[5], [1000]], np.int32)
+    u_acc = np.array([[0.5], [0.5]], np.float32)
+    u_res = np.array([2.0 ** -30, 2.0 ** -22], np.float32)
+    acc, out = run(torch_cuda, target, draft, draft_ids, u_acc, u_res, 1.0, True,
+                   label="early residual stop")
+    assert (acc == 0).all() and (out[:, 0] < V - 20 * 1024).all(), (acc, out)
+
+
 def test_degenerate_rows(torch_cuda):
     B, K, V = 4, 2, 5000
     target = pz.synth_normal(B * (K + 1), V, 2.0, 91).reshape(B, K + 1, V)
