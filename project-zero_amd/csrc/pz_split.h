@@ -1741,7 +1741,9 @@ __device__ __forceinline__ int pz_sp_walk_run(PzAcc& st, const PzWalk& W, float 
 // The walk, then (a walk that reads the ring) the mark that it is over: a
 // walk that stopped early leaves specials its producers would otherwise
 // wait to write, so every producer's wait ends and its loop stops, and the
-// workgroup's next barrier is reached whatever the stop.
+// workgroup's next barrier is reached whatever the stop.  One walk reads
+// the ring per set-up; later walks over the same set-up resume from its
+// recorded states (from).
 template <int MODE, class X>
 __device__ __forceinline__ int pz_sp_walk(PzAcc& st, const PzWalk& W, float thr, const X& x,
                                           PzWalkCk* rec = nullptr,
