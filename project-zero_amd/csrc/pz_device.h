@@ -321,6 +321,17 @@ struct PzTemp {
     return r;
   }
   __device__ __forceinline__ float apply(float x) const { return div ? pz_div(x, t) : x * inv; }
+  // Four values with one choice of form (values past a row's end are
+  // transformed too; callers ignore them).
+  __device__ __forceinline__ void apply4(float (&y)[4]) const {
+    if (div) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) y[c] = pz_div(y[c], t);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++) y[c] = y[c] * inv;
+    }
+  }
 };
 
 // Value the sampling chain sees for raw logit x of id i: penalties (when the

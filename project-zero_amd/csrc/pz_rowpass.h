@@ -76,10 +76,19 @@ struct PzRow {
   __device__ __forceinline__ int load(int e0, float (&y)[4]) const {
     return pz_load4<VEC, false>(x, V, e0, y);
   }
+  // (the history members among the four from one bitmap read, then the
+  // temperature on all four: values past the row's end are ignored by the
+  // callers)
   __device__ __forceinline__ void apply(int e0, int n, float (&y)[4]) const {
+    if (P.active && n > 0) {
+      const uint32_t nib = pz_pen_nibble(P, e0) & ((1u << n) - 1u);
+      if (nib) {
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (c < n) y[c] = pz_transform(P, T, y[c], e0 + c);
+        for (int c = 0; c < 4; c++)
+          if ((nib >> c) & 1u) y[c] = pz_penalize(P, y[c], e0 + c);
+      }
+    }
+    T.apply4(y);
   }
   __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
     const int n = load(e0, y);
@@ -100,9 +109,8 @@ struct PzTempRow {
   }
   __device__ __forceinline__ void apply(int e0, int n, float (&y)[4]) const {
     (void)e0;
-#pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (c < n) y[c] = T.apply(y[c]);
+    (void)n;  // values past the row's end are transformed too and ignored
+    T.apply4(y);
   }
   __device__ __forceinline__ int get(int e0, float (&y)[4]) const {
     const int n = load(e0, y);

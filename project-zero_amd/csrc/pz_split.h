@@ -298,20 +298,26 @@ __device__ __forceinline__ void pz_sp_stat_slice(const Row& R, int row, const Pz
       if (k >= sl.k1) break;
       const int e0 = k * PZ_SP_SEG + 4 * lane;
       R.apply(e0, n[u], y[u]);
+      // (selects, no branches: every element of a segment but the row's last
+      // is valid)
       float m = -__builtin_inff();
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        if (c >= n[u]) continue;
-        if (y[u][c] != y[u][c]) nan = true;
-        else m = fmaxf(m, y[u][c]);
+        const float v = y[u][c];
+        const bool ok = c < n[u];
+        nan |= ok && v != v;
+        m = fmaxf(m, ok && v == v ? v : -__builtin_inff());
       }
       m = pz_wave_max(m);
       if (est) {
         float t = 0.0f;
         if (m > -__builtin_inff() && m < __builtin_inff()) {
 #pragma unroll
-          for (int c = 0; c < 4; c++)  // NaN fails '>'
-            if (c < n[u] && y[u][c] > -__builtin_inff()) t += pz_fast_exp(y[u][c] - m);
+          for (int c = 0; c < 4; c++) {  // NaN fails '>'
+            const float v = y[u][c];
+            const float e = pz_fast_exp(v - m);
+            t += c < n[u] && v > -__builtin_inff() ? e : 0.0f;
+          }
         }
         t = pz_wave_sum(t);
         if (lane == 0) {
@@ -595,9 +601,10 @@ __device__ __forceinline__ bool pz_sp_front(const Row& R, int row, const PzSlice
       float m = -__builtin_inff();
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        if (c >= n[uu]) continue;
-        if (y[uu][c] != y[uu][c]) nan = true;
-        else m = fmaxf(m, y[uu][c]);
+        const float v = y[uu][c];
+        const bool ok = c < n[uu];
+        nan |= ok && v != v;
+        m = fmaxf(m, ok && v == v ? v : -__builtin_inff());
       }
       pz_f4 q;
       q.x = y[uu][0];

@@ -327,9 +327,12 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_est(TOPP_
       R.apply(k * PZ_SP_SEG + 4 * lane, n[u], y[u]);
       float t = 0.0f, mx = -__builtin_inff();
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        if (c < n[u] && y[u][c] >= thr) t += pz_fast_exp(y[u][c] - M);
-        if (c < n[u]) mx = fmaxf(mx, y[u][c]);  // NaN-free maximum (rows with NaN: fmaxf skips it)
+      for (int c = 0; c < 4; c++) {  // (selects)
+        const float v = y[u][c];
+        const bool ok = c < n[u];
+        const float e = pz_fast_exp(v - M);
+        t += ok && v >= thr ? e : 0.0f;
+        mx = fmaxf(mx, ok && v == v ? v : -__builtin_inff());  // NaN-free maximum
       }
       t = pz_wave_sum(t);
       mx = pz_wave_max(mx);
@@ -612,10 +615,11 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       R.apply(e0, n[uu], y[uu]);
       float m = -__builtin_inff();
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        if (c >= n[uu]) continue;
-        if (y[uu][c] != y[uu][c]) nan = true;
-        else m = fmaxf(m, y[uu][c]);
+      for (int c = 0; c < 4; c++) {  // (selects)
+        const float v = y[uu][c];
+        const bool ok = c < n[uu];
+        nan |= ok && v != v;
+        m = fmaxf(m, ok && v == v ? v : -__builtin_inff());
       }
       pz_f4 q;
       q.x = y[uu][0];
