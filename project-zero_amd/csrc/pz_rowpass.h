@@ -454,11 +454,11 @@ struct PzExpTerms {
                                        uint32_t& s, bool& dirty) const {
     uint32_t need = 0;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
+    for (int c = 0; c < 4; c++) {  // (selects: no exec-mask branches per term)
       bool ex;
       const uint32_t i = pz_inc_from_estimate(a[c], y[c] - M, g, &ex);
-      if (ex) need |= 1u << c;
-      else s += i;
+      need |= (ex ? 1u : 0u) << c;
+      s += ex ? 0u : i;
     }
     while (__ballot(need != 0u)) {
       if (need) {
