@@ -270,7 +270,10 @@ def rotation(batch_bytes):
 def roofline(bytes_per_launch, kern_ms, traffic, kernel):
     achieved = bytes_per_launch / (kern_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic, "kernel": kernel,
+            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+            "traffic_source": "profiles/traffic.json (rocprofv3 --pmc DRAM requests of the same "
+                              "kernels on this workload, calibrated on a copy)" if traffic
+                              else None, "kernel": kernel,
             "kernel_us": kern_ms * 1e3, "algorithmic_bytes_per_launch": int(bytes_per_launch)}
 
 

@@ -143,7 +143,7 @@ def split_plan(V, n_rows, target_wg=512, min_chunk=4096, max_split=128):
     return -(-V // c), c
 
 
-@pytest.mark.parametrize("B", [1, 8, 64])
+@pytest.mark.parametrize("B", [1, 8, 64, 128, 256])
 def test_split_rows_small_batches(torch_cuda, B):
     """Small batches split each row over workgroups (ranges of a multiple of
     1024 ids) and merge the ranges' bests: ids stay bit-exact, with ties and
