@@ -385,6 +385,218 @@ int launch_row(pz_sampler* s, const float* d_in, long ld_in, float* d_out, long 
   return launch_row_t<8>(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len, nc, lds);
 }
 
+// ---- long rows split over workgroups -----------------------------------------
+// Rows of more than ATTN_SPLIT_MIN scores: the row-split passes of
+// pz_split.h over the rows' own lengths -- slice maxima and segment
+// estimates (k_attn_stat), the integer increment records at the predicted
+// grids (k_attn_rec), one workgroup per row for the exact sum (k_attn_walk),
+// then every probability (k_attn_write) -- so the per-element work runs on
+// every CU rather than one per row.  Each pass reads the row again (L2 /
+// Infinity Cache: a few MB).
+#ifndef ATTN_SPLIT_MIN
+#define ATTN_SPLIT_MIN 8192
+#endif
+
+struct AttnSplit {
+  const float* in;
+  long ld_in;
+  float* out;
+  long ld_out;
+  int n;
+  const int32_t* lens;
+  PzSplitWs ws;
+  int nseg, spw, S, nc;
+};
+
+__device__ __forceinline__ int attn_len(const AttnSplit& A, int row) {
+  const int len = A.lens ? A.lens[row] : A.n;
+  return len < A.n ? len : A.n;  // (<= 0: the row is left alone)
+}
+
+template <bool VI>
+__device__ __forceinline__ AttnRow attn_row(const AttnSplit& A, int row, int len) {
+  AttnRow R;
+  R.x = A.in + (size_t)row * A.ld_in;
+  R.V = len;
+  R.vec = VI;
+  return R;
+}
+
+__device__ __forceinline__ bool attn_bad(uint32_t flags) {
+  return (flags & (PZ_RS_NAN | PZ_RS_NONFIN)) != 0;  // softmax.c:6-9: NaN everywhere
+}
+
+template <bool VI>
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_attn_stat(AttnSplit A) {
+  __shared__ PzSpShared SS;
+  const int row = blockIdx.y, len = attn_len(A, row);
+  if (len <= 0) return;
+  if (threadIdx.x == 0) SS.any = 0u;
+  __syncthreads();
+  pz_sp_stat_slice(attn_row<VI>(A, row, len), row, pz_sp_slice(A.nseg, A.spw), A.ws, SS, true);
+}
+
+template <bool VI>
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_attn_rec(AttnSplit A) {
+  __shared__ PzSpShared SS;
+  __shared__ uint64_t etab[32];
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = blockIdx.y, len = attn_len(A, row);
+  if (len <= 0) return;
+  pz_sp_row_stat(row, A.S, A.ws, SS);
+  if (attn_bad(SS.any)) return;
+  const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
+  const PzEstRel est{A.ws.seg_m + (size_t)row * A.ws.nsc, A.ws.seg_s + (size_t)row * A.ws.nsc,
+                     SS.M};
+  const float carry = pz_sp_prefix(est, sl.k0, SS);
+  pz_sp_predict(est, carry, row, sl, A.ws, SS);
+  PzExpTerms<AttnRow> X;
+  X.R = attn_row<VI>(A, row, len);
+  X.M = SS.M;
+  X.thr = -__builtin_inff();
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = (const pz_lds_u64*)etab;
+  pz_sp_records(X, row, sl, A.ws, nullptr, true);
+}
+
+// One workgroup per row: wave 0 walks, waves 1..15 pre-evaluate its specials.
+template <bool VI>
+__global__ __launch_bounds__(PZ_SP_BLOCK) void k_attn_walk(AttnSplit A) {
+  extern __shared__ __align__(16) char lds[];
+  __shared__ PzSpShared SS;
+  __shared__ uint64_t etab[32];
+  __shared__ float sum_sh;
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = blockIdx.x, len = attn_len(A, row);
+  if (len <= 0) return;
+  pz_sp_row_stat(row, A.S, A.ws, SS);
+  PzRowState& rs = A.ws.rs[row];
+  if (attn_bad(SS.any)) {
+    if (threadIdx.x == 0) {
+      rs.M = SS.M;
+      rs.flags = SS.any;
+    }
+    return;
+  }
+  PzExpTerms<AttnRow> X;
+  X.R = attn_row<VI>(A, row, len);
+  X.M = SS.M;
+  X.thr = -__builtin_inff();
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = (const pz_lds_u64*)etab;
+  const PzWalk W = pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds, SS);
+  if (threadIdx.x < 64) {
+    PzAcc st;
+    pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
+    if (threadIdx.x == 0) sum_sh = pz_acc_value(st);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    rs.M = SS.M;
+    rs.flags = SS.any;
+    rs.sum = sum_sh;
+    rs.inv = 1.0f / sum_sh;  // softmax.c:19-22
+  }
+}
+
+// p = e * (1 / sum) for every score of the slice (NaN on degenerate rows).
+template <bool VI, bool VO>
+__global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_attn_write(AttnSplit A) {
+  __shared__ uint64_t etab[32];
+  pz_etab_fill((pz_lds_u64*)etab);
+  const int row = blockIdx.y, len = attn_len(A, row);
+  if (len <= 0) return;
+  const PzRowState rs = A.ws.rs[row];
+  const bool bad = attn_bad(rs.flags);
+  PzExpTerms<AttnRow> X;
+  X.R = attn_row<VI>(A, row, len);
+  X.M = rs.M;
+  X.thr = -__builtin_inff();
+  X.inv = 1.0f;
+  X.as_p = false;
+  X.et = (const pz_lds_u64*)etab;
+  __syncthreads();  // the expf table
+  float* o = A.out + (size_t)row * A.ld_out;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
+  for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
+    const int i0 = k * PZ_SP_SEG + 4 * lane;
+    if (i0 >= len) continue;
+    float y[4];
+    X.R.load(i0, y);
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[c] = bad ? __builtin_nanf("") : X.exact_term(y[c]) * rs.inv;
+    if (VO && i0 + 3 < len) {
+      pz_f4 q;
+      q.x = v[0];
+      q.y = v[1];
+      q.z = v[2];
+      q.w = v[3];
+      *reinterpret_cast<pz_f4*>(o + i0) = q;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        if (i0 + c < len) o[i0 + c] = v[c];
+    }
+  }
+}
+
+template <bool VI, bool VO>
+int launch_split_t(pz_sampler* s, const AttnSplit& A, int n_rows, size_t walk_lds) {
+  auto kw = k_attn_walk<VI>;
+  if (walk_lds > 65536 && hipFuncSetAttribute((const void*)kw,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)walk_lds) != hipSuccess)
+    return -1;
+  const dim3 grid(A.S, n_rows), block(PZ_SP_BLOCK);
+  hipLaunchKernelGGL(k_attn_stat<VI>, grid, block, 0, s->stream, A);
+  hipLaunchKernelGGL(k_attn_rec<VI>, grid, block, 0, s->stream, A);
+  hipLaunchKernelGGL(kw, dim3(n_rows), block, walk_lds, s->stream, A);
+  hipLaunchKernelGGL((k_attn_write<VI, VO>), grid, block, 0, s->stream, A);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_split(pz_sampler* s, const float* d_in, long ld_in, float* d_out, long ld_out,
+                 int n_rows, int n, const int32_t* d_len) {
+  const size_t bytes = pz_split_ws_layout(n_rows, n, 0, nullptr, nullptr);
+  if (s->attn_dev_bytes < bytes) {
+    // (earlier launches on the stream may still use the old workspace)
+    if (hipStreamSynchronize(s->stream) != hipSuccess) return -1;
+    (void)hipFree(s->attn_dev);
+    s->attn_dev = nullptr;
+    s->attn_dev_bytes = 0;
+    if (hipMalloc(&s->attn_dev, bytes) != hipSuccess) return -3;
+    s->attn_dev_bytes = bytes;
+  }
+  AttnSplit A;
+  A.in = d_in;
+  A.ld_in = ld_in;
+  A.out = d_out;
+  A.ld_out = ld_out;
+  A.n = n;
+  A.lens = d_len;
+  pz_split_ws_layout(n_rows, n, 0, s->attn_dev, &A.ws);
+  const PzSplitPlan pl = pz_split_plan(n, n_rows, A.ws.smax);
+  A.nseg = pl.nseg;
+  A.spw = pl.spw;
+  A.S = pl.S;
+  const size_t fixed = 4096;
+  int nc = pz_sp_walk_nc(pl.nseg, (size_t)s->max_lds / 2 - fixed);
+  if (nc < 12) nc = pz_sp_walk_nc(pl.nseg, (size_t)s->max_lds - fixed);
+  if (nc < 2) return -2;
+  A.nc = nc;
+  const size_t walk_lds = pz_sp_walk_lds(pl.nseg, nc);
+  const bool vi = (ld_in % 4 == 0) && (((uintptr_t)d_in & 15) == 0);
+  const bool vo = (ld_out % 4 == 0) && (((uintptr_t)d_out & 15) == 0);
+  if (vi) return vo ? launch_split_t<true, true>(s, A, n_rows, walk_lds)
+                    : launch_split_t<true, false>(s, A, n_rows, walk_lds);
+  return vo ? launch_split_t<false, true>(s, A, n_rows, walk_lds)
+            : launch_split_t<false, false>(s, A, n_rows, walk_lds);
+}
+
 }  // namespace
 
 extern "C" int pz_attn_softmax(pz_sampler* s, const float* d_in, long ld_in, float* d_out,
@@ -394,6 +606,12 @@ extern "C" int pz_attn_softmax(pz_sampler* s, const float* d_in, long ld_in, flo
     return fail(s, PZ_EINVAL, "bad attention softmax shape");
   if (n_rows == 0 || n == 0) return PZ_OK;
   PZ_HIP(s, hipSetDevice(s->device));
+  if (n > ATTN_SPLIT_MIN) {
+    const int rc = launch_split(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len);
+    if (rc == 0) return PZ_OK;
+    if (rc == -3) return fail(s, PZ_ENOMEM, "attention softmax workspace");
+    if (rc != -2) return fail(s, PZ_EDEVICE, "attention softmax launch failed");
+  }
   if (n > ATTN_WAVE_SHORT && n <= ATTN_ROW_MAX) {
     const int rc = launch_row(s, d_in, ld_in, d_out, ld_out, n_rows, n, d_len);
     if (rc == 0) return PZ_OK;

@@ -149,6 +149,7 @@ extern "C" void pz_sampler_destroy(pz_sampler* s) {
   (void)hipFree(s->d_scratch);
   (void)hipFree(s->d_split);
   (void)hipFree(s->spec_dev);
+  (void)hipFree(s->attn_dev);
   (void)hipHostFree(s->spec_host);
   (void)hipHostFree(s->h_params);
   (void)hipHostFree(s->h_rows);

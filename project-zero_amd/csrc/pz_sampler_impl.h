@@ -64,6 +64,8 @@ struct pz_sampler {
   // demand by pz_spec_verify
   void* spec_dev = nullptr;
   size_t spec_dev_bytes = 0;
+  void* attn_dev = nullptr;  // the row-split attention softmax's workspace (grown on demand)
+  size_t attn_dev_bytes = 0;
   void* spec_host = nullptr;   // mapped, coherent pinned inputs and outputs
   void* spec_zc = nullptr;     // its device address
   size_t spec_host_bytes = 0;

@@ -102,11 +102,11 @@ def test_in_place_and_padded_output(torch_cuda, n):
     run(torch_cuda, x, ld_out=n + 3, label=f"padded{n}")  # misaligned output rows
 
 
-@pytest.mark.parametrize("n", [700, 5000])
+@pytest.mark.parametrize("n", [700, 5000, 9000])
 def test_special_values(torch_cuda, n):
     """NaN first / later, +inf, all -inf, -inf entries, ties, tiny and huge
-    spreads (sums that leave and re-enter binades); rows of one wave (700)
-    and of one workgroup (5000)."""
+    spreads (sums that leave and re-enter binades); rows of one wave (700),
+    of one workgroup (5000) and split over workgroups (9000)."""
     x = scores(16, n, 0xD0 + n)
     x[0, 0] = np.nan
     x[1, 99] = np.nan
