@@ -11,23 +11,35 @@ __device__ __forceinline__ float pz_readlane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
-// s + v[lane 0] + v[lane 1] + ... + v[lane n-1], left to right (n clamped to
-// 64).  Wave-uniform result.
-__device__ __forceinline__ float pz_seq_sum_lanes(float s, float v, int n) {
-  if (n > 64) n = 64;
-  for (int j = 0; j < n; j++) s = s + pz_readlane_f(v, j);
-  return s;
-}
-
-// Inclusive sequential prefix: lane j receives s + v[0] + ... + v[j] summed
-// left to right; lanes >= n receive the total over the first n lanes.
+// Inclusive sequential prefix: lane j receives ((s + v[0]) + v[1]) + ... +
+// v[j], the additions of a left-to-right loop started at s, in its order;
+// lanes >= n receive the total over the first n lanes (n clamped to 64,
+// wave-uniform).  A systolic chain of DPP adds: lane 0 holds s + v[0], and
+// at every step each lane j > 0 adds its v[j] to lane j-1's value of the
+// step before (wave_shr:1), so lane j holds its final value from step j on
+// and keeps it through further steps; the steps run in groups of eight with
+// no branch inside a group.  s must not be -0.0 (lane 0 receives +0.0 from
+// the shift), which no sum started at +0.0 is.
 __device__ __forceinline__ float pz_seq_scan_lanes(float s, float v, int n) {
   if (n > 64) n = 64;
+  if (n <= 0) return s;
   const int lane = threadIdx.x & 63;
-  float mine = 0.0f;
-  for (int j = 0; j < n; j++) {
-    s = s + pz_readlane_f(v, j);
-    if (lane == j) mine = s;
+  const float w = lane == 0 ? s + v : v;
+  float c = w;
+  for (int g = 1; g < n; g += 8) {
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+      c = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf,
+                                                     true)) + w;
   }
-  return lane < n ? mine : s;
+  const float tot = pz_readlane_f(c, n - 1);
+  return lane < n ? c : tot;
+}
+
+// s + v[lane 0] + v[lane 1] + ... + v[lane n-1], left to right (n clamped to
+// 64; s not -0.0).  Wave-uniform result.
+__device__ __forceinline__ float pz_seq_sum_lanes(float s, float v, int n) {
+  if (n > 64) n = 64;
+  if (n <= 0) return s;
+  return pz_readlane_f(pz_seq_scan_lanes(s, v, n), n - 1);
 }

@@ -28,3 +28,62 @@ __device__ __forceinline__ void pz_bitonic_desc(Ptr buf, int N) {
     }
   }
 }
+
+// ---- wave-wide bitonic merges of 64-entry lists held one entry per lane
+
+// The value lane (l ^ D) holds, D a power of two below 64: DPP within rows
+// of 16 lanes for D = 1, 2 (quad_perm [1,0,3,2], [2,3,0,1]) and 8 (row_ror:8),
+// ds_swizzle's bit mode within 32 lanes for D = 4, 16, ds_bpermute for 32.
+template <int D>
+__device__ __forceinline__ uint64_t pz_lane_xor_u64(uint64_t v) {
+  const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+  int a, b;
+  if constexpr (D == 1 || D == 2 || D == 8) {
+    constexpr int ctrl = D == 1 ? 0xb1 : (D == 2 ? 0x4e : 0x128);
+    a = __builtin_amdgcn_update_dpp(0, lo, ctrl, 0xf, 0xf, false);
+    b = __builtin_amdgcn_update_dpp(0, hi, ctrl, 0xf, 0xf, false);
+  } else if constexpr (D == 4 || D == 16) {
+    constexpr int pat = 0x1f | (D << 10);  // and 0x1f, or 0, xor D
+    a = __builtin_amdgcn_ds_swizzle(lo, pat);
+    b = __builtin_amdgcn_ds_swizzle(hi, pat);
+  } else {
+    static_assert(D == 32, "lane distance");
+    const int addr = (int)((threadIdx.x & 63u) ^ 32u) << 2;
+    a = __builtin_amdgcn_ds_bpermute(addr, lo);
+    b = __builtin_amdgcn_ds_bpermute(addr, hi);
+  }
+  return ((uint64_t)(uint32_t)b << 32) | (uint32_t)a;
+}
+
+// The value lane 63 - l holds (a list's order reversed).
+__device__ __forceinline__ uint64_t pz_lane_rev_u64(uint64_t v) {
+  const int addr = (63 - (int)(threadIdx.x & 63u)) << 2;
+  const int a = __builtin_amdgcn_ds_bpermute(addr, (int)(uint32_t)v);
+  const int b = __builtin_amdgcn_ds_bpermute(addr, (int)(uint32_t)(v >> 32));
+  return ((uint64_t)(uint32_t)b << 32) | (uint32_t)a;
+}
+
+// One half-cleaner of a bitonic sequence over the wave: lanes l and l ^ D
+// exchange so that the lower lane holds the larger (desc) or the smaller.
+template <int D>
+__device__ __forceinline__ uint64_t pz_half_clean_u64(uint64_t c, bool desc) {
+  const uint64_t o = pz_lane_xor_u64<D>(c);
+  const bool keep_max = ((threadIdx.x & (unsigned)D) == 0u) == desc;
+  const bool take = keep_max ? o > c : o < c;
+  return take ? o : c;
+}
+
+// a sorted descending over the lanes, b ascending: the 64 largest of the
+// 128, sorted descending (desc) or ascending.  max(a, b) lane by lane is the
+// upper half of the first half-cleaner of the 128-entry bitonic sequence
+// a ++ b, itself bitonic; six half-cleaners sort it.
+__device__ __forceinline__ uint64_t pz_wave_merge_u64(uint64_t a, uint64_t b, bool desc) {
+  uint64_t c = a > b ? a : b;
+  c = pz_half_clean_u64<32>(c, desc);
+  c = pz_half_clean_u64<16>(c, desc);
+  c = pz_half_clean_u64<8>(c, desc);
+  c = pz_half_clean_u64<4>(c, desc);
+  c = pz_half_clean_u64<2>(c, desc);
+  c = pz_half_clean_u64<1>(c, desc);
+  return c;
+}

@@ -56,6 +56,8 @@ constexpr int TOPK_MAXK = 1024;   // top_k.c:11-17 clamps k to 1024
 constexpr int HBINS = 2048;       // 11-bit digit
 constexpr int TK_U = 4;           // tiles per load group
 constexpr int TK_RANK_MAX = 128;  // survivors ordered by a rank count up to this many
+constexpr int TK_WM = 64;          // split rows with k up to this: sorted range lists, wave merges
+constexpr int TK_WM_WAVES = 4;     // waves merging the lists (16 each: at most 64 ranges)
 
 struct TopkShared {
   uint32_t hist[HBINS];     // sample / radix histograms (kept zeroed), then p and cdf
@@ -675,10 +677,12 @@ struct PzUArg {
   int n;  // rows 0..n-1 take v[row]
 };
 
-// One row split over gridDim.x workgroups of 4096 ids (one tile) each.
-// cand: the row's candidate area (`room` entries per workgroup, room >= k),
-// counts: entries each workgroup wrote ([rows][gridDim.x]); arrive: the
-// rows' arrival counters (zero between launches).
+// One row split over gridDim.x <= 64 workgroups of 4096 ids (one tile) each.
+// cand: the row's candidate area (`room` entries per workgroup, room >= k;
+// for k <= TK_WM exactly the range's min(n, k) largest, in descending
+// order, else a superset of its k largest), counts: entries each workgroup
+// wrote ([rows][gridDim.x]); arrive: the rows' arrival counters (zero
+// between launches).
 template <int BLOCK, bool VEC, bool DIV>
 __global__ __launch_bounds__(BLOCK) void k_topk_split(
     const float* __restrict__ logits, long ld, int V, const int32_t* __restrict__ rows,
@@ -687,6 +691,7 @@ __global__ __launch_bounds__(BLOCK) void k_topk_split(
     const float* __restrict__ u, int32_t* __restrict__ ids_out, float* __restrict__ p_out,
     uint64_t* __restrict__ cand, int capg, int room, uint32_t* __restrict__ counts,
     uint32_t* __restrict__ arrive, PzUArg ua) {
+  static_assert(BLOCK >= TK_WM_WAVES * PZ_WAVE && TK_WM_WAVES * 16 == PZ_WAVE, "merge waves");
   extern __shared__ __align__(16) char lds[];
   __shared__ TopkShared S;
   __shared__ int last_sh;
@@ -765,18 +770,37 @@ __global__ __launch_bounds__(BLOCK) void k_topk_split(
       }
     }
     __syncthreads();
-    thr = S.nbin <= room ? (uint64_t)S.bin << 53
-                         : tk_select_bin<BLOCK>(S, buf, nc, k, ~0ull, 0ull);
+    // k <= TK_WM: up to TK_RANK_MAX entries are ranked below, else room bounds them
+    const int lim = k <= TK_WM ? TK_RANK_MAX : room;
+    thr = S.nbin <= lim ? (uint64_t)S.bin << 53
+                        : tk_select_bin<BLOCK>(S, buf, nc, k, ~0ull, 0ull);
   }
   uint64_t* out = cand + (size_t)row * capg + (size_t)sl * room;
   if (tid == 0) S.ntop = 0;
   __syncthreads();
-  for (int i = tid; i < nc; i += BLOCK) {
-    const uint64_t c = buf[i];
-    if (c >= thr) out[atomicAdd(&S.ntop, 1)] = c;
+  if (k <= TK_WM) {
+    // the range's min(nc, k) largest, in descending order: the survivors
+    // (at most TK_RANK_MAX) each placed by its rank among them (keys distinct)
+    for (int i = tid; i < nc; i += BLOCK) {
+      const uint64_t c = buf[i];
+      if (c >= thr) S.top[atomicAdd(&S.ntop, 1)] = c;
+    }
+    __syncthreads();
+    const int nt = S.ntop;
+    if (tid < nt) {
+      const uint64_t c = S.top[tid];
+      const int r = tk_rank((const pz_lds_u64*)S.top, nt, c);
+      if (r < k) out[r] = c;
+    }
+    if (tid == 0) counts[(size_t)row * S_row + sl] = (uint32_t)(nt < k ? nt : k);
+  } else {
+    for (int i = tid; i < nc; i += BLOCK) {
+      const uint64_t c = buf[i];
+      if (c >= thr) out[atomicAdd(&S.ntop, 1)] = c;
+    }
+    __syncthreads();
+    if (tid == 0) counts[(size_t)row * S_row + sl] = (uint32_t)S.ntop;
   }
-  __syncthreads();
-  if (tid == 0) counts[(size_t)row * S_row + sl] = (uint32_t)S.ntop;
   // the last workgroup of the row merges the ranges' candidates
   if (!pz_sp_arrive(arrive, row, S_row, &last_sh)) return;
   if (tid == 0) {
@@ -795,6 +819,56 @@ __global__ __launch_bounds__(BLOCK) void k_topk_split(
   }
   __syncthreads();
   const int total = off[S_row];  // at most TOPK_CAP: S * room entries
+  if (k <= TK_WM) {
+    // every list is its range's largest (at most 64) in descending order:
+    // wave w merges lists w, w + 4, ... (slot j holds list w + 4j, read
+    // descending in even slots and ascending in odd ones) by a tree of wave
+    // merges whose left inputs are descending and right inputs ascending,
+    // then wave 0 merges the four waves' lists the same way
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint64_t mine = 0ull;
+    if (wv < TK_WM_WAVES) {
+      uint64_t r[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        const int i = wv + TK_WM_WAVES * j;
+        const int cnt = i < S_row ? off[i + 1] - off[i] : 0;
+        const int e = (j & 1) ? 63 - lane : lane;
+        r[j] = e < cnt ? all[(size_t)i * room + e] : 0ull;
+      }
+      const int nl = S_row > wv ? (S_row - wv + TK_WM_WAVES - 1) / TK_WM_WAVES : 0;
+#pragma unroll
+      for (int s = 1; s < 16; s <<= 1) {
+#pragma unroll
+        for (int p = 0; p < 16 / (2 * s); p++) {
+          const bool desc = (p & 1) == 0;
+          if ((2 * p + 1) * s < nl)
+            r[p] = pz_wave_merge_u64(r[2 * p], r[2 * p + 1], desc);
+          else if (2 * p * s < nl)  // the left subtree alone: descending
+            r[p] = desc ? r[2 * p] : pz_lane_rev_u64(r[2 * p]);
+          else
+            r[p] = 0ull;
+        }
+      }
+      mine = r[0];
+      if (wv > 0) S.top[wv * PZ_WAVE + lane] = mine;
+    }
+    __syncthreads();
+    pz_sp_rearm(arrive, row);
+    const int m = total < k ? total : k;
+    if (tid < PZ_WAVE) {
+      const pz_lds_u64* t = (const pz_lds_u64*)S.top;
+      const uint64_t w1 = t[PZ_WAVE + 63 - lane], w2 = t[2 * PZ_WAVE + lane];
+      const uint64_t w3 = t[3 * PZ_WAVE + 63 - lane];
+      const uint64_t m01 = pz_wave_merge_u64(mine, w1, true);
+      const uint64_t m23 = pz_wave_merge_u64(w2, w3, false);
+      const uint64_t fin = pz_wave_merge_u64(m01, m23, true);
+      if (lane < m) S.top[lane] = fin;
+    }
+    __syncthreads();
+    tk_draw(S, (const pz_lds_u64*)S.top, m, k, prm, uu, row, ids_out, p_out);
+    return;
+  }
   // up to four entries per thread, their loads issued together
   uint64_t got[4];
 #pragma unroll
@@ -874,7 +948,8 @@ int pz_launch_topk(const pz_launch& L, int n_rows, const int32_t* d_rows) {
   // the largest k among the rows decides whether the split's merge fits
   // (k is resolved per row on the host: the host passes it as kmax)
   const int S = pz_tiles(L.V);
-  if (S >= 2 && (long)S * n_rows <= TOPK_SPLIT_MAX_WG && L.kmax > 0 &&
+  // at most 64 ranges: the merge scans their counts in one wave
+  if (S >= 2 && S <= PZ_WAVE && (long)S * n_rows <= TOPK_SPLIT_MAX_WG && L.kmax > 0 &&
       (long)S * L.kmax <= TOPK_CAP && (long)S * L.kmax <= L.ws.capg && L.ws.keys) {
     if (L.temp_div)
       return vec ? launch_topk_split_t<true, true>(L, n_rows, d_rows, S, L.kmax)

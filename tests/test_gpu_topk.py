@@ -122,13 +122,17 @@ def test_uniform_one_and_zero(torch_cuda):
         check(torch_cuda, x, [pz.row_params(temperature=1.0, top_k=30)], u, label=f"u={uval} k")
 
 
-@pytest.mark.parametrize("B,V", [(1, 49152), (3, 128256), (8, 4097), (1, 4096), (2, 151936)])
-@pytest.mark.parametrize("k,top_p", [(1, 1.0), (40, 0.95), (100, 1.0), (300, 0.8)])
+@pytest.mark.parametrize("B,V", [(1, 49152), (3, 128256), (8, 4097), (1, 4096), (2, 151936),
+                                 (1, 300000)])
+@pytest.mark.parametrize("k,top_p", [(1, 1.0), (40, 0.95), (64, 0.9), (65, 1.0), (100, 1.0),
+                                     (300, 0.8)])
 def test_small_batch_rows_split_over_workgroups(torch_cuda, B, V, k, top_p):
     """Small batches take the split kernel (each 4096-id range selects its own
     top k, the last workgroup of the row merges) whenever the ranges' k
-    candidates fit its merge buffer; penalties, ties across range boundaries
-    and rows with fewer than k valid values included."""
+    candidates fit its merge buffer and the row has at most 64 ranges (V =
+    300000 has 74: one workgroup per row); k <= 64 merges sorted range lists
+    in registers, larger k the ranges' supersets.  Penalties, ties across
+    range boundaries and rows with fewer than k valid values included."""
     rng = np.random.default_rng(V + k)
     x = (rng.standard_normal((B, V)) * 2.5).astype(np.float32)
     x[0, 4090:4102] = 9.0                      # a tie straddling a range boundary
@@ -143,3 +147,19 @@ def test_small_batch_rows_split_over_workgroups(torch_cuda, B, V, k, top_p):
     params = [pz.row_params(temperature=0.8, top_k=k, top_p=top_p, rep_penalty=1.3)]
     check(torch_cuda, x, params, pz.synth_draws(B, V * 7 + k), hist=hist,
           label=f"split B={B} V={V} k={k}")
+
+
+@pytest.mark.parametrize("V", [49152, 128256])
+@pytest.mark.parametrize("k", [40, 64, 100])
+def test_split_rows_of_equal_values(torch_cuda, V, k):
+    """Every value of a range in one key bin (a constant row: the range's k
+    are its k lowest ids, chosen by the exact select), a row of two levels
+    whose upper level is spread thinly over the ranges, and a row whose
+    ranges each hold a single valid value."""
+    B = 3
+    x = np.full((B, V), 0.5, np.float32)
+    x[1, ::1531] = 2.0
+    x[2, :] = -np.inf
+    x[2, 4095::4096] = np.linspace(-1.0, 1.0, len(range(4095, V, 4096)), dtype=np.float32)
+    params = [pz.row_params(temperature=1.0, top_k=k, top_p=0.9)]
+    check(torch_cuda, x, params, pz.synth_draws(B, V + k), label=f"equal V={V} k={k}")
