@@ -31,9 +31,22 @@ __device__ __forceinline__ void pz_bitonic_desc(Ptr buf, int N) {
 
 // ---- wave-wide bitonic merges of 64-entry lists held one entry per lane
 
-// The value lane (l ^ D) holds, D a power of two below 64: DPP within rows
-// of 16 lanes for D = 1, 2 (quad_perm [1,0,3,2], [2,3,0,1]) and 8 (row_ror:8),
-// ds_swizzle's bit mode within 32 lanes for D = 4, 16, ds_bpermute for 32.
+// The value lane (l ^ D) holds, D a power of two below 64, by VALU lane
+// moves only: DPP within rows of 16 lanes for D = 1, 2 (quad_perm [1,0,3,2],
+// [2,3,0,1]), 4 (row_shl:4 where bit 2 of the lane is clear, row_shr:4
+// where it is set) and 8 (row_ror:8); gfx950's v_permlane16_swap and
+// v_permlane32_swap for 16 and 32 (with both operands the value itself,
+// lanes with bit D set find the partner's value in the first result and
+// the others in the second).
+__device__ __forceinline__ uint32_t pz_lane_xor_u32_16(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16u) ? r[0] : r[1];
+}
+__device__ __forceinline__ uint32_t pz_lane_xor_u32_32(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32u) ? r[0] : r[1];
+}
+
 template <int D>
 __device__ __forceinline__ uint64_t pz_lane_xor_u64(uint64_t v) {
   const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
@@ -42,15 +55,21 @@ __device__ __forceinline__ uint64_t pz_lane_xor_u64(uint64_t v) {
     constexpr int ctrl = D == 1 ? 0xb1 : (D == 2 ? 0x4e : 0x128);
     a = __builtin_amdgcn_update_dpp(0, lo, ctrl, 0xf, 0xf, false);
     b = __builtin_amdgcn_update_dpp(0, hi, ctrl, 0xf, 0xf, false);
-  } else if constexpr (D == 4 || D == 16) {
-    constexpr int pat = 0x1f | (D << 10);  // and 0x1f, or 0, xor D
-    a = __builtin_amdgcn_ds_swizzle(lo, pat);
-    b = __builtin_amdgcn_ds_swizzle(hi, pat);
+  } else if constexpr (D == 4) {
+    const int al = __builtin_amdgcn_update_dpp(0, lo, 0x104, 0xf, 0xf, false);  // lane + 4
+    const int bl = __builtin_amdgcn_update_dpp(0, hi, 0x104, 0xf, 0xf, false);
+    const int ar = __builtin_amdgcn_update_dpp(0, lo, 0x114, 0xf, 0xf, false);  // lane - 4
+    const int br = __builtin_amdgcn_update_dpp(0, hi, 0x114, 0xf, 0xf, false);
+    const bool up = (threadIdx.x & 4u) != 0u;
+    a = up ? ar : al;
+    b = up ? br : bl;
+  } else if constexpr (D == 16) {
+    a = (int)pz_lane_xor_u32_16((uint32_t)lo);
+    b = (int)pz_lane_xor_u32_16((uint32_t)hi);
   } else {
     static_assert(D == 32, "lane distance");
-    const int addr = (int)((threadIdx.x & 63u) ^ 32u) << 2;
-    a = __builtin_amdgcn_ds_bpermute(addr, lo);
-    b = __builtin_amdgcn_ds_bpermute(addr, hi);
+    a = (int)pz_lane_xor_u32_32((uint32_t)lo);
+    b = (int)pz_lane_xor_u32_32((uint32_t)hi);
   }
   return ((uint64_t)(uint32_t)b << 32) | (uint32_t)a;
 }
