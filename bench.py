@@ -588,8 +588,8 @@ def run_attention(args, torch, cpu):
         gbs = 2 * blk / (kern * 1e-3) / 1e9
         e = {"ctx": ctx, "kernel_us": kern * 1e3, "achieved_gbs": gbs, "frac": gbs / HBM_PEAK_GBS,
              "distinct_blocks": nrot,
-             "kernel": ("k_attn_wave" if ctx <= 1024 else
-                        "k_attn_row" if ctx <= 32768 else "k_softmax (row split)")}
+             "kernel": ("k_attn_wave" if ctx <= 1024 else "k_attn_row" if ctx <= 8192 else
+                        "k_attn_stat + k_attn_rec + k_attn_walk + k_attn_write (row split)")}
         if cpu.enabled:
             s.sync()
             got = t_o[:heads].cpu().numpy()
