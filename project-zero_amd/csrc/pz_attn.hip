@@ -179,6 +179,7 @@ struct AttnShared {
   uint32_t bad[AR_WAVES];
   float carry;
   float sum;
+  uint32_t s0;  // segment 0's sequential sum (bits), or 0xffffffff
 };
 
 // NSW: segments per wave (rows of up to 16 NSW segments); each wave holds
@@ -315,9 +316,38 @@ __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_
                 (D2 ? PZ_GF_DIRTY2 : 0u);
     }
   }
+  // wave 0 has no record to make for segment 0 when it is predicted to
+  // cross binades (from a zero sum it nearly always is): it adds up that
+  // segment's exact terms in id order meanwhile (one lane reading them back
+  // from LDS), so the walk starts from that sum without waiting for a
+  // producer to load and add the segment
+  if (w == 0) {
+    uint32_t s0 = 0xffffffffu;
+    if (W.gf[0] & PZ_GF_XING) {
+      pz_f4 q;
+      q.x = 0 < cnt[0] ? X.exact_term(y[0][0]) : 0.0f;
+      q.y = 1 < cnt[0] ? X.exact_term(y[0][1]) : 0.0f;
+      q.z = 2 < cnt[0] ? X.exact_term(y[0][2]) : 0.0f;
+      q.w = 3 < cnt[0] ? X.exact_term(y[0][3]) : 0.0f;
+      const pz_lds_f4* tq = (const pz_lds_f4*)W.tmp;
+      ((pz_lds_f4*)W.tmp)[lane] = q;
+      if (lane == 0) {
+        float sum0 = 0.0f;
+        for (int i = 0; i < PZ_SP_SEG / 4; i++) {
+          const pz_f4 t4 = tq[i];
+          sum0 = sum0 + t4.x;
+          sum0 = sum0 + t4.y;
+          sum0 = sum0 + t4.z;
+          sum0 = sum0 + t4.w;
+        }
+        s0 = __float_as_uint(sum0);
+      }
+    }
+    if (lane == 0) A.s0 = s0;
+  }
   __syncthreads();
   // 5. the walk: wave 0, waves 1..15 pre-evaluating its specials
-  W = pz_sp_walk_start(X, W, SS);
+  W = pz_sp_walk_start(X, W, SS, -1, A.s0);
   if (w == 0) {
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);

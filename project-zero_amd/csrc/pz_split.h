@@ -764,6 +764,7 @@ struct PzWalk {
                       // segment 0 is special 0 (else 0xffffffff)
   pz_lds_f32* tmp;    // [256] terms of a segment evaluated during the walk
   int nseg, nc, n_spec;
+  bool pre0;  // s0 came with the set-up: segment 0 has no ring slot
 };
 
 // LDS of the walk for a row of nseg segments with a ring of nc pre-evaluated
@@ -969,15 +970,20 @@ __device__ __forceinline__ PzWalk pz_sp_walk_layout(char* lds, int nseg, int nc)
   W.chp = (pz_lds_u32*)p;      p += (size_t)(nseg + 1) * 4;
   W.spk = (pz_lds_i32*)p;
   W.n_spec = 0;
+  W.pre0 = false;
   return W;
 }
 
 // The second half of the set-up for records already in LDS (W.d, W.d2,
 // W.gf of a layout from pz_sp_walk_layout, written before a barrier):
-// prefixes, the special list, the ring and its producers.
+// prefixes, the special list, the ring and its producers.  s0_pre: the
+// sequential fp32 sum of segment 0's terms from 0 (bits) when the caller
+// has it already (0xffffffff: the producers add it up); segment 0 then
+// gets no ring slot and the walker starts from that sum at once.
 template <class X>
 __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpShared& S,
-                                                   int n_producers = -1) {
+                                                   int n_producers = -1,
+                                                   uint32_t s0_pre = 0xffffffffu) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nt = (int)blockDim.x, nw = nt >> 6;
   if (n_producers < 0) n_producers = nw - 1;
@@ -1034,10 +1040,11 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
     W.pd[nseg] = base;
     W.chp[nseg] = cbase;
     *W.consumed = 0u;
-    *W.s0 = 0xffffffffu;
+    *W.s0 = s0_pre;
   }
   if (tid < nc) W.rdy[tid] = 0u;
   W.n_spec = sbase;
+  W.pre0 = s0_pre != 0xffffffffu;
   __syncthreads();
   // Waves 1 .. n_producers pre-evaluate the specials in id order into the
   // ring, while wave 0 (the walker) starts at once.  The walker waits only
@@ -1057,6 +1064,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
       }
     if (c == PZ_WALK_DONE) break;
     const int k = W.spk[j];
+    if (j == 0 && k == 0 && W.pre0) continue;  // summed before the walk: no slot
     const int sl = j % nc;
     float v[4];
     x.seg(k, v);
@@ -1122,11 +1130,13 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
 // expected to end in.  Every thread calls it; it returns without a final
 // barrier: waves 1 .. n_producers keep filling the ring while the walker
 // (wave 0) consumes it (pz_sp_load_slot), the other waves may go on to other
-// work.  Any block size that is a multiple of 64, up to 1024.
+// work.  Any block size that is a multiple of 64, up to 1024.  s0_pre as for
+// pz_sp_walk_start.
 template <class X>
 __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg, int nc,
                                                    const PzSplitWs& ws, char* lds,
-                                                   PzSpShared& S, int n_producers = -1) {
+                                                   PzSpShared& S, int n_producers = -1,
+                                                   uint32_t s0_pre = 0xffffffffu) {
   PzWalk W = pz_sp_walk_layout(lds, nseg, nc);
   const uint32_t* rd = pz_sp_rec_d(ws, row);
   const uint32_t* rd2 = pz_sp_rec_d2(ws, row);
@@ -1137,7 +1147,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
     W.gf[k] = rgf[k];
   }
   __syncthreads();
-  return pz_sp_walk_start(x, W, S, n_producers);
+  return pz_sp_walk_start(x, W, S, n_producers, s0_pre);
 }
 
 // Sequential fp32 accumulation of the segment's terms from position start,
@@ -1669,8 +1679,11 @@ __device__ __forceinline__ int pz_sp_walk_run(PzAcc& st, const PzWalk& W, float 
     const int b = __builtin_amdgcn_readlane(m.k, jl);
     const int slot1 = slot + 1 == W.nc ? 0 : slot + 1;  // special j + 1's slot
     PzSpSeg cur = nxt;
+    // segment 0 summed before the walk has no slot: taken from s0, or (a
+    // stop within it) evaluated here
+    const bool self0 = ring && j == 0 && b == 0 && W.pre0;
     if (ring) {
-      if (j < np && !have) pz_sp_load_slot(W, j, cur);
+      if (j < np && !have && !self0) pz_sp_load_slot(W, j, cur);
       // the slots of the specials before j are released to the producers
       // (their reads are done: special j's data came in with the last step's
       // loads; special j's slot stays, the serial path reads its terms
@@ -1716,7 +1729,7 @@ __device__ __forceinline__ int pz_sp_walk_run(PzAcc& st, const PzWalk& W, float 
         taken = true;
       }
     }
-    if (!taken && !ring) {
+    if (!taken && (!ring || self0)) {
       const int r = pz_sp_special<MODE>(st, W, thr, x, b);
       if (r >= 0) return b * PZ_SP_SEG + r;
     } else if (!taken &&
