@@ -27,6 +27,7 @@
 #include "pz_device.h"
 #include "pz_exact.h"
 #include "pz_sampler_impl.h"
+#include "pz_seq.h"
 #include "pz_split.h"
 
 namespace {
@@ -318,30 +319,15 @@ __global__ __launch_bounds__(AR_BLOCK) void k_attn_row(const float* in, long ld_
   }
   // wave 0 has no record to make for segment 0 when it is predicted to
   // cross binades (from a zero sum it nearly always is): it adds up that
-  // segment's exact terms in id order meanwhile (one lane reading them back
-  // from LDS), so the walk starts from that sum without waiting for a
-  // producer to load and add the segment
+  // segment's exact terms in id order meanwhile, so the walk starts from
+  // that sum without waiting for a producer to load and add the segment
   if (w == 0) {
     uint32_t s0 = 0xffffffffu;
     if (W.gf[0] & PZ_GF_XING) {
-      pz_f4 q;
-      q.x = 0 < cnt[0] ? X.exact_term(y[0][0]) : 0.0f;
-      q.y = 1 < cnt[0] ? X.exact_term(y[0][1]) : 0.0f;
-      q.z = 2 < cnt[0] ? X.exact_term(y[0][2]) : 0.0f;
-      q.w = 3 < cnt[0] ? X.exact_term(y[0][3]) : 0.0f;
-      const pz_lds_f4* tq = (const pz_lds_f4*)W.tmp;
-      ((pz_lds_f4*)W.tmp)[lane] = q;
-      if (lane == 0) {
-        float sum0 = 0.0f;
-        for (int i = 0; i < PZ_SP_SEG / 4; i++) {
-          const pz_f4 t4 = tq[i];
-          sum0 = sum0 + t4.x;
-          sum0 = sum0 + t4.y;
-          sum0 = sum0 + t4.z;
-          sum0 = sum0 + t4.w;
-        }
-        s0 = __float_as_uint(sum0);
-      }
+      float t[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) t[c] = c < cnt[0] ? X.exact_term(y[0][c]) : 0.0f;
+      s0 = __float_as_uint(pz_seq_sum_seg4(t));
     }
     if (lane == 0) A.s0 = s0;
   }

@@ -43,3 +43,23 @@ __device__ __forceinline__ float pz_seq_sum_lanes(float s, float v, int n) {
   if (n <= 0) return s;
   return pz_readlane_f(pz_seq_scan_lanes(s, v, n), n - 1);
 }
+
+// The sequential fp32 sum, from +0.0, of the 256 terms a wave holds in id
+// order (lane l: t[0..3] = terms 4l .. 4l+3), in every lane: the DPP chain
+// of pz_seq_scan_lanes with each lane's four terms added in turn, 64 steps
+// (lane j holds ((x + t0) + t1) + t2) + t3 over lane j-1's value x from step
+// j on).  Terms must not be -0.0 where every term before them is zero.
+__device__ __forceinline__ float pz_seq_sum_seg4(const float (&t)[4]) {
+  float c = 0.0f;
+  for (int s = 0; s < 64; s += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      c = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf,
+                                                     true)) + t[0];
+      c = c + t[1];
+      c = c + t[2];
+      c = c + t[3];
+    }
+  }
+  return pz_readlane_f(c, 63);
+}

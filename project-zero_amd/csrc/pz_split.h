@@ -64,6 +64,8 @@ struct PzRowState {
   uint32_t flags;   // PZ_RS_*
   float sum;        // exact sequential normaliser
   float inv;        // 1.0f / sum
+  uint32_t s0;      // sequential sum of segment 0's terms from 0 (bits), where a pass
+                    // posts it for the walk (0xffffffff: not posted)
   float f[3];       // pass-specific values
   int32_t i[8];     // pass-specific values
 };

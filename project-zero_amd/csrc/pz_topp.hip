@@ -40,6 +40,7 @@
 #include "pz_exact.h"
 #include "pz_launch.h"
 #include "pz_rowpass.h"
+#include "pz_seq.h"
 #include "pz_sort.h"
 #include "pz_split.h"
 
@@ -693,6 +694,11 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   }
   const bool degen = topp_degenerate(SS.any);
   const float M = SS.M, thr = M - 20.0f;
+  // segment 0's values, for its sum after the records (wave 1 of slice 0),
+  // held in registers: the gather stages keys over the slice in LDS, and the
+  // row's last slice reaches it without a barrier after its records
+  pz_f4 seg0 = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (blockIdx.x == 0 && w == 1) seg0 = *(const pz_lds_f4*)(ybuf + 4 * lane);
   // 2. the estimated candidate mass of each segment (as k_topp_est) and the
   // histogram of the estimated e (the nucleus bins), the slice's total for
   // the slices after it
@@ -781,6 +787,17 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   X.as_p = false;
   X.et = et;
   pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)sgf, true);
+  if (blockIdx.x == 0 && w == 1) {
+    // the row's first segment, summed for the walk (wave 1: wave 0's first
+    // thread waits for the selection meanwhile)
+    const int e0 = 4 * lane;
+    const int n = V - e0 < 0 ? 0 : (V - e0 > 4 ? 4 : V - e0);
+    const pz_f4 q = seg0;
+    const float t[4] = {0 < n ? X.exact_term(q.x) : 0.0f, 1 < n ? X.exact_term(q.y) : 0.0f,
+                        2 < n ? X.exact_term(q.z) : 0.0f, 3 < n ? X.exact_term(q.w) : 0.0f};
+    const float s0 = pz_seq_sum_seg4(t);
+    if (lane == 0) ws.rs[row].s0 = __float_as_uint(s0);
+  }
   if (blockIdx.x != S - 1) {
     if (tid == 0) {
       uint32_t v = 0;
@@ -1835,7 +1852,8 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   pz_lds_u16* perm = (pz_lds_u16*)(bstart + PBINS / 2);
   pz_lds_u64* bkeys = (pz_lds_u64*)(lds + sort_off + wf_keys_off(cap));
   const uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
-  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, region, SS, 7);
+  // (segment 0's sum: posted by the front launch)
+  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, region, SS, 7, rs0.s0);
   if (w == 0) {
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
