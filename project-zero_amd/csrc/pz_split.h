@@ -990,64 +990,102 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
   const int nt = (int)blockDim.x, nw = nt >> 6;
   if (n_producers < 0) n_producers = nw - 1;
   const int nseg = W.nseg, nc = W.nc;
-  // records, their prefix, the grid changes between clean neighbours, and
-  // the special segments in id order
-  uint32_t base = 0;  // prefix carried over the chunks (thread-uniform)
-  int sbase = 0;      // specials found in earlier chunks
-  uint32_t cbase = 0; // grid changes in earlier chunks
-  for (int c0 = 0; c0 < nseg; c0 += nt) {
-    const int k = c0 + tid;
-    uint32_t d = 0, gf = PZ_NO_RECORD, gfp = PZ_NO_RECORD;
-    if (k < nseg) {
-      d = W.d[k];
-      gf = W.gf[k];
-      if (k > 0) gfp = W.gf[k - 1];
+  if (nseg <= 64) {
+    // one segment per lane of wave 0, one barrier: the record prefix, the
+    // grid changes and the special list by wave scans and ballots (lanes
+    // past the row hold d = 0, so lane 63's prefix is the total)
+    pz_lds_u32* nsp = W.consumed + 2;  // the special count, for every wave
+    if (w == 0) {
+      const int k = lane;
+      uint32_t d = 0, gf = PZ_NO_RECORD, gfp = PZ_NO_RECORD;
+      if (k < nseg) {
+        d = W.d[k];
+        gf = W.gf[k];
+        if (k > 0) gfp = W.gf[k - 1];
+      }
+      const bool special = k < nseg && !pz_sp_clean(gf);
+      const bool chg =
+          k < nseg && pz_sp_clean(gf) && pz_sp_clean(gfp) && ((gf ^ gfp) & 0xffu) != 0u;
+      const uint32_t incl = pz_wave_scan_u32(d);
+      const uint64_t sb = __ballot(special);
+      const uint64_t cb = __ballot(chg);
+      const uint64_t below = (1ull << lane) - 1ull;
+      if (k < nseg) {
+        W.pd[k] = incl - d;
+        W.chp[k] = (uint32_t)__popcll(cb & below);
+        if (special) W.spk[__popcll(sb & below)] = k;
+      }
+      if (lane == 63) {
+        W.pd[nseg] = incl;
+        W.chp[nseg] = (uint32_t)__popcll(cb);
+        *W.consumed = 0u;
+        *W.s0 = s0_pre;
+        *nsp = (uint32_t)__popcll(sb);
+      }
     }
-    const bool special = k < nseg && !pz_sp_clean(gf);
-    const bool chg = k < nseg && pz_sp_clean(gf) && pz_sp_clean(gfp) && ((gf ^ gfp) & 0xffu) != 0u;
-    // exclusive prefixes of d and of the grid changes, and the rank of the
-    // special segments (workgroup scans)
-    const uint32_t incl = pz_wave_scan_u32(d);
-    const uint64_t sb = __ballot(special);
-    const uint64_t cb = __ballot(chg);
+    if (tid < nc) W.rdy[tid] = 0u;
     __syncthreads();
-    if (lane == 63) S.list[w] = (int)incl;  // wave totals
-    if (lane == 0) {
-      S.red[w] = __int_as_float(__popcll(sb));
-      S.red2[w] = (uint32_t)__popcll(cb);
+    W.n_spec = (int)*nsp;
+  } else {
+    // records, their prefix, the grid changes between clean neighbours, and
+    // the special segments in id order
+    uint32_t base = 0;  // prefix carried over the chunks (thread-uniform)
+    int sbase = 0;      // specials found in earlier chunks
+    uint32_t cbase = 0; // grid changes in earlier chunks
+    for (int c0 = 0; c0 < nseg; c0 += nt) {
+      const int k = c0 + tid;
+      uint32_t d = 0, gf = PZ_NO_RECORD, gfp = PZ_NO_RECORD;
+      if (k < nseg) {
+        d = W.d[k];
+        gf = W.gf[k];
+        if (k > 0) gfp = W.gf[k - 1];
+      }
+      const bool special = k < nseg && !pz_sp_clean(gf);
+      const bool chg = k < nseg && pz_sp_clean(gf) && pz_sp_clean(gfp) && ((gf ^ gfp) & 0xffu) != 0u;
+      // exclusive prefixes of d and of the grid changes, and the rank of the
+      // special segments (workgroup scans)
+      const uint32_t incl = pz_wave_scan_u32(d);
+      const uint64_t sb = __ballot(special);
+      const uint64_t cb = __ballot(chg);
+      __syncthreads();
+      if (lane == 63) S.list[w] = (int)incl;  // wave totals
+      if (lane == 0) {
+        S.red[w] = __int_as_float(__popcll(sb));
+        S.red2[w] = (uint32_t)__popcll(cb);
+      }
+      __syncthreads();
+      // the waves' totals, one per lane, summed by wave reductions (mod 2^32)
+      const bool in_w = lane < nw;
+      const uint32_t lt = in_w ? (uint32_t)S.list[lane] : 0u;
+      const uint32_t ls = in_w ? (uint32_t)__float_as_int(S.red[lane]) : 0u;
+      const uint32_t lc = in_w ? S.red2[lane] : 0u;
+      const uint32_t off = base + pz_wave_sum_u32(lane < w ? lt : 0u);
+      const int soff = sbase + (int)pz_wave_sum_u32(lane < w ? ls : 0u);
+      const uint32_t coff = cbase + pz_wave_sum_u32(lane < w ? lc : 0u);
+      const uint32_t tot = pz_wave_sum_u32(lt), ctot = pz_wave_sum_u32(lc);
+      const int stot = (int)pz_wave_sum_u32(ls);
+      const uint64_t below = (1ull << lane) - 1ull;
+      if (k < nseg) {
+        W.pd[k] = off + incl - d;
+        W.chp[k] = coff + (uint32_t)__popcll(cb & below);
+        if (special) W.spk[soff + __popcll(sb & below)] = k;
+      }
+      base += tot;
+      sbase += stot;
+      cbase += ctot;
+      __syncthreads();
     }
-    __syncthreads();
-    // the waves' totals, one per lane, summed by wave reductions (mod 2^32)
-    const bool in_w = lane < nw;
-    const uint32_t lt = in_w ? (uint32_t)S.list[lane] : 0u;
-    const uint32_t ls = in_w ? (uint32_t)__float_as_int(S.red[lane]) : 0u;
-    const uint32_t lc = in_w ? S.red2[lane] : 0u;
-    const uint32_t off = base + pz_wave_sum_u32(lane < w ? lt : 0u);
-    const int soff = sbase + (int)pz_wave_sum_u32(lane < w ? ls : 0u);
-    const uint32_t coff = cbase + pz_wave_sum_u32(lane < w ? lc : 0u);
-    const uint32_t tot = pz_wave_sum_u32(lt), ctot = pz_wave_sum_u32(lc);
-    const int stot = (int)pz_wave_sum_u32(ls);
-    const uint64_t below = (1ull << lane) - 1ull;
-    if (k < nseg) {
-      W.pd[k] = off + incl - d;
-      W.chp[k] = coff + (uint32_t)__popcll(cb & below);
-      if (special) W.spk[soff + __popcll(sb & below)] = k;
+    if (tid == 0) {
+      W.pd[nseg] = base;
+      W.chp[nseg] = cbase;
+      *W.consumed = 0u;
+      *W.s0 = s0_pre;
     }
-    base += tot;
-    sbase += stot;
-    cbase += ctot;
+    if (tid < nc) W.rdy[tid] = 0u;
+    W.n_spec = sbase;
     __syncthreads();
   }
-  if (tid == 0) {
-    W.pd[nseg] = base;
-    W.chp[nseg] = cbase;
-    *W.consumed = 0u;
-    *W.s0 = s0_pre;
-  }
-  if (tid < nc) W.rdy[tid] = 0u;
-  W.n_spec = sbase;
   W.pre0 = s0_pre != 0xffffffffu;
-  __syncthreads();
   // Waves 1 .. n_producers pre-evaluate the specials in id order into the
   // ring, while wave 0 (the walker) starts at once.  The walker waits only
   // for the special it needs next; the producer of that special handles its
@@ -1055,7 +1093,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
   // consumed, which it is by then -- so every wait ends.
   // A walk that stops early (a stop hit) marks itself over
   // (PZ_WALK_DONE), which ends every producer's wait and loop.
-  for (int j = w - 1; w > 0 && w <= n_producers && j < sbase; j += n_producers) {
+  for (int j = w - 1; w > 0 && w <= n_producers && j < W.n_spec; j += n_producers) {
     uint32_t c = __hip_atomic_load((uint32_t*)W.consumed, __ATOMIC_ACQUIRE,
                                    __HIP_MEMORY_SCOPE_WORKGROUP);
     if (j >= nc)
