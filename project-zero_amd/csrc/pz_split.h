@@ -1047,33 +1047,35 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
       const uint32_t incl = pz_wave_scan_u32(d);
       const uint64_t sb = __ballot(special);
       const uint64_t cb = __ballot(chg);
-      __syncthreads();
+      // (the caller's barrier orders the first chunk's writes of S after
+      // earlier uses of it; later chunks wait for the reads of the last)
+      if (c0 > 0) __syncthreads();
       if (lane == 63) S.list[w] = (int)incl;  // wave totals
       if (lane == 0) {
         S.red[w] = __int_as_float(__popcll(sb));
         S.red2[w] = (uint32_t)__popcll(cb);
       }
       __syncthreads();
-      // the waves' totals, one per lane, summed by wave reductions (mod 2^32)
+      // the waves' totals, one per lane: inclusive scans, read at this wave
+      // (exclusive) and at the last (the chunk's totals), mod 2^32
       const bool in_w = lane < nw;
       const uint32_t lt = in_w ? (uint32_t)S.list[lane] : 0u;
       const uint32_t ls = in_w ? (uint32_t)__float_as_int(S.red[lane]) : 0u;
       const uint32_t lc = in_w ? S.red2[lane] : 0u;
-      const uint32_t off = base + pz_wave_sum_u32(lane < w ? lt : 0u);
-      const int soff = sbase + (int)pz_wave_sum_u32(lane < w ? ls : 0u);
-      const uint32_t coff = cbase + pz_wave_sum_u32(lane < w ? lc : 0u);
-      const uint32_t tot = pz_wave_sum_u32(lt), ctot = pz_wave_sum_u32(lc);
-      const int stot = (int)pz_wave_sum_u32(ls);
+      const uint32_t it = pz_wave_scan_u32(lt), is = pz_wave_scan_u32(ls),
+                     ic = pz_wave_scan_u32(lc);
+      const uint32_t off = base + pz_readlane_u32(it - lt, w);
+      const int soff = sbase + (int)pz_readlane_u32(is - ls, w);
+      const uint32_t coff = cbase + pz_readlane_u32(ic - lc, w);
       const uint64_t below = (1ull << lane) - 1ull;
       if (k < nseg) {
         W.pd[k] = off + incl - d;
         W.chp[k] = coff + (uint32_t)__popcll(cb & below);
         if (special) W.spk[soff + __popcll(sb & below)] = k;
       }
-      base += tot;
-      sbase += stot;
-      cbase += ctot;
-      __syncthreads();
+      base += pz_readlane_u32(it, nw - 1);
+      sbase += (int)pz_readlane_u32(is, nw - 1);
+      cbase += pz_readlane_u32(ic, nw - 1);
     }
     if (tid == 0) {
       W.pd[nseg] = base;
