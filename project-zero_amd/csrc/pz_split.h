@@ -1165,6 +1165,29 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
   return W;
 }
 
+// A row's records loaded ahead into registers (thread k: segment k, for rows
+// of at most blockDim.x segments; else off), so that their latency passes
+// while the kernel does other set-up work; pz_sp_walk_setup stores them.
+struct PzRecAhead {
+  uint32_t d, d2, gf;
+  bool on;
+};
+
+__device__ __forceinline__ PzRecAhead pz_sp_rec_ahead(const PzSplitWs& ws, int row, int nseg) {
+  PzRecAhead a;
+  a.on = nseg <= (int)blockDim.x;
+  a.d = 0u;
+  a.d2 = 0u;
+  a.gf = PZ_NO_RECORD;
+  const int k = threadIdx.x;
+  if (a.on && k < nseg) {
+    a.d = pz_sp_rec_d(ws, row)[k];
+    a.d2 = pz_sp_rec_d2(ws, row)[k];
+    a.gf = pz_sp_rec_gf(ws, row)[k];
+  }
+  return a;
+}
+
 // Stages the row's records in LDS, lists every special segment (dirty,
 // crossing, or without a record) in id order, and starts the pre-evaluation
 // of the specials into the ring: exact terms (X::seg) and increment
@@ -1173,20 +1196,30 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
 // barrier: waves 1 .. n_producers keep filling the ring while the walker
 // (wave 0) consumes it (pz_sp_load_slot), the other waves may go on to other
 // work.  Any block size that is a multiple of 64, up to 1024.  s0_pre as for
-// pz_sp_walk_start.
+// pz_sp_walk_start; ahead: the records already loaded (pz_sp_rec_ahead).
 template <class X>
 __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg, int nc,
                                                    const PzSplitWs& ws, char* lds,
                                                    PzSpShared& S, int n_producers = -1,
-                                                   uint32_t s0_pre = 0xffffffffu) {
+                                                   uint32_t s0_pre = 0xffffffffu,
+                                                   const PzRecAhead* ahead = nullptr) {
   PzWalk W = pz_sp_walk_layout(lds, nseg, nc);
-  const uint32_t* rd = pz_sp_rec_d(ws, row);
-  const uint32_t* rd2 = pz_sp_rec_d2(ws, row);
-  const uint32_t* rgf = pz_sp_rec_gf(ws, row);
-  for (int k = threadIdx.x; k < nseg; k += blockDim.x) {
-    W.d[k] = rd[k];
-    W.d2[k] = rd2[k];
-    W.gf[k] = rgf[k];
+  if (ahead && ahead->on) {
+    const int k = threadIdx.x;
+    if (k < nseg) {
+      W.d[k] = ahead->d;
+      W.d2[k] = ahead->d2;
+      W.gf[k] = ahead->gf;
+    }
+  } else {
+    const uint32_t* rd = pz_sp_rec_d(ws, row);
+    const uint32_t* rd2 = pz_sp_rec_d2(ws, row);
+    const uint32_t* rgf = pz_sp_rec_gf(ws, row);
+    for (int k = threadIdx.x; k < nseg; k += blockDim.x) {
+      W.d[k] = rd[k];
+      W.d2[k] = rd2[k];
+      W.gf[k] = rgf[k];
+    }
   }
   __syncthreads();
   return pz_sp_walk_start(x, W, S, n_producers, s0_pre);

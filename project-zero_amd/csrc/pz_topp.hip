@@ -1782,8 +1782,9 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     for (int i = t0; i < S * PZ_TOPP_NB; i += nt) hrow[i] = 0u;
   };
   // the nucleus bins (k_topp_front, workgroup 0): loaded at once, beside the
-  // row's maxima below
+  // row's maxima below, and the row's records for the walk
   const PzRowState rs0 = ws.rs[row];
+  const PzRecAhead ra = pz_sp_rec_ahead(ws, row, nseg);
   if (tid == 0) {
     // the gathered count, re-armed for the next call, and the selection word
     m_sh = (int)ws.arrive[row];
@@ -1853,7 +1854,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
   pz_lds_u64* bkeys = (pz_lds_u64*)(lds + sort_off + wf_keys_off(cap));
   const uint64_t* gkeys = ws.keys + (size_t)row * ws.capg;
   // (segment 0's sum: posted by the front launch)
-  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, region, SS, 7, rs0.s0);
+  const PzWalk W = pz_sp_walk_setup(X, row, nseg, nc, ws, region, SS, 7, rs0.s0, &ra);
   if (w == 0) {
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
