@@ -486,6 +486,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_attn_walk(AttnSplit A) {
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = blockIdx.x, len = attn_len(A, row);
   if (len <= 0) return;
+  const PzRecAhead ra = pz_sp_rec_ahead(A.ws, row, A.nseg);  // in flight beside the maxima
   pz_sp_row_stat(row, A.S, A.ws, SS);
   PzRowState& rs = A.ws.rs[row];
   if (attn_bad(SS.any)) {
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_attn_walk(AttnSplit A) {
   X.inv = 1.0f;
   X.as_p = false;
   X.et = (const pz_lds_u64*)etab;
-  const PzWalk W = pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds, SS);
+  const PzWalk W = pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds, SS, -1, 0xffffffffu, &ra);
   if (threadIdx.x < 64) {
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);

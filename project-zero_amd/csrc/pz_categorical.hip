@@ -243,6 +243,7 @@ __global__ __launch_bounds__(CAT_WALK_BLOCK) void k_cat_walk(CatArgs A, int pen_
   __shared__ float sum_sh;
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = pz_row_of(A.rows, blockIdx.x);
+  const PzRecAhead ra = pz_sp_rec_ahead(A.ws, row, A.nseg);  // in flight beside the maxima
   PzRowState& rs = A.ws.rs[row];
   const int failed = rs.i[7];
   pz_sp_clear_meet(A.ws, row);  // the front launch's meetings are over
@@ -269,7 +270,8 @@ __global__ __launch_bounds__(CAT_WALK_BLOCK) void k_cat_walk(CatArgs A, int pen_
   X.as_p = false;
   X.et = (const pz_lds_u64*)etab;
   __syncthreads();
-  const PzWalk W = pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds + pen_bytes, SS);
+  const PzWalk W =
+      pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds + pen_bytes, SS, -1, 0xffffffffu, &ra);
   if (threadIdx.x < 64) {
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
@@ -320,6 +322,7 @@ __global__ __launch_bounds__(CAT_WALK_BLOCK) void k_cat_draw(CatArgs A, int pen_
   __shared__ int hit_sh;
   pz_etab_fill((pz_lds_u64*)etab);
   const int row = pz_row_of(A.rows, blockIdx.x);
+  const PzRecAhead ra = pz_sp_rec_ahead(A.ws, row, A.nseg);  // in flight beside the row state
   const PzRowState rs = A.ws.rs[row];
   if (cat_bad(rs.flags)) {
     if (threadIdx.x == 0) {
@@ -342,7 +345,8 @@ __global__ __launch_bounds__(CAT_WALK_BLOCK) void k_cat_draw(CatArgs A, int pen_
   X.et = (const pz_lds_u64*)etab;
   const float r = A.u[row];
   __syncthreads();
-  const PzWalk W = pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds + pen_bytes, SS);
+  const PzWalk W =
+      pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds + pen_bytes, SS, -1, 0xffffffffu, &ra);
   if (threadIdx.x < 64) {
     PzAcc st;
     int hit = pz_sp_walk<PZ_STOP_GT>(st, W, r, X);

@@ -200,6 +200,7 @@ __global__ __launch_bounds__(SPEC_WALK_BLOCK) void k_spec_walk(SpecArgs A) {
   __shared__ float sum_sh;
   pz_etab_fill((pz_lds_u64*)etab);
   const int q = blockIdx.x;
+  const PzRecAhead ra = pz_sp_rec_ahead(A.ws, q, A.nseg);  // in flight beside the maxima
   pz_sp_row_stat(q, A.S, A.ws, SS);
   PzRowState& rs = A.ws.rs[q];
   if (spec_bad(SS.any)) {
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(SPEC_WALK_BLOCK) void k_spec_walk(SpecArgs A) {
   X.inv = 1.0f;
   X.as_p = false;
   X.et = (const pz_lds_u64*)etab;
-  const PzWalk W = pz_sp_walk_setup(X, q, A.nseg, A.nc, A.ws, lds, SS);
+  const PzWalk W = pz_sp_walk_setup(X, q, A.nseg, A.nc, A.ws, lds, SS, -1, 0xffffffffu, &ra);
   if (threadIdx.x < 64) {
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
@@ -441,14 +442,15 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vwalk(SpecArgs A) {
   const pz_lds_u64* et = (const pz_lds_u64*)etab;
   pz_etab_fill((pz_lds_u64*)etab);
   const int b = blockIdx.x;
+  const int r = A.NR + b;
+  const PzRecAhead ra = pz_sp_rec_ahead(A.ws, r, A.nseg);  // in flight beside the sequence's
   const SpecSeq s = A.seq[b];
   if (s.mode == SQ_DONE) return;
-  const int r = A.NR + b;
   const float ur = A.u_res[b];
   int tok;
   if (s.mode == SQ_RES) {
     const ResidualTerms<VEC> X = residual_terms<VEC>(A, s, et);
-    const PzWalk W = pz_sp_walk_setup(X, r, A.nseg, A.nc, A.ws, lds, SS);
+    const PzWalk W = pz_sp_walk_setup(X, r, A.nseg, A.nc, A.ws, lds, SS, -1, 0xffffffffu, &ra);
     if (threadIdx.x < 64) {
       PzAcc st;
       PzWalkCk ck;
@@ -481,7 +483,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_spec_vwalk(SpecArgs A) {
     }
   } else {
     const PzExpTerms<PzTempRow<VEC>> X = p_terms<VEC>(A, s.qt, et);
-    const PzWalk W = pz_sp_walk_setup(X, r, A.nseg, A.nc, A.ws, lds, SS);
+    const PzWalk W = pz_sp_walk_setup(X, r, A.nseg, A.nc, A.ws, lds, SS, -1, 0xffffffffu, &ra);
     if (threadIdx.x < 64) {
       PzAcc st;
       int hit = pz_sp_walk<PZ_STOP_GT>(st, W, ur, X);
