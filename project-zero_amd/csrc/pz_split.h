@@ -269,6 +269,7 @@ struct PzSpShared {
   int cnt;
   int tail_end;
   float carry;
+  uint32_t s0;  // a first-segment sum handed to the walk's set-up (bits)
   int list[PZ_SP_NC];
 };
 
@@ -422,6 +423,25 @@ __device__ __forceinline__ void pz_sp_predict(const Est& est, float carry, int r
     if (lgf) pz_lds_barrier();
     else __syncthreads();
   };
+  if (sl.k1 - sl.k0 <= 64) {
+    // one segment per lane of wave 0 (the same scan and sums as below with
+    // a single wave), one barrier
+    if (w == 0) {
+      const int k = sl.k0 + lane;
+      const float e = k < sl.k1 ? est(k) : 0.0f;
+      const float incl = pz_wave_scan_f32(e);
+      const float start = (carry + 0.0f) + (incl - e), end = (carry + 0.0f) + incl;
+      if (k < sl.k1) {
+        const uint32_t v =
+            pz_predict_gf(start) | (pz_grid_of(end) != pz_grid_of(start) ? PZ_GF_XING : 0u);
+        gf[k] = v;
+        if (lgf) lgf[k - sl.k0] = v;
+      }
+      if (lane == 63) S.carry = end;
+    }
+    barrier();
+    return;
+  }
   if (tid == 0) S.carry = carry;
   barrier();
   for (int c0 = sl.k0; c0 < sl.k1; c0 += PZ_SP_BLOCK) {

@@ -1250,7 +1250,12 @@ __device__ __forceinline__ int nucleus_pick(const X& xs, int m, int row0, float 
     float v[4];
     xs.seg(k, v);
     const float t = pz_wave_sum((v[0] + v[1]) + (v[2] + v[3]));
-    if (lane == 0) est[k] = t;
+    // (segment 0: also its sequential sum from zero, for the first walk)
+    const float s0 = k == 0 ? pz_seq_sum_seg4(v) : 0.0f;
+    if (lane == 0) {
+      est[k] = t;
+      if (k == 0) SS.s0 = __float_as_uint(s0);
+    }
   }
   __syncthreads();
   PzSlice sl;
@@ -1290,7 +1295,7 @@ __device__ __forceinline__ int nucleus_pick(const X& xs, int m, int row0, float 
     }
   }
   __syncthreads();
-  const PzWalk W = pz_sp_walk_setup(xs, row, nsl, nc, ws, region, SS);
+  const PzWalk W = pz_sp_walk_setup(xs, row, nsl, nc, ws, region, SS, -1, SS.s0);
   if (w == 0) {
     PzAcc st;
     PzWalkCk ck;

@@ -216,3 +216,24 @@ def test_short_lists(torch_cuda, top_p):
     u[0], u[1], u[70] = 0.0, 1.0, 1.0
     check(torch_cuda, x, [pz.row_params(temperature=1.0, top_p=top_p)], u,
           label=f"short lists p={top_p}")
+
+
+def test_cutoff_inside_the_first_segment_of_a_long_list(torch_cuda):
+    """A long gathered list (3000 candidates spread over the nucleus bins
+    behind 200 large ones) whose cumulative reaches top_p within its first
+    256 sorted keys (row 0: about 33 past the large ones) or well past them
+    (row 1), so the cut-off walk stops inside the list's first segment,
+    whose sum comes with the walk's set-up, or after it."""
+    B, V = 2, 128256
+    rng = np.random.default_rng(77)
+    x = np.full((B, V), -30.0, np.float32)
+    for b, gap in ((0, 4.9), (1, 4.5)):  # cut-offs near 233 and 956
+        big = rng.choice(V, 200, replace=False)
+        rest = np.setdiff1d(np.arange(V), big)
+        small = rng.choice(rest, 3000, replace=False)
+        x[b, small] = (1.0 + rng.uniform(-0.3, 0.3, 3000)).astype(np.float32)
+        x[b, big] = (1.0 + gap + rng.uniform(-1e-3, 1e-3, 200)).astype(np.float32)
+    u = pz.synth_draws(B, 78)
+    check(torch_cuda, x, [pz.row_params(temperature=1.0, top_p=0.9)], u, label="long list")
+    check(torch_cuda, x, [pz.row_params(temperature=1.0, top_p=0.9)], np.array([0.999, 0.0], np.float32),
+          label="long list, u at the ends")
