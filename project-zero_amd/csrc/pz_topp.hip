@@ -582,7 +582,12 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   const int row = pz_row_of(rows, blockIdx.y);
   const pz_row_params_dev& prm = pz_params_of(params, n_params, row);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const PzSlice sl = pz_sp_slice(nseg, spw);
+  // this workgroup's slice: rotated by the row's place in the launch, so that
+  // the slices' roles (slice 0 goes on past meeting 2 at once, the last one
+  // merges the histograms) spread over the XCDs, which receive consecutive
+  // workgroups in turn
+  const int sx = (int)((blockIdx.x + blockIdx.y) % (unsigned)S);
+  const PzSlice sl = pz_sp_slice_at(sx, nseg, spw);
   const int lo = pz_sp_lo(sl);
   pz_lds_u32b* ehist = (pz_lds_u32b*)(lds + pen_bytes);
   pz_lds_f32* ybuf = (pz_lds_f32*)(lds + (((size_t)pen_bytes + PZ_TOPP_NB * 4 + 15) & ~(size_t)15));
@@ -642,14 +647,14 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
                           : 0.0f;
   if (tid == 0) {
     uint32_t f = SS.any;
-    ws.slice_m[(size_t)row * ws.smax + blockIdx.x] = mm;
-    ws.slice_f[(size_t)row * ws.smax + blockIdx.x] = f;
-    if (blockIdx.x == 0) {
+    ws.slice_m[(size_t)row * ws.smax + sx] = mm;
+    ws.slice_f[(size_t)row * ws.smax + sx] = f;
+    if (sx == 0) {
       ws.rs[row].y0 = ybuf[0];
       if (ybuf[0] != ybuf[0]) f |= PZ_RS_Y0NAN;
     }
     // meet 1: every slice's maximum and flags
-    __hip_atomic_store(&meet[blockIdx.x],
+    __hip_atomic_store(&meet[sx],
                        (1ull << 63) | ((uint64_t)f << 32) | (uint64_t)__float_as_uint(mm),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -679,13 +684,13 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   if (fail_sh) {
     // meet 1 gave up: post what the others wait for (an empty histogram, no
     // mass), mark the row and leave
-    uint32_t* gh = ws.hist + ((size_t)blockIdx.y * S + blockIdx.x) * PZ_TOPP_NB;
+    uint32_t* gh = ws.hist + ((size_t)blockIdx.y * S + sx) * PZ_TOPP_NB;
     for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK)
       __hip_atomic_store(&gh[i], topp_hword(0u), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
-      __hip_atomic_store(&meet[ws.smax + blockIdx.x], 1ull << 63, __ATOMIC_RELAXED,
+      __hip_atomic_store(&meet[ws.smax + sx], 1ull << 63, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
-      if (blockIdx.x == S - 1)  // the others wait for its selection
+      if (sx == S - 1)  // the others wait for its selection
         __hip_atomic_store(&ws.rs[row].i[6], (int)topp_sel_word(TOPP_SEL_FAILED, 0u),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       topp_mark_failed(ws, row);
@@ -698,7 +703,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   // held in registers: the gather stages keys over the slice in LDS, and the
   // row's last slice reaches it without a barrier after its records
   pz_f4 seg0 = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (blockIdx.x == 0 && w == 1) seg0 = *(const pz_lds_f4*)(ybuf + 4 * lane);
+  if (sx == 0 && w == 1) seg0 = *(const pz_lds_f4*)(ybuf + 4 * lane);
   // 2. the estimated candidate mass of each segment (as k_topp_est) and the
   // histogram of the estimated e (the nucleus bins), the slice's total for
   // the slices after it
@@ -724,7 +729,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   pz_lds_barrier();
   uint32_t* hrow = ws.hist + (size_t)blockIdx.y * S * PZ_TOPP_NB;
   if (!degen) {
-    uint32_t* gh = hrow + (size_t)blockIdx.x * PZ_TOPP_NB;
+    uint32_t* gh = hrow + (size_t)sx * PZ_TOPP_NB;
     for (int i = tid; i < PZ_TOPP_NB; i += PZ_SP_BLOCK)
       __hip_atomic_store(&gh[i], topp_hword(ehist[i]), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
@@ -734,14 +739,14 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       w == 0 && !degen ? pz_wave_sum(lane < sl.k1 - sl.k0 ? sest[lane] : 0.0f) : 0.0f;
   if (tid == 0) {
     // meet 2: every slice's estimated mass
-    __hip_atomic_store(&meet[ws.smax + blockIdx.x], (1ull << 63) | (uint64_t)__float_as_uint(tot),
+    __hip_atomic_store(&meet[ws.smax + sx], (1ull << 63) | (uint64_t)__float_as_uint(tot),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (degen) return;  // (every workgroup of the row; the words are cleared all the same)
   if (w == 0) {
     uint64_t v = 1ull << 63;
     for (uint32_t n = 1;; n++) {
-      if (lane < (int)blockIdx.x)
+      if (lane < sx)
         v = __hip_atomic_load(&meet[ws.smax + lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (__ballot((v >> 63) == 0) == 0) break;
       if (n >= cap) {
@@ -751,13 +756,13 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       __builtin_amdgcn_s_sleep(1);
     }
     // the estimated mass before this slice
-    const float carry = pz_wave_sum(lane < (int)blockIdx.x ? __uint_as_float((uint32_t)v) : 0.0f);
+    const float carry = pz_wave_sum(lane < sx ? __uint_as_float((uint32_t)v) : 0.0f);
     if (lane == 0) SS.carry = carry;
   }
   pz_lds_barrier();
   if (fail_sh) {  // (this workgroup's histogram and meet-2 word are posted)
     if (tid == 0) topp_mark_failed(ws, row);
-    if (blockIdx.x == S - 1 && tid == 0)  // the others wait for its selection
+    if (sx == S - 1 && tid == 0)  // the others wait for its selection
       __hip_atomic_store(&ws.rs[row].i[6], (int)topp_sel_word(TOPP_SEL_FAILED, 0u),
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
@@ -767,7 +772,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   // polls end at once) and posts the selection for the others, which take
   // it after their records -- one workgroup per row reads the S histograms
   ToppSel sel;
-  if (blockIdx.x == S - 1) {
+  if (sx == S - 1) {
     sel = topp_front_select(hrow, S, cap, ehist, prm.top_p, &sel_sh, part_sh, &fail_sh);
     if (tid == 0)
       __hip_atomic_store(&ws.rs[row].i[6],
@@ -787,7 +792,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   X.as_p = false;
   X.et = et;
   pz_sp_records(X, row, sl, ws, (const pz_lds_u32*)sgf, true);
-  if (blockIdx.x == 0 && w == 1) {
+  if (sx == 0 && w == 1) {
     // the row's first segment, summed for the walk (wave 1: wave 0's first
     // thread waits for the selection meanwhile)
     const int e0 = 4 * lane;
@@ -798,7 +803,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
     const float s0 = pz_seq_sum_seg4(t);
     if (lane == 0) ws.rs[row].s0 = __float_as_uint(s0);
   }
-  if (blockIdx.x != S - 1) {
+  if (sx != S - 1) {
     if (tid == 0) {
       uint32_t v = 0;
       for (uint32_t t = 1;; t++) {
@@ -821,7 +826,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
   const bool all = sel.bsel == 0;
   const float e_gate = all ? 0.0f : ebin_lo(sel.bsel);
   const float dgate = all ? -__builtin_inff() : __logf(e_gate) - 0.01f;
-  if (blockIdx.x == 0 && tid == 0) {
+  if (sx == 0 && tid == 0) {
     PzRowState& rs = ws.rs[row];
     rs.M = M;
     rs.f[0] = e_gate;
