@@ -755,6 +755,23 @@ inline PzSplitPlan pz_front_plan(int V, int nrows, int smax) {
 typedef uint32_t pz_u4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) pz_u4 pz_lds_u4;
 typedef __attribute__((address_space(3))) uint8_t pz_lds_u8;
+typedef __attribute__((address_space(3))) uint16_t pz_lds_u16h;
+
+// One slot of the walk's ring, every part at a fixed offset from the slot's
+// base, so that a slot is read through one address: the exact terms, the
+// inclusive increment prefix at the slot's grid g0 and at g1 (the grid the
+// segment is expected to end in), per lane the flag bits at g0 (low byte)
+// and g1 (high byte), then four scalars (g0; g1 | first tie at g0 << 8 |
+// (last flagged at g1 + 1) << 17; the prefix at g0 at the first tie; the
+// parity corrections of the later ties at g0).  The flag bytes hold per
+// term (low nibble) whether it is flagged (a tie or big) and (high nibble)
+// whether it is a tie.
+constexpr int PZ_SLOT_PA = PZ_SP_SEG * 4;
+constexpr int PZ_SLOT_PB = 2 * PZ_SP_SEG * 4;
+constexpr int PZ_SLOT_FL = 3 * PZ_SP_SEG * 4;
+constexpr int PZ_SLOT_SC = PZ_SLOT_FL + 64 * 2;
+constexpr int PZ_SP_SLOT = PZ_SLOT_SC + 16;  // bytes per slot (a multiple of 16)
+static_assert(PZ_SP_SLOT % 16 == 0, "slots stay 16-byte aligned");
 
 constexpr uint32_t PZ_WALK_DONE = 0xffffffffu;  // consumed: the walk is over
 
@@ -769,16 +786,7 @@ struct PzWalk {
   // Ring of nc pre-evaluated specials: special j sits in slot j % nc once
   // rdy[slot] == j + 1; a producer rewrites a slot only after the walker has
   // consumed the special before (consumed > j - nc).
-  pz_lds_f32* terms;  // [nc][256] exact terms
-  pz_lds_u32* pa;     // [nc][256] inclusive increment prefix at the slot's grid g0
-  pz_lds_u32* pb;     // [nc][256] the same at g1 (the grid the segment is expected to end in)
-  pz_lds_u8* fa;      // [nc][64] per lane: flagged (tie / big) terms at g0 (low nibble)
-                      //          and the ties among them (high nibble)
-  pz_lds_u8* fb;      // [nc][64] the same at g1
-  pz_lds_i32* g0;     // [nc] the grid of pa (the record's grid)
-  pz_lds_u32* sinfo;  // [nc] g1 | first tie at g0 << 8 | (last flagged at g1 + 1) << 17
-  pz_lds_u32* spt1;   // [nc] pa at the first tie
-  pz_lds_u32* stc;    // [nc] parity corrections of the later ties at g0
+  pz_lds_u8* ring;    // [nc][PZ_SP_SLOT] the slots
   pz_lds_u32* rdy;    // [nc] special + 1 held by the slot (0: none yet)
   pz_lds_u32* consumed;  // specials the walker has read out of the ring (PZ_WALK_DONE:
                          // the walk is over, the producers stop)
@@ -792,9 +800,10 @@ struct PzWalk {
 // LDS of the walk for a row of nseg segments with a ring of nc pre-evaluated
 // specials: six words per segment plus the prefixes' extra words, the ring's
 // counter and 1 KB of staging; per slot its terms, two increment prefixes,
-// two flag masks and five scalars.
+// two flag masks and four scalars, and its ready word.
 __host__ __device__ inline size_t pz_sp_walk_lds(int nseg, int nc) {
-  return (size_t)nseg * 24 + 64 + PZ_SP_SEG * 4 + (size_t)nc * (3 * PZ_SP_SEG * 4 + 2 * 64 + 20);
+  return (size_t)nseg * 24 + 64 + PZ_SP_SEG * 4 + (size_t)nc * PZ_SP_SLOT +
+         (((size_t)nc * 4 + 15) & ~(size_t)15);
 }
 
 // Ring slots of the walk within max_lds bytes (0 when fewer than two fit:
@@ -972,16 +981,8 @@ __device__ __forceinline__ PzWalk pz_sp_walk_layout(char* lds, int nseg, int nc)
   W.nseg = nseg;
   W.nc = nc;
   char* p = lds;
-  W.terms = (pz_lds_f32*)p;    p += (size_t)nc * PZ_SP_SEG * 4;
-  W.pa = (pz_lds_u32*)p;       p += (size_t)nc * PZ_SP_SEG * 4;
-  W.pb = (pz_lds_u32*)p;       p += (size_t)nc * PZ_SP_SEG * 4;
-  W.fa = (pz_lds_u8*)p;        p += (size_t)nc * 64;
-  W.fb = (pz_lds_u8*)p;        p += (size_t)nc * 64;
-  W.g0 = (pz_lds_i32*)p;       p += (size_t)nc * 4;
-  W.sinfo = (pz_lds_u32*)p;    p += (size_t)nc * 4;
-  W.spt1 = (pz_lds_u32*)p;     p += (size_t)nc * 4;
-  W.stc = (pz_lds_u32*)p;      p += (size_t)nc * 4;
-  W.rdy = (pz_lds_u32*)p;      p += (size_t)nc * 4;
+  W.ring = (pz_lds_u8*)p;      p += (size_t)nc * PZ_SP_SLOT;
+  W.rdy = (pz_lds_u32*)p;      p += ((size_t)nc * 4 + 15) & ~(size_t)15;
   W.consumed = (pz_lds_u32*)p; p += 16;
   W.s0 = W.consumed + 1;
   W.tmp = (pz_lds_f32*)p;      p += PZ_SP_SEG * 4;
@@ -1128,6 +1129,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
     const int k = W.spk[j];
     if (j == 0 && k == 0 && W.pre0) continue;  // summed before the walk: no slot
     const int sl = j % nc;
+    pz_lds_u8* sb = W.ring + (size_t)sl * PZ_SP_SLOT;
     float v[4];
     x.seg(k, v);
     const uint32_t gf = W.gf[k];
@@ -1146,19 +1148,17 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
     q.y = v[1];
     q.z = v[2];
     q.w = v[3];
-    ((pz_lds_f4*)(W.terms + sl * PZ_SP_SEG))[lane] = q;
+    ((pz_lds_f4*)sb)[lane] = q;
     pz_u4 a4, b4;
     a4.x = d.P[0]; a4.y = d.P[1]; a4.z = d.P[2]; a4.w = d.P[3];
     b4.x = d.Q[0]; b4.y = d.Q[1]; b4.z = d.Q[2]; b4.w = d.Q[3];
-    ((pz_lds_u4*)(W.pa + sl * PZ_SP_SEG))[lane] = a4;
-    ((pz_lds_u4*)(W.pb + sl * PZ_SP_SEG))[lane] = b4;
-    W.fa[sl * 64 + lane] = (uint8_t)d.fa;
-    W.fb[sl * 64 + lane] = (uint8_t)d.fb;
+    ((pz_lds_u4*)(sb + PZ_SLOT_PA))[lane] = a4;
+    ((pz_lds_u4*)(sb + PZ_SLOT_PB))[lane] = b4;
+    ((pz_lds_u16h*)(sb + PZ_SLOT_FL))[lane] = (uint16_t)((d.fa & 0xffu) | ((d.fb & 0xffu) << 8));
     if (lane == 0) {
-      W.g0[sl] = (int)g;
-      W.sinfo[sl] = inf.sinfo;
-      W.spt1[sl] = inf.pt1;
-      W.stc[sl] = inf.tc;
+      pz_u4 sc;
+      sc.x = g; sc.y = inf.sinfo; sc.z = inf.pt1; sc.w = inf.tc;
+      *(pz_lds_u4*)(sb + PZ_SLOT_SC) = sc;
     }
     if (j == 0 && k == 0 && lane == 0) {
       // the row's first segment from a zero sum, where nearly every term is
@@ -1166,7 +1166,7 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
       // one step (one lane, the terms read back in id order; reading them
       // out of the wave's registers with v_readlane is slower: each add
       // waits for the scalar register the readlane writes)
-      const pz_lds_f4* tq = (const pz_lds_f4*)(W.terms + sl * PZ_SP_SEG);
+      const pz_lds_f4* tq = (const pz_lds_f4*)sb;
       float sum0 = 0.0f;
       for (int i = 0; i < PZ_SP_SEG / 4; i++) {
         const pz_f4 t4 = tq[i];
@@ -1582,15 +1582,18 @@ __device__ __forceinline__ int pz_sp_ready_count(const PzWalk& W, int j1, int s1
 // once in the ring.
 __device__ __forceinline__ void pz_sp_load_slot_at(const PzWalk& W, int s, PzSpSeg& d) {
   const int lane = threadIdx.x & 63;
-  d.g0 = (uint32_t)W.g0[s];
-  d.sinfo = W.sinfo[s];
-  d.pt1 = W.spt1[s];
-  d.tc = W.stc[s];
-  const pz_f4 q = ((const pz_lds_f4*)(W.terms + s * PZ_SP_SEG))[lane];
-  const pz_u4 a4 = ((const pz_lds_u4*)(W.pa + s * PZ_SP_SEG))[lane];
-  const pz_u4 b4 = ((const pz_lds_u4*)(W.pb + s * PZ_SP_SEG))[lane];
-  d.fa = W.fa[s * 64 + lane];
-  d.fb = W.fb[s * 64 + lane];
+  const pz_lds_u8* sb = W.ring + (size_t)s * PZ_SP_SLOT;
+  const pz_u4 sc = *(const pz_lds_u4*)(sb + PZ_SLOT_SC);
+  d.g0 = sc.x;
+  d.sinfo = sc.y;
+  d.pt1 = sc.z;
+  d.tc = sc.w;
+  const pz_f4 q = ((const pz_lds_f4*)sb)[lane];
+  const pz_u4 a4 = ((const pz_lds_u4*)(sb + PZ_SLOT_PA))[lane];
+  const pz_u4 b4 = ((const pz_lds_u4*)(sb + PZ_SLOT_PB))[lane];
+  const uint32_t fl = ((const pz_lds_u16h*)(sb + PZ_SLOT_FL))[lane];
+  d.fa = fl & 0xffu;
+  d.fb = fl >> 8;
   d.v[0] = q.x; d.v[1] = q.y; d.v[2] = q.z; d.v[3] = q.w;
   d.P[0] = a4.x; d.P[1] = a4.y; d.P[2] = a4.z; d.P[3] = a4.w;
   d.Q[0] = b4.x; d.Q[1] = b4.y; d.Q[2] = b4.z; d.Q[3] = b4.w;
@@ -1838,7 +1841,8 @@ __device__ __forceinline__ int pz_sp_walk_run(PzAcc& st, const PzWalk& W, float 
           Q[c] = cur.Q[c];
         }
         const int r = pz_sp_events<MODE>(st, cur.v, g0, P, cur.fa & 15u, si & 0xffu, Q,
-                                         cur.fb & 15u, thr, W.terms + slot * PZ_SP_SEG);
+                                         cur.fb & 15u, thr,
+                                         (pz_lds_f32*)(W.ring + (size_t)slot * PZ_SP_SLOT));
         if (r >= 0) return b * PZ_SP_SEG + r;
       }
     }
