@@ -9,11 +9,10 @@
 // per 256-thread workgroup): the row sits in the wave's registers, 4
 // consecutive scores per lane per 256-score segment, so the maximum, the
 // exponentials, the exact sum and the write need no LDS beyond the exp
-// table.  The sum is the exact sequential one (pz_exact.h): the first
-// segment by serial fp32 adds, every later one through the integer state --
-// a segment with at most one binade exit and no tie in one step
-// (pz_sp_fast), else one ballot per event over the segment's increment
-// prefix, each taken with one exact add (pz_sp_events).  Rows of more than
+// table.  The sum is the exact sequential one (pz_exact.h): every segment
+// through the integer state -- a segment with at most one binade exit and
+// no tie before it in one step (pz_sp_fast) -- else, and for the first
+// segment, by its 256 real fp32 adds in order (the DPP chain, pz_sp_chain).  Rows of more than
 // ATTN_WAVE_SHORT scores (and up to ATTN_ROW_MAX) take one 1024-thread
 // workgroup each instead (k_attn_row): its 16 waves estimate every 256-score
 // segment's mass, predict the binade the running sum sits in at each
@@ -39,20 +38,20 @@ constexpr int ATTN_WAVE_MAX = 16 * 256;     // longest row of the wave kernel
 #endif
 
 // One 256-term segment added to the running sum st (the whole wave, lane l
-// holding terms 4l .. 4l+3): serial fp32 adds from a zero sum, else the
-// events of the increment prefixes at the state's binade and the next.  Out
+// holding terms 4l .. 4l+3): the one-step form when no tie or big term comes
+// before the term that leaves the binade, else the sequential chain of real
+// fp32 adds (always from a zero sum).  Out
 // of line so the unrolled segment loop holds one copy.
 __device__ __noinline__ PzAcc attn_seg_sum(PzAcc st, float a, float b, float c, float d) {
   const float v[4] = {a, b, c, d};
   if (st.n == 0u && st.g == 1u) {
-    pz_sp_serial<PZ_STOP_NONE>(st, v, 0, 0.0f);
+    pz_sp_chain<PZ_STOP_NONE>(st, v, 0.0f);
   } else {
     uint32_t P[4], Q[4], fP, fQ;
     const uint32_t g0 = st.g;
     pz_sp_prefix4(v, g0, P, fP);
     pz_sp_prefix4(v, g0 + 1u, Q, fQ);
-    if (!pz_sp_fast<PZ_STOP_NONE>(st, v, P, fP, Q, fQ, 0.0f))
-      pz_sp_events<PZ_STOP_NONE>(st, v, g0, P, fP, g0 + 1u, Q, fQ, 0.0f);
+    if (!pz_sp_fast<PZ_STOP_NONE>(st, v, P, fP, Q, fQ, 0.0f)) pz_sp_chain<PZ_STOP_NONE>(st, v, 0.0f);
   }
   pz_sp_uni(st);
   return st;

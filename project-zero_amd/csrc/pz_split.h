@@ -792,17 +792,16 @@ struct PzWalk {
                          // the walk is over, the producers stop)
   pz_lds_u32* s0;     // the sequential fp32 sum of segment 0's terms from 0 (bits), when
                       // segment 0 is special 0 (else 0xffffffff)
-  pz_lds_f32* tmp;    // [256] terms of a segment evaluated during the walk
   int nseg, nc, n_spec;
   bool pre0;  // s0 came with the set-up: segment 0 has no ring slot
 };
 
 // LDS of the walk for a row of nseg segments with a ring of nc pre-evaluated
-// specials: six words per segment plus the prefixes' extra words, the ring's
-// counter and 1 KB of staging; per slot its terms, two increment prefixes,
-// two flag masks and four scalars, and its ready word.
+// specials: six words per segment plus the prefixes' extra words and the
+// ring's counter; per slot its terms, two increment prefixes, two flag masks
+// and four scalars, and its ready word.
 __host__ __device__ inline size_t pz_sp_walk_lds(int nseg, int nc) {
-  return (size_t)nseg * 24 + 64 + PZ_SP_SEG * 4 + (size_t)nc * PZ_SP_SLOT +
+  return (size_t)nseg * 24 + 64 + (size_t)nc * PZ_SP_SLOT +
          (((size_t)nc * 4 + 15) & ~(size_t)15);
 }
 
@@ -917,6 +916,54 @@ __device__ __forceinline__ uint32_t pz_wave_excl_max_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x138, 0xf, 0xf, true);
 }
 
+// The segment's terms added to the state one at a time in id order with real
+// fp32 adds -- the sequential sum itself, in a systolic DPP chain: at each of
+// 64 steps every lane adds its four terms in turn to its predecessor's value
+// of the step before (wave_shr:1; lane 0 starts from the state's value), so
+// lane j holds its running sums from step j on.  With a stop mode each
+// lane's four running sums are formed again from its predecessor's final
+// value -- the same adds -- and the first that meets the stop is the hit.
+// Returns the hit's index (st = the sum including that term) or -1 (st = the
+// sum over the segment).  For every segment the one-step forms do not take
+// (a fixed 256 dependent adds, about as long as two or three of the
+// exceptional terms -- ties, terms that leave the binade, terms as large as
+// the sum -- taken one at a time).
+template <int MODE>
+__device__ __forceinline__ int pz_sp_chain(PzAcc& st, const float (&v)[4], float thr) {
+  const int lane = threadIdx.x & 63;
+  const float s = pz_acc_value(st);
+  // lane 0's first term carries the state (the shift gives lane 0 a +0.0,
+  // and +0.0 + x == x for the non-negative sums here)
+  const float a0 = lane == 0 ? s + v[0] : v[0];
+  float c = 0.0f;
+  for (int q = 0; q < 64; q += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      c = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf,
+                                                     true)) + a0;
+      c = c + v[1];
+      c = c + v[2];
+      c = c + v[3];
+    }
+  }
+  if (MODE != PZ_STOP_NONE) {
+    const float p = __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf, true));
+    const float p0 = p + a0, p1 = p0 + v[1], p2 = p1 + v[2], p3 = p2 + v[3];
+    const int i = pz_sp_first4(pz_stop_hit(p0, thr, MODE), pz_stop_hit(p1, thr, MODE),
+                               pz_stop_hit(p2, thr, MODE), pz_stop_hit(p3, thr, MODE));
+    if (i < PZ_SP_SEG) {
+      const float pr[4] = {p0, p1, p2, p3};
+      st = pz_acc_of(pz_sp_elemf(pr, i));
+      pz_sp_uni(st);
+      return i;
+    }
+  }
+  st = pz_acc_of(pz_readlane_f32(c, 63));
+  pz_sp_uni(st);
+  return -1;
+}
+
 // A special segment in the walker's registers: its terms, the increment
 // prefixes at its two grids, and per lane the flag bits (tie or big; low
 // nibble) and tie bits (high nibble) at each.
@@ -985,7 +1032,6 @@ __device__ __forceinline__ PzWalk pz_sp_walk_layout(char* lds, int nseg, int nc)
   W.rdy = (pz_lds_u32*)p;      p += ((size_t)nc * 4 + 15) & ~(size_t)15;
   W.consumed = (pz_lds_u32*)p; p += 16;
   W.s0 = W.consumed + 1;
-  W.tmp = (pz_lds_f32*)p;      p += PZ_SP_SEG * 4;
   W.d = (pz_lds_u32*)p;        p += (size_t)nseg * 4;
   W.d2 = (pz_lds_u32*)p;       p += (size_t)nseg * 4;
   W.gf = (pz_lds_u32*)p;       p += (size_t)nseg * 4;
@@ -1160,22 +1206,15 @@ __device__ __forceinline__ PzWalk pz_sp_walk_start(const X& x, PzWalk W, PzSpSha
       sc.x = g; sc.y = inf.sinfo; sc.z = inf.pt1; sc.w = inf.tc;
       *(pz_lds_u4*)(sb + PZ_SLOT_SC) = sc;
     }
-    if (j == 0 && k == 0 && lane == 0) {
-      // the row's first segment from a zero sum, where nearly every term is
-      // an event: its plain sequential fp32 sum, for the walker to take in
-      // one step (one lane, the terms read back in id order; reading them
-      // out of the wave's registers with v_readlane is slower: each add
-      // waits for the scalar register the readlane writes)
-      const pz_lds_f4* tq = (const pz_lds_f4*)sb;
-      float sum0 = 0.0f;
-      for (int i = 0; i < PZ_SP_SEG / 4; i++) {
-        const pz_f4 t4 = tq[i];
-        sum0 = sum0 + t4.x;
-        sum0 = sum0 + t4.y;
-        sum0 = sum0 + t4.z;
-        sum0 = sum0 + t4.w;
-      }
-      *W.s0 = __float_as_uint(sum0);
+    if (j == 0 && k == 0) {
+      // the row's first segment from a zero sum, where nearly every term
+      // leaves the binade: its plain sequential fp32 sum (the wave's chain
+      // of real adds), for the walker to take in one step
+      PzAcc z;
+      z.n = 0u;
+      z.g = 1u;
+      pz_sp_chain<PZ_STOP_NONE>(z, v, 0.0f);
+      if (lane == 0) *W.s0 = __float_as_uint(pz_acc_value(z));
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     if (lane == 0)
@@ -1245,224 +1284,6 @@ __device__ __forceinline__ PzWalk pz_sp_walk_setup(const X& x, int row, int nseg
   return pz_sp_walk_start(x, W, S, n_producers, s0_pre);
 }
 
-// Sequential fp32 accumulation of the segment's terms from position start,
-// one real add each, by the whole wave in lockstep (terms read from their
-// lanes): for stretches where nearly every term is an event, e.g. the start
-// of a row.  Returns the first hit index or -1.
-template <int MODE>
-__device__ __forceinline__ int pz_sp_serial(PzAcc& st, const float (&v)[4], int start, float thr) {
-  float s = pz_acc_value(st);
-  int i = start;
-  for (; i < PZ_SP_SEG && (i & 15); i++) {
-    const float sn = s + pz_sp_elemf(v, i);
-    if (MODE != PZ_STOP_NONE && pz_stop_hit(sn, thr, MODE)) {
-      st = pz_acc_of(sn);
-      return i;
-    }
-    s = sn;
-  }
-  // 16 terms per step: the reads of four lanes' terms are independent of
-  // the chain of adds and issue ahead of it
-  for (int l = i >> 2; l < 64; l += 4) {
-    float x[16];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      x[4 * j + 0] = pz_readlane_f32(v[0], l + j);
-      x[4 * j + 1] = pz_readlane_f32(v[1], l + j);
-      x[4 * j + 2] = pz_readlane_f32(v[2], l + j);
-      x[4 * j + 3] = pz_readlane_f32(v[3], l + j);
-    }
-    if (MODE == PZ_STOP_NONE) {
-#pragma unroll
-      for (int j = 0; j < 16; j++) s = s + x[j];
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const float sn = s + x[j];
-        if (pz_stop_hit(sn, thr, MODE)) {
-          st = pz_acc_of(sn);
-          return 4 * l + j;
-        }
-        s = sn;
-      }
-    }
-  }
-  st = pz_acc_of(s);
-  return -1;
-}
-
-// pz_sp_serial over terms [start, end) in LDS (tl[i]; end a multiple of 16):
-// every lane reads the same addresses (broadcast), so the chain of fp32 adds
-// takes its operands from VGPRs; the next 16 terms load while the current
-// 16 are added, and a stop is tested once per 16 terms (sums only grow: when
-// the 16th running sum does not hit, none of the 16 does).
-template <int MODE>
-__device__ __forceinline__ int pz_sp_serial_lds(PzAcc& st, const pz_lds_f32* tl, int start,
-                                                int end, float thr) {
-  float s = pz_acc_value(st);
-  int i = start;
-  for (; i < end && (i & 15); i++) {
-    const float sn = s + tl[i];
-    if (MODE != PZ_STOP_NONE && pz_stop_hit(sn, thr, MODE)) {
-      st = pz_acc_of(sn);
-      return i;
-    }
-    s = sn;
-  }
-  if (i < end) {
-    const pz_lds_f4* q = (const pz_lds_f4*)tl;
-    pz_f4 a = q[i / 4], b = q[i / 4 + 1], c = q[i / 4 + 2], d = q[i / 4 + 3];
-    for (; i < end; i += 16) {
-      const float x[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w,
-                           c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
-      if (i + 16 < end) {
-        const int n4 = (i + 16) / 4;
-        a = q[n4];
-        b = q[n4 + 1];
-        c = q[n4 + 2];
-        d = q[n4 + 3];
-      }
-      float t = s;
-#pragma unroll
-      for (int j = 0; j < 16; j++) t = t + x[j];
-      if (MODE != PZ_STOP_NONE && pz_stop_hit(t, thr, MODE)) {
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-          const float sn = s + x[j];
-          if (pz_stop_hit(sn, thr, MODE)) {
-            st = pz_acc_of(sn);
-            return i + j;
-          }
-          s = sn;
-        }
-      }
-      s = t;
-    }
-  }
-  st = pz_acc_of(s);
-  return -1;
-}
-
-// The increment dd from the state (n, g) at which the running sum meets the
-// stop (value(n + dd) >= thr, or > thr): positive floats order as their
-// bits, so the test is one integer compare.  0xffffffff: never inside the
-// binade (no stop, or a NaN threshold).
-template <int MODE>
-__device__ __forceinline__ uint32_t pz_sp_hit_room(uint32_t n, uint32_t g, float thr) {
-  if (MODE == PZ_STOP_NONE || thr != thr) return 0xffffffffu;
-  int64_t tb;  // the least bit pattern that hits
-  if (thr > 0.0f) tb = (int64_t)__float_as_uint(thr) + (MODE == PZ_STOP_GT ? 1 : 0);
-  else tb = (MODE == PZ_STOP_GT && thr == 0.0f) ? 1 : 0;
-  const int64_t need = tb - (int64_t)((g - 1u) << 23) - (int64_t)n;
-  return need <= 0 ? 0u : (need >= (int64_t)0xffffffffu ? 0xffffffffu : (uint32_t)need);
-}
-
-// One segment element by element from the state st: the next event (a
-// term that leaves the binade, a tie, a term as large as the sum, a stop
-// hit) is found from the increment prefix at the state's grid -- P at gP, Q
-// at gQ, both recomputed from the terms at any other grid -- in integer
-// arithmetic per lane and one ballot; the terms before it are one integer
-// step and the event term is taken exactly (pz_acc_add; a plain term that
-// leaves the binade with one real fp32 add).  Dense events go to the serial
-// loop (from tl, an LDS copy of the terms, when there is one).  Returns the
-// first hit index or -1.
-template <int MODE>
-__device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint32_t gP,
-                                            uint32_t (&P)[4], uint32_t fP, uint32_t gQ,
-                                            uint32_t (&Q)[4], uint32_t fQ, float thr,
-                                            const pz_lds_f32* tl = nullptr) {
-  const int lane = threadIdx.x & 63;
-  int pos = 0;
-  pz_sp_uni(st);
-  gP = (uint32_t)__builtin_amdgcn_readfirstlane((int)gP);
-  gQ = (uint32_t)__builtin_amdgcn_readfirstlane((int)gQ);
-  for (int nev = 0; pos < PZ_SP_SEG; nev++) {
-    if (nev >= 8 || (st.n == 0u && st.g == 1u)) {
-      if (!tl) return pz_sp_serial<MODE>(st, v, pos, thr);
-      // dense events (a sum still comparable to its terms, e.g. at the start
-      // of a row): up to 64 terms by real adds, then events again.  From a
-      // zero sum the zero terms before the first nonzero one change nothing
-      // (unless a zero sum already meets the stop).
-      if (st.n == 0u && st.g == 1u &&
-          !(MODE != PZ_STOP_NONE && pz_stop_hit(0.0f, thr, MODE))) {
-        bool nz[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) nz[c] = 4 * lane + c >= pos && v[c] != 0.0f;
-        pos = pz_sp_first4(nz[0], nz[1], nz[2], nz[3]);
-        if (pos >= PZ_SP_SEG) return -1;
-      }
-      const int end = ((pos + 64) & ~15) < PZ_SP_SEG ? ((pos + 64) & ~15) : PZ_SP_SEG;
-      const int r = pz_sp_serial_lds<MODE>(st, tl, pos, end, thr);
-      pz_sp_uni(st);
-      if (r >= 0 || end >= PZ_SP_SEG) return r;
-      pos = end;
-      nev = -1;
-      continue;
-    }
-    if (st.g != gP && st.g != gQ) {
-      gP = st.g;
-      gQ = st.g + 1u;
-      pz_sp_prefix4(v, gP, P, fP);
-      pz_sp_prefix4(v, gQ, Q, fQ);
-    }
-    const bool hi = st.g != gP;
-    uint32_t a[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) a[c] = hi ? Q[c] : P[c];
-    const uint32_t fl4 = hi ? fQ : fP;
-    const uint32_t before = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)a[3], 0x138, 0xf, 0xf, true);
-    const uint32_t base = pos > 0 ? pz_sp_elem(a, pos - 1) : 0u;
-    const uint32_t room = (1u << 24) - st.n;
-    const uint32_t hroom = pz_sp_hit_room<MODE>(st.n, st.g, thr);
-    const uint32_t rmin = room < hroom ? room : hroom;
-    // per lane, in integer arithmetic (no per-element booleans): bit c of m
-    // for a live element that is flagged or whose prefix reaches rmin (dd <
-    // 2^31 decides by the sign of dd - rmin; dd >= 2^31 always reaches it)
-    const int rel = 4 * lane - pos;
-    uint32_t m = 0;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const uint32_t dd = a[c] - base;
-      const uint32_t reach = (dd >> 31) | (((dd - rmin) >> 31) ^ 1u);
-      const uint32_t live = ((uint32_t)(rel + c) >> 31) ^ 1u;
-      m |= ((((fl4 >> c) & 1u) | reach) & live) << c;
-    }
-    const uint64_t ball = __ballot(m != 0u);
-    if (!ball) {
-      st.n += pz_readlane_u32(a[3], 63) - base;
-      return -1;
-    }
-    // this lane's first event: the prefix before it, its own, its term, its flag
-    const int c = (int)__builtin_ctz(m | 16u);
-    const uint32_t prv = pz_sel4(before, a[0], a[1], a[2], c);
-    const uint32_t cur = pz_sel4(a[0], a[1], a[2], a[3], c & 3);
-    const float tv = pz_sel4f(v[0], v[1], v[2], v[3], c & 3);
-    const uint32_t flg = (fl4 >> c) & 1u;
-    const int L = (int)__builtin_ctzll(ball);
-    const int i = 4 * L + __builtin_amdgcn_readlane(c, L);
-    const uint32_t prev = i == pos ? base : pz_readlane_u32(prv, L);
-    const uint32_t curL = pz_readlane_u32(cur, L);
-    const float t = pz_readlane_f32(tv, L);
-    const bool flagged = pz_readlane_u32(flg, L) != 0u;
-    st.n += prev - base;
-    if (flagged) {
-      st = pz_acc_add(st, t);  // a tie or a term as large as the sum
-    } else {
-      const uint32_t inc = curL - prev;
-      if (inc < (1u << 24) - st.n) {  // neither flagged nor leaving the binade: a stop hit
-        st.n += inc;
-        pz_sp_uni(st);
-        return i;
-      }
-      st = pz_acc_of(pz_acc_value(st) + t);  // leaves the binade: one real add
-    }
-    pz_sp_uni(st);
-    if (MODE != PZ_STOP_NONE && pz_stop_hit(pz_acc_value(st), thr, MODE)) return i;
-    pos = i + 1;
-  }
-  return -1;
-}
-
 // The common special segment in one step: at the state's grid no tie or big
 // term comes before the first term that leaves the binade, that term is
 // taken with one real fp32 add, and the rest of the segment fits the next
@@ -1470,7 +1291,7 @@ __device__ __forceinline__ int pz_sp_events(PzAcc& st, const float (&v)[4], uint
 // total decides).  Also a segment with no event at all.  Needs st.g == the
 // grid of P; Q is the prefix at the grid above.  Returns false, leaving st
 // alone, for anything else (and for a stop hit anywhere in the segment),
-// which the caller hands to pz_sp_events.
+// which the caller hands to pz_sp_chain.
 template <int MODE>
 __device__ __forceinline__ bool pz_sp_fast(PzAcc& st, const float (&v)[4], const uint32_t (&P)[4],
                                            uint32_t fP, const uint32_t (&Q)[4], uint32_t fQ,
@@ -1654,12 +1475,11 @@ __device__ __forceinline__ bool pz_sp_has2(PzAcc& st, uint32_t gf, uint32_t d2, 
 
 // Segment k from the state st when its primary record cannot serve it and
 // it has no pre-evaluated slot: the record at the grid below (HAS2), else
-// its exact terms (X::seg) through pz_sp_fast or the events.  Returns the
+// its exact terms (X::seg) through pz_sp_fast or the chain.  Returns the
 // index of a stop hit in the segment, or -1.
 template <int MODE, class X>
 __device__ __forceinline__ int pz_sp_special(PzAcc& st, const PzWalk& W, float thr, const X& x,
                                              int k) {
-  const int lane = threadIdx.x & 63;
   if (pz_sp_has2<MODE>(st, W.gf[k], W.d2[k], thr)) return -1;
   float v[4];
   uint32_t P[4], Q[4], fP, fQ;
@@ -1667,11 +1487,8 @@ __device__ __forceinline__ int pz_sp_special(PzAcc& st, const PzWalk& W, float t
   const uint32_t g0 = st.g;
   pz_sp_prefix4(v, g0, P, fP);
   pz_sp_prefix4(v, g0 + 1u, Q, fQ);
-  pz_f4 q;
-  q.x = v[0]; q.y = v[1]; q.z = v[2]; q.w = v[3];
-  ((pz_lds_f4*)W.tmp)[lane] = q;
   if (pz_sp_fast<MODE>(st, v, P, fP, Q, fQ, thr)) return -1;
-  return pz_sp_events<MODE>(st, v, g0, P, fP, g0 + 1u, Q, fQ, thr, W.tmp);
+  return pz_sp_chain<MODE>(st, v, thr);
 }
 
 // Segments [k, kend) one record at a time: runs of clean records at the
@@ -1834,15 +1651,7 @@ __device__ __forceinline__ int pz_sp_walk_run(PzAcc& st, const PzWalk& W, float 
                !pz_sp_has2<MODE>(st, pz_readlane_u32(m.gf, jl), pz_readlane_u32(m.d2, jl), thr)) {
       const uint32_t g0 = cur.g0, si = cur.sinfo;
       if (!(st.g == g0 && pz_sp_fast_pre<MODE>(st, cur, si, cur.pt1, cur.tc, thr))) {
-        uint32_t P[4], Q[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          P[c] = cur.P[c];
-          Q[c] = cur.Q[c];
-        }
-        const int r = pz_sp_events<MODE>(st, cur.v, g0, P, cur.fa & 15u, si & 0xffu, Q,
-                                         cur.fb & 15u, thr,
-                                         (pz_lds_f32*)(W.ring + (size_t)slot * PZ_SP_SLOT));
+        const int r = pz_sp_chain<MODE>(st, cur.v, thr);
         if (r >= 0) return b * PZ_SP_SEG + r;
       }
     }
