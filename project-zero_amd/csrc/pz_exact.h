@@ -153,37 +153,78 @@ __device__ __forceinline__ bool pz_stop_hit(float s, float thr, int mode) {
   return mode == PZ_STOP_GT ? (thr < s) : (mode == PZ_STOP_GE ? (s >= thr) : false);
 }
 
-// The same accumulation as pz_wave_accumulate over elements [start, end),
-// one real fp32 add per term (wave-uniform): faster when events are dense,
-// e.g. while the running sum is still smaller than the terms at the start of
-// a row.  Returns the first hit index, or -1.
-template <int C>
-__device__ __forceinline__ int pz_wave_serial(PzAcc& st, const float (&v)[C], int start, int end,
-                                              float thr, int stop_mode, float* cum) {
+// The same accumulation as pz_wave_accumulate over elements [start, 256) of
+// the 4 per lane a wave holds, by real fp32 adds in id order: a systolic DPP
+// chain in which, at each of 64 steps, every lane adds its four terms in
+// turn to its predecessor's value of the step before (wave_shr:1; the terms
+// before start count as 0, and lane 0 starts from the state's value), so
+// lane j holds its running sums from step j on.  With a stop mode, or cum,
+// each lane's four running sums are formed again from its predecessor's
+// final value -- the same adds.  A fixed 256 dependent adds: for segments
+// whose exceptional terms (ties, binade exits, terms as large as the sum)
+// are too many to take one at a time.  Returns the first hit index, or -1;
+// cum receives the running sums up to the hit.
+__device__ __forceinline__ int pz_wave_chain4(PzAcc& st, const float (&v)[4], int start, float thr,
+                                              int stop_mode, float* cum) {
   const int lane = threadIdx.x & 63;
-  float s = pz_acc_value(st);
-  int idx = start;
-  while (idx < end) {
-    const int l = idx / C;
-    float x[C];
+  const float s = pz_acc_value(st);
+  float t[4];
 #pragma unroll
-    for (int c = 0; c < C; c++) x[c] = pz_readlane_f32(v[c], l);
-    const int cs = idx - l * C;                            // first term of lane l to add
-    const int ce = end - l * C < C ? end - l * C : C;      // one past its last
+  for (int c = 0; c < 4; c++) t[c] = 4 * lane + c >= start ? v[c] : 0.0f;
+  // lane 0's first term carries the state (the shift gives lane 0 a +0.0,
+  // and +0.0 + x == x for the non-negative sums here)
+  const float a0 = lane == 0 ? s + t[0] : t[0];
+  float c = 0.0f;
+  for (int q = 0; q < 64; q += 8) {
 #pragma unroll
-    for (int c = 0; c < C; c++) {
-      const bool in = c >= cs && c < ce;
-      const float sn = s + x[c];
-      if (cum && lane == 0 && in) cum[l * C + c] = sn;
-      if (stop_mode != PZ_STOP_NONE && in && pz_stop_hit(sn, thr, stop_mode)) {
-        st = pz_acc_of(sn);
-        return l * C + c;
-      }
-      s = in ? sn : s;
+    for (int u = 0; u < 8; u++) {
+      c = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf,
+                                                     true)) + a0;
+      c = c + t[1];
+      c = c + t[2];
+      c = c + t[3];
     }
-    idx = l * C + ce;
   }
-  st = pz_acc_of(s);
+  if (stop_mode != PZ_STOP_NONE || cum) {
+    const float p = __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf, true));
+    float pc[4];
+    pc[0] = p + a0;
+    pc[1] = pc[0] + t[1];
+    pc[2] = pc[1] + t[2];
+    pc[3] = pc[2] + t[3];
+    int hit = 256;
+    if (stop_mode != PZ_STOP_NONE) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        m |= (4 * lane + e >= start && pz_stop_hit(pc[e], thr, stop_mode) ? 1u : 0u) << e;
+      const uint64_t ball = __ballot(m != 0u);
+      if (ball) {
+        const int L = (int)__builtin_ctzll(ball);
+        hit = 4 * L + (int)__builtin_ctz(pz_readlane_u32(m, L));
+      }
+    }
+    if (cum) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int idx = 4 * lane + e;
+        if (idx >= start && idx <= hit) cum[idx] = pc[e];
+      }
+    }
+    if (hit < 256) {
+      const int L = hit >> 2, e = hit & 3;
+      float h = pz_readlane_f32(pc[0], L);
+#pragma unroll
+      for (int q = 1; q < 4; q++) {
+        const float x = pz_readlane_f32(pc[q], L);
+        h = q == e ? x : h;
+      }
+      st = pz_acc_of(h);
+      return hit;
+    }
+  }
+  st = pz_acc_of(pz_readlane_f32(c, 63));
   return -1;
 }
 
@@ -199,16 +240,10 @@ __device__ __forceinline__ int pz_wave_accumulate(PzAcc& st, const float (&v)[C]
   const int lane = threadIdx.x & 63;
   int pos = start;
   int rounds = 0;
+  static_assert(C == 4, "four terms per lane");
   while (pos < 64 * C) {
-    if (++rounds > 4) {
-      // dense events: the next 64 terms one real add at a time, then rounds again
-      const int end = pos + 64 < 64 * C ? pos + 64 : 64 * C;
-      const int r = pz_wave_serial<C>(st, v, pos, end, thr, stop_mode, cum);
-      if (r >= 0) return r;
-      pos = end;
-      rounds = 0;
-      continue;
-    }
+    // past the first event: the rest of the segment by the chain of real adds
+    if (++rounds > 1) return pz_wave_chain4(st, v, pos, thr, stop_mode, cum);
     // increments at the current grid; a flagged term (tie or big) ends the
     // lane's run of plain terms
     uint32_t inc[C];

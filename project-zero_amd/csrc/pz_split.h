@@ -917,51 +917,15 @@ __device__ __forceinline__ uint32_t pz_wave_excl_max_u32(uint32_t v) {
 }
 
 // The segment's terms added to the state one at a time in id order with real
-// fp32 adds -- the sequential sum itself, in a systolic DPP chain: at each of
-// 64 steps every lane adds its four terms in turn to its predecessor's value
-// of the step before (wave_shr:1; lane 0 starts from the state's value), so
-// lane j holds its running sums from step j on.  With a stop mode each
-// lane's four running sums are formed again from its predecessor's final
-// value -- the same adds -- and the first that meets the stop is the hit.
-// Returns the hit's index (st = the sum including that term) or -1 (st = the
-// sum over the segment).  For every segment the one-step forms do not take
-// (a fixed 256 dependent adds, about as long as two or three of the
-// exceptional terms -- ties, terms that leave the binade, terms as large as
-// the sum -- taken one at a time).
+// fp32 adds -- the sequential sum itself, by the wave's DPP chain
+// (pz_wave_chain4) -- for every segment the one-step forms do not take.
+// Returns the index of a stop hit (st = the sum including that term) or -1
+// (st = the sum over the segment).
 template <int MODE>
 __device__ __forceinline__ int pz_sp_chain(PzAcc& st, const float (&v)[4], float thr) {
-  const int lane = threadIdx.x & 63;
-  const float s = pz_acc_value(st);
-  // lane 0's first term carries the state (the shift gives lane 0 a +0.0,
-  // and +0.0 + x == x for the non-negative sums here)
-  const float a0 = lane == 0 ? s + v[0] : v[0];
-  float c = 0.0f;
-  for (int q = 0; q < 64; q += 8) {
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      c = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf,
-                                                     true)) + a0;
-      c = c + v[1];
-      c = c + v[2];
-      c = c + v[3];
-    }
-  }
-  if (MODE != PZ_STOP_NONE) {
-    const float p = __int_as_float(
-        __builtin_amdgcn_update_dpp(0, __float_as_int(c), 0x138, 0xf, 0xf, true));
-    const float p0 = p + a0, p1 = p0 + v[1], p2 = p1 + v[2], p3 = p2 + v[3];
-    const int i = pz_sp_first4(pz_stop_hit(p0, thr, MODE), pz_stop_hit(p1, thr, MODE),
-                               pz_stop_hit(p2, thr, MODE), pz_stop_hit(p3, thr, MODE));
-    if (i < PZ_SP_SEG) {
-      const float pr[4] = {p0, p1, p2, p3};
-      st = pz_acc_of(pz_sp_elemf(pr, i));
-      pz_sp_uni(st);
-      return i;
-    }
-  }
-  st = pz_acc_of(pz_readlane_f32(c, 63));
+  const int r = pz_wave_chain4(st, v, 0, thr, MODE, nullptr);
   pz_sp_uni(st);
-  return -1;
+  return r;
 }
 
 // A special segment in the walker's registers: its terms, the increment
