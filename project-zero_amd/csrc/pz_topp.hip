@@ -1724,6 +1724,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_fallback(
 // (which follows; the fallback pass in this launch would spill its
 // registers).
 constexpr int WF_SORT = PZ_SP_BLOCK / 2;  // threads of the sort (waves 8..15)
+constexpr int WF_KR = 16;                  // keys per sort thread held in registers
 
 __host__ __device__ inline int pz_pow2_ceil(int v) {
   int p = 1;
@@ -1879,20 +1880,37 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
     const int tt = tid - (PZ_SP_BLOCK - WF_SORT);
     const int shw = wf_shift(all ? 0x1p-29f : e_gate * (1.0f - 0x1p-21f));
     int gen = 0;
+    // a list of at most WF_KR keys per thread is loaded once, every load in
+    // flight together, and both passes read the registers; a longer one is
+    // read twice, four keys' loads in flight per thread and trip
+    const bool inreg = m <= WF_KR * WF_SORT;
+    uint64_t kr[WF_KR];
+    if (inreg) {
+#pragma unroll
+      for (int r = 0; r < WF_KR; r++) kr[r] = tt + r * WF_SORT < m ? gkeys[tt + r * WF_SORT] : 0ull;
+    }
     for (int i = tt; i < PBINS / 2; i += WF_SORT) bcnt[i] = 0u;
     if (tt == 0) T.bmax = 0u;
     wf_sub_barrier(&sb_ctr, gen);
-    // (four keys' loads in flight per thread and trip in both passes)
-    for (int i0 = tt; i0 < m; i0 += 4 * WF_SORT) {
-      uint64_t kq[4];
+    if (inreg) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) kq[r] = i0 + r * WF_SORT < m ? gkeys[i0 + r * WF_SORT] : 0ull;
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        if (i0 + r * WF_SORT < m) {
-          const int q = wf_bin(kq[r], shw);
+      for (int r = 0; r < WF_KR; r++)
+        if (tt + r * WF_SORT < m) {
+          const int q = wf_bin(kr[r], shw);
           atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
         }
+    } else {
+      for (int i0 = tt; i0 < m; i0 += 4 * WF_SORT) {
+        uint64_t kq[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) kq[r] = i0 + r * WF_SORT < m ? gkeys[i0 + r * WF_SORT] : 0ull;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (i0 + r * WF_SORT < m) {
+            const int q = wf_bin(kq[r], shw);
+            atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
+          }
+      }
     }
     wf_sub_barrier(&sb_ctr, gen);
     // exclusive bin starts: thread tt owns bins 8 tt .. 8 tt + 7 (words 4 tt ..)
@@ -1924,17 +1942,27 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_topp_walkf(TOPP_ARGS, int pen_b
       run = s1 + c[j + 1];
     }
     wf_sub_barrier(&sb_ctr, gen);
-    for (int i0 = tt; i0 < m; i0 += 4 * WF_SORT) {
-      uint64_t kq[4];
+    if (inreg) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) kq[r] = i0 + r * WF_SORT < m ? gkeys[i0 + r * WF_SORT] : 0ull;
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        if (i0 + r * WF_SORT < m) {
-          const int q = wf_bin(kq[r], shw);
+      for (int r = 0; r < WF_KR; r++)
+        if (tt + r * WF_SORT < m) {
+          const int q = wf_bin(kr[r], shw);
           const uint32_t old = atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
-          bkeys[(old >> (16 * (q & 1))) & 0xffffu] = kq[r];
+          bkeys[(old >> (16 * (q & 1))) & 0xffffu] = kr[r];
         }
+    } else {
+      for (int i0 = tt; i0 < m; i0 += 4 * WF_SORT) {
+        uint64_t kq[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) kq[r] = i0 + r * WF_SORT < m ? gkeys[i0 + r * WF_SORT] : 0ull;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (i0 + r * WF_SORT < m) {
+            const int q = wf_bin(kq[r], shw);
+            const uint32_t old = atomicAdd((uint32_t*)&bcnt[q >> 1], 1u << (16 * (q & 1)));
+            bkeys[(old >> (16 * (q & 1))) & 0xffffu] = kq[r];
+          }
+      }
     }
     wf_sub_barrier(&sb_ctr, gen);
     if (T.bmax <= (uint32_t)TOPP_BIN_MAX) {
