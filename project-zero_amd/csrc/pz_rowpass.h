@@ -438,11 +438,25 @@ struct PzExpTerms {
   }
   __device__ __forceinline__ void prep(int e0, int n, Raw& r, float (&a)[4]) const {
     R.apply(e0, n, r);
+    if (n < 4) {  // (only at the row's end)
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      if (c >= n) r[c] = -__builtin_inff();
-      const float e = r[c] >= thr ? pz_fast_exp(r[c] - M) : 0.0f;
-      a[c] = as_p ? e * inv : e;
+      for (int c = 0; c < 4; c++)
+        if (c >= n) r[c] = -__builtin_inff();
+    }
+    if (thr == -__builtin_inff()) {
+      // no threshold: every term is estimated (exp2(-inf) = 0 past the end;
+      // the callers without a threshold have no NaN row here)
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float e = pz_fast_exp(r[c] - M);
+        a[c] = as_p ? e * inv : e;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const float e = r[c] >= thr ? pz_fast_exp(r[c] - M) : 0.0f;
+        a[c] = as_p ? e * inv : e;
+      }
     }
   }
   __device__ __forceinline__ void observe(int, const Raw&, const float (&)[4]) {}
