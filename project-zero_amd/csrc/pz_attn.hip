@@ -473,6 +473,17 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_attn_rec(AttnS
   X.as_p = false;
   X.et = (const pz_lds_u64*)etab;
   pz_sp_records(X, row, sl, A.ws, nullptr, true);
+  if (sl.k0 == 0 && threadIdx.x < 64) {
+    // the row's first segment summed from zero (the DPP chain of real adds),
+    // for the walk to start from instead of waiting for a producer
+    float v[4];
+    X.seg(0, v);
+    PzAcc z;
+    z.n = 0u;
+    z.g = 1u;
+    pz_sp_chain<PZ_STOP_NONE>(z, v, 0.0f);
+    if (threadIdx.x == 0) A.ws.rs[row].s0 = __float_as_uint(pz_acc_value(z));
+  }
 }
 
 // One workgroup per row: wave 0 walks, waves 1..15 pre-evaluate its specials.
@@ -486,6 +497,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_attn_walk(AttnSplit A) {
   const int row = blockIdx.x, len = attn_len(A, row);
   if (len <= 0) return;
   const PzRecAhead ra = pz_sp_rec_ahead(A.ws, row, A.nseg);  // in flight beside the maxima
+  const uint32_t s0 = A.ws.rs[row].s0;  // segment 0's sum (k_attn_rec)
   pz_sp_row_stat(row, A.S, A.ws, SS);
   PzRowState& rs = A.ws.rs[row];
   if (attn_bad(SS.any)) {
@@ -502,7 +514,7 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) void k_attn_walk(AttnSplit A) {
   X.inv = 1.0f;
   X.as_p = false;
   X.et = (const pz_lds_u64*)etab;
-  const PzWalk W = pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds, SS, -1, 0xffffffffu, &ra);
+  const PzWalk W = pz_sp_walk_setup(X, row, A.nseg, A.nc, A.ws, lds, SS, -1, s0, &ra);
   if (threadIdx.x < 64) {
     PzAcc st;
     pz_sp_walk<PZ_STOP_NONE>(st, W, 0.0f, X);
