@@ -415,11 +415,12 @@ __device__ __forceinline__ uint32_t pz_inc_from_estimate(float a, float d, uint3
                                                          bool* exact) {
   const uint32_t gc = g < 50u ? 50u : g;
   const float t = a * __uint_as_float((277u - gc) << 23);  // a / 2^(g - 150), exact
-  const float fl = floorf(t);
-  const float fr = t - fl;
+  // the nearest integer and the distance to it: a fraction at least the
+  // margin away from one half rounds to that integer (round to nearest)
+  const float r = __builtin_rintf(t);
   const float eps = (fabsf(d) + 3.0f) * 0x1p-22f;
-  *exact = (g < 50u) | (t >= 1048576.0f) | (fabsf(fr - 0.5f) <= t * eps + 0x1p-20f);
-  return (uint32_t)fminf(fl, 1048576.0f) + (fr > 0.5f ? 1u : 0u);
+  *exact = (g < 50u) | (t >= 1048576.0f) | (0.5f - fabsf(t - r) <= t * eps + 0x1p-20f);
+  return (uint32_t)fminf(r, 1048576.0f);
 }
 
 // Terms of one row: e = expf(y - M) for y >= thr (0 otherwise), times inv
