@@ -301,26 +301,27 @@ __device__ __forceinline__ void pz_sp_stat_slice(const Row& R, int row, const Pz
       if (k >= sl.k1) break;
       const int e0 = k * PZ_SP_SEG + 4 * lane;
       R.apply(e0, n[u], y[u]);
-      // (selects, no branches: every element of a segment but the row's last
-      // is valid)
+      if (n[u] < 4) {  // (only at the row's end: nothing past it counts)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          if (c >= n[u]) y[u][c] = -__builtin_inff();
+      }
+      // (fmaxf passes over a NaN)
       float m = -__builtin_inff();
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         const float v = y[u][c];
-        const bool ok = c < n[u];
-        nan |= ok && v != v;
-        m = fmaxf(m, ok && v == v ? v : -__builtin_inff());
+        nan |= v != v;
+        m = fmaxf(m, v);
       }
       m = pz_wave_max(m);
       if (est) {
+        // exp2(-inf) = 0 past the end; a NaN makes the row's flags say so,
+        // and the callers that ask for estimates skip such rows
         float t = 0.0f;
         if (m > -__builtin_inff() && m < __builtin_inff()) {
 #pragma unroll
-          for (int c = 0; c < 4; c++) {  // NaN fails '>'
-            const float v = y[u][c];
-            const float e = pz_fast_exp(v - m);
-            t += c < n[u] && v > -__builtin_inff() ? e : 0.0f;
-          }
+          for (int c = 0; c < 4; c++) t += pz_fast_exp(y[u][c] - m);
         }
         t = pz_wave_sum(t);
         if (lane == 0) {
