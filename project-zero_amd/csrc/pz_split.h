@@ -621,13 +621,18 @@ __device__ __forceinline__ bool pz_sp_front(const Row& R, int row, const PzSlice
       if (k >= sl.k1) break;
       const int e0 = k * PZ_SP_SEG + 4 * lane;
       R.apply(e0, n[uu], y[uu]);
+      if (n[uu] < 4) {  // (only at the row's end: -inf past it)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          if (c >= n[uu]) y[uu][c] = -__builtin_inff();
+      }
+      // (fmaxf passes over a NaN)
       float m = -__builtin_inff();
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         const float v = y[uu][c];
-        const bool ok = c < n[uu];
-        nan |= ok && v != v;
-        m = fmaxf(m, ok && v == v ? v : -__builtin_inff());
+        nan |= v != v;
+        m = fmaxf(m, v);
       }
       pz_f4 q;
       q.x = y[uu][0];
@@ -685,16 +690,21 @@ __device__ __forceinline__ bool pz_sp_front(const Row& R, int row, const PzSlice
   }
   const float M = SS.M, thr = M + thr_rel;
   // 2. the estimated mass of each segment's terms
+  // (the slice in LDS holds -inf past the row's end, whose terms are 0, and
+  // no NaN: such a row has left at meeting 1)
   for (int k = sl.k0 + w; k < sl.k1; k += PZ_SP_WAVES) {
     const int e0 = k * PZ_SP_SEG + 4 * lane;
-    int n = V - e0;
-    n = n < 0 ? 0 : (n > 4 ? 4 : n);
     const pz_f4 q = *(const pz_lds_f4*)(ybuf + (e0 - lo));
     const float y[4] = {q.x, q.y, q.z, q.w};
     float t = 0.0f;
+    if (thr == -__builtin_inff()) {
 #pragma unroll
-    for (int c = 0; c < 4; c++)
-      if (c < n && y[c] >= thr) t += pz_fast_exp(y[c] - M);
+      for (int c = 0; c < 4; c++) t += pz_fast_exp(y[c] - M);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        if (y[c] >= thr) t += pz_fast_exp(y[c] - M);
+    }
     t = pz_wave_sum(t);
     if (lane == 0) {
       F.sest[k - sl.k0] = t;

@@ -619,13 +619,18 @@ __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_topp_front(TOP
       if (k >= sl.k1) break;
       const int e0 = k * PZ_SP_SEG + 4 * lane;
       R.apply(e0, n[uu], y[uu]);
+      if (n[uu] < 4) {  // (only at the row's end: -inf past it)
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          if (c >= n[uu]) y[uu][c] = -__builtin_inff();
+      }
+      // (fmaxf passes over a NaN)
       float m = -__builtin_inff();
 #pragma unroll
-      for (int c = 0; c < 4; c++) {  // (selects)
+      for (int c = 0; c < 4; c++) {
         const float v = y[uu][c];
-        const bool ok = c < n[uu];
-        nan |= ok && v != v;
-        m = fmaxf(m, ok && v == v ? v : -__builtin_inff());
+        nan |= v != v;
+        m = fmaxf(m, v);
       }
       pz_f4 q;
       q.x = y[uu][0];
