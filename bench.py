@@ -67,7 +67,7 @@ KERNELS = {
     "c2": "k_topp_front + k_topp_walkf + k_topp_fallback",
     "c3": "k_topk",
     "c1": "k_topk",
-    "c5": "k_spec_stat + k_spec_rec + k_spec_walk + k_spec_accept + k_spec_vest + "
+    "c5": "k_spec_stat + k_spec_rec + k_spec_walk + k_spec_vest + "
           "k_spec_vrec + k_spec_vwalk",
 }
 SWEEP_B = (1, 8, 64, 256, 1024)

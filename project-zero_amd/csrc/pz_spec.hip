@@ -20,9 +20,10 @@
 //   k_spec_stat   every target and draft row: maximum, segment estimates;
 //   k_spec_rec    their exact-term records;
 //   k_spec_walk   one workgroup per row: the exact softmax normaliser;
-//   k_spec_accept one wave per sequence: the acceptance tests (one draft per
-//                 lane), the row the token is drawn from;
-//   k_spec_vest   per sequence the estimated residual (or p) mass per segment;
+//   k_spec_vest   per sequence: the acceptance tests (one draft per lane of
+//                 wave 0 in each workgroup; the first posts the outcome and
+//                 the row the token is drawn from), then the estimated
+//                 residual (or p) mass per segment;
 //   k_spec_vrec   its exact-term records;
 //   k_spec_vwalk  one workgroup per sequence: Z and the residual draw (or the
 //                 categorical draw from p), the output row.
@@ -233,10 +234,10 @@ __global__ __launch_bounds__(SPEC_WALK_BLOCK) void k_spec_walk(SpecArgs A) {
   }
 }
 
-// ---- one wave per sequence: acceptance tests ------------------------------
+// ---- acceptance tests of a sequence (one wave) ----------------------------
 template <bool VEC>
-__global__ __launch_bounds__(64) void k_spec_accept(SpecArgs A) {
-  const int b = blockIdx.x, lane = threadIdx.x;
+__device__ __forceinline__ SpecSeq spec_accept(const SpecArgs& A, int b, bool post) {
+  const int lane = threadIdx.x & 63;
   const PzRowState* rs = A.ws.rs;
   bool accept = false;
   if (lane < A.K) {
@@ -248,6 +249,8 @@ __global__ __launch_bounds__(64) void k_spec_accept(SpecArgs A) {
       accept = qv > 0.0f && A.u_acc[b * A.K + lane] < pd / qv;
     }
   }
+  SpecSeq s;
+  memset(&s, 0, sizeof(s));
   // a row whose front wait gave up fails the whole sequence
   bool failed = false;
   for (int j = lane; j < A.KT; j += 64) failed |= (rs[b * A.KT + j].flags & PZ_RS_FAILED) != 0;
@@ -255,20 +258,16 @@ __global__ __launch_bounds__(64) void k_spec_accept(SpecArgs A) {
     for (int j = lane; j < A.K; j += 64)
       failed |= (rs[A.NT + b * A.K + j].flags & PZ_RS_FAILED) != 0;
   if (__ballot(failed)) {
-    if (lane == 0) {
-      SpecSeq s;
-      memset(&s, 0, sizeof(s));
-      s.mode = SQ_DONE;
+    s.mode = SQ_DONE;
+    if (post && lane == 0) {
       A.seq[b] = s;
       A.acc_len[b] = PZ_ID_FAILED;
       for (int j = 0; j <= A.K; j++) A.ids_out[(long)b * (A.K + 1) + j] = PZ_ID_FAILED;
     }
-    return;
+    return s;
   }
   const uint64_t rej = __ballot(lane < A.K && !accept);
   const int js = rej ? (int)__builtin_ctzll(rej) : A.K;
-  if (lane != 0) return;
-  SpecSeq s;
   s.js = js;
   s.last = -1;
   s.qt = s.qd = -1;
@@ -296,12 +295,16 @@ __global__ __launch_bounds__(64) void k_spec_accept(SpecArgs A) {
       s.qt = qt;
     }
   }
-  A.seq[b] = s;
-  if (s.mode == SQ_DONE) {
-    A.acc_len[b] = js;
-    for (int j = 0; j <= A.K; j++)
-      A.ids_out[(long)b * (A.K + 1) + j] = j < js ? A.draft_ids[b * A.K + j] : (j == js ? tok : -1);
+  if (post && lane == 0) {
+    A.seq[b] = s;
+    if (s.mode == SQ_DONE) {
+      A.acc_len[b] = js;
+      for (int j = 0; j <= A.K; j++)
+        A.ids_out[(long)b * (A.K + 1) + j] =
+            j < js ? A.draft_ids[b * A.K + j] : (j == js ? tok : -1);
+    }
   }
+  return s;
 }
 
 template <bool VEC>
@@ -337,8 +340,17 @@ __device__ __forceinline__ PzExpTerms<PzTempRow<VEC>> p_terms(const SpecArgs& A,
 // ---- per sequence: estimated mass of the draw's terms per segment ----------
 template <bool VEC>
 __global__ __launch_bounds__(PZ_SP_BLOCK) PZ_SP_TWO_PER_CU void k_spec_vest(SpecArgs A) {
+  __shared__ SpecSeq s_sh;
   const int b = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const SpecSeq s = A.seq[b];
+  // the sequence's acceptance tests, by wave 0 of each of its workgroups
+  // (the same reads and ballots in each); the first posts the outcome for
+  // the launches after it, and the output row when the sequence is done
+  if (w == 0) {
+    const SpecSeq sq = spec_accept<VEC>(A, b, blockIdx.x == 0);
+    if (lane == 0) s_sh = sq;
+  }
+  __syncthreads();
+  const SpecSeq s = s_sh;
   if (s.mode == SQ_DONE) return;
   const PzSlice sl = pz_sp_slice(A.nseg, A.spw);
   const PzTempRow<VEC> T = temp_row<VEC>(A, s.qt);
@@ -556,7 +568,6 @@ int launch_spec(pz_sampler* s, SpecArgs& A) {
   hipLaunchKernelGGL(k_spec_stat<VEC>, dim3(pl.S, A.NR), block, 0, s->stream, A);
   hipLaunchKernelGGL(k_spec_rec<VEC>, dim3(pl.S, A.NR), block, 0, s->stream, A);
   hipLaunchKernelGGL(kw, dim3(A.NR), dim3(SPEC_WALK_BLOCK), walk, s->stream, A);
-  hipLaunchKernelGGL(k_spec_accept<VEC>, dim3(A.B), dim3(64), 0, s->stream, A);
   A.spw = pv.spw;
   A.S = pv.S;
   hipLaunchKernelGGL(k_spec_vest<VEC>, dim3(pv.S, A.B), block, 0, s->stream, A);
